@@ -1,0 +1,170 @@
+/*
+ * lik.h — C ABI of the MI355X (gfx950) MaxSim engine, liblik_hip.so.
+ *
+ * Every entry point takes raw device pointers, element strides and scalars,
+ * launches on the caller's HIP stream, performs no device allocation and no
+ * host synchronisation, and returns a status code (LIK_OK == 0, negative on
+ * error). Scratch memory, where an entry point needs it, is passed in by the
+ * caller; its size comes from the matching *_workspace_size() query.
+ *
+ * The reference library (late-interaction-kernels v0.4.5) has no native ABI:
+ * its "FFI" is Triton's Python launcher. Each declaration below names the
+ * reference launcher whose behaviour it replaces. The Python binding that
+ * calls these through ctypes lives in late_interaction_kernels/_lib.py.
+ */
+#ifndef LIK_H_
+#define LIK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* lik_stream_t; /* == hipStream_t */
+
+enum {
+  LIK_OK = 0,
+  LIK_ERR_INVALID = -1,     /* bad shape / pointer / argument */
+  LIK_ERR_UNSUPPORTED = -2, /* shape or dtype outside what the kernels handle */
+  LIK_ERR_WORKSPACE = -3,   /* workspace missing or too small */
+  LIK_ERR_LAUNCH = -4       /* hipLaunchKernel / hipGetLastError failure */
+};
+
+typedef enum {
+  LIK_BF16 = 0,
+  LIK_F16 = 1,
+  LIK_F32 = 2,
+  LIK_FP8_E4M3 = 3 /* OCP e4m3fn, torch.float8_e4m3fn */
+} lik_dtype_t;
+
+/*
+ * A batch of token sequences, either padded or packed:
+ *   padded: sequence i, token t at  data + i*stride_n + t*stride_l   (elements)
+ *   packed: cu_seqlens != NULL; token t of sequence i at
+ *           data + (cu_seqlens[i] + t)*stride_l, length cu_seqlens[i+1]-cu_seqlens[i]
+ * The embedding dim is contiguous (stride 1) and each token row starts on a
+ * 16-byte boundary; dim*elem_size is a multiple of 16.
+ * lengths (optional, padded only): valid length of each sequence (prefix).
+ * mask (optional, padded only): int8 keep-flags, mask[i*mask_stride_n + t*mask_stride_l].
+ * token_scale (optional, fp8 only): fp32 per-token dequant scale,
+ *           token_scale[i*scale_stride_n + t*scale_stride_l].
+ */
+typedef struct {
+  const void* data;
+  int32_t dtype;      /* lik_dtype_t */
+  int32_t dim;        /* embedding dim d */
+  int64_t n;          /* number of sequences */
+  int64_t len;        /* padded length (max length for packed input) */
+  int64_t stride_n;
+  int64_t stride_l;
+  const int32_t* cu_seqlens;
+  const int32_t* lengths;
+  const int8_t* mask;
+  int64_t mask_stride_n;
+  int64_t mask_stride_l;
+  const float* token_scale;
+  int64_t scale_stride_n;
+  int64_t scale_stride_l;
+} lik_seqs_t;
+
+/* flags for lik_maxsim */
+#define LIK_NORMALIZE 1u /* per-token L2 normalise Q and D (F.normalize, eps 1e-12) */
+#define LIK_KD_LAYOUT 2u /* D holds n = Nq*K docs; query i scores docs [i*K, (i+1)*K) */
+
+/*
+ * score[i, j] = out_scale * sum_{s valid in Q_i} max_{t valid in D_j} <Q_i[s], D_j[t]>
+ * with a row whose max ranges over no valid token contributing 0.
+ * Cross-product layout: out is [Q->n, D->n]; KD layout: out is [Q->n, D->n / Q->n].
+ * out[i*out_stride_q + j*out_stride_d], fp32.
+ *
+ * Replaces forward.py:_run_forward (forward.py:228-346) launching
+ * _maxsim_fwd_kernel (forward.py:45-186) — both the in-batch and the
+ * kd_layout variants — varlen.py:_varlen_forward (varlen.py:271-364) and
+ * fp8.py:maxsim_inference_fp8's launch of _maxsim_fp8_fwd_kernel
+ * (fp8.py:234-422; Q and D fp8, per-tensor scales passed as out_scale,
+ * per-token scales as token_scale).
+ */
+int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale,
+               float* out, int64_t out_stride_q, int64_t out_stride_d, void* workspace,
+               size_t workspace_bytes, lik_stream_t stream);
+size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags);
+
+/*
+ * Pair-list scoring: out[p] = MaxSim(Q_{pair_q[p]}, D_{pair_d[p]}).
+ * Replaces score_pairs.py:_scatter_forward / _scatter_fwd_kernel
+ * (score_pairs.py:33, launcher score_pairs.py:318).
+ */
+int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q,
+                     const int32_t* pair_d, int64_t num_pairs, uint32_t flags, float* out,
+                     lik_stream_t stream);
+
+/*
+ * PLAID compressed documents: token t of doc j has centroid code
+ * codes[tok] and packed residual bytes residuals[tok*res_stride + 0..packed_dim),
+ * tok = cu_seqlens[j] + t (packed) or j*codes_stride_n + t (padded, with
+ * lengths[j] valid tokens). Decoded token:
+ *   emb[f] = centroids[code*cent_stride + f]
+ *          + bucket_weights[(byte[f / (8/nbits)] >> ((f % (8/nbits))*nbits)) & (2^nbits-1)]
+ */
+typedef struct {
+  const int32_t* codes;
+  const uint8_t* residuals;
+  const int32_t* cu_seqlens; /* packed layout */
+  const int32_t* lengths;    /* padded layout: [n] valid lengths */
+  int64_t n;                 /* number of docs */
+  int64_t max_len;           /* padded length / max doc length */
+  int64_t codes_stride_n;    /* padded: codes row stride (tokens) */
+  int64_t res_stride_tok;    /* bytes between consecutive tokens' residuals */
+  const void* centroids;
+  int32_t centroid_dtype; /* LIK_BF16 / LIK_F16 / LIK_F32 */
+  int32_t dim;
+  int64_t n_centroids;
+  int64_t cent_stride; /* elements between centroid rows */
+  const float* bucket_weights;
+  int32_t n_buckets;
+  int32_t nbits; /* 2, 4 or 8 */
+} lik_plaid_docs_t;
+
+/*
+ * Fused PLAID decode + L2-normalise + MaxSim. out[i*out_stride_q + j*out_stride_d].
+ * Replaces plaid.py:_maxsim_residual_forward (plaid.py:404-516, kernel
+ * plaid.py:144-300) and plaid.py:maxsim_residual_varlen's launch of
+ * _maxsim_residual_varlen_kernel (plaid.py:832-963, kernel plaid.py:684-829).
+ */
+int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t flags, float* out,
+                     int64_t out_stride_q, int64_t out_stride_d, lik_stream_t stream);
+
+/*
+ * PLAID approximate (centroid-only) score: out[b] = sum_{s<Lq} max_{t<len_b} qcs[codes[b,t], s],
+ * with out-of-range codes clamped to centroid 0 and an empty doc scoring 0.
+ * Replaces plaid.py:plaid_approx_score (plaid.py:82-136, kernel plaid.py:28-79).
+ */
+int lik_plaid_approx_score(const float* qcs, int64_t n_centroids, int64_t lq, int64_t qcs_stride_c,
+                           int64_t qcs_stride_l, const int32_t* codes, int64_t B, int64_t max_len,
+                           int64_t codes_stride_b, const int64_t* doc_lengths, float* out,
+                           lik_stream_t stream);
+
+/*
+ * Chunk top-k merge. For each row r, the candidates are the running list
+ * (prev_scores[r*prev_ld + i], prev_idx[r*prev_ld + i]) for i < prev_k, and
+ * (scores[r*ld + c], idx_base + c) for c < n. Writes the k best, ordered by
+ * score (descending if largest, else ascending) and then by lower index,
+ * to out_scores/out_idx[r*out_ld + i]. k <= prev_k + n, k <= 2048,
+ * n <= 4096, indices < 2^32. prev may alias out.
+ * Replaces the torch.topk + cat + gather merge of topk.py:41-86 /
+ * retrieve.py:278-305 with a deterministic tie order (lower index first).
+ */
+int lik_topk_merge(const float* scores, int64_t rows, int64_t n, int64_t ld, int64_t idx_base,
+                   const float* prev_scores, const int64_t* prev_idx, int64_t prev_k,
+                   int64_t prev_ld, int64_t k, int largest, float* out_scores, int64_t* out_idx,
+                   int64_t out_ld, lik_stream_t stream);
+
+/* Library version string and the gfx target it was built for. */
+const char* lik_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LIK_H_ */

@@ -1,0 +1,97 @@
+"""Build liblik_hip.so (the gfx950 MaxSim engine) from csrc/ with hipcc.
+
+Usage: python build_lib.py [--jobs N]
+
+Each csrc/*.hip file is compiled to an object in parallel, then linked into
+late_interaction_kernels/_lib/liblik_hip.so, in-tree so that it ships with the
+package. Always rebuilds (a build is a few tens of seconds).
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+INCLUDE = HERE.parent / "include"
+OUT_DIR = HERE / "late_interaction_kernels" / "_lib"
+LIB_NAME = "liblik_hip.so"
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+# Packed-FP32 VALU ops are disabled for all device code.
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+
+
+def _compile(src: Path, obj: Path) -> tuple[Path, str]:
+    cmd = [hipcc(), *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    msg = "\n".join(
+        line
+        for line in (proc.stdout + proc.stderr).splitlines()
+        if "packed-fp32-ops" not in line  # host pass does not know the feature; harmless
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{msg}")
+    return obj, msg
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    OUT_DIR.mkdir(parents=True, exist_ok=True)
+    obj_dir = HERE / "_build"
+    obj_dir.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no sources in {CSRC}")
+    jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
+    objs = []
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [ex.submit(_compile, s, obj_dir / (s.stem + ".o")) for s in sources]
+        for f in futs:
+            obj, msg = f.result()
+            objs.append(obj)
+            if verbose and msg.strip():
+                print(msg, file=sys.stderr)
+    out = OUT_DIR / LIB_NAME
+    tmp = OUT_DIR / (LIB_NAME + ".tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("-v", "--verbose", action="store_true")
+    args = ap.parse_args()
+    print(build(args.jobs, args.verbose))
+
+
+if __name__ == "__main__":
+    main()

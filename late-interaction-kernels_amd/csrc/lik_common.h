@@ -1,0 +1,142 @@
+// Shared device-side definitions for the gfx950 MaxSim kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lik.h"
+
+namespace lik {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Element kinds of the token embeddings. F32 is computed as three bf16 MFMAs
+// (hi*hi + hi*lo + lo*hi), giving ~16 mantissa bits per product.
+enum { EK_BF16 = 0, EK_F16 = 1, EK_F32 = 2, EK_FP8 = 3 };
+
+// Compile-time layout of one 32-token tile for element kind EK and padded
+// embedding dim DPAD. MFMA 32x32xK: the doc tile is the A operand (32 rows =
+// doc tokens), the query block is the B operand (32 columns = query tokens).
+// Lane l holds row/column l%32; its half h=l/32 covers embedding elements
+// [h*DPAD/2, (h+1)*DPAD/2). The same element order is used for A and B, so
+// the dot product is over the same dims whatever the hardware k-ordering is.
+template <int EK, int DPAD>
+struct KT {
+  static constexpr int IN_B = EK == EK_F32 ? 4 : (EK == EK_FP8 ? 1 : 2);  // input bytes/elem
+  static constexpr int CB = EK == EK_FP8 ? 1 : 2;          // bytes/elem in LDS
+  static constexpr bool SPLIT = EK == EK_F32;
+  static constexpr int FE = EK == EK_FP8 ? 32 : 8;          // elems per lane per MFMA
+  static constexpr int KSTEPS = DPAD / (2 * FE);            // MFMAs per 32x32 tile
+  static constexpr int FRAG_B = FE * CB;                    // 16 or 32 bytes
+  static constexpr int FRAG_V = FRAG_B / 16;                // u32x4 per fragment
+  static constexpr int HALF_B = DPAD * CB / 2;
+  static constexpr int ROW_B = DPAD * CB + 16;              // +16 B pad: conflict-free ds_read_b128
+  static constexpr int TILE_B = 32 * ROW_B;
+  static constexpr int NARR = SPLIT ? 2 : 1;
+  static constexpr int CPR = DPAD * IN_B / 16;              // 16-B input chunks per row
+  static constexpr int CHUNK_E = 16 / IN_B;                 // elements per input chunk
+  static_assert(KSTEPS >= 1, "DPAD too small for element kind");
+  static_assert(CPR <= 64, "a row must be reduced within one wavefront");
+};
+
+template <int EK>
+__device__ __forceinline__ void mfma32(f32x16& c, const u32x4* a, const u32x4* b) {
+  if constexpr (EK == EK_BF16 || EK == EK_F32) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
+  } else if constexpr (EK == EK_F16) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
+                                               __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
+  } else {
+    const i32x8 av = __builtin_bit_cast(i32x8, __builtin_shufflevector(a[0], a[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    const i32x8 bv = __builtin_bit_cast(i32x8, __builtin_shufflevector(b[0], b[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    // cbsz = blgp = 0: both operands OCP fp8 e4m3; E8M0 scale 127 == 1.0.
+    c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+  }
+}
+
+__device__ __forceinline__ float bf16lo_to_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi_to_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// OCP e4m3fn -> fp32 (exact). Used only for the norms of fp8 rows.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  const uint32_t s = (b >> 7) & 1u, e = (b >> 3) & 15u, m = b & 7u;
+  float v;
+  if (e == 0) v = (float)m * 0.001953125f;  // m * 2^-9
+  else if (e == 15 && m == 7) v = __builtin_nanf("");
+  else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return s ? -v : v;
+}
+
+// Sum of squares of a 16-byte chunk of elements of kind EK (F32: 4 floats).
+template <int EK>
+__device__ __forceinline__ float chunk_sumsq(const u32x4& v) {
+  float s = 0.f;
+  if constexpr (EK == EK_BF16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = bf16lo_to_f32(v[i]), b = bf16hi_to_f32(v[i]);
+      s = fmaf(a, a, s);
+      s = fmaf(b, b, s);
+    }
+  } else if constexpr (EK == EK_F16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = f16_to_f32((uint16_t)(v[i] & 0xffffu)), b = f16_to_f32((uint16_t)(v[i] >> 16));
+      s = fmaf(a, a, s);
+      s = fmaf(b, b, s);
+    }
+  } else if constexpr (EK == EK_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = __uint_as_float(v[i]);
+      s = fmaf(a, a, s);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float a = e4m3_to_f32((v[i] >> (8 * k)) & 0xffu);
+        s = fmaf(a, a, s);
+      }
+    }
+  }
+  return s;
+}
+
+// Split 4 floats into bf16 hi and lo parts (x ~= hi + lo), packed 2 per u32.
+__device__ __forceinline__ void split4(const u32x4& v, u32x2& hi, u32x2& lo) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float a = __uint_as_float(v[2 * i]), b = __uint_as_float(v[2 * i + 1]);
+    const uint32_t ha = f32_to_bf16_bits(a), hb = f32_to_bf16_bits(b);
+    const float ra = a - __uint_as_float(ha << 16), rb = b - __uint_as_float(hb << 16);
+    hi[i] = ha | (hb << 16);
+    lo[i] = f32_to_bf16_bits(ra) | (f32_to_bf16_bits(rb) << 16);
+  }
+}
+
+__device__ __forceinline__ float inv_norm(float ss) {
+  // F.normalize: x / max(||x||, 1e-12)
+  return 1.0f / fmaxf(sqrtf(ss), 1e-12f);
+}
+
+}  // namespace lik

@@ -1,0 +1,197 @@
+"""Shared launch path for the dense-embedding MaxSim entry points.
+
+Every public scoring function (``maxsim``, ``maxsim_pairs``, ``maxsim_varlen``,
+``maxsim_padded``, ``score_pairs_packed``, ``maxsim_inference_fp8``,
+``retrieve``) normalises its inputs here and calls ``lik_maxsim`` /
+``lik_maxsim_pairs`` from liblik_hip.so.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_FP8 = getattr(torch, "float8_e4m3fn", None)
+
+
+def unify_dtype(Q: torch.Tensor, D: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Pick one compute dtype for Q and D.
+
+    bf16 if either side is bf16 (the reference's rule, ``_utils.py:137-148``),
+    fp16 if both are fp16, otherwise fp32. fp32 is computed as a three-term
+    bf16 split on the MFMA units (about 16 mantissa bits per product), where
+    the reference truncates fp32 to fp16.
+    """
+    if Q.dtype == _FP8 or D.dtype == _FP8:
+        raise TypeError("fp8 inputs go through late_interaction_kernels.fp8.maxsim_inference_fp8")
+    if not (Q.is_floating_point() and D.is_floating_point()):
+        raise TypeError(f"Q and D must be floating point; got {Q.dtype} and {D.dtype}")
+    if torch.bfloat16 in (Q.dtype, D.dtype):
+        t = torch.bfloat16
+    elif Q.dtype == torch.float16 and D.dtype == torch.float16:
+        t = torch.float16
+    else:
+        t = torch.float32
+    return Q.to(t), D.to(t)
+
+
+def _mask_i8(m: torch.Tensor | None, shape: tuple[int, int]) -> torch.Tensor | None:
+    if m is None:
+        return None
+    if tuple(m.shape) != tuple(shape):
+        m = m.expand(shape)
+    return m.to(torch.int8).contiguous()
+
+
+def _i32(t: torch.Tensor | None) -> torch.Tensor | None:
+    return None if t is None else t.to(torch.int32).contiguous()
+
+
+def dense_maxsim(
+    Q: torch.Tensor,
+    D: torch.Tensor,
+    q_mask: torch.Tensor | None = None,
+    d_mask: torch.Tensor | None = None,
+    *,
+    normalize: bool = False,
+    kd: bool = False,
+    q_lengths: torch.Tensor | None = None,
+    d_lengths: torch.Tensor | None = None,
+    q_scale: torch.Tensor | None = None,
+    d_scale: torch.Tensor | None = None,
+    out_scale: float = 1.0,
+) -> torch.Tensor:
+    """``Q[Nq, Lq, d]`` x ``D[Nd, Ld, d]`` -> ``[Nq, Nd]`` fp32 (KD: ``D[Nq*K, Ld, d]`` -> ``[Nq, K]``).
+
+    Masks are ``[N, L]`` keep-flags; lengths are valid prefix lengths per
+    sequence; scales are fp8 per-token dequant scales ``[N, L]``.
+    """
+    _lib.require_gpu(Q, D, q_mask, d_mask, q_lengths, d_lengths, q_scale, d_scale)
+    Nq, Lq, _ = Q.shape
+    Nd, Ld, _ = D.shape
+    Nd_eff = (Nd // Nq if Nq else 0) if kd else Nd
+    out = torch.empty(Nq, Nd_eff, device=Q.device, dtype=torch.float32)
+    if Nq == 0 or Nd_eff == 0:
+        return out
+    if Lq == 0 or Ld == 0:
+        return out.zero_()
+    Q = _lib.prepare_tokens(Q)
+    D = _lib.prepare_tokens(D)
+    qm = _mask_i8(q_mask, (Nq, Lq))
+    dm = _mask_i8(d_mask, (Nd, Ld))
+    ql = _i32(q_lengths)
+    dl = _i32(d_lengths)
+    qsc = None if q_scale is None else q_scale.to(torch.float32).expand(Nq, Lq).contiguous()
+    dsc = None if d_scale is None else d_scale.to(torch.float32).expand(Nd, Ld).contiguous()
+    qs = _lib.seqs(
+        Q, n=Nq, length=Lq, stride_n=Q.stride(0), stride_l=Q.stride(1), lengths=ql, mask=qm,
+        mask_strides=(qm.stride(0), qm.stride(1)) if qm is not None else (0, 0),
+        token_scale=qsc, scale_strides=(qsc.stride(0), qsc.stride(1)) if qsc is not None else (0, 0),
+    )
+    ds = _lib.seqs(
+        D, n=Nd, length=Ld, stride_n=D.stride(0), stride_l=D.stride(1), lengths=dl, mask=dm,
+        mask_strides=(dm.stride(0), dm.stride(1)) if dm is not None else (0, 0),
+        token_scale=dsc, scale_strides=(dsc.stride(0), dsc.stride(1)) if dsc is not None else (0, 0),
+    )
+    flags = (_lib.LIK_NORMALIZE if normalize else 0) | (_lib.LIK_KD_LAYOUT if kd else 0)
+    _launch(qs, ds, flags, out_scale, out, Q.device)
+    return out
+
+
+def packed_maxsim(
+    Q_packed: torch.Tensor,
+    D_packed: torch.Tensor,
+    cu_q: torch.Tensor,
+    cu_d: torch.Tensor,
+    max_q: int,
+    max_d: int,
+    *,
+    normalize: bool = False,
+) -> torch.Tensor:
+    """Packed (cu_seqlens) Q and D -> ``[Nq, Nd]`` fp32."""
+    _lib.require_gpu(Q_packed, D_packed, cu_q, cu_d)
+    Nq = cu_q.numel() - 1
+    Nd = cu_d.numel() - 1
+    out = torch.empty(max(Nq, 0), max(Nd, 0), device=Q_packed.device, dtype=torch.float32)
+    if Nq <= 0 or Nd <= 0:
+        return out
+    if max_q <= 0 or Q_packed.shape[0] == 0 or D_packed.shape[0] == 0:
+        return out.zero_()
+    Qp = _lib.prepare_tokens(Q_packed)
+    Dp = _lib.prepare_tokens(D_packed)
+    cq = _i32(cu_q)
+    cd = _i32(cu_d)
+    # max_d is not a kernel bound (each doc's tile loop ends at its own length)
+    qs = _lib.seqs(Qp, n=Nq, length=max_q, stride_l=Qp.stride(0), cu=cq)
+    ds = _lib.seqs(Dp, n=Nd, length=max(int(max_d), 0), stride_l=Dp.stride(0), cu=cd)
+    flags = _lib.LIK_NORMALIZE if normalize else 0
+    _launch(qs, ds, flags, 1.0, out, Q_packed.device)
+    return out
+
+
+def _launch(qs, ds, flags: int, out_scale: float, out: torch.Tensor, device: torch.device) -> None:
+    lib = _lib.load()
+    nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
+    ws = _lib.workspace(nbytes, device)
+    with torch.cuda.device(device):
+        rc = lib.lik_maxsim(
+            ctypes.byref(qs), ctypes.byref(ds), flags, float(out_scale), out.data_ptr(), out.stride(0),
+            out.stride(1), _lib.ptr(ws), nbytes, _lib.stream_of(out),
+        )
+    _lib.check(rc, "lik_maxsim")
+
+
+def pairs_maxsim(
+    Q_packed: torch.Tensor,
+    D_packed: torch.Tensor,
+    cu_q: torch.Tensor,
+    cu_d: torch.Tensor,
+    pair_q: torch.Tensor,
+    pair_d: torch.Tensor,
+    max_q: int,
+    max_d: int,
+) -> torch.Tensor:
+    """Pair-list MaxSim over packed Q and D -> ``[num_pairs]`` fp32."""
+    _lib.require_gpu(Q_packed, D_packed, cu_q, cu_d, pair_q, pair_d)
+    P = pair_q.numel()
+    out = torch.empty(P, device=Q_packed.device, dtype=torch.float32)
+    if P == 0:
+        return out
+    if max_q <= 0 or Q_packed.shape[0] == 0 or D_packed.shape[0] == 0:
+        return out.zero_()
+    Qp = _lib.prepare_tokens(Q_packed)
+    Dp = _lib.prepare_tokens(D_packed)
+    cq, cd, pq, pd = _i32(cu_q), _i32(cu_d), _i32(pair_q), _i32(pair_d)
+    qs = _lib.seqs(Qp, n=cq.numel() - 1, length=max_q, stride_l=Qp.stride(0), cu=cq)
+    ds = _lib.seqs(Dp, n=cd.numel() - 1, length=max(int(max_d), 0), stride_l=Dp.stride(0), cu=cd)
+    lib = _lib.load()
+    with torch.cuda.device(Q_packed.device):
+        rc = lib.lik_maxsim_pairs(
+            ctypes.byref(qs), ctypes.byref(ds), pq.data_ptr(), pd.data_ptr(), P, 0, out.data_ptr(),
+            _lib.stream_of(out),
+        )
+    _lib.check(rc, "lik_maxsim_pairs")
+    return out
+
+
+def seqlen_max(cu: torch.Tensor) -> int:
+    """Longest sequence in ``cu_seqlens`` (one device->host sync)."""
+    if cu.numel() <= 1:
+        return 0
+    return int((cu[1:] - cu[:-1]).max().item())
+
+
+def assert_max_seqlen_covers(cu: torch.Tensor, max_seqlen: int, name: str) -> None:
+    """On-device check that a caller-supplied bound covers every sequence
+    (``_utils.py:32-50``): the bound sizes the query block, so a too-small
+    value would drop tokens."""
+    if cu.numel() <= 1:
+        return
+    torch._assert_async(
+        (cu[1:] - cu[:-1]).max().le(max_seqlen),
+        f"{name}={max_seqlen} is smaller than the longest sequence in cu_seqlens; "
+        "it is a hard bound and would silently truncate tokens.",
+    )

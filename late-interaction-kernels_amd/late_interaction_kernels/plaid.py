@@ -1,0 +1,294 @@
+"""PLAID / ColBERTv2 compressed-index scoring (reference plaid.py).
+
+* :func:`plaid_approx_score` — centroid-only approximate score (IVF prune).
+* :func:`maxsim_residual` — padded ``(codes, residuals)`` decode + L2-normalise + MaxSim.
+* :func:`maxsim_residual_varlen` — the same on ragged ``cu_seqlens`` buffers
+  (the fast-plaid / ColBERTv2 on-disk layout).
+* :func:`retrieve_residual_varlen` — chunked decode+MaxSim followed by the
+  fused top-k merge, the end-to-end rerank-and-select step.
+
+A token's embedding is ``centroids[code] + bucket_weights[b_f]`` per feature
+``f``, where ``b_f`` is the ``nbits``-bit field ``f`` of the packed residual
+row, little-endian within each byte (``reference.py:124-139``). Decode,
+normalise and MaxSim are one kernel: the decoded tile only ever lives in LDS.
+Out-of-range centroid codes are clamped to 0 and bucket codes to the last
+bucket, so corrupt indices cannot fault.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._core import assert_max_seqlen_covers
+from .topk import topk_update
+
+_CENT_CODE = {torch.bfloat16: _lib.LIK_BF16, torch.float16: _lib.LIK_F16, torch.float32: _lib.LIK_F32}
+
+
+def _lq_max(d: int) -> int:
+    """Query tokens one launch holds in its column block (B-fragment VGPR budget)."""
+    return 512 if d <= 128 else 256
+
+
+def plaid_approx_score(
+    query_centroid_scores: torch.Tensor,
+    codes: torch.Tensor,
+    doc_lengths: torch.Tensor,
+) -> torch.Tensor:
+    """``out[b] = sum_s max_{t < len_b} qcs[codes[b, t], s]`` -> ``[B]`` fp32 (empty doc -> 0)."""
+    if query_centroid_scores.dim() != 2:
+        raise ValueError("query_centroid_scores must be [n_centroids, Lq]")
+    if codes.dim() != 2:
+        raise ValueError("codes must be [B, max_Ld]")
+    if doc_lengths.dim() != 1 or doc_lengths.shape[0] != codes.shape[0]:
+        raise ValueError("doc_lengths must be [B] with B matching codes")
+    _lib.require_gpu(query_centroid_scores, codes, doc_lengths)
+    qcs = query_centroid_scores.contiguous().to(torch.float32)
+    codes = codes.contiguous().to(torch.int32)
+    lens = doc_lengths.contiguous().to(torch.int64)
+    n_cent, Lq = qcs.shape
+    B, L = codes.shape
+    out = torch.empty(B, device=codes.device, dtype=torch.float32)
+    if B == 0:
+        return out
+    lib = _lib.load()
+    with torch.cuda.device(codes.device):
+        rc = lib.lik_plaid_approx_score(
+            qcs.data_ptr(), n_cent, Lq, qcs.stride(0), qcs.stride(1), codes.data_ptr(), B, L,
+            codes.stride(0), lens.data_ptr(), out.data_ptr(), _lib.stream_of(out),
+        )
+    _lib.check(rc, "lik_plaid_approx_score")
+    return out
+
+
+def _check_nbits(nbits: int) -> None:
+    if nbits not in (2, 4, 8):
+        raise ValueError(f"nbits must be 2, 4, or 8; got {nbits}")
+
+
+def _prep_q(Q: torch.Tensor) -> torch.Tensor:
+    # Compute dtype: fp16 if Q is fp16, else bf16 (reference plaid.py:914).
+    Q = Q.to(torch.float16 if Q.dtype == torch.float16 else torch.bfloat16)
+    return _lib.prepare_tokens(Q)
+
+
+def _plaid_launch(Q, docs: _lib.LikPlaidDocs, normalize: bool, out: torch.Tensor) -> None:
+    Nq, Lq, d = Q.shape
+    lib = _lib.load()
+    flags = _lib.LIK_NORMALIZE if normalize else 0
+    # Long queries: MaxSim adds over query tokens, so score column-block-sized
+    # query slices and sum them.
+    step = _lq_max(d)
+    starts = list(range(0, Lq, step)) or [0]
+    tmp = out if len(starts) == 1 else torch.empty_like(out)
+    for n, s0 in enumerate(starts):
+        Qc = Q[:, s0 : s0 + step]
+        qs = _lib.seqs(Qc, n=Nq, length=Qc.shape[1], stride_n=Qc.stride(0), stride_l=Qc.stride(1))
+        dst = out if n == 0 else tmp
+        with torch.cuda.device(Q.device):
+            rc = lib.lik_plaid_maxsim(
+                ctypes.byref(qs), ctypes.byref(docs), flags, dst.data_ptr(), dst.stride(0), dst.stride(1),
+                _lib.stream_of(dst),
+            )
+        _lib.check(rc, "lik_plaid_maxsim")
+        if n > 0:
+            out.add_(tmp)
+
+
+def _plaid_docs(codes, residuals, centroids, bucket_weights, nbits, d, *, cu=None, lengths=None,
+                n: int, max_len: int, codes_stride_n: int = 0) -> _lib.LikPlaidDocs:
+    p = _lib.LikPlaidDocs()
+    p.codes = codes.data_ptr()
+    p.residuals = residuals.data_ptr()
+    p.cu_seqlens = _lib.ptr(cu)
+    p.lengths = _lib.ptr(lengths)
+    p.n = n
+    p.max_len = max_len
+    p.codes_stride_n = codes_stride_n
+    p.res_stride_tok = residuals.shape[-1]
+    p.centroids = centroids.data_ptr()
+    p.centroid_dtype = _CENT_CODE[centroids.dtype]
+    p.dim = d
+    p.n_centroids = centroids.shape[0]
+    p.cent_stride = centroids.stride(0)
+    p.bucket_weights = bucket_weights.data_ptr()
+    p.n_buckets = bucket_weights.numel()
+    p.nbits = nbits
+    return p
+
+
+def _prep_index(residuals, centroids, bucket_weights, nbits, d):
+    if d % 8 != 0:
+        raise ValueError(f"PLAID scoring needs d % 8 == 0; got d={d}")
+    packed_dim = residuals.shape[-1]
+    expected = (d * nbits + 7) // 8
+    if packed_dim != expected:
+        raise ValueError(f"residuals last dim {packed_dim} != expected {expected} for d={d}, nbits={nbits}")
+    if centroids.dim() != 2 or centroids.shape[1] != d:
+        raise ValueError(f"centroids must be [n_centroids, d={d}]; got {tuple(centroids.shape)}")
+    if centroids.dtype not in _CENT_CODE:
+        centroids = centroids.to(torch.float32)
+    centroids = centroids.contiguous()
+    bw = bucket_weights.contiguous().to(torch.float32)
+    if not 1 <= bw.numel() <= 256:
+        raise ValueError("bucket_weights must hold 1..256 values")
+    return residuals.contiguous().to(torch.uint8), centroids, bw
+
+
+def maxsim_residual(
+    Q: torch.Tensor,
+    codes: torch.Tensor,
+    residuals: torch.Tensor,
+    doc_lengths: torch.Tensor,
+    centroids: torch.Tensor,
+    bucket_weights: torch.Tensor,
+    nbits: int,
+    *,
+    normalize: bool = True,
+) -> torch.Tensor:
+    """Fused PLAID residual decode + L2-normalise + MaxSim on padded docs.
+
+    Args:
+        Q: ``[Nq, Lq, d]`` (or ``[Lq, d]``).
+        codes: ``[Nd, max_Ld]`` integer centroid codes.
+        residuals: ``[Nd, max_Ld, ceil(d*nbits/8)]`` uint8.
+        doc_lengths: ``[Nd]`` valid lengths.
+        centroids: ``[n_centroids, d]`` fp16/bf16/fp32.
+        bucket_weights: ``[2**nbits]`` fp32.
+        nbits: 2, 4 or 8.
+    Returns:
+        ``[Nq, Nd]`` fp32 (``[Nd]`` for 2-D Q). Inference only.
+    """
+    _check_nbits(nbits)
+    if codes.dim() != 2:
+        raise ValueError("codes must be [Nd, max_Ld]")
+    if residuals.dim() != 3:
+        raise ValueError("residuals must be [Nd, max_Ld, packed_dim]")
+    q_squeeze = Q.dim() == 2
+    if q_squeeze:
+        Q = Q.unsqueeze(0)
+    if torch.is_grad_enabled() and Q.requires_grad:
+        raise NotImplementedError("maxsim_residual: gradients are not available in the MI355X build")
+    _lib.require_gpu(Q, codes, residuals, doc_lengths, centroids, bucket_weights)
+    Nq, Lq, d = Q.shape
+    Nd, L = codes.shape
+    residuals, centroids, bw = _prep_index(residuals, centroids, bucket_weights, nbits, d)
+    out = torch.empty(Nq, Nd, device=Q.device, dtype=torch.float32)
+    if Nq and Nd:
+        if Lq == 0 or L == 0:
+            out.zero_()
+        else:
+            codes = codes.contiguous().to(torch.int32)
+            lens = doc_lengths.contiguous().to(torch.int32)
+            docs = _plaid_docs(codes, residuals, centroids, bw, nbits, d, lengths=lens, n=Nd, max_len=L,
+                               codes_stride_n=L)
+            _plaid_launch(_prep_q(Q), docs, normalize, out)
+    return out.squeeze(0) if q_squeeze else out
+
+
+def maxsim_residual_varlen(
+    Q: torch.Tensor,
+    codes_flat: torch.Tensor,
+    residuals_flat: torch.Tensor,
+    cu_seqlens_d: torch.Tensor,
+    centroids: torch.Tensor,
+    bucket_weights: torch.Tensor,
+    nbits: int,
+    *,
+    max_seqlen_d: int | None = None,
+    normalize: bool = True,
+) -> torch.Tensor:
+    """Ragged PLAID decode + MaxSim on ``cu_seqlens``-indexed flat buffers.
+
+    ``max_seqlen_d`` is accepted for API compatibility (checked on device if
+    given); the kernel does not need it, so no device->host sync happens.
+    Returns ``[Nq, Nd]`` fp32 (``[Nd]`` for 2-D Q); an empty doc scores 0.
+    """
+    _check_nbits(nbits)
+    q_squeeze = Q.dim() == 2
+    if q_squeeze:
+        Q = Q.unsqueeze(0)
+    if codes_flat.dim() != 1:
+        raise ValueError("codes_flat must be 1-D [total_d_tokens]")
+    if residuals_flat.dim() != 2:
+        raise ValueError("residuals_flat must be 2-D [total_d_tokens, packed_dim]")
+    if cu_seqlens_d.dim() != 1:
+        raise ValueError("cu_seqlens_d must be 1-D [Nd + 1]")
+    if torch.is_grad_enabled() and Q.requires_grad:
+        raise NotImplementedError("maxsim_residual_varlen is inference-only")
+    _lib.require_gpu(Q, codes_flat, residuals_flat, cu_seqlens_d, centroids, bucket_weights)
+    Nq, Lq, d = Q.shape
+    residuals_flat, centroids, bw = _prep_index(residuals_flat, centroids, bucket_weights, nbits, d)
+    cu = cu_seqlens_d.contiguous().to(torch.int32)
+    Nd = cu.numel() - 1
+    if max_seqlen_d is not None:
+        assert_max_seqlen_covers(cu, int(max_seqlen_d), "max_seqlen_d")
+    out = torch.empty(Nq, max(Nd, 0), device=Q.device, dtype=torch.float32)
+    if Nq and Nd > 0:
+        if Lq == 0 or codes_flat.numel() == 0:
+            out.zero_()
+        else:
+            codes = codes_flat.contiguous().to(torch.int32)
+            docs = _plaid_docs(codes, residuals_flat, centroids, bw, nbits, d, cu=cu, n=Nd,
+                               max_len=int(max_seqlen_d or 0))
+            _plaid_launch(_prep_q(Q), docs, normalize, out)
+    return out.squeeze(0) if q_squeeze else out
+
+
+def retrieve_residual_varlen(
+    Q: torch.Tensor,
+    codes_flat: torch.Tensor,
+    residuals_flat: torch.Tensor,
+    cu_seqlens_d: torch.Tensor,
+    centroids: torch.Tensor,
+    bucket_weights: torch.Tensor,
+    nbits: int,
+    top_k: int,
+    *,
+    chunk: int | None = 4096,
+    normalize: bool = True,
+    largest: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-``top_k`` documents of a PLAID-compressed corpus per query.
+
+    Scores ``chunk`` documents at a time with :func:`maxsim_residual_varlen`
+    and folds each ``[Nq, chunk]`` block into the running top-k with the fused
+    merge (``retrieve``'s chunk semantics, ties to the lower doc index).
+    Returns ``(scores [Nq, k], indices [Nq, k])`` with ``k = min(top_k, Nd)``.
+    """
+    if top_k <= 0:
+        raise ValueError(f"top_k must be positive, got {top_k}")
+    q_squeeze = Q.dim() == 2
+    if q_squeeze:
+        Q = Q.unsqueeze(0)
+    cu = cu_seqlens_d.contiguous().to(torch.int32)
+    Nd = cu.numel() - 1
+    k = min(top_k, max(Nd, 0))
+    Nq = Q.shape[0]
+    if k == 0:
+        e = torch.empty(Nq, 0, device=Q.device)
+        return (e[0], e.long()[0]) if q_squeeze else (e, e.long())
+    cs = Nd if chunk is None or chunk >= Nd else int(chunk)
+    if cs <= 0:
+        raise ValueError(f"chunk must be positive, got {chunk}")
+    run_s = run_i = None
+    with torch.no_grad():
+        for start in range(0, Nd, cs):
+            end = min(start + cs, Nd)
+            s = maxsim_residual_varlen(Q, codes_flat, residuals_flat, cu[start : end + 1], centroids,
+                                       bucket_weights, nbits, normalize=normalize)
+            run_s, run_i = topk_update(s, start, run_s, run_i, k, largest)
+    if q_squeeze:
+        return run_s[0], run_i[0]
+    return run_s, run_i
+
+
+__all__ = [
+    "plaid_approx_score",
+    "maxsim_residual",
+    "maxsim_residual_varlen",
+    "retrieve_residual_varlen",
+]

@@ -1,0 +1,356 @@
+"""CPU oracle for the MaxSim hot path — TEST INFRASTRUCTURE ONLY.
+
+A numpy restatement of the reference library's ground truth
+(late_interaction_kernels/reference.py, fp8.py quantisers, topk.py /
+retrieve.py chunk merge). Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import it, and only as the checker (or, for the CPU
+baseline, as the thing timed on the host). The product package never
+imports it and has no CPU fallback.
+
+Arithmetic is float64 unless a function says otherwise, so the oracle is at
+least as accurate as the reference's fp32 einsum.
+
+Pinning (how each function is checked, see tests/test_oracle.py):
+  maxsim / maxsim_kd / maxsim_varlen / maxsim_pairs / maxsim_padded
+      - brute-force triple loops on tiny inputs (reference test pattern
+        tests/test_reference_cpu.py:117-145), closed forms (Q row == D row
+        after normalise -> 1; orthogonal -> 0; all-masked -> 0), and
+        cross-identities (varlen == padded, pairs == kd == per-query loop).
+  unpack_residuals / pack_residuals
+      - exact integer round trip (tests/test_reference_cpu.py:55-72) and
+        hand-computed bytes.
+  maxsim_residual(_varlen)
+      - identity buckets reduce to dense MaxSim over centroids[codes]
+        (tests/test_reference_cpu.py:81-104); decode checked on hand bytes.
+  quantize_fp8_* / e4m3_round
+      - against torch's float8_e4m3fn cast (a library RNE routine) over all
+        finite e4m3 values, midpoints and saturation.
+  topk_stable / retrieve_chunked
+      - against Python's sorted() with key (-score, index); chunked ==
+        unchunked (tests/test_retrieve_cpu.py:191-231).
+  plaid_approx_score
+      - brute force loop, empty docs -> 0, padding invariance
+        (tests/test_reference_cpu.py:25-47).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+NEG_INF = -np.inf
+
+
+# --------------------------------------------------------------------------- #
+# dense MaxSim                                                                #
+# --------------------------------------------------------------------------- #
+
+
+def _normalize(x: np.ndarray) -> np.ndarray:
+    """F.normalize(p=2, dim=-1, eps=1e-12): x / max(||x||, 1e-12) (reference.py:73-74)."""
+    n = np.sqrt((x * x).sum(-1, keepdims=True))
+    return x / np.maximum(n, 1e-12)
+
+
+def maxsim(Q, D, q_mask=None, d_mask=None, *, normalize=False, dtype=np.float64, q_chunk=64):
+    """score[i, j] = sum_{s: q_mask} max_{t: d_mask} <Q[i,s], D[j,t]>  (reference.py:26-98).
+
+    Q [Nq, Lq, d] or [Lq, d]; D [Nd, Ld, d] or [Ld, d]; masks bool [N, L] or [L].
+    A row whose max is over no token (or is non-finite) contributes 0
+    (reference.py:82-85); masked query tokens contribute 0 (reference.py:87-91).
+    2-D inputs squeeze the matching output dim.
+    """
+    Q = np.asarray(Q, dtype=dtype)
+    D = np.asarray(D, dtype=dtype)
+    q2, d2 = Q.ndim == 2, D.ndim == 2
+    if q2:
+        Q = Q[None]
+    if d2:
+        D = D[None]
+    if Q.shape[-1] != D.shape[-1]:
+        raise ValueError("embedding dims don't match")
+    if normalize:
+        Q = _normalize(Q)
+        D = _normalize(D)
+    Nq, Lq, d = Q.shape
+    Nd, Ld, _ = D.shape
+    dm = None
+    if d_mask is not None:
+        dm = np.asarray(d_mask, dtype=bool)
+        if dm.ndim == 1:
+            dm = dm[None]
+        dm = np.broadcast_to(dm, (Nd, Ld))
+    qm = None
+    if q_mask is not None:
+        qm = np.asarray(q_mask, dtype=bool)
+        if qm.ndim == 1:
+            qm = qm[None]
+        qm = np.broadcast_to(qm, (Nq, Lq))
+    Df = D.reshape(Nd * Ld, d)
+    out = np.zeros((Nq, Nd), dtype=dtype)
+    for i0 in range(0, Nq, q_chunk):
+        i1 = min(i0 + q_chunk, Nq)
+        S = (Q[i0:i1].reshape(-1, d) @ Df.T).reshape(i1 - i0, Lq, Nd, Ld)
+        if dm is not None:
+            S = np.where(dm[None, None, :, :], S, NEG_INF)
+        m = S.max(axis=-1) if Ld > 0 else np.full((i1 - i0, Lq, Nd), NEG_INF)
+        m = np.where(np.isfinite(m), m, 0.0)
+        if qm is not None:
+            m = m * qm[i0:i1, :, None]
+        out[i0:i1] = m.sum(axis=1)
+    if q2 and d2:
+        return out.reshape(())
+    if q2:
+        return out[0]
+    if d2:
+        return out[:, 0]
+    return out
+
+
+def maxsim_kd(Q, D, q_mask=None, d_mask=None, *, normalize=False, dtype=np.float64):
+    """KD layout Q [Nq, Lq, d] x D [Nq, K, Ld, d] -> [Nq, K]: query i against its own
+    K docs (the per-query loop the reference tests use, tests/test_forward.py:318-320)."""
+    Q = np.asarray(Q)
+    D = np.asarray(D)
+    Nq, K = D.shape[:2]
+    out = np.zeros((Nq, K), dtype=dtype)
+    for i in range(Nq):
+        out[i] = maxsim(
+            Q[i : i + 1], D[i],
+            None if q_mask is None else np.asarray(q_mask)[i : i + 1],
+            None if d_mask is None else np.asarray(d_mask)[i],
+            normalize=normalize, dtype=dtype,
+        )[0]
+    return out
+
+
+def maxsim_varlen(Qp, Dp, cu_q, cu_d, *, dtype=np.float64):
+    """Packed MaxSim (reference.py:213-245): empty query or doc -> 0."""
+    Qp = np.asarray(Qp, dtype=dtype)
+    Dp = np.asarray(Dp, dtype=dtype)
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_d = np.asarray(cu_d, dtype=np.int64)
+    Nq, Nd = len(cu_q) - 1, len(cu_d) - 1
+    out = np.zeros((Nq, Nd), dtype=dtype)
+    for i in range(Nq):
+        qi = Qp[cu_q[i] : cu_q[i + 1]]
+        if qi.shape[0] == 0:
+            continue
+        for j in range(Nd):
+            dj = Dp[cu_d[j] : cu_d[j + 1]]
+            if dj.shape[0] == 0:
+                continue
+            out[i, j] = (qi @ dj.T).max(axis=1).sum()
+    return out
+
+
+def maxsim_pairs(Qp, Dp, cu_q, cu_d, pair_q, pair_d, *, dtype=np.float64):
+    """Pair-list MaxSim (reference.py:248-269)."""
+    Qp = np.asarray(Qp, dtype=dtype)
+    Dp = np.asarray(Dp, dtype=dtype)
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_d = np.asarray(cu_d, dtype=np.int64)
+    out = np.zeros(len(pair_q), dtype=dtype)
+    for k, (i, j) in enumerate(zip(np.asarray(pair_q), np.asarray(pair_d))):
+        qi = Qp[cu_q[i] : cu_q[i + 1]]
+        dj = Dp[cu_d[j] : cu_d[j + 1]]
+        if qi.shape[0] == 0 or dj.shape[0] == 0:
+            continue
+        out[k] = (qi @ dj.T).max(axis=1).sum()
+    return out
+
+
+def maxsim_padded(queries, documents, query_lengths, doc_lengths, *, dtype=np.float64):
+    """[B, Lq, d] x [B, C, Ld, d] with valid prefix lengths -> [B, C] (reference.py:272-306)."""
+    Q = np.asarray(queries, dtype=dtype)
+    D = np.asarray(documents, dtype=dtype)
+    ql = np.asarray(query_lengths, dtype=np.int64)
+    dl = np.asarray(doc_lengths, dtype=np.int64)
+    B, C = D.shape[:2]
+    out = np.zeros((B, C), dtype=dtype)
+    for b in range(B):
+        q = Q[b, : ql[b]]
+        for c in range(C):
+            dd = D[b, c, : dl[b, c]]
+            if q.shape[0] == 0 or dd.shape[0] == 0:
+                continue
+            out[b, c] = (q @ dd.T).max(axis=1).sum()
+    return out
+
+
+# --------------------------------------------------------------------------- #
+# PLAID residuals                                                             #
+# --------------------------------------------------------------------------- #
+
+
+def unpack_residuals(residuals, nbits: int, d: int) -> np.ndarray:
+    """Bucket code of feature f = (byte[f // cpb] >> ((f % cpb) * nbits)) & (2^nbits - 1),
+    cpb = 8 // nbits: little-endian within each byte (reference.py:124-139)."""
+    r = np.asarray(residuals, dtype=np.uint8).astype(np.int64)
+    cpb = 8 // nbits
+    mask = (1 << nbits) - 1
+    f = np.arange(d)
+    return (r[..., f // cpb] >> ((f % cpb) * nbits)) & mask
+
+
+def pack_residuals(bucket_codes, nbits: int) -> np.ndarray:
+    """Inverse of unpack_residuals: [..., d] codes -> [..., ceil(d*nbits/8)] uint8."""
+    bc = np.asarray(bucket_codes, dtype=np.int64)
+    d = bc.shape[-1]
+    cpb = 8 // nbits
+    pd = (d * nbits + 7) // 8
+    out = np.zeros(bc.shape[:-1] + (pd,), dtype=np.int64)
+    for f in range(d):
+        out[..., f // cpb] |= bc[..., f] << ((f % cpb) * nbits)
+    return out.astype(np.uint8)
+
+
+def decode_residual_tokens(codes, residuals, centroids, bucket_weights, nbits: int, dtype=np.float64):
+    """emb = centroids[code] + bucket_weights[clamp(bucket code)] (reference.py:158-163)."""
+    cent = np.asarray(centroids, dtype=dtype)
+    bw = np.asarray(bucket_weights, dtype=dtype)
+    d = cent.shape[1]
+    bc = np.clip(unpack_residuals(residuals, nbits, d), 0, bw.size - 1)
+    return cent[np.asarray(codes, dtype=np.int64)] + bw[bc]
+
+
+def maxsim_residual(Q, codes, residuals, doc_lengths, centroids, bucket_weights, nbits, *, normalize=True,
+                    dtype=np.float64):
+    """Padded decode + (normalise) + MaxSim (reference.py:142-179)."""
+    Q = np.asarray(Q, dtype=dtype)
+    if Q.ndim == 2:
+        Q = Q[None]
+    emb = decode_residual_tokens(codes, residuals, centroids, bucket_weights, nbits, dtype)
+    L = emb.shape[1]
+    dmask = np.arange(L)[None, :] < np.asarray(doc_lengths)[:, None]
+    return maxsim(Q, emb, None, dmask, normalize=normalize, dtype=dtype)
+
+
+def maxsim_residual_varlen(Q, codes_flat, residuals_flat, cu_seqlens_d, centroids, bucket_weights, nbits, *,
+                           normalize=True, dtype=np.float64):
+    """Ragged decode + MaxSim: the varlen twin of maxsim_residual (reference plaid.py:832-963)."""
+    Q = np.asarray(Q, dtype=dtype)
+    if Q.ndim == 2:
+        Q = Q[None]
+    emb = decode_residual_tokens(codes_flat, residuals_flat, centroids, bucket_weights, nbits, dtype)
+    if normalize:
+        emb = _normalize(emb)
+        Q = _normalize(Q)
+    Nq, Lq, d = Q.shape
+    cu_q = np.arange(Nq + 1) * Lq
+    return maxsim_varlen(Q.reshape(-1, d), emb, cu_q, cu_seqlens_d, dtype=dtype)
+
+
+def plaid_approx_score(qcs, codes, doc_lengths, *, dtype=np.float64):
+    """out[b] = sum_s max_{t < len_b} qcs[codes[b,t], s]; empty doc -> 0
+    (reference.py:101-121; out-of-range codes clamp to 0 as in plaid.py:66-67)."""
+    qcs = np.asarray(qcs, dtype=dtype)
+    codes = np.asarray(codes, dtype=np.int64)
+    n_cent = qcs.shape[0]
+    codes = np.where((codes >= 0) & (codes < n_cent), codes, 0)
+    B, L = codes.shape
+    lens = np.asarray(doc_lengths, dtype=np.int64)
+    g = qcs[codes.reshape(-1)].reshape(B, L, -1)
+    mask = np.arange(L)[None, :] < lens[:, None]
+    g = np.where(mask[:, :, None], g, NEG_INF)
+    m = g.max(axis=1) if L > 0 else np.full((B, qcs.shape[1]), NEG_INF)
+    m = np.where(np.isfinite(m), m, 0.0)
+    return m.sum(axis=-1)
+
+
+# --------------------------------------------------------------------------- #
+# fp8 e4m3fn                                                                  #
+# --------------------------------------------------------------------------- #
+
+E4M3_MAX = 448.0
+
+
+def _e4m3_table() -> np.ndarray:
+    """All 127 non-negative finite e4m3fn values, ascending (bias 7, no inf,
+    S.1111.111 is NaN; subnormals m * 2^-9)."""
+    vals = []
+    for e in range(16):
+        for m in range(8):
+            if e == 15 and m == 7:
+                continue
+            vals.append(m * 2.0**-9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
+    return np.array(vals, dtype=np.float64)
+
+
+_E4M3_POS = _e4m3_table()
+
+
+def e4m3_round(x) -> np.ndarray:
+    """Round to the nearest e4m3fn value, ties to even mantissa, saturating
+    to +-448 (inputs are pre-clamped by the quantisers, fp8.py:44-46)."""
+    x = np.asarray(x, dtype=np.float64)
+    a = np.minimum(np.abs(x), E4M3_MAX)
+    hi = np.searchsorted(_E4M3_POS, a, side="left")
+    hi = np.clip(hi, 0, len(_E4M3_POS) - 1)
+    lo = np.clip(hi - 1, 0, len(_E4M3_POS) - 1)
+    vhi, vlo = _E4M3_POS[hi], _E4M3_POS[lo]
+    dlo, dhi = a - vlo, vhi - a
+    # ties: the table index parity is the mantissa parity (8 mantissas per exponent)
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    r = np.where(a == vhi, vhi, np.where(pick_hi, vhi, vlo))
+    return np.sign(x) * r
+
+
+def quantize_fp8_per_tensor(X):
+    """scale = max(amax, 1e-6) / 448; q = e4m3(clamp(x / scale, +-448)) (fp8.py:35-47).
+    Returns (dequantised-grid values as float64, scale)."""
+    X = np.asarray(X, dtype=np.float32)
+    if X.size == 0:
+        return X.astype(np.float64), np.float32(1.0)
+    amax = np.float32(max(np.abs(X).max(), np.float32(1e-6)))
+    scale = np.float32(amax / np.float32(E4M3_MAX))
+    q = e4m3_round(np.clip((X / scale).astype(np.float32), -E4M3_MAX, E4M3_MAX))
+    return q, scale
+
+
+def quantize_fp8_per_token(X):
+    """Per-row scale along the last axis (fp8.py:50-59)."""
+    X = np.asarray(X, dtype=np.float32)
+    amax = np.maximum(np.abs(X).max(axis=-1), np.float32(1e-6)).astype(np.float32)
+    scale = (amax / np.float32(E4M3_MAX)).astype(np.float32)
+    q = e4m3_round(np.clip((X / scale[..., None]).astype(np.float32), -E4M3_MAX, E4M3_MAX))
+    return q, scale
+
+
+# --------------------------------------------------------------------------- #
+# top-k                                                                       #
+# --------------------------------------------------------------------------- #
+
+
+def topk_stable(scores, k: int, *, largest=True, index_base=0):
+    """Top-k per row ordered by score (desc if largest) then lower index —
+    the deterministic tie rule the north star fixes (torch.topk leaves it open)."""
+    s = np.asarray(scores)
+    k = min(k, s.shape[-1])
+    key = -s if largest else s
+    order = np.argsort(key, axis=-1, kind="stable")[..., :k]
+    return np.take_along_axis(s, order, -1), order.astype(np.int64) + index_base
+
+
+def retrieve_chunked(scores, k: int, chunk: int | None, *, largest=True):
+    """Chunk-merge top-k over precomputed [Nq, Nd] scores, mirroring the loop of
+    topk.py:54-86 / retrieve.py:284-305 (per-chunk top-k, concat with the
+    running list, re-select min(k, width)) with the stable tie rule."""
+    s = np.asarray(scores)
+    Nd = s.shape[-1]
+    k = min(k, Nd)
+    if chunk is None or chunk >= Nd:
+        return topk_stable(s, k, largest=largest)
+    run_s = run_i = None
+    for start in range(0, Nd, chunk):
+        end = min(start + chunk, Nd)
+        cs, ci = topk_stable(s[:, start:end], min(k, end - start), largest=largest, index_base=start)
+        if run_s is None:
+            run_s, run_i = cs, ci
+        else:
+            ms = np.concatenate([run_s, cs], -1)
+            mi = np.concatenate([run_i, ci], -1)
+            key = np.stack([mi, -ms if largest else ms])  # lexsort: last key primary
+            order = np.lexsort(key, axis=-1)[..., : min(k, ms.shape[-1])]
+            run_s = np.take_along_axis(ms, order, -1)
+            run_i = np.take_along_axis(mi, order, -1)
+    return run_s, run_i

@@ -1,0 +1,215 @@
+"""GPU parity: fp8 MaxSim, PLAID decode+MaxSim, fused top-k merge, approx score.
+
+fp8 tolerance 3e-2 against the fp32 oracle on the original (unquantised)
+inputs and 2e-3 against the oracle on the exact dequantised values the kernel
+sees; PLAID 1e-2 (bf16 compute); top-k indices bit-exact against a stable
+sort (score, then lower index) of the GPU's own scores.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import lik_oracle as O
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _case(tag):
+    print(f"[case] {tag}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("Nq,Lq,Nd,Ld", [(4, 24, 16, 1030), (3, 32, 10, 77), (1, 32, 5, 64)])
+def test_fp8_per_tensor(Nq, Lq, Nd, Ld):
+    from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_tensor
+
+    _case(f"fp8 {Nq},{Lq},{Nd},{Ld}")
+    g = torch.Generator().manual_seed(Ld)
+    Q = torch.nn.functional.normalize(torch.randn(Nq, Lq, 128, generator=g), dim=-1)
+    D = torch.nn.functional.normalize(torch.randn(Nd, Ld, 128, generator=g), dim=-1)
+    Qf, sq = quantize_fp8_per_tensor(Q.cuda())
+    Df, sd = quantize_fp8_per_tensor(D.cuda())
+    got = _np(maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd))
+    ref = O.maxsim(Q.numpy(), D.numpy())
+    assert rel_err(got, ref) < 3e-2
+    deq = O.maxsim(_np(Qf) * sq.item(), _np(Df) * sd.item())
+    assert rel_err(got, deq) < 2e-3
+
+
+def test_fp8_per_token_and_masks():
+    from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_token
+
+    _case("fp8 per-token")
+    g = torch.Generator().manual_seed(8)
+    Q = torch.randn(3, 32, 128, generator=g)
+    D = torch.randn(7, 90, 128, generator=g)
+    qm = torch.rand(3, 32, generator=g) > 0.2
+    dm = torch.rand(7, 90, generator=g) > 0.2
+    Qf, sq = quantize_fp8_per_token(Q.cuda())
+    Df, sd = quantize_fp8_per_token(D.cuda())
+    got = _np(maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd, q_mask=qm.cuda(), d_mask=dm.cuda()))
+    Qd = _np(Qf) * sq.cpu().numpy()[..., None]
+    Dd = _np(Df) * sd.cpu().numpy()[..., None]
+    assert rel_err(got, O.maxsim(Qd, Dd, qm.numpy(), dm.numpy())) < 2e-3
+    assert rel_err(got, O.maxsim(Q.numpy(), D.numpy(), qm.numpy(), dm.numpy())) < 3e-2
+
+
+def _index(Nd, max_Ld, d, n_cent, nbits, seed, cdtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    cent = (torch.randn(n_cent, d, generator=g) * 0.3)
+    bw = torch.linspace(-0.1, 0.1, 2**nbits)
+    lens = torch.randint(max_Ld // 2, max_Ld + 1, (Nd,), generator=g)
+    lens[0] = 0
+    codes = torch.randint(0, n_cent, (Nd, max_Ld), generator=g)
+    bcodes = np.random.default_rng(seed).integers(0, 2**nbits, (Nd, max_Ld, d))
+    res = torch.from_numpy(O.pack_residuals(bcodes, nbits))
+    return cent.to(cdtype), bw, lens, codes, res
+
+
+@pytest.mark.parametrize("nbits", [2, 4, 8])
+@pytest.mark.parametrize("cdtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_plaid_padded(nbits, cdtype):
+    from late_interaction_kernels.plaid import maxsim_residual
+
+    _case(f"plaid padded {nbits} {cdtype}")
+    cent, bw, lens, codes, res = _index(12, 70, 128, 64, nbits, nbits, cdtype)
+    g = torch.Generator().manual_seed(1)
+    Q = torch.randn(5, 32, 128, generator=g).to(torch.bfloat16)
+    got = maxsim_residual(Q.cuda(), codes.cuda(), res.cuda(), lens.cuda(), cent.cuda(), bw.cuda(), nbits)
+    ref = O.maxsim_residual(_np(Q), codes.numpy(), res.numpy(), lens.numpy(), _np(cent), bw.numpy(), nbits)
+    gn = _np(got)
+    assert np.all(gn[:, 0] == 0)
+    assert rel_err(gn, ref) < 1e-2
+
+
+@pytest.mark.parametrize("nbits", [2, 4])
+@pytest.mark.parametrize("Nq,Lq", [(1, 32), (40, 32), (2, 600)])
+def test_plaid_varlen(nbits, Nq, Lq):
+    from late_interaction_kernels.plaid import maxsim_residual, maxsim_residual_varlen
+
+    _case(f"plaid varlen {nbits} {Nq} {Lq}")
+    cent, bw, lens, codes, res = _index(30, 90, 128, 256, nbits, 100 + nbits)
+    keep = torch.arange(90)[None] < lens[:, None]
+    codes_flat = codes[keep]
+    res_flat = res[keep]
+    cu = torch.zeros(31, dtype=torch.int32)
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    g = torch.Generator().manual_seed(Nq)
+    Q = torch.randn(Nq, Lq, 128, generator=g).to(torch.bfloat16)
+    got = maxsim_residual_varlen(Q.cuda(), codes_flat.cuda(), res_flat.cuda(), cu.cuda(), cent.cuda(), bw.cuda(),
+                                 nbits)
+    ref = O.maxsim_residual_varlen(_np(Q), codes_flat.numpy(), res_flat.numpy(), cu.numpy(), _np(cent),
+                                   bw.numpy(), nbits)
+    assert rel_err(_np(got), ref) < 1e-2
+    pad = maxsim_residual(Q.cuda(), codes.cuda(), res.cuda(), lens.cuda(), cent.cuda(), bw.cuda(), nbits)
+    assert torch.allclose(got, pad, atol=1e-4)
+
+
+def test_plaid_identity_buckets_equals_dense():
+    from late_interaction_kernels import maxsim
+    from late_interaction_kernels.plaid import maxsim_residual
+
+    _case("plaid identity")
+    g = torch.Generator().manual_seed(3)
+    cent = torch.randn(16, 64, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 16, (3, 10), generator=g)
+    res = torch.zeros(3, 10, 64, dtype=torch.uint8)
+    Q = torch.randn(2, 6, 64, generator=g).to(torch.bfloat16)
+    args = (Q.cuda(), codes.cuda(), res.cuda(), torch.full((3,), 10).cuda(), cent.cuda(), torch.zeros(256).cuda(), 8)
+    # no normalisation: decoded tokens are exactly the bf16 centroids -> same products
+    got = maxsim_residual(*args, normalize=False)
+    dense = maxsim(Q.cuda(), cent[codes].cuda(), normalize=False)
+    assert torch.allclose(got, dense, atol=1e-5)
+    # normalised: PLAID rounds the fp32-normalised token to bf16, the dense path
+    # scales the dot product instead -> equal to bf16 accuracy
+    got = maxsim_residual(*args, normalize=True)
+    dense = maxsim(Q.cuda(), cent[codes].cuda(), normalize=True)
+    assert rel_err(_np(got), _np(dense)) < 1e-2
+
+
+def test_plaid_empty_corpus():
+    from late_interaction_kernels.plaid import maxsim_residual_varlen
+
+    _case("plaid empty")
+    Q = torch.randn(2, 8, 128, device="cuda", dtype=torch.bfloat16)
+    out = maxsim_residual_varlen(Q, torch.zeros(0, dtype=torch.int32, device="cuda"),
+                                 torch.zeros(0, 32, dtype=torch.uint8, device="cuda"),
+                                 torch.zeros(1, dtype=torch.int32, device="cuda"),
+                                 torch.randn(4, 128, device="cuda"), torch.zeros(4, device="cuda"), 2)
+    assert out.shape == (2, 0)
+
+
+@pytest.mark.parametrize("largest", [True, False])
+@pytest.mark.parametrize("n,k,chunk", [(100, 10, None), (5000, 100, 4096), (9000, 1000, 2048), (37, 37, 5),
+                                       (300, 7, 1)])
+def test_topk_merge_bit_exact(largest, n, k, chunk):
+    from late_interaction_kernels.topk import topk_update
+
+    _case(f"topk {largest} {n} {k} {chunk}")
+    g = torch.Generator().manual_seed(n + k)
+    s = (torch.randint(0, 50, (6, n), generator=g).float() / 7.0)  # heavy ties
+    s[0, 3] = float("inf")
+    s[1, :] = 0.0
+    sc = s.cuda()
+    run_s = run_i = None
+    cs = n if chunk is None else chunk
+    for st in range(0, n, cs):
+        run_s, run_i = topk_update(sc[:, st:st + cs], st, run_s, run_i, k, largest)
+    ws, wi = O.topk_stable(s.numpy(), k, largest=largest)
+    np.testing.assert_array_equal(run_i.cpu().numpy(), wi)
+    np.testing.assert_array_equal(run_s.cpu().numpy(), ws)
+
+
+def test_retrieve_matches_oracle_on_gpu_scores():
+    from late_interaction_kernels import maxsim, retrieve
+
+    _case("retrieve")
+    g = torch.Generator().manual_seed(12)
+    Q = torch.randn(7, 32, 128, generator=g).to(torch.bfloat16).cuda()
+    D = torch.randn(900, 40, 128, generator=g).to(torch.bfloat16).cuda()
+    full = maxsim(Q, D, normalize=True)
+    ws, wi = O.topk_stable(full.cpu().numpy(), 50)
+    for chunk in (None, 128, 899, 4096):
+        s, i = retrieve(Q, D, top_k=50, chunk=chunk)
+        np.testing.assert_array_equal(i.cpu().numpy(), wi)
+        np.testing.assert_array_equal(s.cpu().numpy(), ws)
+
+
+def test_plaid_retrieve():
+    from late_interaction_kernels.plaid import maxsim_residual_varlen, retrieve_residual_varlen
+
+    _case("plaid retrieve")
+    cent, bw, lens, codes, res = _index(700, 40, 128, 128, 2, 77)
+    keep = torch.arange(40)[None] < lens[:, None]
+    cu = torch.zeros(701, dtype=torch.int32)
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    args = (codes[keep].cuda(), res[keep].cuda(), cu.cuda(), cent.cuda(), bw.cuda(), 2)
+    Q = torch.randn(3, 32, 128).to(torch.bfloat16).cuda()
+    full = maxsim_residual_varlen(Q, *args)
+    ws, wi = O.topk_stable(full.cpu().numpy(), 100)
+    s, i = retrieve_residual_varlen(Q, *args, 100, chunk=256)
+    np.testing.assert_array_equal(i.cpu().numpy(), wi)
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
+
+
+def test_plaid_approx_score_gpu():
+    from late_interaction_kernels.plaid import plaid_approx_score
+
+    _case("approx")
+    g = torch.Generator().manual_seed(6)
+    qcs = torch.randn(64, 32, generator=g)
+    codes = torch.randint(-3, 70, (20, 50), generator=g)
+    lens = torch.randint(0, 51, (20,), generator=g)
+    lens[3] = 0
+    got = plaid_approx_score(qcs.cuda(), codes.cuda(), lens.cuda())
+    ref = O.plaid_approx_score(qcs.numpy(), codes.numpy(), lens.numpy())
+    assert got[3].item() == 0.0
+    np.testing.assert_allclose(_np(got), ref, rtol=1e-6, atol=1e-5)

@@ -1,0 +1,247 @@
+"""Pins the CPU oracle (oracle/lik_oracle.py) before anything is checked against it.
+
+Each check is independent of the oracle's own formula: pure-Python brute
+force loops, exact known answers (tests/golden/known_answers.json, made with
+fractions.Fraction), closed forms, cross-identities between entry points,
+and torch's fp8 cast as the library routine for e4m3 rounding.
+"""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import lik_oracle as O
+
+GOLD = json.loads((Path(__file__).parent / "golden" / "known_answers.json").read_text())
+
+
+def brute(Q, D, qm=None, dm=None):
+    """Triple loop, reference tests/test_reference_cpu.py:117-145 pattern."""
+    Nq, Lq, _ = Q.shape
+    Nd, Ld, _ = D.shape
+    out = np.zeros((Nq, Nd))
+    for i in range(Nq):
+        for j in range(Nd):
+            tot = 0.0
+            for s in range(Lq):
+                if qm is not None and not qm[i, s]:
+                    continue
+                best = -np.inf
+                for t in range(Ld):
+                    if dm is not None and not dm[j, t]:
+                        continue
+                    best = max(best, float(sum(float(a) * float(b) for a, b in zip(Q[i, s], D[j, t]))))
+                tot += best if best != -np.inf else 0.0
+            out[i, j] = tot
+    return out
+
+
+@pytest.mark.parametrize("case", GOLD["maxsim"], ids=lambda c: c["name"])
+def test_oracle_known_answers(case):
+    got = O.maxsim(np.array(case["Q"], float), np.array(case["D"], float),
+                   np.array(case["q_mask"], bool), np.array(case["d_mask"], bool), normalize=case["normalize"])
+    np.testing.assert_allclose(got, np.array(case["expected"]), rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("masks", ["none", "q", "d", "both"])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_oracle_matches_bruteforce(masks, normalize):
+    rng = np.random.default_rng(7)
+    Q = rng.standard_normal((3, 5, 8))
+    D = rng.standard_normal((4, 7, 8))
+    qm = rng.random((3, 5)) > 0.3 if masks in ("q", "both") else None
+    dm = rng.random((4, 7)) > 0.3 if masks in ("d", "both") else None
+    if dm is not None:
+        dm[1] = False  # a fully masked doc
+    got = O.maxsim(Q, D, qm, dm, normalize=normalize)
+    Qb = Q / np.linalg.norm(Q, axis=-1, keepdims=True) if normalize else Q
+    Db = D / np.linalg.norm(D, axis=-1, keepdims=True) if normalize else D
+    np.testing.assert_allclose(got, brute(Qb, Db, qm, dm), atol=1e-12)
+
+
+def test_oracle_closed_forms():
+    # identical rows after normalisation: every valid query token's max is 1
+    rng = np.random.default_rng(1)
+    X = rng.standard_normal((1, 6, 16))
+    got = O.maxsim(X * 3.0, X * 0.5, normalize=True)
+    assert abs(got[0, 0] - 6.0) < 1e-12
+    # orthogonal supports: all dots 0 -> score 0
+    Q = np.zeros((1, 2, 4)); Q[0, :, :2] = 1
+    D = np.zeros((1, 3, 4)); D[0, :, 2:] = 1
+    assert O.maxsim(Q, D)[0, 0] == 0.0
+    # fully masked query row and doc contribute 0, never -inf
+    got = O.maxsim(rng.standard_normal((2, 3, 4)), rng.standard_normal((2, 3, 4)),
+                   np.array([[0, 0, 0], [1, 1, 1]], bool), np.array([[0, 0, 0], [1, 1, 1]], bool))
+    assert np.all(got[0] == 0) and np.all(got[:, 0] == 0) and np.isfinite(got).all()
+    # zero vector under normalize: eps clamp gives 0, not NaN
+    Z = np.zeros((1, 1, 4))
+    assert O.maxsim(Z, np.ones((1, 2, 4)), normalize=True)[0, 0] == 0.0
+
+
+def test_oracle_squeeze_and_1d_masks():
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((5, 8))
+    d = rng.standard_normal((6, 8))
+    assert O.maxsim(q, d).shape == ()
+    assert O.maxsim(q, d[None]).shape == (1,)
+    assert O.maxsim(q[None], d).shape == (1,)
+    qm = np.array([1, 0, 1, 1, 0], bool)
+    dm = np.array([1, 1, 0, 1, 0, 1], bool)
+    np.testing.assert_allclose(O.maxsim(q[None], d[None], qm, dm), O.maxsim(q[None], d[None], qm[None], dm[None]))
+
+
+def test_oracle_varlen_pairs_padded_kd_agree():
+    rng = np.random.default_rng(3)
+    ql = [3, 0, 5]
+    dl = [4, 1, 0, 6]
+    d = 8
+    Qp = rng.standard_normal((sum(ql), d))
+    Dp = rng.standard_normal((sum(dl), d))
+    cu_q = np.concatenate([[0], np.cumsum(ql)])
+    cu_d = np.concatenate([[0], np.cumsum(dl)])
+    v = O.maxsim_varlen(Qp, Dp, cu_q, cu_d)
+    # padded + masks view of the same data
+    Qpad = np.zeros((3, 5, d)); Dpad = np.zeros((4, 6, d))
+    for i, L in enumerate(ql):
+        Qpad[i, :L] = Qp[cu_q[i]:cu_q[i + 1]]
+    for j, L in enumerate(dl):
+        Dpad[j, :L] = Dp[cu_d[j]:cu_d[j + 1]]
+    qm = np.arange(5)[None] < np.array(ql)[:, None]
+    dm = np.arange(6)[None] < np.array(dl)[:, None]
+    np.testing.assert_allclose(v, O.maxsim(Qpad, Dpad, qm, dm), atol=1e-12)
+    pq = np.array([0, 2, 2, 1, 0])
+    pd = np.array([3, 0, 2, 1, 1])
+    np.testing.assert_allclose(O.maxsim_pairs(Qp, Dp, cu_q, cu_d, pq, pd), v[pq, pd], atol=1e-12)
+    # padded reranking == per-(b, c) loop; KD == per-query loop
+    B, C = 2, 3
+    Qb = rng.standard_normal((B, 4, d)); Db = rng.standard_normal((B, C, 5, d))
+    qlen = np.array([4, 2]); dlen = np.array([[5, 1, 3], [2, 5, 0]])
+    want = np.array([[O.maxsim(Qb[b, :qlen[b]], Db[b, c, :dlen[b, c]]) if dlen[b, c] else 0.0 for c in range(C)]
+                     for b in range(B)])
+    np.testing.assert_allclose(O.maxsim_padded(Qb, Db, qlen, dlen), want, atol=1e-12)
+    dm_kd = np.arange(5)[None, None] < dlen[:, :, None]
+    qm_kd = np.arange(4)[None] < qlen[:, None]
+    np.testing.assert_allclose(O.maxsim_kd(Qb, Db, qm_kd, dm_kd), want, atol=1e-12)
+
+
+@pytest.mark.parametrize("nbits", [2, 4, 8])
+def test_oracle_residual_pack_roundtrip(nbits):
+    rng = np.random.default_rng(nbits)
+    codes = rng.integers(0, 1 << nbits, size=(3, 7, 64))
+    packed = O.pack_residuals(codes, nbits)
+    assert packed.shape == (3, 7, 64 * nbits // 8)
+    np.testing.assert_array_equal(O.unpack_residuals(packed, nbits, 64), codes)
+
+
+@pytest.mark.parametrize("case", GOLD["residual_decode"], ids=lambda c: f"{c['nbits']}b-{len(c['bytes'])}")
+def test_oracle_residual_known_bytes(case):
+    got = O.unpack_residuals(np.array(case["bytes"], np.uint8), case["nbits"], case["d"])
+    np.testing.assert_array_equal(got, case["codes"])
+
+
+def test_oracle_residual_identity_buckets_is_dense_maxsim():
+    # reference tests/test_reference_cpu.py:81-104
+    rng = np.random.default_rng(4)
+    cent = rng.standard_normal((16, 64))
+    codes = rng.integers(0, 16, (3, 10))
+    res = np.zeros((3, 10, 64), np.uint8)
+    Q = rng.standard_normal((2, 6, 64))
+    got = O.maxsim_residual(Q, codes, res, np.full(3, 10), cent, np.zeros(256), 8, normalize=False)
+    np.testing.assert_allclose(got, O.maxsim(Q, cent[codes]), atol=1e-10)
+
+
+def test_oracle_residual_decode_formula_on_hand_values():
+    cent = np.array([[1.0, 2.0, 3.0, 4.0], [10.0, 20.0, 30.0, 40.0]])
+    bw = np.array([-0.5, 0.0, 0.25, 1.0])
+    # token codes 1; bucket fields [3, 0, 2, 1] -> byte 0b01_10_00_11 = 0x63
+    emb = O.decode_residual_tokens(np.array([1]), np.array([[0x63]], np.uint8), cent, bw, 2)
+    np.testing.assert_array_equal(emb, [[11.0, 19.5, 30.25, 40.0]])
+
+
+def test_oracle_residual_varlen_matches_padded():
+    rng = np.random.default_rng(5)
+    cent = rng.standard_normal((32, 16))
+    bw = np.linspace(-0.1, 0.1, 4)
+    lens = np.array([5, 0, 8, 3])
+    L = 8
+    codes = rng.integers(0, 32, (4, L))
+    res = O.pack_residuals(rng.integers(0, 4, (4, L, 16)), 2)
+    Q = rng.standard_normal((3, 4, 16))
+    padded = O.maxsim_residual(Q, codes, res, lens, cent, bw, 2)
+    keep = np.arange(L)[None] < lens[:, None]
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    var = O.maxsim_residual_varlen(Q, codes[keep], res[keep], cu, cent, bw, 2)
+    np.testing.assert_allclose(var, padded, atol=1e-12)
+
+
+def test_oracle_e4m3_round_matches_torch_cast():
+    import torch
+
+    grid = np.concatenate([
+        O._E4M3_POS, -O._E4M3_POS,
+        (O._E4M3_POS[1:] + O._E4M3_POS[:-1]) / 2,  # exact midpoints: ties-to-even
+        np.random.default_rng(0).uniform(-448, 448, 20000),
+        np.random.default_rng(1).uniform(-0.02, 0.02, 20000),
+    ]).astype(np.float32)
+    want = torch.from_numpy(grid).to(torch.float8_e4m3fn).to(torch.float64).numpy()
+    np.testing.assert_array_equal(O.e4m3_round(grid), want)
+
+
+def test_oracle_quantize_fp8_matches_torch_formula():
+    import torch
+
+    X = np.random.default_rng(2).standard_normal((4, 9, 16)).astype(np.float32)
+    q, s = O.quantize_fp8_per_tensor(X)
+    Xt = torch.from_numpy(X)
+    st = Xt.abs().amax().clamp_min(1e-6) / 448.0
+    qt = (Xt / st).clamp(-448, 448).to(torch.float8_e4m3fn).double().numpy()
+    assert np.float32(s) == np.float32(st.item())
+    np.testing.assert_array_equal(q, qt)
+    q2, s2 = O.quantize_fp8_per_token(X)
+    st2 = Xt.abs().amax(-1).clamp_min(1e-6) / 448.0
+    qt2 = (Xt / st2[..., None]).clamp(-448, 448).to(torch.float8_e4m3fn).double().numpy()
+    np.testing.assert_array_equal(s2, st2.numpy())
+    np.testing.assert_array_equal(q2, qt2)
+
+
+def test_oracle_topk_known_answer():
+    t = GOLD["topk"]
+    s = np.array([t["scores"]])
+    _, i = O.topk_stable(s, t["k"])
+    assert i[0].tolist() == t["largest_idx"]
+    _, i = O.topk_stable(s, t["k"], largest=False)
+    assert i[0].tolist() == t["smallest_idx"]
+
+
+@pytest.mark.parametrize("largest", [True, False])
+def test_oracle_topk_matches_sorted_and_chunking(largest):
+    rng = np.random.default_rng(6)
+    s = rng.integers(0, 6, (5, 97)).astype(np.float32)  # many ties
+    k = 13
+    for r in range(5):
+        want = sorted(range(97), key=lambda c: ((-s[r, c]) if largest else s[r, c], c))[:k]
+        _, i = O.topk_stable(s[r:r + 1], k, largest=largest)
+        assert i[0].tolist() == want
+    full = O.retrieve_chunked(s, k, None, largest=largest)
+    for chunk in (1, 4, 10, 13, 50, 96):
+        got = O.retrieve_chunked(s, k, chunk, largest=largest)
+        np.testing.assert_array_equal(got[1], full[1])
+        np.testing.assert_array_equal(got[0], full[0])
+
+
+def test_oracle_plaid_approx():
+    rng = np.random.default_rng(8)
+    qcs = rng.standard_normal((20, 6))
+    codes = rng.integers(-2, 22, (4, 7))  # includes out-of-range codes
+    lens = np.array([0, 3, 7, 1])
+    got = O.plaid_approx_score(qcs, codes, lens)
+    assert got[0] == 0.0
+    for b in range(1, 4):
+        cc = [c if 0 <= c < 20 else 0 for c in codes[b, : lens[b]]]
+        want = sum(max(qcs[c, s] for c in cc) for s in range(6))
+        assert abs(got[b] - want) < 1e-12
+    # padding beyond the length does not matter
+    codes2 = codes.copy(); codes2[1, 3:] = 0
+    np.testing.assert_allclose(O.plaid_approx_score(qcs, codes2, lens)[1], got[1])

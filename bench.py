@@ -1,0 +1,319 @@
+"""Benchmark of the MaxSim hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Default workload (the configuration BASELINE.json quotes its MaxSim TFLOP/s
+on, configs[1]): ColBERT-scale in-batch scoring, bf16, Q[512, 32, 128] x
+D[4096, 300, 128], values N(0,1) L2-normalised per token, document valid
+length ~ U[50, 300] as a prefix d_mask. One step = one ``maxsim(Q, D,
+d_mask=...)`` call over the whole batch (inputs resident in HBM).
+
+Other workloads (``--workload``): ``kd`` (D_kd[512, 64, 300, 128], HBM-bound),
+``varlen`` (65,536 packed docs, log-uniform [16, 2048] tokens, 256 queries),
+``fp8`` (ColPali Q[256, 24, 128] x D[8192, 1030, 128] e4m3), ``plaid``
+(1M compressed docs, 1,024 queries, retrieve top-100 with chunk 4096),
+``inbatch_norm`` (the default with normalize=True).
+
+Prints one JSON line (rank 0). ``value`` is the algorithmic throughput of
+the whole step: valid FLOPs 2*d*sum(Lq)*sum(Ld_valid) per second for the
+MFMA-bound workloads, algorithmic bytes per second for ``kd``, queries per
+second for ``plaid``. ``roofline`` prices the dominant kernel against the
+MI355X peak (bf16 dense MFMA 2.5 PFLOP/s, fp8 5.0 PFLOP/s, HBM 8 TB/s).
+``cpu_baseline`` times the repo's CPU oracle (oracle/lik_oracle.py, numpy on
+the host cores) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "late-interaction-kernels_amd"))
+
+PEAK = {"bf16": 2500.0, "fp8": 5000.0, "hbm": 8000.0}  # TFLOP/s, TFLOP/s, GB/s
+
+
+def _sync():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+def _time_steps(fn, steps: int, warmup: int) -> float:
+    """ms per step: W untimed steps, then K steps between events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    _sync()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    _sync()
+    return start.elapsed_time(end) / steps
+
+
+def _normed(shape, gen, dtype):
+    import torch
+
+    x = torch.randn(*shape, generator=gen, device="cuda", dtype=torch.float32)
+    x = torch.nn.functional.normalize(x, dim=-1)
+    return x.to(dtype)
+
+
+def _cpu_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        n = [i.get("num_threads", 0) for i in threadpool_info() if i.get("user_api") == "blas"]
+        if n:
+            return max(n)
+    except Exception:
+        pass
+    return os.cpu_count() or 1
+
+
+# --------------------------------------------------------------------------- #
+# workloads                                                                   #
+# --------------------------------------------------------------------------- #
+
+
+def wl_inbatch(args, normalize=False):
+    import numpy as np
+    import torch
+
+    from late_interaction_kernels import maxsim
+
+    Nq, Lq, Nd, Ld, d = 512, 32, 4096, 300, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    Q = _normed((Nq, Lq, d), g, torch.bfloat16)
+    D = _normed((Nd, Ld, d), g, torch.bfloat16)
+    dlen = torch.randint(50, Ld + 1, (Nd,), generator=g, device="cuda")
+    dm = torch.arange(Ld, device="cuda")[None] < dlen[:, None]
+    flops = 2.0 * d * (Nq * Lq) * float(dlen.sum().item())
+
+    def step():
+        return maxsim(Q, D, d_mask=dm, normalize=normalize)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "MaxSim TFLOP/s (% MFMA peak) bf16/fp8; PLAID retrieve queries/s at top-100",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4),
+        "dtype": "bf16",
+        "config": {"workload": "in-batch MaxSim bf16 (BASELINE configs[1])", "Nq": Nq, "Lq": Lq, "Nd": Nd,
+                   "Ld": Ld, "d": d, "doc_valid_len": "U[50,300] prefix d_mask", "normalize": normalize,
+                   "valid_flops_per_step": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK["bf16"], 4), "traffic": None},
+    }
+    if args.cpu_baseline:
+        import lik_oracle as O
+
+        nqs = args.cpu_sample_queries
+        Qs = Q[:nqs].float().cpu().numpy()
+        Ds = D.float().cpu().numpy()
+        dms = dm.cpu().numpy()
+        t0 = time.perf_counter()
+        O.maxsim(Qs, Ds, None, dms, normalize=normalize, dtype=np.float32, q_chunk=1)
+        dt = time.perf_counter() - t0
+        cpu_flops = 2.0 * d * (nqs * Lq) * float(dlen.sum().item())
+        res["cpu_baseline"] = {"value": round(cpu_flops / dt / 1e12, 5), "unit": "TFLOP/s",
+                               "cores": _cpu_threads(), "kind": "port",
+                               "sample": f"{nqs} of {Nq} queries x all {Nd} docs (oracle/lik_oracle.maxsim, "
+                                         f"numpy fp32), {dt:.1f} s"}
+    return res
+
+
+def wl_kd(args):
+    import torch
+
+    from late_interaction_kernels import maxsim
+
+    Nq, K, Lq, Ld, d = 512, 64, 32, 300, 128
+    g = torch.Generator(device="cuda").manual_seed(1)
+    Q = _normed((Nq, Lq, d), g, torch.bfloat16)
+    D = torch.empty(Nq, K, Ld, d, device="cuda", dtype=torch.bfloat16)
+    for i in range(0, Nq, 64):  # chunked init keeps the fp32 temporary small
+        D[i:i + 64] = _normed((64, K, Ld, d), g, torch.bfloat16)
+    dlen = torch.randint(50, Ld + 1, (Nq, K), generator=g, device="cuda")
+    dm = torch.arange(Ld, device="cuda")[None, None] < dlen[..., None]
+
+    def step():
+        return maxsim(Q, D, d_mask=dm, normalize=False)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    # algorithmic bytes: every valid doc token once + masks + Q + out
+    nbytes = float(dlen.sum().item()) * d * 2 + dm.numel() + Q.numel() * 2 + Nq * K * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "MaxSim KD-layout GB/s", "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 4),
+        "dtype": "bf16",
+        "config": {"workload": "KD layout D_kd[512,64,300,128] (BASELINE configs[1])", "bytes_per_step": nbytes,
+                   "padded_bytes": D.numel() * 2},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm"], "unit": "GB/s",
+                     "frac": round(gbs / PEAK["hbm"], 4), "traffic": None},
+    }
+
+
+def wl_varlen(args):
+    import torch
+
+    from late_interaction_kernels import maxsim_varlen
+
+    Nd, Nq, Lq, d = 65536, 256, 32, 128
+    g = torch.Generator(device="cuda").manual_seed(2)
+    u = torch.rand(Nd, generator=g, device="cuda")
+    lens = torch.floor(torch.exp(math.log(16) + u * (math.log(2049) - math.log(16)))).clamp(16, 2048).long()
+    cu_d = torch.zeros(Nd + 1, dtype=torch.int32, device="cuda")
+    cu_d[1:] = lens.cumsum(0).to(torch.int32)
+    tot = int(cu_d[-1].item())
+    Dp = torch.empty(tot, d, device="cuda", dtype=torch.bfloat16)
+    for s in range(0, tot, 1 << 22):
+        e = min(tot, s + (1 << 22))
+        Dp[s:e] = _normed((e - s, d), g, torch.bfloat16)
+    Qp = _normed((Nq * Lq, d), g, torch.bfloat16)
+    cu_q = torch.arange(0, (Nq + 1) * Lq, Lq, device="cuda", dtype=torch.int32)
+
+    def step():
+        return maxsim_varlen(Qp, Dp, cu_q, cu_d, max_seqlen_q=Lq, max_seqlen_d=2048)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    flops = 2.0 * d * Nq * Lq * tot
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "MaxSim varlen TFLOP/s", "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+        "dtype": "bf16",
+        "config": {"workload": "varlen 65,536 docs log-U[16,2048], 256x32 queries (BASELINE configs[2])",
+                   "doc_tokens": tot, "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK["bf16"], 4), "traffic": None},
+    }
+
+
+def wl_fp8(args):
+    import torch
+
+    from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_tensor
+
+    Nq, Lq, Nd, Ld, d = 256, 24, 8192, 1030, 128
+    g = torch.Generator(device="cuda").manual_seed(3)
+    Qf, sq = quantize_fp8_per_tensor(_normed((Nq, Lq, d), g, torch.float32))
+    D8 = torch.empty(Nd, Ld, d, device="cuda", dtype=torch.float8_e4m3fn)
+    Dn = [_normed((512, Ld, d), g, torch.bfloat16) for _ in range(Nd // 512)]
+    amax = max(float(x.abs().amax().item()) for x in Dn)
+    sd = torch.tensor(max(amax, 1e-6) / 448.0, device="cuda")
+    for i, x in enumerate(Dn):
+        D8[i * 512:(i + 1) * 512] = (x.float() / sd).clamp(-448, 448).to(torch.float8_e4m3fn)
+    del Dn
+
+    def step():
+        return maxsim_inference_fp8(Qf, D8, scale_Q=sq, scale_D=sd)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    flops = 2.0 * d * Nq * Lq * Nd * Ld
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "MaxSim fp8 TFLOP/s", "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+        "dtype": "fp8-e4m3",
+        "config": {"workload": "ColPali fp8 Q[256,24,128] x D[8192,1030,128] (BASELINE configs[3])",
+                   "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["fp8"], "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK["fp8"], 4), "traffic": None},
+    }
+
+
+def wl_plaid(args):
+    import torch
+
+    from late_interaction_kernels.plaid import retrieve_residual_varlen
+
+    Nd, Nq, Lq, d, ncent, nbits = args.plaid_docs, args.plaid_queries, 32, 128, 65536, 2
+    g = torch.Generator(device="cuda").manual_seed(4)
+    lens = torch.randint(30, 301, (Nd,), generator=g, device="cuda")
+    cu = torch.zeros(Nd + 1, dtype=torch.int32, device="cuda")
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    tot = int(cu[-1].item())
+    cent = _normed((ncent, d), g, torch.bfloat16)
+    codes = torch.randint(0, ncent, (tot,), generator=g, device="cuda", dtype=torch.int32)
+    res = torch.randint(0, 256, (tot, d * nbits // 8), generator=g, device="cuda", dtype=torch.uint8)
+    bw = torch.linspace(-0.1, 0.1, 4, device="cuda")
+    Q = _normed((Nq, Lq, d), g, torch.bfloat16)
+
+    def step():
+        return retrieve_residual_varlen(Q, codes, res, cu, cent, bw, nbits, 100, chunk=4096)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    qps = Nq / (ms * 1e-3)
+    flops = 2.0 * d * Nq * Lq * tot
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "PLAID retrieve queries/s at top-100", "value": round(qps, 1), "unit": "queries/s",
+        "ms_per_step": round(ms, 3), "dtype": "bf16",
+        "config": {"workload": f"PLAID {Nd} docs U[30,300], {Nq}x32 queries, nbits=2, top-100, chunk 4096 "
+                               "(BASELINE configs[4])", "doc_tokens": tot, "flops_per_step": flops,
+                   "compressed_bytes": tot * (4 + d * nbits // 8)},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK["bf16"], 4), "traffic": None},
+    }
+
+
+WORKLOADS = {
+    "inbatch": wl_inbatch,
+    "inbatch_norm": lambda a: wl_inbatch(a, normalize=True),
+    "kd": wl_kd,
+    "varlen": wl_varlen,
+    "fp8": wl_fp8,
+    "plaid": wl_plaid,
+}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="inbatch")
+    ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    ap.add_argument("--cpu-sample-queries", type=int, default=16)
+    ap.add_argument("--plaid-docs", type=int, default=1_000_000)
+    ap.add_argument("--plaid-queries", type=int, default=1024)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build's hot path runs on a single MI355X "
+              "(multi-GPU sharding is described in DESIGN.md, not built). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if args.workload != "inbatch":
+        args.cpu_baseline = False  # the CPU baseline is defined on the default workload
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    res = WORKLOADS[args.workload](args)
+    out = {
+        "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": res["dtype"], "data": "synthetic (seeded N(0,1), L2-normalised)",
+        "config": res["config"], "roofline": res["roofline"],
+    }
+    if "cpu_baseline" in res:
+        out["cpu_baseline"] = res["cpu_baseline"]
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

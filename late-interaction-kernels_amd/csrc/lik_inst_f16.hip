@@ -1,0 +1,9 @@
+// Instantiations of the dense MaxSim kernel for f16 tokens, all features
+// selected at run time (FEAT = F_ALL).
+#include "lik_kernel.h"
+
+namespace lik {
+int launch_dense_f16_generic(const Plan& pl, const Params& p, int64_t nb, hipStream_t s) {
+  return launch_dpad<EK_F16, SRC_DENSE, 0, F_ALL>(pl, p, nb, s);
+}
+}  // namespace lik

@@ -1,0 +1,22 @@
+// Instantiations of the dense MaxSim kernel for fp8 tokens at d <= 128 with
+// the feature set compiled to exactly what the call uses (fewer live scalars,
+// no dead branches in the tile loop). Anything else goes to the generic
+// instantiation.
+#include "lik_kernel.h"
+
+namespace lik {
+int launch_dense_fp8_generic(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
+
+int launch_dense_fp8(const Plan& pl, const Params& p, int64_t nb, hipStream_t s) {
+  if (pl.dpad == 128) {
+    switch (needed_feat(p)) {
+    case 0: return launch_cfg<EK_FP8, 128, SRC_DENSE, 0, 0>(pl, p, nb, s);
+    case F_MASK: return launch_cfg<EK_FP8, 128, SRC_DENSE, 0, F_MASK>(pl, p, nb, s);
+    case F_TS: return launch_cfg<EK_FP8, 128, SRC_DENSE, 0, F_TS>(pl, p, nb, s);
+    case F_TS | F_MASK: return launch_cfg<EK_FP8, 128, SRC_DENSE, 0, F_TS | F_MASK>(pl, p, nb, s);
+      default: break;
+    }
+  }
+  return launch_dense_fp8_generic(pl, p, nb, s);
+}
+}  // namespace lik

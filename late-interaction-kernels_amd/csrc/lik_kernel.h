@@ -40,15 +40,12 @@ __device__ __forceinline__ uint32_t span_bytes(int64_t len, int64_t stride, int6
 // A tile of the workgroup's sequence: tile t of the m-th non-empty document.
 // Everything else about the document lives in the LDS table s_nz.
 struct Tile {
-  int m;    // index into s_nz; >= nnz: past the end
-  int t;    // tile index within the doc
-  int len;  // doc length in tokens
-};
-struct DocInfo {
-  int k;      // doc index within the workgroup's range (jl - jl0)
-  int len;    // tokens
-  int start;  // packed layouts: first token row
-  bool holes; // dense + mask: a dropped token inside [0, len)
+  int m;       // index into s_nz; >= nnz: past the end
+  int t;       // tile index within the doc
+  int len;     // doc length in tokens
+  int k;       // doc index within the workgroup's range (jl - jl0)
+  int start;   // packed layouts: first token row of the doc
+  bool holes;  // dense + mask: a dropped token inside [0, len)
 };
 
 constexpr int kRMax = 512;  // docs per workgroup (host caps R)
@@ -76,14 +73,17 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) char s_tile[2][T::NARR][T::TILE_B];
   __shared__ __attribute__((aligned(16))) float s_rs[3][32];
   __shared__ __attribute__((aligned(16))) float s_rb[3][32];
-  // per-unit partial sums of one doc: unit t owns kmax slots, one per 32-column
-  // block it touches; QPG * kmax <= 2*COLS + COLS/32 for any unit length.
-  __shared__ float s_part[2 * COLS + COLS / 32 + 2];
+  // Finished documents: per-column maxima (already scaled, 0 for invalid
+  // columns) of the last 16 docs and their local indices. A half (8 docs) is
+  // summed per unit and written out one iteration after it fills.
+  constexpr int NSLOT = 16;
+  __shared__ __attribute__((aligned(16))) float s_colb[NSLOT][COLS];
+  __shared__ int s_slotk[NSLOT];
   __shared__ float s_bw[SRC == SRC_PLAID ? 256 : 1];
   __shared__ int32_t s_dstart[kRMax];
   __shared__ int32_t s_dlen[kRMax];  // length | holes << 31
   __shared__ __attribute__((aligned(16))) i32x4 s_nz[kRMax];  // {k, length | holes << 31, start, 0}
-  __shared__ int s_nnz;
+  __shared__ int s_nnz, s_ntiles;
 
   const bool f_mask = (FEAT & F_MASK) && p.d.mask != nullptr;
   const bool f_ts = (FEAT & F_TS) && p.d.ts != nullptr;
@@ -91,7 +91,6 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   const bool f_cu = (FEAT & F_CU) && p.d.cu != nullptr;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wv = tid >> 6, h = lane >> 5, l32 = lane & 31;
-  const int kmax = (p.LU + 31) / 32 + 1;
 
   int64_t g, r;
   {
@@ -212,47 +211,55 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   }
   __syncthreads();
   if (wv == 0) {
-    int base = 0;
+    int base = 0, ntl = 0;
     for (int k0 = 0; k0 < nloc; k0 += 64) {
       const int k = k0 + lane;
       const int v = k < nloc ? s_dlen[k] : 0;
-      const bool nz = (v & 0x7fffffff) > 0;
+      const int L = v & 0x7fffffff;
+      const bool nz = L > 0;
       const uint64_t bal = __ballot(nz);
       const int pos = base + (int)__popcll(bal & ((1ull << lane) - 1ull));
       if (nz) s_nz[pos] = (i32x4){k, v, s_dstart[k], 0};
       base += (int)__popcll(bal);
+      int nt = (L + 31) >> 5;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) nt += __shfl_xor(nt, o);
+      ntl += nt;
     }
-    if (lane == 0) s_nnz = base;
+    if (lane == 0) {
+      s_nnz = base;
+      s_ntiles = ntl;
+    }
   }
   __syncthreads();
   const int nnz = __builtin_amdgcn_readfirstlane(s_nnz);
+  const int ntiles = __builtin_amdgcn_readfirstlane(s_ntiles);
   if (nnz == 0) return;
 
-  auto doc_info = [&](int m) -> DocInfo {
-    const i32x4 e = s_nz[m];
-    DocInfo d;
-    d.k = __builtin_amdgcn_readfirstlane(e[0]);
-    const int v = __builtin_amdgcn_readfirstlane(e[1]);
-    d.len = v & 0x7fffffff;
-    d.holes = v < 0;
-    d.start = __builtin_amdgcn_readfirstlane(e[2]);
-    return d;
-  };
-  auto tile_at = [&](int m) -> Tile {
-    Tile x;
-    x.m = m;
-    x.t = 0;
-    x.len = m < nnz ? doc_info(m).len : 0;
-    return x;
-  };
-  auto tile_next = [&](const Tile& c) -> Tile {
-    if (c.m >= nnz) return c;
-    if ((c.t + 1) * 32 < c.len) {
-      Tile n = c;
-      n.t = c.t + 1;
-      return n;
+  // Cursor over the workgroup's tile sequence: tile t of the m-th non-empty
+  // doc. The doc fields are refreshed from the LDS table only when the cursor
+  // crosses a document boundary.
+  auto cur_load = [&](Tile& c, int m) {
+    c.m = m;
+    c.t = 0;
+    if (m < nnz) {
+      const i32x4 e = s_nz[m];
+      c.k = __builtin_amdgcn_readfirstlane(e[0]);
+      const int v = __builtin_amdgcn_readfirstlane(e[1]);
+      c.len = v & 0x7fffffff;
+      c.holes = v < 0;
+      c.start = __builtin_amdgcn_readfirstlane(e[2]);
+    } else {
+      c.k = 0;
+      c.len = 0;
+      c.holes = false;
+      c.start = 0;
     }
-    return tile_at(c.m + 1);
+  };
+  auto cur_adv = [&](Tile& c) {
+    if (c.m >= nnz) return;
+    if ((c.t + 1) * 32 < c.len) ++c.t;
+    else cur_load(c, c.m + 1);
   };
 
   // ---------------- staging: fetch (global -> VGPR ring) and commit (-> LDS) ----------------
@@ -275,8 +282,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     if constexpr (SRC == SRC_PLAID) {
       constexpr int S = decltype(SS)::value;
       if (x.m >= nnz) return;
-      const DocInfo di = doc_info(x.m);
-      const int64_t tok0 = p.pl.cu ? (int64_t)di.start : dglob(jl0 + di.k) * p.pl.codes_sn;
+      const int64_t tok0 = p.pl.cu ? (int64_t)x.start : dglob(jl0 + x.k) * p.pl.codes_sn;
       const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.pl.codes + tok0, sat_u32((int64_t)x.len * 4));
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
@@ -293,10 +299,9 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   auto fetch_data = [&](auto SS, const Tile& x) {
     constexpr int S = decltype(SS)::value;
     if (x.m >= nnz) return;
-    const DocInfo di = doc_info(x.m);
-    const int64_t doc = dglob(jl0 + di.k);
+    const int64_t doc = dglob(jl0 + x.k);
     if constexpr (SRC == SRC_DENSE) {
-      const char* base = f_cu ? p.d.data + (int64_t)di.start * p.d.sl_b : p.d.data + doc * p.d.sn_b;
+      const char* base = f_cu ? p.d.data + (int64_t)x.start * p.d.sl_b : p.d.data + doc * p.d.sn_b;
       const __amdgpu_buffer_rsrc_t rd =
           make_rsrc(base, sat_u32((int64_t)(x.len - 1) * p.d.sl_b + (int64_t)p.d.dim * T::IN_B));
 #pragma unroll
@@ -336,7 +341,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
         }
       }
     } else {
-      const int64_t tok0 = p.pl.cu ? (int64_t)di.start : doc * p.pl.codes_sn;
+      const int64_t tok0 = p.pl.cu ? (int64_t)x.start : doc * p.pl.codes_sn;
       const __amdgpu_buffer_rsrc_t rcent = make_rsrc(p.pl.cent, sat_u32(p.pl.ncent * p.pl.cent_sb));
       const __amdgpu_buffer_rsrc_t rres =
           make_rsrc(p.pl.res + tok0 * p.pl.res_st, sat_u32((int64_t)x.len * p.pl.res_st));
@@ -441,14 +446,19 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   };
 
   // ---------------- compute pieces ----------------
-  f32x16 acc[2][NSUB];
+  // W=8: two waves of one workgroup share a SIMD, so each wave double-buffers
+  // its accumulators and overlaps tile i's MFMAs with tile i-1's epilogue.
+  // W<=4: a single accumulator set keeps a wave under 256 registers, so two
+  // workgroups fit per CU and hide each other's epilogues and barriers.
+  constexpr bool DACC = W == 8;
+  f32x16 acc[DACC ? 2 : 1][NSUB];
   float m[NSUB];
 #pragma unroll
   for (int sub = 0; sub < NSUB; ++sub) m[sub] = NEG_INF;
   const bool dense_fix = SRC == SRC_DENSE && (f_norm || f_ts);
 
   auto mma_tile = [&](auto PP, int buf) {
-    constexpr int P = decltype(PP)::value;
+    constexpr int P = DACC ? decltype(PP)::value : 0;
     const char* A = s_tile[buf][0] + l32 * T::ROW_B + h * T::HALF_B;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -480,12 +490,43 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     }
   };
 
+  int nend = 0;  // documents finished so far
+
+  // Sum the per-column maxima of finished docs [s0, s0+n) per unit and write
+  // scores: one thread per (doc, unit), columns added in a fixed (rotated)
+  // order, so results are bitwise reproducible.
+  auto flush = [&](int s0, int n) {
+    const int tasks = n * p.QPG;
+    for (int task = tid; task < tasks; task += NT) {
+      const int sl = (s0 + task / p.QPG) % NSLOT;
+      const int t = task % p.QPG;
+      const int64_t u = unit_of(t);
+      if (u >= p.nunits) continue;
+      const float* cv = &s_colb[sl][t * p.LU];
+      float sum = 0.f;
+      if ((p.LU & 3) == 0) {
+        const int nv = p.LU >> 2;
+        int c = t % nv;
+        for (int j = 0; j < nv; ++j) {
+          const f32x4 v = *(const f32x4*)(cv + 4 * c);
+          sum += v[0];
+          sum += v[1];
+          sum += v[2];
+          sum += v[3];
+          c = (c + 1 == nv) ? 0 : c + 1;
+        }
+      } else {
+        for (int j = 0; j < p.LU; ++j) sum += cv[j];
+      }
+      p.out[u * p.osq + (jl0 + s_slotk[sl]) * p.osd] = sum * p.out_scale;
+    }
+  };
+
   auto epilogue = [&](auto PP, const Tile& x, int rslot) {
-    constexpr int P = decltype(PP)::value;
+    constexpr int P = DACC ? decltype(PP)::value : 0;
     const bool partial = (x.t + 1) * 32 > x.len;
     bool fix = dense_fix || partial;
-    const DocInfo di = doc_info(x.m);
-    if constexpr (SRC == SRC_DENSE) fix = fix || di.holes;
+    if constexpr (SRC == SRC_DENSE) fix = fix || x.holes;
     if (fix) {
       f32x4 sc[4], bi[4];
 #pragma unroll
@@ -505,96 +546,94 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) m[sub] = fmaxf(m[sub], acc[P][sub][e]);
     }
-    if ((x.t + 1) * 32 >= x.len) {  // last tile of the doc: per-column max -> per-unit sum
-      // Columns of one unit are contiguous. A segmented inclusive scan over
-      // the 32 columns of each block leaves one partial per (unit, block) at
-      // the segment's last lane; partials go to LDS and one thread per unit
-      // adds its (at most kmax) partials in block order: deterministic.
+    if ((x.t + 1) * 32 >= x.len) {  // last tile of the doc: park the per-column maxima
+      const int sl = nend % NSLOT;
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
-        const float mm = fmaxf(m[sub], __shfl_xor(m[sub], 32));
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
+        const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over lanes l, l^32
+        if (h == 0) s_colb[sl][(wv * NSUB + sub) * 32 + l32] = __builtin_isfinite(mm) ? mm * qsc[sub] : 0.f;
         m[sub] = NEG_INF;
-        const int blk = wv * NSUB + sub;
-        const int col = blk * 32 + l32;
-        const int ul = col / p.LU;
-        float v = (__builtin_isfinite(mm) && ul < p.QPG) ? mm * qsc[sub] : 0.f;
-        const int seg0 = max(ul * p.LU - blk * 32, 0);  // first lane of this lane's unit in the block
-#pragma unroll
-        for (int d = 1; d < 32; d <<= 1) {
-          const float o = __shfl_up(v, d, 32);
-          if (l32 - d >= seg0) v += o;
-        }
-        const bool seg_end = l32 == 31 || col + 1 == (ul + 1) * p.LU;
-        if (h == 0 && seg_end && ul < p.QPG) s_part[ul * kmax + (blk - (ul * p.LU) / 32)] = v;
       }
-      __syncthreads();
-      for (int t = tid; t < p.QPG; t += NT) {
-        const int64_t u = unit_of(t);
-        if (u < p.nunits) {
-          const int nparts = (t * p.LU + p.LU - 1) / 32 - (t * p.LU) / 32 + 1;
-          float sum = 0.f;
-          for (int k = 0; k < nparts; ++k) sum += s_part[t * kmax + k];
-          p.out[u * p.osq + (jl0 + di.k) * p.osd] = sum * p.out_scale;
-        }
-      }
+      if (tid == 0) s_slotk[sl] = x.k;
+      ++nend;
     }
   };
 
   // ---------------- prologue ----------------
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  Tile tm1;
-  tm1.m = nnz;
-  tm1.t = 0;
-  tm1.len = 0;
-  Tile t0 = tile_at(0);
-  Tile t1 = tile_next(t0);
-  Tile t2 = tile_next(t1);
-  Tile t3 = tile_next(t2);
-  Tile t4 = tile_next(t3);
-  fetch_codes(I0{}, t0);
-  fetch_codes(I1{}, t1);
-  fetch_data(I0{}, t0);
-  fetch_data(I1{}, t1);
-  fetch_codes(I0{}, t2);
-  fetch_codes(I1{}, t3);
-  int rs_commit = 0;  // s_rs/s_rb slot of the tile committed next
-  commit(I0{}, t0, 0, rs_commit);
-  rs_commit = 1;
-  fetch_data(I0{}, t2);
+  // cursors: ce epilogue (tile i-1), cm commit (i+1), cf fetch (i+3), cp codes (i+4)
+  Tile ce, cm, cf, cp;
+  cur_load(ce, 0);
+  cm = ce;
+  fetch_codes(I0{}, cm);  // tile 0
+  fetch_data(I0{}, cm);
+  cur_adv(cm);            // tile 1
+  fetch_codes(I1{}, cm);
+  fetch_data(I1{}, cm);
+  cf = cm;
+  cur_adv(cf);            // tile 2
+  fetch_codes(I0{}, cf);
+  cp = cf;
+  cur_adv(cp);            // tile 3
+  fetch_codes(I1{}, cp);
+  commit(I0{}, ce, 0, 0); // tile 0 -> LDS[0], row slot 0
+  fetch_data(I0{}, cf);   // tile 2 into slot 0
+  cf = cp;                // tile 3
+  cur_adv(cp);            // tile 4
   __syncthreads();
-  int rs_epi = 0;  // slot of the tile whose epilogue runs next
+  int rs_commit = 1;      // row-scale slot of tile i+1
+  int rs_epi = 0;         // row-scale slot of tile i-1
+  int flush_half = -1;    // slot half whose flush is due (after the barrier it waited for)
 
   // ---------------- main loop (unrolled by 2 so register slots are static) ----------------
-  auto step = [&](auto PP) -> bool {
+  auto step = [&](auto PP, int i) -> bool {
     constexpr int P = decltype(PP)::value;
     using IP = std::integral_constant<int, P>;
     using IQ = std::integral_constant<int, 1 - P>;
-    if (t0.m < nnz) mma_tile(IP{}, P);
-    if (tm1.m < nnz) {
-      epilogue(IQ{}, tm1, rs_epi);
-      rs_epi = rs_epi == 2 ? 0 : rs_epi + 1;
+    if (flush_half >= 0) {
+      flush(flush_half * 8, 8);
+      flush_half = -1;
     }
-    if (t0.m >= nnz) return false;
-    if (t1.m < nnz) {
-      commit(IQ{}, t1, 1 - P, rs_commit);
+    const int nend0 = nend;
+    if constexpr (DACC) {
+      if (i < ntiles) mma_tile(IP{}, P);
+      if (i >= 1) {
+        epilogue(IQ{}, ce, rs_epi);
+        rs_epi = rs_epi == 2 ? 0 : rs_epi + 1;
+        cur_adv(ce);
+      }
+    } else {
+      if (i >= 1) {
+        epilogue(IQ{}, ce, rs_epi);
+        rs_epi = rs_epi == 2 ? 0 : rs_epi + 1;
+        cur_adv(ce);
+      }
+      if (i < ntiles) mma_tile(IP{}, P);
+    }
+    if (nend != nend0 && (nend & 7) == 0) flush_half = ((nend >> 3) - 1) & 1;
+    if (i >= ntiles) return false;
+    if (i + 1 < ntiles) {
+      commit(IQ{}, cm, 1 - P, rs_commit);
       rs_commit = rs_commit == 2 ? 0 : rs_commit + 1;
+      cur_adv(cm);
     }
-    fetch_data(IQ{}, t3);   // uses codes slot (i+3)%2 == 1-P
-    fetch_codes(IP{}, t4);  // codes of tile i+4 into slot P
+    fetch_data(IQ{}, cf);   // tile i+3 into slot (i+3)%2, codes from slot (i+3)%2
+    cur_adv(cf);
+    fetch_codes(IP{}, cp);  // codes of tile i+4 into slot P
+    cur_adv(cp);
     __syncthreads();
-    tm1 = t0;
-    t0 = t1;
-    t1 = t2;
-    t2 = t3;
-    t3 = t4;
-    t4 = tile_next(t4);
     return true;
   };
-  while (true) {
-    if (!step(I0{})) break;
-    if (!step(I1{})) break;
+  for (int i = 0;; i += 2) {
+    if (!step(I0{}, i)) break;
+    if (!step(I1{}, i + 1)) break;
   }
+  // remaining finished docs: the due half (if any) and the partial half
+  __syncthreads();
+  if (flush_half >= 0) flush(flush_half * 8, 8);
+  if (nend & 7) flush(nend & ~7, nend & 7);
 }
 
 

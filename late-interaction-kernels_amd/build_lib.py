@@ -46,8 +46,8 @@ DEVICE_FLAGS = [
 ]
 
 
-def _compile(src: Path, obj: Path) -> tuple[Path, str]:
-    cmd = [hipcc(), *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
+    cmd = [hipcc(), *DEVICE_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     msg = "\n".join(
         line
@@ -59,9 +59,13 @@ def _compile(src: Path, obj: Path) -> tuple[Path, str]:
     return obj, msg
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    OUT_DIR.mkdir(parents=True, exist_ok=True)
-    obj_dir = HERE / "_build"
+def build(jobs: int | None = None, verbose: bool = False, out_dir: Path | None = None,
+          extra_flags: list[str] | None = None) -> Path:
+    """Compile and link; ``extra_flags`` (e.g. -DLIK_PROF) and ``out_dir`` are for
+    instrumented side builds that must not replace the product library."""
+    out_dir = Path(out_dir) if out_dir else OUT_DIR
+    out_dir.mkdir(parents=True, exist_ok=True)
+    obj_dir = HERE / ("_build" if not extra_flags else "_build_extra")
     obj_dir.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
@@ -69,14 +73,14 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
     objs = []
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_compile, s, obj_dir / (s.stem + ".o")) for s in sources]
+        futs = [ex.submit(_compile, s, obj_dir / (s.stem + ".o"), extra_flags or []) for s in sources]
         for f in futs:
             obj, msg = f.result()
             objs.append(obj)
             if verbose and msg.strip():
                 print(msg, file=sys.stderr)
-    out = OUT_DIR / LIB_NAME
-    tmp = OUT_DIR / (LIB_NAME + ".tmp")
+    out = out_dir / LIB_NAME
+    tmp = out_dir / (LIB_NAME + ".tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -89,8 +93,10 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--out-dir", default=None, help="side build directory (instrumented builds)")
+    ap.add_argument("--define", action="append", default=[], help="extra -D macro, e.g. LIK_PROF")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose))
+    print(build(args.jobs, args.verbose, args.out_dir, [f"-D{d}" for d in args.define]))
 
 
 if __name__ == "__main__":

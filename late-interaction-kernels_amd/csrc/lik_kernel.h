@@ -40,15 +40,27 @@ __device__ __forceinline__ uint32_t span_bytes(int64_t len, int64_t stride, int6
 // A tile of the workgroup's sequence: tile t of the m-th non-empty document.
 // Everything else about the document lives in the LDS table s_nz.
 struct Tile {
-  int m;       // index into s_nz; >= nnz: past the end
-  int t;       // tile index within the doc
-  int len;     // doc length in tokens
-  int k;       // doc index within the workgroup's range (jl - jl0)
-  int start;   // packed layouts: first token row of the doc
-  bool holes;  // dense + mask: a dropped token inside [0, len)
+  int m;        // index into s_nz; >= nnz: past the end
+  int t;        // tile index within the doc
+  int len;      // doc length in tokens
+  int k;        // doc index within the workgroup's range (jl - jl0)
+  bool holes;   // dense + mask: a dropped token inside [0, len)
+  int64_t off;  // dense: byte offset of the doc's token 0 from the data base; PLAID: its first token index
 };
 
 constexpr int kRMax = 512;  // docs per workgroup (host caps R)
+
+#ifdef LIK_PROF
+// Profiling builds only: per-phase cycle totals of the tile loop, summed over
+// all waves (lane 0 of each wave adds its totals at exit).
+#define LIK_PROF_DECL unsigned long long prof_acc[6] = {0, 0, 0, 0, 0, 0}; unsigned long long prof_t = __builtin_readcyclecounter();
+#define LIK_PROF_MARK(k) do { const unsigned long long t_ = __builtin_readcyclecounter(); prof_acc[k] += t_ - prof_t; prof_t = t_; } while (0)
+#define LIK_PROF_FLUSH() do { if (lane == 0 && p.prof) { for (int k_ = 0; k_ < 6; ++k_) atomicAdd(&p.prof[k_], prof_acc[k_]); atomicAdd(&p.prof[6], 1ull); } } while (0)
+#else
+#define LIK_PROF_DECL
+#define LIK_PROF_MARK(k) do { } while (0)
+#define LIK_PROF_FLUSH() do { } while (0)
+#endif
 
 // FEAT: features compiled in (a cleared bit removes the code path; the host
 // picks an instantiation whose bits cover the call): F_MASK doc mask,
@@ -71,8 +83,8 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   static_assert(SRC == SRC_DENSE || (!T::SPLIT && EK != EK_FP8), "PLAID computes in bf16/f16");
 
   __shared__ __attribute__((aligned(16))) char s_tile[2][T::NARR][T::TILE_B];
-  __shared__ __attribute__((aligned(16))) float s_rs[3][32];
-  __shared__ __attribute__((aligned(16))) float s_rb[3][32];
+  __shared__ __attribute__((aligned(16))) float s_rs[3][32];  // per-row scale (normalise / fp8 token scale)
+  __shared__ uint32_t s_tb[3];  // per-tile row-validity words of docs with mask holes
   // Finished documents: per-column maxima (already scaled, 0 for invalid
   // columns) of the last 16 docs and their local indices. A half (8 docs) is
   // summed per unit and written out one iteration after it fills.
@@ -80,7 +92,8 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) float s_colb[NSLOT][COLS];
   __shared__ int s_slotk[NSLOT];
   __shared__ float s_bw[SRC == SRC_PLAID ? 256 : 1];
-  __shared__ int32_t s_dstart[kRMax];
+  __shared__ int64_t s_doff[kRMax];  // dense: byte offset of token 0; PLAID: first token index
+  __shared__ float* s_outp[COLS];      // per unit of the group: &out[u, jl0] (null: no unit)
   __shared__ int32_t s_dlen[kRMax];  // length | holes << 31
   __shared__ __attribute__((aligned(16))) i32x4 s_nz[kRMax];  // {k, length | holes << 31, start, 0}
   __shared__ int s_nnz, s_ntiles;
@@ -112,6 +125,80 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   if constexpr (SRC == SRC_PLAID) {
     for (int i = tid; i < 256; i += NT) s_bw[i] = i < p.pl.nb ? p.pl.bw[i] : 0.f;
   }
+
+  // ---------------- document range and tile cursor ----------------
+  const int64_t jl0 = r * (int64_t)p.R;
+  const int64_t jl1 = (jl0 + p.R < p.ndocs_pg) ? jl0 + p.R : p.ndocs_pg;
+  const int64_t kd_base = p.kd_K ? (g / p.nc) * p.kd_K : 0;  // KD: one query per group
+  int64_t pair_doc = -1;
+  if (p.pair_d) {
+    const int64_t pd = p.pair_d[g];
+    pair_doc = (pd >= 0 && pd < p.d.n) ? pd : -1;
+  }
+  auto dglob = [&](int64_t jl) -> int64_t { return p.pair_d ? pair_doc : kd_base + jl; };
+  auto unit_of = [&](int t) -> int64_t { return p.pair_q ? g : g * p.QPG + t; };
+
+  // Output row pointers of the group's units (shifted to doc jl0), so the doc
+  // flush needs only the column stride.
+  for (int t = tid; t < COLS; t += NT) {
+    const int64_t u = unit_of(t);
+    s_outp[t] = (t < p.QPG && u < p.nunits) ? p.out + u * p.osq + jl0 * p.osd : nullptr;
+  }
+  __syncthreads();
+  // Per-doc metadata for this workgroup's range, staged once in LDS so the
+  // tile cursor never issues a vector load inside the pipelined loop; then
+  // wavefront 0 compacts the non-empty docs into s_nz (ballot + popcount).
+  const int nloc = (int)(jl1 - jl0);
+  for (int k = tid; k < nloc; k += NT) {
+    const int64_t jl = jl0 + k;
+    const int64_t dg = dglob(jl);
+    const int64_t L = doc_len<SRC>(p, dg);
+    int64_t off = 0;
+    bool holes = false, skip = false;
+    if (dg >= 0) {
+      if constexpr (SRC == SRC_DENSE) {
+        off = f_cu ? (int64_t)p.d.cu[dg] * p.d.sl_b : dg * p.d.sn_b;
+        const bool h = p.holes != nullptr && p.holes[dg] != 0;
+        holes = f_mask && h;
+        // two-launch mask handling: 1 = docs without holes only, 2 = docs with holes only
+        skip = (p.doc_filter == 1 && h) || (p.doc_filter == 2 && !h);
+      } else {
+        off = p.pl.cu ? (int64_t)p.pl.cu[dg] : dg * p.pl.codes_sn;
+      }
+    }
+    s_doff[k] = off;
+    s_dlen[k] = skip ? 0 : ((int32_t)L | (holes ? (int32_t)0x80000000 : 0));
+    if (L == 0 && !skip) {
+      for (int t = 0; t < p.QPG; ++t)
+        if (float* o = s_outp[t]) o[k * p.osd] = 0.f;
+    }
+  }
+  __syncthreads();
+  if (wv == 0) {
+    int base = 0, ntl = 0;
+    for (int k0 = 0; k0 < nloc; k0 += 64) {
+      const int k = k0 + lane;
+      const int v = k < nloc ? s_dlen[k] : 0;
+      const int L = v & 0x7fffffff;
+      const bool nz = L > 0;
+      const uint64_t bal = __ballot(nz);
+      const int pos = base + (int)__popcll(bal & ((1ull << lane) - 1ull));
+      if (nz) s_nz[pos] = (i32x4){k, v, (int)(uint32_t)s_doff[k], (int)(s_doff[k] >> 32)};
+      base += (int)__popcll(bal);
+      int nt = (L + 31) >> 5;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) nt += __shfl_xor(nt, o);
+      ntl += nt;
+    }
+    if (lane == 0) {
+      s_nnz = base;
+      s_ntiles = ntl;
+    }
+  }
+  __syncthreads();
+  const int nnz = __builtin_amdgcn_readfirstlane(s_nnz);
+  const int ntiles = __builtin_amdgcn_readfirstlane(s_ntiles);
+  if (nnz == 0) return;
 
   // ---------------- query block -> B fragments in VGPRs ----------------
   u32x4 bq[NSUB][KS][FV];
@@ -169,72 +256,6 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     qsc[sub] = valid ? sc : 0.f;
   }
 
-  // ---------------- document range and tile cursor ----------------
-  const int64_t jl0 = r * (int64_t)p.R;
-  const int64_t jl1 = (jl0 + p.R < p.ndocs_pg) ? jl0 + p.R : p.ndocs_pg;
-  const int64_t kd_base = p.kd_K ? (g / p.nc) * p.kd_K : 0;  // KD: one query per group
-  auto dglob = [&](int64_t jl) -> int64_t {
-    if (p.pair_d) {
-      const int64_t pd = p.pair_d[g];
-      return (pd >= 0 && pd < p.d.n) ? pd : -1;
-    }
-    return kd_base + jl;
-  };
-  auto unit_of = [&](int t) -> int64_t { return p.pair_q ? g : g * p.QPG + t; };
-
-  // Per-doc metadata for this workgroup's range, staged once in LDS so the
-  // tile cursor never issues a vector load inside the pipelined loop; then
-  // wavefront 0 compacts the non-empty docs into s_nz (ballot + popcount).
-  const int nloc = (int)(jl1 - jl0);
-  for (int k = tid; k < nloc; k += NT) {
-    const int64_t jl = jl0 + k;
-    const int64_t dg = dglob(jl);
-    const int64_t L = doc_len<SRC>(p, dg);
-    int32_t start = 0;
-    bool holes = false;
-    if (dg >= 0) {
-      if constexpr (SRC == SRC_DENSE) {
-        if (f_cu) start = p.d.cu[dg];
-        holes = f_mask && p.holes != nullptr && p.holes[dg] != 0;
-      } else {
-        if (p.pl.cu) start = p.pl.cu[dg];
-      }
-    }
-    s_dstart[k] = start;
-    s_dlen[k] = (int32_t)L | (holes ? (int32_t)0x80000000 : 0);
-    if (L == 0) {
-      for (int t = 0; t < p.QPG; ++t) {
-        const int64_t u = unit_of(t);
-        if (u < p.nunits) p.out[u * p.osq + jl * p.osd] = 0.f;
-      }
-    }
-  }
-  __syncthreads();
-  if (wv == 0) {
-    int base = 0, ntl = 0;
-    for (int k0 = 0; k0 < nloc; k0 += 64) {
-      const int k = k0 + lane;
-      const int v = k < nloc ? s_dlen[k] : 0;
-      const int L = v & 0x7fffffff;
-      const bool nz = L > 0;
-      const uint64_t bal = __ballot(nz);
-      const int pos = base + (int)__popcll(bal & ((1ull << lane) - 1ull));
-      if (nz) s_nz[pos] = (i32x4){k, v, s_dstart[k], 0};
-      base += (int)__popcll(bal);
-      int nt = (L + 31) >> 5;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) nt += __shfl_xor(nt, o);
-      ntl += nt;
-    }
-    if (lane == 0) {
-      s_nnz = base;
-      s_ntiles = ntl;
-    }
-  }
-  __syncthreads();
-  const int nnz = __builtin_amdgcn_readfirstlane(s_nnz);
-  const int ntiles = __builtin_amdgcn_readfirstlane(s_ntiles);
-  if (nnz == 0) return;
 
   // Cursor over the workgroup's tile sequence: tile t of the m-th non-empty
   // doc. The doc fields are refreshed from the LDS table only when the cursor
@@ -248,12 +269,13 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
       const int v = __builtin_amdgcn_readfirstlane(e[1]);
       c.len = v & 0x7fffffff;
       c.holes = v < 0;
-      c.start = __builtin_amdgcn_readfirstlane(e[2]);
+      c.off = (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane(e[2]) |
+              ((int64_t)__builtin_amdgcn_readfirstlane(e[3]) << 32);
     } else {
       c.k = 0;
       c.len = 0;
       c.holes = false;
-      c.start = 0;
+      c.off = 0;
     }
   };
   auto cur_adv = [&](Tile& c) {
@@ -264,7 +286,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
 
   // ---------------- staging: fetch (global -> VGPR ring) and commit (-> LDS) ----------------
   u32x4 st[2][NCH][NCV];
-  uint32_t sm[SRC == SRC_DENSE ? 2 : 1][NCH];     // dense: mask byte per row
+  uint32_t sm[SRC == SRC_DENSE ? 2 : 1];          // dense + mask holes: the tile's row-validity word
   float sts[SRC == SRC_DENSE ? 2 : 1][NCH];       // dense fp8: token scale per row
   uint32_t sb0[SRC == SRC_PLAID ? 2 : 1][NCH];    // PLAID: residual bits (low)
   uint32_t sb1[SRC == SRC_PLAID ? 2 : 1][NCH];    // PLAID: residual bits (high)
@@ -282,7 +304,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     if constexpr (SRC == SRC_PLAID) {
       constexpr int S = decltype(SS)::value;
       if (x.m >= nnz) return;
-      const int64_t tok0 = p.pl.cu ? (int64_t)x.start : dglob(jl0 + x.k) * p.pl.codes_sn;
+      const int64_t tok0 = x.off;
       const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.pl.codes + tok0, sat_u32((int64_t)x.len * 4));
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
@@ -299,9 +321,9 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   auto fetch_data = [&](auto SS, const Tile& x) {
     constexpr int S = decltype(SS)::value;
     if (x.m >= nnz) return;
-    const int64_t doc = dglob(jl0 + x.k);
     if constexpr (SRC == SRC_DENSE) {
-      const char* base = f_cu ? p.d.data + (int64_t)x.start * p.d.sl_b : p.d.data + doc * p.d.sn_b;
+      const int64_t doc = dglob(jl0 + x.k);
+      const char* base = p.d.data + x.off;
       const __amdgpu_buffer_rsrc_t rd =
           make_rsrc(base, sat_u32((int64_t)(x.len - 1) * p.d.sl_b + (int64_t)p.d.dim * T::IN_B));
 #pragma unroll
@@ -311,21 +333,13 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
         chunk_geom(i, row, cc, inr);
         const int64_t tok = (int64_t)x.t * 32 + row;
         const bool ok = inr && tok < x.len && cc * T::CHUNK_E < p.d.dim;
-        const uint32_t off = ok ? sat_u32(tok * p.d.sl_b + cc * 16) : kOOB;
+        // valid offsets are < the 4 GiB buffer range, so 32-bit arithmetic is exact
+        const uint32_t off = ok ? (uint32_t)tok * (uint32_t)p.d.sl_b + (uint32_t)(cc * 16) : kOOB;
         st[S][i][0] = __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, 0);
       }
-      if (f_mask) {
-        const __amdgpu_buffer_rsrc_t rm =
-            make_rsrc(p.d.mask + doc * p.d.msn, span_bytes(x.len, p.d.msl, 1));
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-          int row, cc;
-          bool inr;
-          chunk_geom(i, row, cc, inr);
-          const int64_t tok = (int64_t)x.t * 32 + row;
-          const uint32_t off = (inr && tok < x.len) ? sat_u32(tok * p.d.msl) : kOOB;
-          sm[S][i] = __builtin_amdgcn_raw_buffer_load_b8(rm, off, 0, 0);
-        }
+      if (f_mask && x.holes) {  // prefix-valid docs need no validity word
+        const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.tbits + doc * p.tbits_sn, sat_u32(p.tbits_sn * 4));
+        sm[S] = __builtin_amdgcn_raw_buffer_load_b32(rm, (uint32_t)x.t * 4u, 0, 0);
       }
       if (f_ts) {
         const __amdgpu_buffer_rsrc_t rt =
@@ -341,7 +355,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
         }
       }
     } else {
-      const int64_t tok0 = p.pl.cu ? (int64_t)x.start : doc * p.pl.codes_sn;
+      const int64_t tok0 = x.off;
       const __amdgpu_buffer_rsrc_t rcent = make_rsrc(p.pl.cent, sat_u32(p.pl.ncent * p.pl.cent_sb));
       const __amdgpu_buffer_rsrc_t rres =
           make_rsrc(p.pl.res + tok0 * p.pl.res_st, sat_u32((int64_t)x.len * p.pl.res_st));
@@ -375,6 +389,9 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
 
   auto commit = [&](auto SS, const Tile& x, int buf, int rslot) {
     constexpr int S = decltype(SS)::value;
+    if constexpr (SRC == SRC_DENSE) {
+      if (f_mask && x.holes && tid == 0) s_tb[rslot] = sm[S];
+    }
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       int row, cc;
@@ -398,13 +415,10 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
           } else {
             *(u32x4*)(rowp + cc * 16) = st[S][i][0];
           }
-          if (cc == 0) {
-            const bool ok = live && (!f_mask || (sm[S][i] & 0xffu) != 0);
-            s_rs[rslot][row] = (f_norm ? inv_norm(ss) : 1.f) * (f_ts ? sts[S][i] : 1.f);
-            s_rb[rslot][row] = ok ? 0.f : NEG_INF;
-          }
+          if (cc == 0 && (f_norm || f_ts)) s_rs[rslot][row] = (f_norm ? inv_norm(ss) : 1.f) * (f_ts ? sts[S][i] : 1.f);
         }
       } else {
+        (void)rslot;
         const uint32_t bmask = (1u << p.pl.nbits) - 1u;
         const uint64_t bits = ((uint64_t)sb1[S][i] << 32) | sb0[S][i];
         float x8[8];
@@ -436,10 +450,6 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
               w[e] = f32_to_bf16_bits(x8[2 * e] * sc) | (f32_to_bf16_bits(x8[2 * e + 1] * sc) << 16);
           }
           *(u32x4*)(s_tile[buf][0] + row * T::ROW_B + cc * 16) = w;
-          if (cc == 0) {
-            s_rs[rslot][row] = 1.f;
-            s_rb[rslot][row] = live ? 0.f : NEG_INF;
-          }
         }
       }
     }
@@ -450,7 +460,10 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   // its accumulators and overlaps tile i's MFMAs with tile i-1's epilogue.
   // W<=4: a single accumulator set keeps a wave under 256 registers, so two
   // workgroups fit per CU and hide each other's epilogues and barriers.
-  constexpr bool DACC = W == 8;
+#ifndef LIK_DACC_W8
+#define LIK_DACC_W8 1
+#endif
+  constexpr bool DACC = W == 8 && LIK_DACC_W8;
   f32x16 acc[DACC ? 2 : 1][NSUB];
   float m[NSUB];
 #pragma unroll
@@ -500,8 +513,8 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     for (int task = tid; task < tasks; task += NT) {
       const int sl = (s0 + task / p.QPG) % NSLOT;
       const int t = task % p.QPG;
-      const int64_t u = unit_of(t);
-      if (u >= p.nunits) continue;
+      float* const orow = s_outp[t];
+      if (!orow) continue;
       const float* cv = &s_colb[sl][t * p.LU];
       float sum = 0.f;
       if ((p.LU & 3) == 0) {
@@ -518,28 +531,39 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
       } else {
         for (int j = 0; j < p.LU; ++j) sum += cv[j];
       }
-      p.out[u * p.osq + (jl0 + s_slotk[sl]) * p.osd] = sum * p.out_scale;
+      orow[s_slotk[sl] * p.osd] = sum * p.out_scale;
     }
   };
 
   auto epilogue = [&](auto PP, const Tile& x, int rslot) {
     constexpr int P = DACC ? decltype(PP)::value : 0;
-    const bool partial = (x.t + 1) * 32 > x.len;
-    bool fix = dense_fix || partial;
-    if constexpr (SRC == SRC_DENSE) fix = fix || x.holes;
-    if (fix) {
-      f32x4 sc[4], bi[4];
+    // Row validity: rows past the doc end, and (dense + mask holes) rows whose
+    // bit in the tile's validity word is clear, never win the max.
+    const int nv = x.len - x.t * 32;
+    bool holes = false;
+    if constexpr (SRC == SRC_DENSE) holes = f_mask && x.holes;
+    const uint32_t vbits = (holes ? s_tb[rslot] : 0xffffffffu) & (nv >= 32 ? 0xffffffffu : ((1u << nv) - 1u));
+    if (dense_fix) {
+      f32x4 sc[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sc[j] = *(const f32x4*)&s_rs[rslot][8 * j + 4 * h];
-        bi[j] = *(const f32x4*)&s_rb[rslot][8 * j + 4 * h];
-      }
+      for (int j = 0; j < 4; ++j) sc[j] = *(const f32x4*)&s_rs[rslot][8 * j + 4 * h];
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) m[sub] = fmaxf(m[sub], fmaf(acc[P][sub][4 * j + e], sc[j][e], bi[j][e]));
+          for (int e = 0; e < 4; ++e) {
+            const float v = acc[P][sub][4 * j + e] * sc[j][e];
+            m[sub] = fmaxf(m[sub], ((vbits >> (8 * j + 4 * h + e)) & 1u) ? v : NEG_INF);
+          }
+    } else if (vbits != 0xffffffffu) {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            m[sub] = fmaxf(m[sub], ((vbits >> (8 * j + 4 * h + e)) & 1u) ? acc[P][sub][4 * j + e] : NEG_INF);
     } else {
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub)
@@ -588,6 +612,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   int flush_half = -1;    // slot half whose flush is due (after the barrier it waited for)
 
   // ---------------- main loop (unrolled by 2 so register slots are static) ----------------
+  LIK_PROF_DECL
   auto step = [&](auto PP, int i) -> bool {
     constexpr int P = decltype(PP)::value;
     using IP = std::integral_constant<int, P>;
@@ -596,6 +621,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
       flush(flush_half * 8, 8);
       flush_half = -1;
     }
+    LIK_PROF_MARK(0);
     const int nend0 = nend;
     if constexpr (DACC) {
       if (i < ntiles) mma_tile(IP{}, P);
@@ -613,17 +639,23 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
       if (i < ntiles) mma_tile(IP{}, P);
     }
     if (nend != nend0 && (nend & 7) == 0) flush_half = ((nend >> 3) - 1) & 1;
+    LIK_PROF_MARK(1);
     if (i >= ntiles) return false;
     if (i + 1 < ntiles) {
       commit(IQ{}, cm, 1 - P, rs_commit);
       rs_commit = rs_commit == 2 ? 0 : rs_commit + 1;
       cur_adv(cm);
     }
+    LIK_PROF_MARK(2);
     fetch_data(IQ{}, cf);   // tile i+3 into slot (i+3)%2, codes from slot (i+3)%2
     cur_adv(cf);
-    fetch_codes(IP{}, cp);  // codes of tile i+4 into slot P
-    cur_adv(cp);
+    if constexpr (SRC == SRC_PLAID) {
+      fetch_codes(IP{}, cp);  // codes of tile i+4 into slot P
+      cur_adv(cp);
+    }
+    LIK_PROF_MARK(3);
     __syncthreads();
+    LIK_PROF_MARK(4);
     return true;
   };
   for (int i = 0;; i += 2) {
@@ -634,6 +666,8 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   __syncthreads();
   if (flush_half >= 0) flush(flush_half * 8, 8);
   if (nend & 7) flush(nend & ~7, nend & 7);
+  LIK_PROF_MARK(5);
+  LIK_PROF_FLUSH();
 }
 
 

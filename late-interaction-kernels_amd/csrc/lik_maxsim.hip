@@ -29,11 +29,15 @@
 namespace lik {
 
 
-// Per-document valid extent of a boolean mask: extent = last kept token + 1,
-// holes = some token inside [0, extent) is dropped. One wavefront per doc.
+// Per-document summary of a boolean mask: extent = last kept token + 1,
+// holes = some token inside [0, extent) is dropped, and one 32-bit
+// row-validity word per 32-token tile (bit r = token 32*t + r kept), which
+// the tile kernel applies in its epilogue. One wavefront per doc; each pass
+// covers two tiles (lanes 0-31 and 32-63) with one ballot.
 __global__ void __launch_bounds__(256) doc_extent_kernel(const int8_t* mask, int64_t msn, int64_t msl,
                                                          int64_t n, int64_t L, const int32_t* lengths,
-                                                         int32_t* extent, uint8_t* holes) {
+                                                         int32_t* extent, uint8_t* holes, uint32_t* tbits,
+                                                         int64_t tbits_sn) {
   const int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (j >= n) return;
@@ -43,11 +47,17 @@ __global__ void __launch_bounds__(256) doc_extent_kernel(const int8_t* mask, int
     Lj = l < 0 ? 0 : (l > L ? L : l);
   }
   int last = -1, cnt = 0;
-  for (int64_t t = lane; t < Lj; t += 64) {
-    if (mask[j * msn + t * msl] != 0) {
+  for (int64_t t0 = 0; t0 < tbits_sn * 32; t0 += 64) {
+    const int64_t t = t0 + lane;
+    const bool keep = t < Lj && mask[j * msn + t * msl] != 0;
+    if (keep) {
       last = (int)t;
       ++cnt;
     }
+    const uint64_t bal = __ballot(keep);
+    const int64_t tile = t0 >> 5;
+    if (lane == 0 && tile < tbits_sn) tbits[j * tbits_sn + tile] = (uint32_t)bal;
+    if (lane == 32 && tile + 1 < tbits_sn) tbits[j * tbits_sn + tile + 1] = (uint32_t)(bal >> 32);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
@@ -234,7 +244,7 @@ int launch_plaid(int dt, int cd, const Plan& pl, const Params& p, int64_t nb, hi
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t extent_off = 0, holes_off = 0, part_off = 0, total = 0;
+  size_t extent_off = 0, holes_off = 0, tbits_off = 0, part_off = 0, total = 0;
   bool need_extent = false, need_part = false;
 };
 
@@ -247,6 +257,8 @@ WsLayout ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, con
     off = align256(off + sizeof(int32_t) * (size_t)D->n);
     w.holes_off = off;
     off = align256(off + (size_t)D->n);
+    w.tbits_off = off;
+    off = align256(off + sizeof(uint32_t) * (size_t)D->n * (size_t)((D->len + 31) / 32));
   }
   if (pl.nc > 1) {
     const bool kd = (flags & LIK_KD_LAYOUT) != 0;
@@ -260,6 +272,23 @@ WsLayout ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, con
 }
 
 }  // namespace
+
+#ifdef LIK_PROF
+static unsigned long long* g_prof = nullptr;
+static unsigned long long* prof_buf() {
+  if (!g_prof && hipMalloc((void**)&g_prof, 64) == hipSuccess) (void)hipMemset(g_prof, 0, 64);
+  return g_prof;
+}
+extern "C" int lik_prof_read(unsigned long long* out, int reset) {
+  if (!prof_buf() || hipDeviceSynchronize() != hipSuccess) return LIK_ERR_LAUNCH;
+  if (hipMemcpy(out, g_prof, 64, hipMemcpyDeviceToHost) != hipSuccess) return LIK_ERR_LAUNCH;
+  if (reset && hipMemset(g_prof, 0, 64) != hipSuccess) return LIK_ERR_LAUNCH;
+  return LIK_OK;
+}
+#define LIK_SET_PROF(p) (p).prof = prof_buf()
+#else
+#define LIK_SET_PROF(p) (p).prof = nullptr
+#endif
 
 extern "C" {
 
@@ -308,9 +337,12 @@ int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float o
   if (wl.need_extent) {
     p.extent = (const int32_t*)(ws + wl.extent_off);
     p.holes = (const uint8_t*)(ws + wl.holes_off);
+    p.tbits = (const uint32_t*)(ws + wl.tbits_off);
+    p.tbits_sn = (D->len + 31) / 32;
     hipLaunchKernelGGL(doc_extent_kernel, dim3((unsigned)((D->n + 3) / 4)), dim3(256), 0, s, D->mask,
                        D->mask_stride_n, D->mask_stride_l, D->n, D->len, D->lengths,
-                       (int32_t*)(ws + wl.extent_off), (uint8_t*)(ws + wl.holes_off));
+                       (int32_t*)(ws + wl.extent_off), (uint8_t*)(ws + wl.holes_off),
+                       (uint32_t*)(ws + wl.tbits_off), p.tbits_sn);
     if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
   }
   if (wl.need_part) {
@@ -325,7 +357,19 @@ int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float o
   p.R = pick_R(p.ngroups, p.ndocs_pg);
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   p.xcd_map = p.NR >= 8 ? 1 : 0;
+  LIK_SET_PROF(p);
   const int64_t nb = p.xcd_map ? p.ngroups * ((p.NR + 7) / 8) * 8 : p.ngroups * p.NR;
+  if (wl.need_extent) {
+    // Masks: docs whose kept tokens form a prefix (no holes) are scored by the
+    // mask-free kernel with the extent as length; a second launch of the
+    // masked kernel scores only the docs with holes (its other workgroups exit
+    // right after reading the doc table).
+    Params p1 = p;
+    p1.d.mask = nullptr;
+    p1.doc_filter = 1;
+    if ((rc = launch_dense(Q->dtype, pl, p1, nb, s)) != LIK_OK) return rc;
+    p.doc_filter = 2;
+  }
   if ((rc = launch_dense(Q->dtype, pl, p, nb, s)) != LIK_OK) return rc;
   if (wl.need_part) {
     const int64_t tot = Q->n * p.ndocs_pg;

@@ -36,6 +36,9 @@ struct Params {
   PlaidDev pl;
   const int32_t* extent;  // per-doc valid extent from the mask pre-pass
   const uint8_t* holes;   // per-doc: mask has a False inside [0, extent)
+  const uint32_t* tbits;  // per (doc, 32-token tile): row-validity bits of the mask
+  int64_t tbits_sn;       // tiles per doc in tbits
+  int doc_filter;         // 0: all docs; 1: docs without mask holes; 2: docs with holes
   const int32_t* pair_q;
   const int32_t* pair_d;
   int64_t nunits;  // query units (query x Lq-chunk); pair mode: number of pairs
@@ -52,6 +55,7 @@ struct Params {
   float out_scale;
   float* out;
   int64_t osq, osd;
+  unsigned long long* prof;  // profiling builds (-DLIK_PROF): per-phase cycle totals
 };
 
 enum { SRC_DENSE = 0, SRC_PLAID = 1 };

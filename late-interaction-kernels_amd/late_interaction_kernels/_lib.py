@@ -9,11 +9,12 @@ tensors are not on a ROCm GPU, the ops raise — there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch
 
-_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblik_hip.so"
+_LIB_PATH = Path(os.environ.get("LIK_LIBRARY") or Path(__file__).resolve().parent / "_lib" / "liblik_hip.so")
 
 LIK_OK = 0
 LIK_ERR_INVALID = -1

@@ -286,7 +286,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="inbatch")
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
-    ap.add_argument("--cpu-sample-queries", type=int, default=16)
+    ap.add_argument("--cpu-sample-queries", type=int, default=256)
     ap.add_argument("--plaid-docs", type=int, default=1_000_000)
     ap.add_argument("--plaid-queries", type=int, default=1024)
     args = ap.parse_args()

@@ -151,7 +151,7 @@ int lik_plaid_approx_score(const float* qcs, int64_t n_centroids, int64_t lq, in
  * (prev_scores[r*prev_ld + i], prev_idx[r*prev_ld + i]) for i < prev_k, and
  * (scores[r*ld + c], idx_base + c) for c < n. Writes the k best, ordered by
  * score (descending if largest, else ascending) and then by lower index,
- * to out_scores/out_idx[r*out_ld + i]. k <= prev_k + n, k <= 2048,
+ * to out_scores/out_idx[r*out_ld + i]. k <= prev_k + n, k <= 1024,
  * n <= 4096, indices < 2^32. prev may alias out.
  * Replaces the torch.topk + cat + gather merge of topk.py:41-86 /
  * retrieve.py:278-305 with a deterministic tie order (lower index first).

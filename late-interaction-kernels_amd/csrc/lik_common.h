@@ -47,19 +47,20 @@ struct KT {
   static_assert(CPR <= 64, "a row must be reduced within one wavefront");
 };
 
+// D = A x B + C for one 32x32 tile step (A, B: this lane's fragments).
 template <int EK>
-__device__ __forceinline__ void mfma32(f32x16& c, const u32x4* a, const u32x4* b) {
+__device__ __forceinline__ f32x16 mfma32(const f32x16& c, const u32x4* a, const u32x4* b) {
   if constexpr (EK == EK_BF16 || EK == EK_F32) {
-    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
-                                                __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                   __builtin_bit_cast(bf16x8, b[0]), c, 0, 0, 0);
   } else if constexpr (EK == EK_F16) {
-    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
-                                               __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                  __builtin_bit_cast(f16x8, b[0]), c, 0, 0, 0);
   } else {
     const i32x8 av = __builtin_bit_cast(i32x8, __builtin_shufflevector(a[0], a[1], 0, 1, 2, 3, 4, 5, 6, 7));
     const i32x8 bv = __builtin_bit_cast(i32x8, __builtin_shufflevector(b[0], b[1], 0, 1, 2, 3, 4, 5, 6, 7));
     // cbsz = blgp = 0: both operands OCP fp8 e4m3; E8M0 scale 127 == 1.0.
-    c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 127, 0, 127);
   }
 }
 

@@ -37,30 +37,9 @@ __device__ __forceinline__ uint32_t span_bytes(int64_t len, int64_t stride, int6
   return len <= 0 ? 0u : sat_u32(((len - 1) * stride + 1) * elem);
 }
 
-// A tile of the workgroup's sequence: tile t of the m-th non-empty document.
-// Everything else about the document lives in the LDS table s_nz.
-struct Tile {
-  int m;        // index into s_nz; >= nnz: past the end
-  int t;        // tile index within the doc
-  int len;      // doc length in tokens
-  int k;        // doc index within the workgroup's range (jl - jl0)
-  bool holes;   // dense + mask: a dropped token inside [0, len)
-  int64_t off;  // dense: byte offset of the doc's token 0 from the data base; PLAID: its first token index
-};
 
 constexpr int kRMax = 512;  // docs per workgroup (host caps R)
 
-#ifdef LIK_PROF
-// Profiling builds only: per-phase cycle totals of the tile loop, summed over
-// all waves (lane 0 of each wave adds its totals at exit).
-#define LIK_PROF_DECL unsigned long long prof_acc[6] = {0, 0, 0, 0, 0, 0}; unsigned long long prof_t = __builtin_readcyclecounter();
-#define LIK_PROF_MARK(k) do { const unsigned long long t_ = __builtin_readcyclecounter(); prof_acc[k] += t_ - prof_t; prof_t = t_; } while (0)
-#define LIK_PROF_FLUSH() do { if (lane == 0 && p.prof) { for (int k_ = 0; k_ < 6; ++k_) atomicAdd(&p.prof[k_], prof_acc[k_]); atomicAdd(&p.prof[6], 1ull); } } while (0)
-#else
-#define LIK_PROF_DECL
-#define LIK_PROF_MARK(k) do { } while (0)
-#define LIK_PROF_FLUSH() do { } while (0)
-#endif
 
 // FEAT: features compiled in (a cleared bit removes the code path; the host
 // picks an instantiation whose bits cover the call): F_MASK doc mask,
@@ -82,9 +61,10 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   constexpr float NEG_INF = -__builtin_huge_valf();
   static_assert(SRC == SRC_DENSE || (!T::SPLIT && EK != EK_FP8), "PLAID computes in bf16/f16");
 
-  __shared__ __attribute__((aligned(16))) char s_tile[2][T::NARR][T::TILE_B];
-  __shared__ __attribute__((aligned(16))) float s_rs[3][32];  // per-row scale (normalise / fp8 token scale)
-  __shared__ uint32_t s_tb[3];  // per-tile row-validity words of docs with mask holes
+  // tile j lives in LDS buffer j % 3: tile i is being multiplied (from
+  // registers), tile i+1's A fragments are being read, tile i+2 is being written
+  __shared__ __attribute__((aligned(16))) char s_tile[3][T::NARR][T::TILE_B];
+  __shared__ __attribute__((aligned(16))) float s_rs[4][32];  // fp8 per-row scale of tile j in slot j % 4
   // Finished documents: per-column maxima (already scaled, 0 for invalid
   // columns) of the last 16 docs and their local indices. A half (8 docs) is
   // summed per unit and written out one iteration after it fills.
@@ -95,7 +75,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   __shared__ int64_t s_doff[kRMax];  // dense: byte offset of token 0; PLAID: first token index
   __shared__ float* s_outp[COLS];      // per unit of the group: &out[u, jl0] (null: no unit)
   __shared__ int32_t s_dlen[kRMax];  // length | holes << 31
-  __shared__ __attribute__((aligned(16))) i32x4 s_nz[kRMax];  // {k, length | holes << 31, start, 0}
+  __shared__ __attribute__((aligned(16))) i32x4 s_nz[kRMax + 1];  // {k, length | holes << 31, start lo, hi}; [nnz] = sentinel
   __shared__ int s_nnz, s_ntiles;
 
   const bool f_mask = (FEAT & F_MASK) && p.d.mask != nullptr;
@@ -193,6 +173,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     if (lane == 0) {
       s_nnz = base;
       s_ntiles = ntl;
+      s_nz[base] = (i32x4){0, 0, 0, 0};  // sentinel: an empty doc past the last one
     }
   }
   __syncthreads();
@@ -257,121 +238,151 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   }
 
 
-  // Cursor over the workgroup's tile sequence: tile t of the m-th non-empty
-  // doc. The doc fields are refreshed from the LDS table only when the cursor
-  // crosses a document boundary.
-  auto cur_load = [&](Tile& c, int m) {
+  // ---------------- tile cursor and descriptors ----------------
+  // One cursor walks the workgroup's tiles in order (tile t of the m-th
+  // non-empty doc). Each iteration it emits the descriptor of the newest tile
+  // (the one being fetched) and advances, branch-free: a doc boundary selects
+  // the next table entry, and past the last doc the sentinel entry (length
+  // 0) makes every further tile empty. Older tiles' descriptors move down a
+  // short register queue (fetch -> commit -> MFMA -> epilogue).
+  struct Cur {
+    int m, t, len, k;
+    bool holes;
+    int64_t off;  // dense: byte offset of the doc's token 0; PLAID: its first token index
+  };
+  struct Desc {
+    int nv;       // valid rows of the tile (0..32)
+    int k;        // doc index within the workgroup's range
+    bool docend;  // last tile of its doc
+    bool holes;   // doc has a mask with holes (dense)
+    int64_t tok;  // PLAID: index of the tile's first token
+  };
+  auto cur_entry = [&](Cur& c, int m) {
+    const i32x4 e = s_nz[m];
+    const int v = __builtin_amdgcn_readfirstlane(e[1]);
     c.m = m;
     c.t = 0;
-    if (m < nnz) {
-      const i32x4 e = s_nz[m];
-      c.k = __builtin_amdgcn_readfirstlane(e[0]);
-      const int v = __builtin_amdgcn_readfirstlane(e[1]);
-      c.len = v & 0x7fffffff;
-      c.holes = v < 0;
-      c.off = (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane(e[2]) |
-              ((int64_t)__builtin_amdgcn_readfirstlane(e[3]) << 32);
-    } else {
-      c.k = 0;
-      c.len = 0;
-      c.holes = false;
-      c.off = 0;
-    }
+    c.k = __builtin_amdgcn_readfirstlane(e[0]);
+    c.len = v & 0x7fffffff;
+    c.holes = v < 0;
+    c.off = (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane(e[2]) |
+            ((int64_t)__builtin_amdgcn_readfirstlane(e[3]) << 32);
   };
-  auto cur_adv = [&](Tile& c) {
-    if (c.m >= nnz) return;
-    if ((c.t + 1) * 32 < c.len) ++c.t;
-    else cur_load(c, c.m + 1);
+  auto cur_adv = [&](Cur& c) {
+    const bool last = (c.t + 1) * 32 >= c.len;
+    Cur n;
+    cur_entry(n, c.m + 1 < nnz ? c.m + 1 : nnz);
+    c.t = last ? 0 : c.t + 1;
+    c.m = last ? n.m : c.m;
+    c.k = last ? n.k : c.k;
+    c.len = last ? n.len : c.len;
+    c.holes = last ? n.holes : c.holes;
+    c.off = last ? n.off : c.off;
+  };
+  auto produce = [&](const Cur& c) -> Desc {
+    Desc d;
+    const int rem = c.len - c.t * 32;
+    d.nv = rem >= 32 ? 32 : (rem > 0 ? rem : 0);
+    d.k = c.k;
+    d.docend = c.len > 0 && rem <= 32;
+    d.holes = c.holes;
+    d.tok = c.off + (int64_t)c.t * 32;
+    return d;
   };
 
   // ---------------- staging: fetch (global -> VGPR ring) and commit (-> LDS) ----------------
   u32x4 st[2][NCH][NCV];
-  uint32_t sm[SRC == SRC_DENSE ? 2 : 1];          // dense + mask holes: the tile's row-validity word
+  uint32_t sm[SRC == SRC_DENSE ? 2 : 1];          // dense + mask: the tile's row-validity word
   float sts[SRC == SRC_DENSE ? 2 : 1][NCH];       // dense fp8: token scale per row
   uint32_t sb0[SRC == SRC_PLAID ? 2 : 1][NCH];    // PLAID: residual bits (low)
   uint32_t sb1[SRC == SRC_PLAID ? 2 : 1][NCH];    // PLAID: residual bits (high)
   int32_t scode[SRC == SRC_PLAID ? 2 : 1][NCH];   // PLAID: centroid code per row
 
-  auto chunk_geom = [&](int i, int& row, int& cc, bool& inr) {
+  // Per-lane constants of the staging chunks: chunk i of this thread is
+  // (row, 16-byte column cc) of the tile. lrow is the row, or 64 for chunks
+  // that are padding (past the 32 rows or past the embedding dim), so the
+  // single test lrow < nv selects the loads that happen. loff is the byte
+  // offset of the chunk from the tile's row 0.
+  int lrow[NCH];
+  uint32_t loff[NCH];
+  int lcc[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
     const int c = tid + i * NT;
-    row = c / SCPR;
-    cc = c % SCPR;
-    inr = FULLCH || c < 32 * SCPR;
-  };
+    const int row = c / SCPR, cc = c % SCPR;
+    const bool inr = FULLCH || c < 32 * SCPR;
+    lcc[i] = cc;
+    if constexpr (SRC == SRC_DENSE) {
+      lrow[i] = (inr && cc * T::CHUNK_E < p.d.dim) ? row : 64;
+      loff[i] = (uint32_t)row * (uint32_t)p.d.sl_b + (uint32_t)cc * 16u;
+    } else {
+      lrow[i] = (inr && cc * 8 < p.q.dim) ? row : 64;
+      loff[i] = (uint32_t)row;
+    }
+  }
 
-  // PLAID phase A: centroid codes of tile x
-  auto fetch_codes = [&](auto SS, const Tile& x) {
+  // PLAID phase A: centroid codes of tile d
+  auto fetch_codes = [&](auto SS, const Desc& d) {
     if constexpr (SRC == SRC_PLAID) {
       constexpr int S = decltype(SS)::value;
-      if (x.m >= nnz) return;
-      const int64_t tok0 = x.off;
-      const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.pl.codes + tok0, sat_u32((int64_t)x.len * 4));
+      const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.pl.codes + d.tok, (uint32_t)d.nv * 4u);
 #pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        int row, cc;
-        bool inr;
-        chunk_geom(i, row, cc, inr);
-        const uint32_t off = inr ? (uint32_t)(x.t * 32 + row) * 4u : kOOB;
-        scode[S][i] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, off, 0, 0);
+      for (int i = 0; i < NCH; ++i)
+        scode[S][i] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, lrow[i] < d.nv ? loff[i] * 4u : kOOB, 0, 0);
+    }
+  };
+
+  // Dense: token data of the cursor's current tile into slot S (rows past
+  // the doc end and padding chunks are out of range and read as 0).
+  auto fetch_dense = [&](auto SS, const Cur& c, const Desc& d) {
+    if constexpr (SRC == SRC_DENSE) {
+      constexpr int S = decltype(SS)::value;
+      // one doc spans < 4 GiB (checked on the host), so 32-bit math is exact
+      const uint32_t span = (uint32_t)(c.len > 1 ? c.len - 1 : 0) * (uint32_t)p.d.sl_b + (uint32_t)(p.d.dim * T::IN_B);
+      const __amdgpu_buffer_rsrc_t rd = make_rsrc(p.d.data + c.off, span);
+      const uint32_t toff = (uint32_t)c.t * 32u * (uint32_t)p.d.sl_b;
+#pragma unroll
+      for (int i = 0; i < NCH; ++i)
+        st[S][i][0] = __builtin_amdgcn_raw_buffer_load_b128(rd, lrow[i] < d.nv ? loff[i] + toff : kOOB, 0, 0);
+      if constexpr ((FEAT & (F_MASK | F_TS)) != 0) {
+        const int64_t doc = dglob(jl0 + c.k);
+        if constexpr ((FEAT & F_MASK) != 0) {
+          // validity word of the tile (only docs with mask holes have one)
+          const __amdgpu_buffer_rsrc_t rm =
+              make_rsrc(p.tbits + (doc >= 0 ? doc : 0) * p.tbits_sn, sat_u32(p.tbits_sn * 4));
+          sm[S] = __builtin_amdgcn_raw_buffer_load_b32(rm, (f_mask && c.holes) ? (uint32_t)c.t * 4u : kOOB, 0, 0);
+        }
+        if constexpr ((FEAT & F_TS) != 0) {
+          const __amdgpu_buffer_rsrc_t rt =
+              make_rsrc(p.d.ts + (doc >= 0 ? doc : 0) * p.d.tsn, f_ts ? span_bytes(c.len, p.d.tsl, 4) : 0u);
+#pragma unroll
+          for (int i = 0; i < NCH; ++i) {
+            const int64_t tok = (int64_t)c.t * 32 + (lrow[i] & 31);
+            sts[S][i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rt, lrow[i] < d.nv ? sat_u32(tok * p.d.tsl * 4) : kOOB, 0, 0));
+          }
+        }
       }
     }
   };
 
-  // phase B (dense: the only phase): token data of tile x into slot S
-  auto fetch_data = [&](auto SS, const Tile& x) {
-    constexpr int S = decltype(SS)::value;
-    if (x.m >= nnz) return;
-    if constexpr (SRC == SRC_DENSE) {
-      const int64_t doc = dglob(jl0 + x.k);
-      const char* base = p.d.data + x.off;
-      const __amdgpu_buffer_rsrc_t rd =
-          make_rsrc(base, sat_u32((int64_t)(x.len - 1) * p.d.sl_b + (int64_t)p.d.dim * T::IN_B));
-#pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        int row, cc;
-        bool inr;
-        chunk_geom(i, row, cc, inr);
-        const int64_t tok = (int64_t)x.t * 32 + row;
-        const bool ok = inr && tok < x.len && cc * T::CHUNK_E < p.d.dim;
-        // valid offsets are < the 4 GiB buffer range, so 32-bit arithmetic is exact
-        const uint32_t off = ok ? (uint32_t)tok * (uint32_t)p.d.sl_b + (uint32_t)(cc * 16) : kOOB;
-        st[S][i][0] = __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, 0);
-      }
-      if (f_mask && x.holes) {  // prefix-valid docs need no validity word
-        const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.tbits + doc * p.tbits_sn, sat_u32(p.tbits_sn * 4));
-        sm[S] = __builtin_amdgcn_raw_buffer_load_b32(rm, (uint32_t)x.t * 4u, 0, 0);
-      }
-      if (f_ts) {
-        const __amdgpu_buffer_rsrc_t rt =
-            make_rsrc(p.d.ts + doc * p.d.tsn, span_bytes(x.len, p.d.tsl, 4));
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-          int row, cc;
-          bool inr;
-          chunk_geom(i, row, cc, inr);
-          const int64_t tok = (int64_t)x.t * 32 + row;
-          const uint32_t off = (inr && tok < x.len) ? sat_u32(tok * p.d.tsl * 4) : kOOB;
-          sts[S][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rt, off, 0, 0));
-        }
-      }
-    } else {
-      const int64_t tok0 = x.off;
-      const __amdgpu_buffer_rsrc_t rcent = make_rsrc(p.pl.cent, sat_u32(p.pl.ncent * p.pl.cent_sb));
+  // PLAID phase B: centroid rows (by the codes in slot S) and residual bits of tile d.
+  const __amdgpu_buffer_rsrc_t rcent =
+      SRC == SRC_PLAID ? make_rsrc(p.pl.cent, sat_u32(p.pl.ncent * p.pl.cent_sb)) : make_rsrc(nullptr, 0u);
+  auto fetch_plaid = [&](auto SS, const Desc& d) {
+    if constexpr (SRC == SRC_PLAID) {
+      constexpr int S = decltype(SS)::value;
       const __amdgpu_buffer_rsrc_t rres =
-          make_rsrc(p.pl.res + tok0 * p.pl.res_st, sat_u32((int64_t)x.len * p.pl.res_st));
+          make_rsrc(p.pl.res + d.tok * p.pl.res_st, sat_u32((int64_t)d.nv * p.pl.res_st));
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
-        int row, cc;
-        bool inr;
-        chunk_geom(i, row, cc, inr);
-        const int64_t tl = (int64_t)x.t * 32 + row;
-        const bool ok = inr && tl < x.len && cc * 8 < p.q.dim;
+        const bool ok = lrow[i] < d.nv;
         int64_t code = scode[S][i];
         code = (code < 0 || code >= p.pl.ncent) ? 0 : code;
-        const uint32_t coff = ok ? sat_u32(code * p.pl.cent_sb + (int64_t)cc * 8 * CSZ) : kOOB;
+        const uint32_t coff = ok ? (uint32_t)(code * p.pl.cent_sb) + (uint32_t)(lcc[i] * 8 * CSZ) : kOOB;
         st[S][i][0] = __builtin_amdgcn_raw_buffer_load_b128(rcent, coff, 0, 0);
-        if constexpr (NCV > 1) st[S][i][1] = __builtin_amdgcn_raw_buffer_load_b128(rcent, coff + 16u, 0, 0);
-        const uint32_t roff = ok ? sat_u32(tl * p.pl.res_st + (int64_t)cc * p.pl.nbits) : kOOB;
+        if constexpr (NCV > 1) st[S][i][1] = __builtin_amdgcn_raw_buffer_load_b128(rcent, ok ? coff + 16u : kOOB, 0, 0);
+        const uint32_t roff = ok ? loff[i] * (uint32_t)p.pl.res_st + (uint32_t)(lcc[i] * p.pl.nbits) : kOOB;
         if (p.pl.nbits == 2) {
           sb0[S][i] = __builtin_amdgcn_raw_buffer_load_b16(rres, roff, 0, 0);
           sb1[S][i] = 0;
@@ -387,17 +398,21 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     }
   };
 
-  auto commit = [&](auto SS, const Tile& x, int buf, int rslot) {
+  // fp8 rows cannot be rescaled in place, so an fp8 doc with a per-row scale
+  // (token scale or normalise) keeps it in s_rs and the epilogue applies it.
+  constexpr bool kRowScaleEpi = SRC == SRC_DENSE && EK == EK_FP8 && (FEAT & (F_TS | F_NORM)) != 0;
+  const bool row_scale = kRowScaleEpi && (f_norm || f_ts);
+
+  // Commit the tile staged in VGPR slot S to LDS buffer `buf`: dense
+  // bf16/f16/f32 rows are L2-normalised here (scaled in fp32, rounded once
+  // to the MFMA type); PLAID rows are decoded, normalised and rounded. Rows
+  // past the tile's valid ones are written as zeros.
+  auto commit = [&](auto SS, const Desc& d, int buf, int rslot) {
     constexpr int S = decltype(SS)::value;
-    if constexpr (SRC == SRC_DENSE) {
-      if (f_mask && x.holes && tid == 0) s_tb[rslot] = sm[S];
-    }
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      int row, cc;
-      bool inr;
-      chunk_geom(i, row, cc, inr);
-      const bool live = x.t * 32 + row < x.len;
+      const int row = (tid + i * NT) / SCPR, cc = lcc[i];
+      const bool inr = FULLCH || tid + i * NT < 32 * SCPR;
       if constexpr (SRC == SRC_DENSE) {
         float ss = 0.f;
         if (f_norm) {
@@ -405,20 +420,42 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
 #pragma unroll
           for (int o = 1; o < SCPR; o <<= 1) ss += __shfl_xor(ss, o);
         }
+        u32x4 v = st[S][i][0];
+        if constexpr (EK != EK_FP8) {
+          if (f_norm) {
+            const float sc = inv_norm(ss);
+            if constexpr (EK == EK_BF16) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                v[e] = f32_to_bf16_bits(bf16lo_to_f32(v[e]) * sc) | (f32_to_bf16_bits(bf16hi_to_f32(v[e]) * sc) << 16);
+            } else if constexpr (EK == EK_F16) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                v[e] = f32_to_f16_bits(f16_to_f32((uint16_t)(v[e] & 0xffffu)) * sc) |
+                       (f32_to_f16_bits(f16_to_f32((uint16_t)(v[e] >> 16)) * sc) << 16);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = __float_as_uint(__uint_as_float(v[e]) * sc);
+            }
+          }
+        }
         if (inr) {
           char* rowp = s_tile[buf][0] + row * T::ROW_B;
           if constexpr (T::SPLIT) {
             u32x2 hi, lo;
-            split4(st[S][i][0], hi, lo);
+            split4(v, hi, lo);
             *(u32x2*)(rowp + cc * 8) = hi;
             *(u32x2*)(s_tile[buf][1] + row * T::ROW_B + cc * 8) = lo;
           } else {
-            *(u32x4*)(rowp + cc * 16) = st[S][i][0];
+            *(u32x4*)(rowp + cc * 16) = v;
           }
-          if (cc == 0 && (f_norm || f_ts)) s_rs[rslot][row] = (f_norm ? inv_norm(ss) : 1.f) * (f_ts ? sts[S][i] : 1.f);
+          if constexpr (kRowScaleEpi) {
+            if (cc == 0) s_rs[rslot][row] = (f_norm ? inv_norm(ss) : 1.f) * (f_ts ? sts[S][i] : 1.f);
+          }
         }
       } else {
         (void)rslot;
+        const bool live = row < d.nv;
         const uint32_t bmask = (1u << p.pl.nbits) - 1u;
         const uint64_t bits = ((uint64_t)sb1[S][i] << 32) | sb0[S][i];
         float x8[8];
@@ -456,49 +493,63 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   };
 
   // ---------------- compute pieces ----------------
-  // W=8: two waves of one workgroup share a SIMD, so each wave double-buffers
-  // its accumulators and overlaps tile i's MFMAs with tile i-1's epilogue.
-  // W<=4: a single accumulator set keeps a wave under 256 registers, so two
-  // workgroups fit per CU and hide each other's epilogues and barriers.
-#ifndef LIK_DACC_W8
-#define LIK_DACC_W8 1
-#endif
-  constexpr bool DACC = W == 8 && LIK_DACC_W8;
-  f32x16 acc[DACC ? 2 : 1][NSUB];
+  // Accumulators: set P holds tile i (MFMA in flight), set 1-P holds tile i-1
+  // (epilogue), so one wave overlaps tile i's MFMAs with tile i-1's max. Row
+  // masking is folded into the MFMA C operand: the first k-step of a tile
+  // adds `bias` (0 for valid rows, -inf for rows past the doc end or
+  // dropped by the mask), so the epilogue is a plain running max.
+  // Two accumulator sets unless they do not fit in 256 registers next to the
+  // query fragments (8 waves x 4 blocks): then one set, the epilogue runs
+  // before the tile's MFMAs and the SIMD's second wave covers the gap.
+  constexpr int NACC = (W == 8 && NSUB >= 4) ? 1 : 2;
+  f32x16 acc[NACC][NSUB];
   float m[NSUB];
 #pragma unroll
-  for (int sub = 0; sub < NSUB; ++sub) m[sub] = NEG_INF;
-  const bool dense_fix = SRC == SRC_DENSE && (f_norm || f_ts);
+  for (int sub = 0; sub < NSUB; ++sub) {
+    m[sub] = NEG_INF;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[NACC - 1][sub][e] = NEG_INF;
+  }
+  f32x16 bias;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) bias[e] = 0.f;
+  uint32_t bias_bits = 0xffffffffu;
+  // accumulator element e of lane (h, l32) is doc row 8*(e/4) + 4*h + e%4
+  auto set_bias = [&](uint32_t vb) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bias[e] = ((vb >> (8 * (e >> 2) + 4 * h + (e & 3))) & 1u) ? 0.f : NEG_INF;
+    bias_bits = vb;
+  };
 
-  auto mma_tile = [&](auto PP, int buf) {
-    constexpr int P = DACC ? decltype(PP)::value : 0;
+  // A fragments (this lane's doc row, both k-halves) of a tile, read from
+  // LDS one iteration ahead of their MFMAs into register set S.
+  u32x4 af[2][KS][FV];
+  u32x4 afl[2][T::SPLIT ? KS : 1];
+  auto load_a = [&](auto SS, int buf) {
+    constexpr int S = decltype(SS)::value;
     const char* A = s_tile[buf][0] + l32 * T::ROW_B + h * T::HALF_B;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      u32x4 a[FV];
 #pragma unroll
-      for (int v = 0; v < FV; ++v) a[v] = *(const u32x4*)(A + ks * T::FRAG_B + v * 16);
-      if constexpr (T::SPLIT) {
-        const u32x4 al = *(const u32x4*)(s_tile[buf][1] + l32 * T::ROW_B + h * T::HALF_B + ks * T::FRAG_B);
+      for (int v = 0; v < FV; ++v) af[S][ks][v] = *(const u32x4*)(A + ks * T::FRAG_B + v * 16);
+      if constexpr (T::SPLIT)
+        afl[S][ks] = *(const u32x4*)(s_tile[buf][1] + l32 * T::ROW_B + h * T::HALF_B + ks * T::FRAG_B);
+    }
+  };
+  auto mma_tile = [&](auto PP, auto SS) {
+    constexpr int P = NACC == 2 ? decltype(PP)::value : 0;
+    constexpr int S = decltype(SS)::value;
 #pragma unroll
-        for (int sub = 0; sub < NSUB; ++sub) {
-          if (ks == 0) {
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[P][sub][e] = 0.f;
-          }
-          mfma32<EK>(acc[P][sub], a, bq[sub][ks]);
-          mfma32<EK>(acc[P][sub], a, &bql[sub][ks]);
-          mfma32<EK>(acc[P][sub], &al, bq[sub][ks]);
+      for (int sub = 0; sub < NSUB; ++sub) {
+        f32x16 c = ks == 0 ? bias : acc[P][sub];
+        c = mfma32<EK>(c, af[S][ks], bq[sub][ks]);
+        if constexpr (T::SPLIT) {
+          c = mfma32<EK>(c, af[S][ks], &bql[sub][ks]);
+          c = mfma32<EK>(c, &afl[S][ks], bq[sub][ks]);
         }
-      } else {
-#pragma unroll
-        for (int sub = 0; sub < NSUB; ++sub) {
-          if (ks == 0) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[P][sub][e] = 0.f;
-          }
-          mfma32<EK>(acc[P][sub], a, bq[sub][ks]);
-        }
+        acc[P][sub] = c;
       }
     }
   };
@@ -535,85 +586,104 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     }
   };
 
-  auto epilogue = [&](auto PP, const Tile& x, int rslot) {
-    constexpr int P = DACC ? decltype(PP)::value : 0;
-    // Row validity: rows past the doc end, and (dense + mask holes) rows whose
-    // bit in the tile's validity word is clear, never win the max.
-    const int nv = x.len - x.t * 32;
-    bool holes = false;
-    if constexpr (SRC == SRC_DENSE) holes = f_mask && x.holes;
-    const uint32_t vbits = (holes ? s_tb[rslot] : 0xffffffffu) & (nv >= 32 ? 0xffffffffu : ((1u << nv) - 1u));
-    if (dense_fix) {
-      f32x4 sc[4];
+  // Running max over the rows of the previous tile (accumulator set P).
+  auto epilogue = [&](auto PP, int rslot) {
+    constexpr int P = NACC == 2 ? decltype(PP)::value : 0;
+    if constexpr (kRowScaleEpi) {
+      if (row_scale) {
+        f32x4 sc[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sc[j] = *(const f32x4*)&s_rs[rslot][8 * j + 4 * h];
+        for (int j = 0; j < 4; ++j) sc[j] = *(const f32x4*)&s_rs[rslot][8 * j + 4 * h];
 #pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub)
+        for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float v = acc[P][sub][4 * j + e] * sc[j][e];
-            m[sub] = fmaxf(m[sub], ((vbits >> (8 * j + 4 * h + e)) & 1u) ? v : NEG_INF);
-          }
-    } else if (vbits != 0xffffffffu) {
-#pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            m[sub] = fmaxf(m[sub], ((vbits >> (8 * j + 4 * h + e)) & 1u) ? acc[P][sub][4 * j + e] : NEG_INF);
-    } else {
-#pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) m[sub] = fmaxf(m[sub], acc[P][sub][e]);
-    }
-    if ((x.t + 1) * 32 >= x.len) {  // last tile of the doc: park the per-column maxima
-      const int sl = nend % NSLOT;
-#pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
-        const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over lanes l, l^32
-        if (h == 0) s_colb[sl][(wv * NSUB + sub) * 32 + l32] = __builtin_isfinite(mm) ? mm * qsc[sub] : 0.f;
-        m[sub] = NEG_INF;
+            for (int e = 0; e < 4; ++e) m[sub] = fmaxf(m[sub], acc[P][sub][4 * j + e] * sc[j][e]);
+        return;
       }
-      if (tid == 0) s_slotk[sl] = x.k;
-      ++nend;
     }
+    (void)rslot;
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) m[sub] = fmaxf(m[sub], acc[P][sub][e]);
+  };
+
+  // The previous tile was the last of doc k: park the per-column maxima.
+  auto doc_end = [&](int k) {
+    const int sl = nend % NSLOT;
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
+      const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over lanes l, l^32
+      if (h == 0) s_colb[sl][(wv * NSUB + sub) * 32 + l32] = __builtin_isfinite(mm) ? mm * qsc[sub] : 0.f;
+      m[sub] = NEG_INF;
+    }
+    if (tid == 0) s_slotk[sl] = k;
+    ++nend;
   };
 
   // ---------------- prologue ----------------
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  // cursors: ce epilogue (tile i-1), cm commit (i+1), cf fetch (i+3), cp codes (i+4)
-  Tile ce, cm, cf, cp;
-  cur_load(ce, 0);
-  cm = ce;
-  fetch_codes(I0{}, cm);  // tile 0
-  fetch_data(I0{}, cm);
-  cur_adv(cm);            // tile 1
-  fetch_codes(I1{}, cm);
-  fetch_data(I1{}, cm);
-  cf = cm;
-  cur_adv(cf);            // tile 2
-  fetch_codes(I0{}, cf);
-  cp = cf;
-  cur_adv(cp);            // tile 3
-  fetch_codes(I1{}, cp);
-  commit(I0{}, ce, 0, 0); // tile 0 -> LDS[0], row slot 0
-  fetch_data(I0{}, cf);   // tile 2 into slot 0
-  cf = cp;                // tile 3
-  cur_adv(cp);            // tile 4
+  // Pipeline at iteration i: MFMA tile i (A fragments already in registers),
+  // read tile i+1's A fragments from LDS, max of tile i-1, commit tile i+2 to
+  // LDS, fetch tile i+4 (PLAID: data of tile i+4, codes of tile i+5).
+  // Descriptor queue: qm1 = tile i-1, q0 = i, q1 = i+1, q2 = i+2, q3 = i+3
+  // (PLAID also q4 = i+4); the cursor produces the newest tile.
+  Cur cur;
+  cur_entry(cur, 0);
+  Desc qm1{}, q0, q1, q2, q3, q4{};
+  // mask words of tiles i, i+1, i+2 (dense + mask; taken from the staged loads at commit)
+  uint32_t vw0 = 0xffffffffu, vw1 = 0xffffffffu, vw2 = 0xffffffffu;
+  q0 = produce(cur);
+  if constexpr (SRC == SRC_DENSE) {
+    fetch_dense(I0{}, cur, q0);
+    cur_adv(cur);
+    q1 = produce(cur);
+    fetch_dense(I1{}, cur, q1);
+    cur_adv(cur);
+    commit(I0{}, q0, 0, 0);
+    if constexpr ((FEAT & F_MASK) != 0) vw0 = sm[0];
+    q2 = produce(cur);
+    fetch_dense(I0{}, cur, q2);
+    cur_adv(cur);
+    commit(I1{}, q1, 1, 1);
+    if constexpr ((FEAT & F_MASK) != 0) vw1 = sm[1];
+    q3 = produce(cur);
+    fetch_dense(I1{}, cur, q3);
+    cur_adv(cur);
+  } else {
+    fetch_codes(I0{}, q0);
+    cur_adv(cur);
+    q1 = produce(cur);
+    fetch_codes(I1{}, q1);
+    cur_adv(cur);
+    fetch_plaid(I0{}, q0);
+    fetch_plaid(I1{}, q1);
+    q2 = produce(cur);
+    fetch_codes(I0{}, q2);
+    cur_adv(cur);
+    commit(I0{}, q0, 0, 0);
+    fetch_plaid(I0{}, q2);
+    q3 = produce(cur);
+    fetch_codes(I1{}, q3);
+    cur_adv(cur);
+    commit(I1{}, q1, 1, 1);
+    fetch_plaid(I1{}, q3);
+    q4 = produce(cur);
+    fetch_codes(I0{}, q4);
+    cur_adv(cur);
+  }
   __syncthreads();
-  int rs_commit = 1;      // row-scale slot of tile i+1
-  int rs_epi = 0;         // row-scale slot of tile i-1
+  load_a(I0{}, 0);
+  int buf_a = 1;          // LDS buffer of tile i+1
+  int buf_c = 2;          // LDS buffer of tile i+2
   int flush_half = -1;    // slot half whose flush is due (after the barrier it waited for)
 
   // ---------------- main loop (unrolled by 2 so register slots are static) ----------------
-  LIK_PROF_DECL
-  auto step = [&](auto PP, int i) -> bool {
+  auto step = [&](auto PP, int i) {
     constexpr int P = decltype(PP)::value;
     using IP = std::integral_constant<int, P>;
     using IQ = std::integral_constant<int, 1 - P>;
@@ -621,57 +691,86 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
       flush(flush_half * 8, 8);
       flush_half = -1;
     }
-    LIK_PROF_MARK(0);
-    const int nend0 = nend;
-    if constexpr (DACC) {
-      if (i < ntiles) mma_tile(IP{}, P);
-      if (i >= 1) {
-        epilogue(IQ{}, ce, rs_epi);
-        rs_epi = rs_epi == 2 ? 0 : rs_epi + 1;
-        cur_adv(ce);
+    {
+      // row validity of tile i (uniform): rows past the doc end, and rows the
+      // mask drops in docs with holes
+      uint32_t vb = q0.nv >= 32 ? 0xffffffffu : ((1u << q0.nv) - 1u);
+      if constexpr (SRC == SRC_DENSE && (FEAT & F_MASK) != 0) {
+        if (q0.holes) vb &= vw0;
       }
+      vb = __builtin_amdgcn_readfirstlane(vb);
+      if (vb != bias_bits) set_bias(vb);
+    }
+    // one block: MFMA tile i, read A of tile i+1, max of tile i-1, commit
+    // tile i+2, fetch tile i+4
+    const Desc qn = produce(cur);
+    if constexpr (NACC == 2) {
+      mma_tile(IP{}, IP{});
+      epilogue(IQ{}, (i + 3) & 3);
     } else {
-      if (i >= 1) {
-        epilogue(IQ{}, ce, rs_epi);
-        rs_epi = rs_epi == 2 ? 0 : rs_epi + 1;
-        cur_adv(ce);
+      epilogue(IQ{}, (i + 3) & 3);
+      mma_tile(IP{}, IP{});
+    }
+    load_a(IQ{}, buf_a);
+    commit(IP{}, q2, buf_c, (i + 2) & 3);
+    if constexpr (SRC == SRC_DENSE && (FEAT & F_MASK) != 0) vw2 = sm[P];
+    if constexpr (SRC == SRC_DENSE) {
+      fetch_dense(IP{}, cur, qn);  // tile i+4 into slot (i+4)%2
+    } else {
+      fetch_plaid(IP{}, q4);       // tile i+4, codes from slot (i+4)%2
+      fetch_codes(IQ{}, qn);       // codes of tile i+5 into slot (i+5)%2
+    }
+    cur_adv(cur);
+    if constexpr (SRC == SRC_DENSE && NACC == 2) {
+      // Interleave the block: each MFMA is followed by a few VALU / SALU
+      // instructions (epilogue max, commit, fetch addressing, cursor), an LDS
+      // read (next tile's A fragments) and a buffer load, so one wave keeps
+      // the matrix core fed while it does the tile bookkeeping. The commit's
+      // LDS write goes near the end, so its wait for the staged data (loaded
+      // two iterations earlier) comes as late as possible.
+      constexpr int NM = KS * NSUB * (T::SPLIT ? 3 : 1);
+#pragma unroll
+      for (int k = 0; k < NM; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x004, 2, 0);  // SALU
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+        if (k == NM - 3) __builtin_amdgcn_sched_group_barrier(0x200, 4 * NCH, 0);  // DS write
       }
-      if (i < ntiles) mma_tile(IP{}, P);
     }
-    if (nend != nend0 && (nend & 7) == 0) flush_half = ((nend >> 3) - 1) & 1;
-    LIK_PROF_MARK(1);
-    if (i >= ntiles) return false;
-    if (i + 1 < ntiles) {
-      commit(IQ{}, cm, 1 - P, rs_commit);
-      rs_commit = rs_commit == 2 ? 0 : rs_commit + 1;
-      cur_adv(cm);
+    if (i >= 1 && qm1.docend) {
+      doc_end(qm1.k);
+      if ((nend & 7) == 0) flush_half = ((nend >> 3) - 1) & 1;
     }
-    LIK_PROF_MARK(2);
-    fetch_data(IQ{}, cf);   // tile i+3 into slot (i+3)%2, codes from slot (i+3)%2
-    cur_adv(cf);
-    if constexpr (SRC == SRC_PLAID) {
-      fetch_codes(IP{}, cp);  // codes of tile i+4 into slot P
-      cur_adv(cp);
+    qm1 = q0;
+    q0 = q1;
+    q1 = q2;
+    q2 = q3;
+    if constexpr (SRC == SRC_DENSE) {
+      q3 = qn;
+    } else {
+      q3 = q4;
+      q4 = qn;
     }
-    LIK_PROF_MARK(3);
+    vw0 = vw1;
+    vw1 = vw2;
+    buf_a = buf_a == 2 ? 0 : buf_a + 1;
+    buf_c = buf_c == 2 ? 0 : buf_c + 1;
     __syncthreads();
-    LIK_PROF_MARK(4);
-    return true;
   };
+  // iterations 0..ntiles: iteration ntiles only finishes tile ntiles-1 (its
+  // MFMA, commit and fetch work on empty tiles and are discarded)
   for (int i = 0;; i += 2) {
-    if (!step(I0{}, i)) break;
-    if (!step(I1{}, i + 1)) break;
+    step(I0{}, i);
+    if (i + 1 > ntiles) break;
+    step(I1{}, i + 1);
+    if (i + 2 > ntiles) break;
   }
   // remaining finished docs: the due half (if any) and the partial half
-  __syncthreads();
   if (flush_half >= 0) flush(flush_half * 8, 8);
   if (nend & 7) flush(nend & ~7, nend & 7);
-  LIK_PROF_MARK(5);
-  LIK_PROF_FLUSH();
 }
-
-
-
 template <int EK, int DPAD, int W, int NSUB, int SRC, int CD, int FEAT>
 int launch_one(const Params& p, int64_t nblocks, hipStream_t s) {
   if constexpr (!cfg_ok<EK, DPAD, NSUB>()) {
@@ -695,6 +794,7 @@ int launch_cfg(const Plan& pl, const Params& p, int64_t nb, hipStream_t s) {
   if (pl.W == 4 && pl.NSUB == 4) return launch_one<EK, DPAD, 4, 4, SRC, CD, FEAT>(p, nb, s);
   if (pl.W == 8 && pl.NSUB == 1) return launch_one<EK, DPAD, 8, 1, SRC, CD, FEAT>(p, nb, s);
   if (pl.W == 8 && pl.NSUB == 2) return launch_one<EK, DPAD, 8, 2, SRC, CD, FEAT>(p, nb, s);
+  if (pl.W == 8 && pl.NSUB == 4) return launch_one<EK, DPAD, 8, 4, SRC, CD, FEAT>(p, nb, s);
   return LIK_ERR_UNSUPPORTED;
 }
 

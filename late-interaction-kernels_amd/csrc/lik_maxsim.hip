@@ -93,10 +93,12 @@ namespace {
 struct Cfg {
   int W, NSUB;
 };
-// Column-block configurations, smallest first.
-// 8x2: two wavefronts per SIMD (each ~140 VGPRs) so one wave's epilogue and
-// barrier waits hide under the other's MFMAs.
-constexpr Cfg kCfgs[] = {{1, 1}, {1, 2}, {1, 4}, {4, 1}, {4, 2}, {8, 1}, {8, 2}};
+// Column-block configurations, smallest first. The largest ones put two
+// wavefronts on each SIMD (8 per workgroup) so one wave's bookkeeping hides
+// under the other's MFMAs: 8x2 for 16-bit types; fp8 (half the fragment
+// registers, twice the MFMA rate) goes to 8x4 to amortise the per-tile work
+// over more MFMAs.
+constexpr Cfg kCfgs[] = {{1, 1}, {1, 2}, {1, 4}, {4, 1}, {4, 2}, {8, 1}, {8, 2}, {8, 4}};
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 int elem_bytes(int dt) { return dt == LIK_F32 ? 4 : (dt == LIK_FP8_E4M3 ? 1 : 2); }
@@ -153,6 +155,8 @@ int check_seqs(const lik_seqs_t* s) {
   if (!s->cu_seqlens && (s->stride_n * eb) % 16 != 0) return LIK_ERR_UNSUPPORTED;
   if (s->cu_seqlens && (s->mask || s->lengths)) return LIK_ERR_INVALID;
   if (s->token_scale && s->dtype != LIK_FP8_E4M3) return LIK_ERR_INVALID;
+  // the tile loads address one sequence with 32-bit byte offsets
+  if (s->len > 0 && ((s->len - 1) * s->stride_l + s->dim) * (int64_t)eb >= (int64_t)1 << 32) return LIK_ERR_UNSUPPORTED;
   return LIK_OK;
 }
 
@@ -169,6 +173,7 @@ int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group,
   int best = -1;
   for (int i = 0; i < kNumCfgs; ++i) {
     if (kCfgs[i].NSUB > nsmax) continue;
+    if (kCfgs[i].W == 8 && kCfgs[i].NSUB == 4 && dt != LIK_FP8_E4M3) continue;
     if (best >= 0 && kCfgs[i].W * kCfgs[i].NSUB <= kCfgs[best].W * kCfgs[best].NSUB) continue;
     best = i;
     if ((int64_t)kCfgs[i].W * kCfgs[i].NSUB * 32 >= need) break;
@@ -181,7 +186,7 @@ int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group,
     int w = 0, ns = 0;
     if (sscanf(e, "%d,%d", &w, &ns) == 2 && ns >= 1 && ns <= nsmax &&
         ((w == 1 && (ns == 1 || ns == 2 || ns == 4)) || (w == 4 && (ns == 1 || ns == 2 || ns == 4)) ||
-         (w == 8 && (ns == 1 || ns == 2)))) {
+         (w == 8 && (ns == 1 || ns == 2 || ns == 4)))) {
       pl.W = w;
       pl.NSUB = ns;
     }
@@ -273,22 +278,6 @@ WsLayout ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, con
 
 }  // namespace
 
-#ifdef LIK_PROF
-static unsigned long long* g_prof = nullptr;
-static unsigned long long* prof_buf() {
-  if (!g_prof && hipMalloc((void**)&g_prof, 64) == hipSuccess) (void)hipMemset(g_prof, 0, 64);
-  return g_prof;
-}
-extern "C" int lik_prof_read(unsigned long long* out, int reset) {
-  if (!prof_buf() || hipDeviceSynchronize() != hipSuccess) return LIK_ERR_LAUNCH;
-  if (hipMemcpy(out, g_prof, 64, hipMemcpyDeviceToHost) != hipSuccess) return LIK_ERR_LAUNCH;
-  if (reset && hipMemset(g_prof, 0, 64) != hipSuccess) return LIK_ERR_LAUNCH;
-  return LIK_OK;
-}
-#define LIK_SET_PROF(p) (p).prof = prof_buf()
-#else
-#define LIK_SET_PROF(p) (p).prof = nullptr
-#endif
 
 extern "C" {
 
@@ -357,7 +346,6 @@ int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float o
   p.R = pick_R(p.ngroups, p.ndocs_pg);
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   p.xcd_map = p.NR >= 8 ? 1 : 0;
-  LIK_SET_PROF(p);
   const int64_t nb = p.xcd_map ? p.ngroups * ((p.NR + 7) / 8) * 8 : p.ngroups * p.NR;
   if (wl.need_extent) {
     // Masks: docs whose kept tokens form a prefix (no holes) are scored by the
@@ -436,6 +424,8 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   if (((uintptr_t)docs->residuals) % 8 != 0 || docs->res_stride_tok % docs->nbits != 0)
     return LIK_ERR_UNSUPPORTED;
   if (docs->res_stride_tok * 8 < (int64_t)docs->dim * docs->nbits) return LIK_ERR_INVALID;
+  // centroid rows are gathered with 32-bit byte offsets
+  if (docs->n_centroids * docs->cent_stride * ceb >= (int64_t)1 << 32) return LIK_ERR_UNSUPPORTED;
 
   Plan pl;
   if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, false, pl)) != LIK_OK) return rc;

@@ -55,7 +55,6 @@ struct Params {
   float out_scale;
   float* out;
   int64_t osq, osd;
-  unsigned long long* prof;  // profiling builds (-DLIK_PROF): per-phase cycle totals
 };
 
 enum { SRC_DENSE = 0, SRC_PLAID = 1 };

@@ -45,21 +45,60 @@ def _sync():
     torch.cuda.synchronize()
 
 
+KERNEL_MS = {}  # filled by _time_steps: summed duration and count of the MaxSim tile-kernel launches
+
+
 def _time_steps(fn, steps: int, warmup: int) -> float:
-    """ms per step: W untimed steps, then K steps between events on the current stream."""
+    """ms per step: W untimed steps, then K steps between events on the current
+    stream (the stream every op launches on). Inside the timed region the
+    library also brackets each MaxSim tile-kernel launch with HIP events on
+    that stream (lik_timing_begin/end); their summed duration is what
+    ``roofline.achieved`` divides by."""
     import torch
+
+    from late_interaction_kernels import _lib
 
     for _ in range(warmup):
         fn()
     _sync()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    _lib.timing_begin()
     start.record()
     for _ in range(steps):
         fn()
     end.record()
     _sync()
+    kms, n = _lib.timing_end()
+    KERNEL_MS.update(total=kms, launches=n, steps=steps)
     return start.elapsed_time(end) / steps
+
+
+def _kernel_rate(work_per_step: float, scale: float) -> tuple[float, float]:
+    """(achieved rate, kernel ms per launch) of the tile kernel: algorithmic work
+    of the timed steps / summed launch durations, times ``scale`` (1e-9 for
+    TFLOP/s from FLOP/ms, 1e-6 for GB/s from B/ms)."""
+    tot, n, steps = KERNEL_MS["total"], KERNEL_MS["launches"], KERNEL_MS["steps"]
+    return work_per_step * steps / tot * scale, tot / max(n, 1)
+
+
+def _roofline(bound: str, work_per_step: float, peak: str, workload: str) -> dict:
+    """Roofline of the dominant kernel (the MaxSim tile kernel): algorithmic work
+    per step over its measured launch time. ``traffic`` is the HBM bytes per
+    launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (profiles/traffic.json,
+    scaled by the same counters on a copy kernel), when measured for this
+    workload."""
+    unit = "GB/s" if bound == "hbm" else "TFLOP/s"
+    rate, kms = _kernel_rate(work_per_step, 1e-6 if bound == "hbm" else 1e-9)
+    out = {"bound": bound, "achieved": round(rate, 2), "peak": PEAK[peak], "unit": unit,
+           "frac": round(rate / PEAK[peak], 4), "traffic": None, "kernel_ms": round(kms, 4),
+           "kernel_launches_per_step": KERNEL_MS["launches"] // max(KERNEL_MS["steps"], 1)}
+    tf = ROOT / "profiles" / "traffic.json"
+    if tf.exists():
+        t = json.loads(tf.read_text()).get(workload)
+        if t:
+            out["traffic"] = t["hbm_bytes_per_launch"]
+    return out
 
 
 def _normed(shape, gen, dtype):
@@ -115,8 +154,7 @@ def wl_inbatch(args, normalize=False):
         "config": {"workload": "in-batch MaxSim bf16 (BASELINE configs[1])", "Nq": Nq, "Lq": Lq, "Nd": Nd,
                    "Ld": Ld, "d": d, "doc_valid_len": "U[50,300] prefix d_mask", "normalize": normalize,
                    "valid_flops_per_step": flops},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK["bf16"], 4), "traffic": None},
+        "roofline": _roofline("mfma", flops, "bf16", "inbatch_norm" if normalize else "inbatch"),
     }
     if args.cpu_baseline:
         import lik_oracle as O
@@ -162,8 +200,7 @@ def wl_kd(args):
         "dtype": "bf16",
         "config": {"workload": "KD layout D_kd[512,64,300,128] (BASELINE configs[1])", "bytes_per_step": nbytes,
                    "padded_bytes": D.numel() * 2},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm"], "unit": "GB/s",
-                     "frac": round(gbs / PEAK["hbm"], 4), "traffic": None},
+        "roofline": _roofline("hbm", nbytes, "hbm", "kd"),
     }
 
 
@@ -197,8 +234,7 @@ def wl_varlen(args):
         "dtype": "bf16",
         "config": {"workload": "varlen 65,536 docs log-U[16,2048], 256x32 queries (BASELINE configs[2])",
                    "doc_tokens": tot, "flops_per_step": flops},
-        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                     "frac": round(tf / PEAK["bf16"], 4), "traffic": None},
+        "roofline": _roofline("mfma", flops, "bf16", "varlen"),
     }
 
 
@@ -229,8 +265,7 @@ def wl_fp8(args):
         "dtype": "fp8-e4m3",
         "config": {"workload": "ColPali fp8 Q[256,24,128] x D[8192,1030,128] (BASELINE configs[3])",
                    "flops_per_step": flops},
-        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["fp8"], "unit": "TFLOP/s",
-                     "frac": round(tf / PEAK["fp8"], 4), "traffic": None},
+        "roofline": _roofline("mfma", flops, "fp8", "fp8"),
     }
 
 
@@ -264,12 +299,42 @@ def wl_plaid(args):
         "config": {"workload": f"PLAID {Nd} docs U[30,300], {Nq}x32 queries, nbits=2, top-100, chunk 4096 "
                                "(BASELINE configs[4])", "doc_tokens": tot, "flops_per_step": flops,
                    "compressed_bytes": tot * (4 + d * nbits // 8)},
-        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                     "frac": round(tf / PEAK["bf16"], 4), "traffic": None},
+        "roofline": _roofline("mfma", flops, "bf16", "plaid"),
     }
 
 
+def wl_hbm_copy(args):
+    """Calibration: a plain 2 GiB device copy (torch's copy kernel). Its GB/s is the
+    achievable HBM rate on this box, and its rocprofv3 FETCH_SIZE / WRITE_SIZE
+    against the known 2 GiB read + 2 GiB written give the counter scale used
+    for ``roofline.traffic``."""
+    import torch
+
+    n = 1 << 30  # bf16 elements = 2 GiB
+    x = torch.ones(n, device="cuda", dtype=torch.bfloat16)
+    y = torch.empty_like(x)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    for _ in range(args.warmup):
+        y.copy_(x)
+    _sync()
+    start.record()
+    for _ in range(args.steps):
+        y.copy_(x)
+    end.record()
+    _sync()
+    ms = start.elapsed_time(end) / args.steps
+    gbs = 2.0 * n * 2 / (ms * 1e-3) / 1e9
+    return {"metric": "device copy GB/s (read + write)", "value": round(gbs, 1), "unit": "GB/s",
+            "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": "hbm_copy 2 GiB -> 2 GiB (counter calibration)", "bytes_read": 2 * n,
+                       "bytes_written": 2 * n},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm"], "unit": "GB/s",
+                         "frac": round(gbs / PEAK["hbm"], 4), "traffic": 4.0 * n}}
+
+
 WORKLOADS = {
+    "hbm_copy": wl_hbm_copy,
     "inbatch": wl_inbatch,
     "inbatch_norm": lambda a: wl_inbatch(a, normalize=True),
     "kd": wl_kd,

@@ -164,6 +164,17 @@ int lik_topk_merge(const float* scores, int64_t rows, int64_t n, int64_t ld, int
 /* Library version string and the gfx target it was built for. */
 const char* lik_version(void);
 
+/*
+ * Launch timing (measurement aid, no counterpart in the reference, which
+ * times with CUDA events around whole Python calls): between
+ * lik_timing_begin() and lik_timing_end(), each scoring call brackets its
+ * MaxSim tile-kernel launch with HIP events on the call's stream.
+ * lik_timing_end() waits for the recorded launches and returns their summed
+ * duration and count. Process-wide and not thread-safe: for benchmarks.
+ */
+int lik_timing_begin(void);
+int lik_timing_end(double* total_ms, int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif

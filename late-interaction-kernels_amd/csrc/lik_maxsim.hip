@@ -24,6 +24,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <vector>
+
 #include "lik_params.h"
 
 namespace lik {
@@ -248,6 +250,34 @@ int launch_plaid(int dt, int cd, const Plan& pl, const Params& p, int64_t nb, hi
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Launch timing, a measurement aid that is off unless lik_timing_begin() was
+// called: the tile-kernel launch of each scoring call (the one that scores
+// the mask-free docs, i.e. all of them unless a mask has holes) is bracketed
+// by a pair of HIP events on the call's stream. Events are created once and
+// reused; not thread-safe, meant for a benchmark driver.
+struct LaunchTimer {
+  bool on = false;
+  std::vector<hipEvent_t> ev;  // pairs: start, stop
+  size_t used = 0;             // pairs recorded since lik_timing_begin
+};
+LaunchTimer g_timer;
+
+template <typename F>
+int timed_launch(hipStream_t s, F&& launch) {
+  if (!g_timer.on) return launch();
+  const size_t k = g_timer.used;
+  while (g_timer.ev.size() < 2 * (k + 1)) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return LIK_ERR_LAUNCH;
+    g_timer.ev.push_back(e);
+  }
+  if (hipEventRecord(g_timer.ev[2 * k], s) != hipSuccess) return LIK_ERR_LAUNCH;
+  const int rc = launch();
+  if (hipEventRecord(g_timer.ev[2 * k + 1], s) != hipSuccess) return LIK_ERR_LAUNCH;
+  g_timer.used = k + 1;
+  return rc;
+}
+
 struct WsLayout {
   size_t extent_off = 0, holes_off = 0, tbits_off = 0, part_off = 0, total = 0;
   bool need_extent = false, need_part = false;
@@ -282,6 +312,27 @@ WsLayout ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, con
 extern "C" {
 
 const char* lik_version(void) { return "lik-hip 0.1.0 gfx950"; }
+
+int lik_timing_begin(void) {
+  g_timer.on = true;
+  g_timer.used = 0;
+  return LIK_OK;
+}
+
+int lik_timing_end(double* total_ms, int64_t* launches) {
+  double tot = 0.0;
+  for (size_t k = 0; k < g_timer.used; ++k) {
+    if (hipEventSynchronize(g_timer.ev[2 * k + 1]) != hipSuccess) return LIK_ERR_LAUNCH;
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, g_timer.ev[2 * k], g_timer.ev[2 * k + 1]) != hipSuccess) return LIK_ERR_LAUNCH;
+    tot += ms;
+  }
+  if (total_ms) *total_ms = tot;
+  if (launches) *launches = (int64_t)g_timer.used;
+  g_timer.on = false;
+  g_timer.used = 0;
+  return LIK_OK;
+}
 
 size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
   if (check_seqs(Q) != LIK_OK || check_seqs(D) != LIK_OK) return 0;
@@ -355,10 +406,14 @@ int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float o
     Params p1 = p;
     p1.d.mask = nullptr;
     p1.doc_filter = 1;
-    if ((rc = launch_dense(Q->dtype, pl, p1, nb, s)) != LIK_OK) return rc;
+    if ((rc = timed_launch(s, [&] { return launch_dense(Q->dtype, pl, p1, nb, s); })) != LIK_OK) return rc;
     p.doc_filter = 2;
   }
-  if ((rc = launch_dense(Q->dtype, pl, p, nb, s)) != LIK_OK) return rc;
+  if (wl.need_extent) {
+    if ((rc = launch_dense(Q->dtype, pl, p, nb, s)) != LIK_OK) return rc;
+  } else if ((rc = timed_launch(s, [&] { return launch_dense(Q->dtype, pl, p, nb, s); })) != LIK_OK) {
+    return rc;
+  }
   if (wl.need_part) {
     const int64_t tot = Q->n * p.ndocs_pg;
     hipLaunchKernelGGL(unit_sum_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
@@ -400,7 +455,7 @@ int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pa
   p.out = out;
   p.osq = 1;
   p.osd = 0;
-  return launch_dense(Q->dtype, pl, p, num_pairs, (hipStream_t)stream);
+  return timed_launch((hipStream_t)stream, [&] { return launch_dense(Q->dtype, pl, p, num_pairs, (hipStream_t)stream); });
 }
 
 int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t flags, float* out,
@@ -463,7 +518,8 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   p.xcd_map = p.NR >= 8 ? 1 : 0;
   const int64_t nb = p.xcd_map ? p.ngroups * ((p.NR + 7) / 8) * 8 : p.ngroups * p.NR;
-  return launch_plaid(Q->dtype, docs->centroid_dtype, pl, p, nb, (hipStream_t)stream);
+  return timed_launch((hipStream_t)stream,
+                      [&] { return launch_plaid(Q->dtype, docs->centroid_dtype, pl, p, nb, (hipStream_t)stream); });
 }
 
 }  // extern "C"

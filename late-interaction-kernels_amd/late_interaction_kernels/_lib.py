@@ -42,6 +42,8 @@ EXPORTED_SYMBOLS = (
     "lik_plaid_approx_score",
     "lik_topk_merge",
     "lik_version",
+    "lik_timing_begin",
+    "lik_timing_end",
 )
 
 _p = ctypes.c_void_p
@@ -130,6 +132,10 @@ def load() -> ctypes.CDLL:
     lib.lik_topk_merge.restype = ctypes.c_int
     lib.lik_version.argtypes = []
     lib.lik_version.restype = ctypes.c_char_p
+    lib.lik_timing_begin.argtypes = []
+    lib.lik_timing_begin.restype = ctypes.c_int
+    lib.lik_timing_end.argtypes = [P(ctypes.c_double), P(ctypes.c_int64)]
+    lib.lik_timing_end.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -201,6 +207,19 @@ def seqs(
 
 def version() -> str:
     return load().lik_version().decode()
+
+
+def timing_begin() -> None:
+    """Start bracketing each scoring call's MaxSim tile-kernel launch with HIP events."""
+    check(load().lik_timing_begin(), "lik_timing_begin")
+
+
+def timing_end() -> tuple[float, int]:
+    """Wait for the launches recorded since :func:`timing_begin`; return (summed ms, count)."""
+    ms = ctypes.c_double()
+    n = ctypes.c_int64()
+    check(load().lik_timing_end(ctypes.byref(ms), ctypes.byref(n)), "lik_timing_end")
+    return float(ms.value), int(n.value)
 
 
 def _elem_align(dtype: torch.dtype) -> int:

@@ -274,16 +274,8 @@ def wl_plaid(args):
 
     from late_interaction_kernels.plaid import retrieve_residual_varlen
 
-    Nd, Nq, Lq, d, ncent, nbits = args.plaid_docs, args.plaid_queries, 32, 128, 65536, 2
-    g = torch.Generator(device="cuda").manual_seed(4)
-    lens = torch.randint(30, 301, (Nd,), generator=g, device="cuda")
-    cu = torch.zeros(Nd + 1, dtype=torch.int32, device="cuda")
-    cu[1:] = lens.cumsum(0).to(torch.int32)
-    tot = int(cu[-1].item())
-    cent = _normed((ncent, d), g, torch.bfloat16)
-    codes = torch.randint(0, ncent, (tot,), generator=g, device="cuda", dtype=torch.int32)
-    res = torch.randint(0, 256, (tot, d * nbits // 8), generator=g, device="cuda", dtype=torch.uint8)
-    bw = torch.linspace(-0.1, 0.1, 4, device="cuda")
+    Nd, Nq, Lq, d, nbits = args.plaid_docs, args.plaid_queries, 32, 128, 2
+    g, cu, tot, cent, codes, res, bw = _plaid_index(Nd, 4)
     Q = _normed((Nq, Lq, d), g, torch.bfloat16)
 
     def step():
@@ -301,6 +293,173 @@ def wl_plaid(args):
                    "compressed_bytes": tot * (4 + d * nbits // 8)},
         "roofline": _roofline("mfma", flops, "bf16", "plaid"),
     }
+
+
+def _plaid_index(Nd, seed, ncent=65536, d=128, nbits=2):
+    """C5's synthetic compressed corpus: doc lengths U[30,300], uniform codes,
+    uniform 2-bit bucket codes, N(0,1) normalised bf16 centroids,
+    bucket_weights linspace(-0.1, 0.1, 4)."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    lens = torch.randint(30, 301, (Nd,), generator=g, device="cuda")
+    cu = torch.zeros(Nd + 1, dtype=torch.int32, device="cuda")
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    tot = int(cu[-1].item())
+    cent = _normed((ncent, d), g, torch.bfloat16)
+    codes = torch.randint(0, ncent, (tot,), generator=g, device="cuda", dtype=torch.int32)
+    res = torch.randint(0, 256, (tot, d * nbits // 8), generator=g, device="cuda", dtype=torch.uint8)
+    bw = torch.linspace(-0.1, 0.1, 2**nbits, device="cuda")
+    return g, cu, tot, cent, codes, res, bw
+
+
+def wl_plaid_q1(args):
+    """The HBM side of PLAID: one query (Lq=32) over the full 1M-doc compressed
+    corpus, top-100, one fused decode+normalise+MaxSim launch over all docs
+    (chunk=None) then the top-k merge. Nq=1 is where the path is HBM-bound;
+    ``value`` is compressed index bytes (int32 code + 32 B residual per
+    token) per second of the tile kernel."""
+    import torch
+
+    from late_interaction_kernels.plaid import retrieve_residual_varlen
+
+    Nd, d, nbits = args.plaid_docs, 128, 2
+    g, cu, tot, cent, codes, res, bw = _plaid_index(Nd, 4)
+    Q = _normed((1, 32, d), g, torch.bfloat16)
+
+    def step():
+        return retrieve_residual_varlen(Q, codes, res, cu, cent, bw, nbits, 100, chunk=None)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    nbytes = float(tot) * (4 + d * nbits // 8)
+    roof = _roofline("hbm", nbytes, "hbm", "plaid_q1")
+    return {"metric": "PLAID compressed-index GB/s at Nq=1 (decode+MaxSim kernel)", "value": roof["achieved"],
+            "unit": "GB/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": f"PLAID {Nd} docs U[30,300], 1x32 query, nbits=2, top-100, fused route",
+                       "doc_tokens": tot, "compressed_bytes": nbytes,
+                       "queries_per_s": round(1000.0 / ms, 1)},
+            "roofline": roof}
+
+
+def wl_plaid_decode(args):
+    """Decode-only pass of the 1M-doc corpus in 16M-token slices: codes +
+    residual bits -> normalised bf16 rows. ``value`` = (compressed bytes read
+    + decoded bytes written) per second."""
+    import ctypes
+
+    import torch
+
+    from late_interaction_kernels import _lib
+    from late_interaction_kernels.plaid import _decode_into, _plaid_docs
+
+    Nd, d, nbits = args.plaid_docs, 128, 2
+    g, cu, tot, cent, codes, res, bw = _plaid_index(Nd, 4)
+    docs = _plaid_docs(codes, res, cent, bw, nbits, d, n=0, max_len=0)
+    sl = 1 << 24
+    buf = torch.empty(sl, d, device="cuda", dtype=torch.bfloat16)
+
+    def step():
+        for t0 in range(0, tot, sl):
+            _decode_into(docs, t0, min(tot, t0 + sl), True, buf)
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    for _ in range(args.warmup):
+        step()
+    _sync()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    _sync()
+    ms = start.elapsed_time(end) / args.steps
+    nbytes = float(tot) * (4 + d * nbits // 8 + 2 * d)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"metric": "PLAID decode GB/s (compressed read + bf16 rows written)", "value": round(gbs, 1),
+            "unit": "GB/s", "ms_per_step": round(ms, 4), "dtype": "bf16",
+            "config": {"workload": f"PLAID decode {tot} tokens (1M docs U[30,300]), nbits=2, normalise",
+                       "bytes_per_step": nbytes},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm"], "unit": "GB/s",
+                         "frac": round(gbs / PEAK["hbm"], 4), "traffic": None}}
+
+
+# The reference's own published forward shapes (docs/benchmarks.md:76-88,
+# 270-272, 211-212; 1x H100, bf16, no masks, CUDA-event timing) and its times.
+REF_SHAPES = [
+    ("text-short", 1, 1000, 32, 300, 128, 0.094),
+    ("text-long", 1, 1000, 32, 1024, 128, 0.096),
+    ("colpali", 1, 1000, 128, 1024, 128, 0.097),
+    ("corpus-5k", 1, 5000, 32, 300, 128, 0.129),
+    ("corpus-10k", 1, 10000, 32, 300, 128, 0.247),
+    ("train-batch-128", 128, 128, 32, 300, 128, 0.226),
+    ("large-d-512", 1, 1000, 32, 300, 512, 0.108),
+    ("mxbai-edge-corpus-10k", 1, 10000, 32, 300, 64, 0.130),
+]
+
+
+def wl_ref_shapes(args):
+    """Per-call time of maxsim() on each of the reference's published shapes
+    (plus its fp8 'batched-rerank-16k' and PLAID 10k-doc rows), next to the
+    published H100 time. ``value`` = geometric mean speedup over the
+    published times."""
+    import torch
+
+    from late_interaction_kernels import maxsim
+    from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_tensor
+    from late_interaction_kernels.plaid import retrieve_residual_varlen
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    rows = []
+
+    def timeit(fn, n=50):
+        for _ in range(5):
+            fn()
+        _sync()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        _sync()
+        return a.elapsed_time(b) / n
+
+    for name, Nq, Nd, Lq, Ld, d, ref_ms in REF_SHAPES:
+        Q = _normed((Nq, Lq, d), g, torch.bfloat16)
+        D = _normed((Nd, Ld, d), g, torch.bfloat16)
+        ms = timeit(lambda: maxsim(Q, D))
+        rows.append({"shape": name, "Nq": Nq, "Nd": Nd, "Lq": Lq, "Ld": Ld, "d": d, "ms": round(ms, 4),
+                     "ref_h100_ms": ref_ms, "speedup": round(ref_ms / ms, 2),
+                     "tflops": round(2.0 * Nq * Nd * Lq * Ld * d / ms / 1e9, 1)})
+    # fp8 batched-rerank-16k: Nq=4, Nd=4k, Lq=32, Ld=256 (reference bench_fp8.py:37)
+    Q = _normed((4, 32, 128), g, torch.float32)
+    D = _normed((4096, 256, 128), g, torch.float32)
+    Qf, sq = quantize_fp8_per_tensor(Q)
+    Df, sd = quantize_fp8_per_tensor(D)
+    ms = timeit(lambda: maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd))
+    rows.append({"shape": "fp8 batched-rerank-16k", "ms": round(ms, 4), "ref_h100_ms": 0.346,
+                 "speedup": round(0.346 / ms, 2)})
+    # PLAID full decompress+MaxSim+top-10: 10k docs x U[150,300] tokens, nbits=2, Nq=1, Lq=32
+    Nd, nbits = 10000, 2
+    lens = torch.randint(150, 301, (Nd,), generator=g, device="cuda")
+    cu = torch.zeros(Nd + 1, dtype=torch.int32, device="cuda")
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    tot = int(cu[-1].item())
+    cent = _normed((65536, 128), g, torch.bfloat16)
+    codes = torch.randint(0, 65536, (tot,), generator=g, device="cuda", dtype=torch.int32)
+    res = torch.randint(0, 256, (tot, 32), generator=g, device="cuda", dtype=torch.uint8)
+    bw = torch.linspace(-0.1, 0.1, 4, device="cuda")
+    Q = _normed((1, 32, 128), g, torch.bfloat16)
+    ms = timeit(lambda: retrieve_residual_varlen(Q, codes, res, cu, cent, bw, nbits, 10, chunk=None), n=20)
+    rows.append({"shape": "plaid full 10k docs x U[150,300], top-10", "ms": round(ms, 4), "ref_h100_ms": 3.78,
+                 "speedup": round(3.78 / ms, 2)})
+    gm = math.exp(sum(math.log(r["speedup"]) for r in rows) / len(rows))
+    return {"metric": "speedup over the reference's published H100 times on its own shapes (geomean)",
+            "value": round(gm, 2), "unit": "x", "ms_per_step": round(sum(r["ms"] for r in rows), 4),
+            "dtype": "bf16",
+            "config": {"workload": "reference headline shapes (docs/benchmarks.md), per-call maxsim()/retrieve",
+                       "shapes": rows},
+            "roofline": None}
 
 
 def wl_hbm_copy(args):
@@ -335,6 +494,9 @@ def wl_hbm_copy(args):
 
 WORKLOADS = {
     "hbm_copy": wl_hbm_copy,
+    "plaid_q1": wl_plaid_q1,
+    "ref_shapes": wl_ref_shapes,
+    "plaid_decode": wl_plaid_decode,
     "inbatch": wl_inbatch,
     "inbatch_norm": lambda a: wl_inbatch(a, normalize=True),
     "kd": wl_kd,

@@ -72,6 +72,7 @@ typedef struct {
 /* flags for lik_maxsim */
 #define LIK_NORMALIZE 1u /* per-token L2 normalise Q and D (F.normalize, eps 1e-12) */
 #define LIK_KD_LAYOUT 2u /* D holds n = Nq*K docs; query i scores docs [i*K, (i+1)*K) */
+#define LIK_NORMALIZE_Q 4u /* normalise query tokens only (docs already unit rows, e.g. decoded PLAID) */
 
 /*
  * score[i, j] = out_scale * sum_{s valid in Q_i} max_{t valid in D_j} <Q_i[s], D_j[t]>
@@ -135,6 +136,21 @@ typedef struct {
  */
 int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t flags, float* out,
                      int64_t out_stride_q, int64_t out_stride_d, lik_stream_t stream);
+
+/*
+ * Decode PLAID tokens [tok_begin, tok_end) of `docs`, indexed flat
+ * (codes[tok], residuals[tok*res_stride_tok ...]; cu_seqlens / lengths are
+ * not used), into rows of out_dtype (LIK_BF16 / LIK_F16):
+ * out[(tok - tok_begin)*out_stride + f], L2-normalised per token when flags
+ * has LIK_NORMALIZE. The rows are bitwise the ones lik_plaid_maxsim stages
+ * in LDS, so decode + lik_maxsim(..., LIK_NORMALIZE_Q) scores exactly like
+ * the fused call; that route decodes each doc once instead of once per
+ * query block, which wins when many queries share the corpus.
+ * Replaces the decode step of plaid.py:_maxsim_residual_varlen_kernel
+ * (plaid.py:780-801) and reference.py:124-139,164-167.
+ */
+int lik_plaid_decode(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end, uint32_t flags,
+                     int32_t out_dtype, void* out, int64_t out_stride, lik_stream_t stream);
 
 /*
  * PLAID approximate (centroid-only) score: out[b] = sum_{s<Lq} max_{t<len_b} qcs[codes[b,t], s],

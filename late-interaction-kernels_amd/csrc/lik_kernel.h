@@ -80,7 +80,9 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
 
   const bool f_mask = (FEAT & F_MASK) && p.d.mask != nullptr;
   const bool f_ts = (FEAT & F_TS) && p.d.ts != nullptr;
-  const bool f_norm = (SRC == SRC_PLAID || (FEAT & F_NORM)) && p.normalize;
+  // p.normalize: bit 0 normalises query tokens, bit 1 doc tokens
+  const bool f_norm_q = (SRC == SRC_PLAID || (FEAT & F_NORM)) && (p.normalize & 1);
+  const bool f_norm = (SRC == SRC_PLAID || (FEAT & F_NORM)) && (p.normalize & 2);
   const bool f_cu = (FEAT & F_CU) && p.d.cu != nullptr;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wv = tid >> 6, h = lane >> 5, l32 = lane & 31;
@@ -105,6 +107,10 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   if constexpr (SRC == SRC_PLAID) {
     for (int i = tid; i < 256; i += NT) s_bw[i] = i < p.pl.nb ? p.pl.bw[i] : 0.f;
   }
+  // Row scales start at 0: the first iteration's epilogue runs on the
+  // -inf-initialised accumulator set, and -inf * 0 (NaN) is ignored by the
+  // max, where stale LDS holding a negative scale would give +inf.
+  for (int i = tid; i < 4 * 32; i += NT) s_rs[i >> 5][i & 31] = 0.f;
 
   // ---------------- document range and tile cursor ----------------
   const int64_t jl0 = r * (int64_t)p.R;
@@ -218,7 +224,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
         const int e = h * (DPAD / 2) + ks * T::FE + c * T::CHUNK_E;
         raw[c] = (valid && e < p.q.dim) ? *(const u32x4*)(rowp + (int64_t)e * T::IN_B)
                                         : (u32x4){0u, 0u, 0u, 0u};
-        if (f_norm) ss += chunk_sumsq<EK>(raw[c]);
+        if (f_norm_q) ss += chunk_sumsq<EK>(raw[c]);
       }
       if constexpr (T::SPLIT) {
         u32x2 h0, l0, h1, l1;
@@ -232,7 +238,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
       }
     }
     ss += __shfl_xor(ss, 32);
-    float sc = f_norm ? inv_norm(ss) : 1.f;
+    float sc = f_norm_q ? inv_norm(ss) : 1.f;
     if (valid && p.q.ts) sc *= p.q.ts[q * p.q.tsn + tok * p.q.tsl];
     qsc[sub] = valid ? sc : 0.f;
   }
@@ -476,7 +482,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
         for (int e = 0; e < 8; ++e) ss = fmaf(x8[e], x8[e], ss);
 #pragma unroll
         for (int o = 1; o < SCPR; o <<= 1) ss += __shfl_xor(ss, o);
-        const float sc = p.normalize ? inv_norm(ss) : 1.f;
+        const float sc = (p.normalize & 2) ? inv_norm(ss) : 1.f;
         if (inr) {
           u32x4 w;
 #pragma unroll
@@ -522,11 +528,14 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   };
 
   // A fragments (this lane's doc row, both k-halves) of a tile, read from
-  // LDS one iteration ahead of their MFMAs into register set S.
-  u32x4 af[2][KS][FV];
-  u32x4 afl[2][T::SPLIT ? KS : 1];
+  // LDS one iteration ahead of their MFMAs into register set S. For large
+  // embedding dims the two sets would not fit next to the query fragments,
+  // so the MFMA loop reads them from the tile's LDS buffer instead.
+  constexpr bool kPrefetchA = KS * FV <= 8;
+  u32x4 af[kPrefetchA ? 2 : 1][KS][FV];
+  u32x4 afl[kPrefetchA ? 2 : 1][T::SPLIT ? KS : 1];
   auto load_a = [&](auto SS, int buf) {
-    constexpr int S = decltype(SS)::value;
+    constexpr int S = kPrefetchA ? decltype(SS)::value : 0;
     const char* A = s_tile[buf][0] + l32 * T::ROW_B + h * T::HALF_B;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -536,11 +545,18 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
         afl[S][ks] = *(const u32x4*)(s_tile[buf][1] + l32 * T::ROW_B + h * T::HALF_B + ks * T::FRAG_B);
     }
   };
-  auto mma_tile = [&](auto PP, auto SS) {
+  auto mma_tile = [&](auto PP, auto SS, int buf) {
     constexpr int P = NACC == 2 ? decltype(PP)::value : 0;
-    constexpr int S = decltype(SS)::value;
+    constexpr int S = kPrefetchA ? decltype(SS)::value : 0;
+    const char* A = s_tile[buf][0] + l32 * T::ROW_B + h * T::HALF_B;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (!kPrefetchA) {
+#pragma unroll
+        for (int v = 0; v < FV; ++v) af[0][ks][v] = *(const u32x4*)(A + ks * T::FRAG_B + v * 16);
+        if constexpr (T::SPLIT)
+          afl[0][ks] = *(const u32x4*)(s_tile[buf][1] + l32 * T::ROW_B + h * T::HALF_B + ks * T::FRAG_B);
+      }
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
         f32x16 c = ks == 0 ? bias : acc[P][sub];
@@ -677,7 +693,8 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     cur_adv(cur);
   }
   __syncthreads();
-  load_a(I0{}, 0);
+  if constexpr (kPrefetchA) load_a(I0{}, 0);
+  int buf_x = 0;          // LDS buffer of tile i
   int buf_a = 1;          // LDS buffer of tile i+1
   int buf_c = 2;          // LDS buffer of tile i+2
   int flush_half = -1;    // slot half whose flush is due (after the barrier it waited for)
@@ -705,13 +722,13 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     // tile i+2, fetch tile i+4
     const Desc qn = produce(cur);
     if constexpr (NACC == 2) {
-      mma_tile(IP{}, IP{});
+      mma_tile(IP{}, IP{}, buf_x);
       epilogue(IQ{}, (i + 3) & 3);
     } else {
       epilogue(IQ{}, (i + 3) & 3);
-      mma_tile(IP{}, IP{});
+      mma_tile(IP{}, IP{}, buf_x);
     }
-    load_a(IQ{}, buf_a);
+    if constexpr (kPrefetchA) load_a(IQ{}, buf_a);
     commit(IP{}, q2, buf_c, (i + 2) & 3);
     if constexpr (SRC == SRC_DENSE && (FEAT & F_MASK) != 0) vw2 = sm[P];
     if constexpr (SRC == SRC_DENSE) {
@@ -755,6 +772,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     }
     vw0 = vw1;
     vw1 = vw2;
+    buf_x = buf_a;
     buf_a = buf_a == 2 ? 0 : buf_a + 1;
     buf_c = buf_c == 2 ? 0 : buf_c + 1;
     __syncthreads();

@@ -100,7 +100,9 @@ struct Cfg {
 // under the other's MFMAs: 8x2 for 16-bit types; fp8 (half the fragment
 // registers, twice the MFMA rate) goes to 8x4 to amortise the per-tile work
 // over more MFMAs.
-constexpr Cfg kCfgs[] = {{1, 1}, {1, 2}, {1, 4}, {4, 1}, {4, 2}, {8, 1}, {8, 2}, {8, 4}};
+// At equal column count the wider workgroup comes first: more waves share
+// each tile's staging work.
+constexpr Cfg kCfgs[] = {{1, 1}, {1, 2}, {4, 1}, {1, 4}, {8, 1}, {4, 2}, {8, 2}, {4, 4}, {8, 4}};
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 int elem_bytes(int dt) { return dt == LIK_F32 ? 4 : (dt == LIK_FP8_E4M3 ? 1 : 2); }
@@ -116,13 +118,17 @@ int pick_dpad(int dt, int dim) {
   return -1;
 }
 
-int max_nsub(int dt, int dpad) {
+// VGPRs of query (B) fragments one 32-column block holds per lane.
+int bfrag_regs(int dt, int dpad) {
   const int fe = dt == LIK_FP8_E4M3 ? 32 : 8;
   const int cb = dt == LIK_FP8_E4M3 ? 1 : 2;
   const int ks = dpad / (2 * fe);
   const int fv = fe * cb / 16;
-  const int per = ks * fv * 4 * (dt == LIK_F32 ? 2 : 1);
-  int n = 128 / per;
+  return ks * fv * 4 * (dt == LIK_F32 ? 2 : 1);
+}
+
+int max_nsub(int dt, int dpad) {
+  int n = 128 / bfrag_regs(dt, dpad);
   return n > 4 ? 4 : n;
 }
 
@@ -166,16 +172,21 @@ int check_seqs(const lik_seqs_t* s) {
 // Choose the column block, Lq chunking and grouping for `nq` queries of
 // (max) length `lq`. `one_query_per_group` is true when each query owns its
 // documents (KD / pairs).
-int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group, Plan& pl) {
+int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group, Plan& pl, int min_w = 1) {
   pl.dpad = pick_dpad(dt, dim);
   if (pl.dpad < 0) return LIK_ERR_UNSUPPORTED;
   const int nsmax = max_nsub(dt, pl.dpad);
+  // wide rows: a one-wave workgroup would stage 32+ chunks per thread
+  if (pl.dpad >= 256 && min_w < 4) min_w = 4;
   if (lq < 1) lq = 1;
   const int64_t need = one_query_per_group ? lq : nq * lq;
   int best = -1;
   for (int i = 0; i < kNumCfgs; ++i) {
     if (kCfgs[i].NSUB > nsmax) continue;
     if (kCfgs[i].W == 8 && kCfgs[i].NSUB == 4 && dt != LIK_FP8_E4M3) continue;
+    if (kCfgs[i].W < min_w) continue;
+    // two waves per SIMD (W = 8) leave about 64 VGPRs for query fragments
+    if (kCfgs[i].W == 8 && kCfgs[i].NSUB * bfrag_regs(dt, pl.dpad) > 64) continue;
     if (best >= 0 && kCfgs[i].W * kCfgs[i].NSUB <= kCfgs[best].W * kCfgs[best].NSUB) continue;
     best = i;
     if ((int64_t)kCfgs[i].W * kCfgs[i].NSUB * 32 >= need) break;
@@ -363,7 +374,7 @@ int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float o
   Params p{};
   p.q = to_dev(*Q);
   p.d = to_dev(*D);
-  p.normalize = (flags & LIK_NORMALIZE) ? 1 : 0;
+  p.normalize = (flags & LIK_NORMALIZE) ? 3 : ((flags & LIK_NORMALIZE_Q) ? 1 : 0);
   p.out_scale = out_scale;
   p.nunits = pl.nunits;
   p.nc = pl.nc;
@@ -439,7 +450,7 @@ int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pa
   Params p{};
   p.q = to_dev(*Q);
   p.d = to_dev(*D);
-  p.normalize = (flags & LIK_NORMALIZE) ? 1 : 0;
+  p.normalize = (flags & LIK_NORMALIZE) ? 3 : ((flags & LIK_NORMALIZE_Q) ? 1 : 0);
   p.out_scale = 1.f;
   p.pair_q = pair_q;
   p.pair_d = pair_d;
@@ -483,7 +494,9 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   if (docs->n_centroids * docs->cent_stride * ceb >= (int64_t)1 << 32) return LIK_ERR_UNSUPPORTED;
 
   Plan pl;
-  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, false, pl)) != LIK_OK) return rc;
+  // PLAID tiles carry the decode VALU work: at least 4 waves share each tile
+  // even when the query block would fit one wave's columns.
+  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, false, pl, 4)) != LIK_OK) return rc;
   if (pl.dpad > 256) return LIK_ERR_UNSUPPORTED;
   if (pl.nc != 1) return LIK_ERR_UNSUPPORTED;  // Lq > 512: chunk on the caller side
   Params p{};
@@ -502,7 +515,7 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   p.pl.bw = docs->bucket_weights;
   p.pl.nb = docs->n_buckets;
   p.pl.nbits = docs->nbits;
-  p.normalize = (flags & LIK_NORMALIZE) ? 1 : 0;
+  p.normalize = (flags & LIK_NORMALIZE) ? 3 : ((flags & LIK_NORMALIZE_Q) ? 1 : 0);
   p.out_scale = 1.f;
   p.nunits = pl.nunits;
   p.nc = 1;

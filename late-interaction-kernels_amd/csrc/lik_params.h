@@ -51,7 +51,7 @@ struct Params {
   int R;             // docs per workgroup
   int64_t NR;        // doc ranges per group
   int xcd_map;
-  int normalize;
+  int normalize;  // bit 0: L2-normalise query tokens; bit 1: doc tokens
   float out_scale;
   float* out;
   int64_t osq, osd;

@@ -1,0 +1,147 @@
+// PLAID token decode for gfx950: centroid code + n-bit residual fields ->
+// (optionally L2-normalised) bf16 / fp16 token rows in HBM.
+//
+// emb[f] = centroids[code, f] + bucket_weights[field_f], field_f the nbits-bit
+// field f of the token's packed residual row, little-endian within each
+// byte (reference.py:124-139, plaid.py:240-274). Out-of-range codes decode
+// as centroid 0 and out-of-range bucket codes as the last bucket, as in the
+// fused tile kernel.
+//
+// The arithmetic is the fused kernel's staging pass, element for element:
+// the same fp32 adds, the same per-lane fma chain over 8 elements, the same
+// xor-shuffle reduction over the lanes of a row (lane group = padded dim / 8,
+// zeros past the dim), the same rounding. A decoded row is therefore
+// bitwise the row the fused kernel would have put in LDS, so decode-then-
+// dense-MaxSim and fused decode+MaxSim give identical scores.
+//
+// Work: one lane per 8 embedding elements (16 bytes out); a 256-thread
+// workgroup covers 256 / (dpad / 8) tokens. Per token it reads 4 bytes of
+// code, dim*nbits/8 bytes of residual and one centroid row (L2 / MALL
+// resident for typical tables), and writes dim*2 bytes: an HBM-bound kernel.
+#include "lik_common.h"
+
+namespace lik {
+
+template <int LPT, int CD, int OUTK>
+__global__ void __launch_bounds__(256)
+    plaid_decode_kernel(const int32_t* __restrict__ codes, const uint8_t* __restrict__ res, int64_t res_st,
+                        const char* __restrict__ cent, int64_t cent_sb, int64_t ncent,
+                        const float* __restrict__ bw, int nb, int nbits, int dim, int normalize,
+                        uint16_t* __restrict__ out, int64_t out_stride, int64_t ntok) {
+  constexpr int TPB = 256 / LPT;  // tokens per workgroup
+  constexpr int CSZ = CD == EK_F32 ? 4 : 2;
+  __shared__ float s_bw[256];
+  for (int i = threadIdx.x; i < 256; i += 256) s_bw[i] = i < nb ? bw[i] : 0.f;
+  __syncthreads();
+  const int cc = threadIdx.x % LPT;  // 8-element chunk of the row
+  const int64_t tok = (int64_t)blockIdx.x * TPB + threadIdx.x / LPT;
+  const bool tok_ok = tok < ntok;
+  const bool live = tok_ok && cc * 8 < dim;
+  float x8[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x8[e] = 0.f;
+  if (live) {
+    int64_t code = codes[tok];
+    code = (code < 0 || code >= ncent) ? 0 : code;
+    const char* crow = cent + code * cent_sb + (int64_t)cc * 8 * CSZ;
+    const uint8_t* rrow = res + tok * res_st + (int64_t)cc * nbits;
+    uint64_t bits;
+    if (nbits == 2) bits = *(const uint16_t*)rrow;
+    else if (nbits == 4) bits = *(const uint32_t*)rrow;
+    else bits = *(const uint64_t*)rrow;
+    const uint32_t bmask = (1u << nbits) - 1u;
+    u32x4 cv4[CD == EK_F32 ? 2 : 1];
+    cv4[0] = *(const u32x4*)crow;
+    if constexpr (CD == EK_F32) cv4[1] = *(const u32x4*)(crow + 16);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float cv;
+      if constexpr (CD == EK_F32) cv = __uint_as_float(cv4[e >> 2][e & 3]);
+      else if constexpr (CD == EK_BF16)
+        cv = (e & 1) ? bf16hi_to_f32(cv4[0][e >> 1]) : bf16lo_to_f32(cv4[0][e >> 1]);
+      else
+        cv = f16_to_f32((uint16_t)((e & 1) ? (cv4[0][e >> 1] >> 16) : (cv4[0][e >> 1] & 0xffffu)));
+      uint32_t bc = (uint32_t)(bits >> (e * nbits)) & bmask;
+      bc = bc < (uint32_t)nb ? bc : (uint32_t)(nb - 1);
+      x8[e] = (cc * 8 + e) < dim ? cv + s_bw[bc] : 0.f;
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = fmaf(x8[e], x8[e], ss);
+#pragma unroll
+  for (int o = 1; o < LPT; o <<= 1) ss += __shfl_xor(ss, o);
+  const float sc = normalize ? inv_norm(ss) : 1.f;
+  if (live) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (OUTK == EK_F16)
+        w[e] = f32_to_f16_bits(x8[2 * e] * sc) | (f32_to_f16_bits(x8[2 * e + 1] * sc) << 16);
+      else
+        w[e] = f32_to_bf16_bits(x8[2 * e] * sc) | (f32_to_bf16_bits(x8[2 * e + 1] * sc) << 16);
+    }
+    *(u32x4*)(out + tok * out_stride + cc * 8) = w;
+  }
+}
+
+template <int LPT, int CD>
+int launch_decode_cd(int outk, const lik_plaid_docs_t* d, const int32_t* codes, const uint8_t* res, int norm,
+                     uint16_t* out, int64_t out_stride, int64_t ntok, hipStream_t s) {
+  constexpr int TPB = 256 / LPT;
+  const int ceb = CD == EK_F32 ? 4 : 2;
+  const dim3 grid((unsigned)((ntok + TPB - 1) / TPB));
+  if (outk == EK_F16)
+    hipLaunchKernelGGL((plaid_decode_kernel<LPT, CD, EK_F16>), grid, dim3(256), 0, s, codes, res, d->res_stride_tok,
+                       (const char*)d->centroids, d->cent_stride * ceb, d->n_centroids, d->bucket_weights,
+                       d->n_buckets, d->nbits, d->dim, norm, out, out_stride, ntok);
+  else
+    hipLaunchKernelGGL((plaid_decode_kernel<LPT, CD, EK_BF16>), grid, dim3(256), 0, s, codes, res, d->res_stride_tok,
+                       (const char*)d->centroids, d->cent_stride * ceb, d->n_centroids, d->bucket_weights,
+                       d->n_buckets, d->nbits, d->dim, norm, out, out_stride, ntok);
+  return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+}
+
+template <int LPT>
+int launch_decode(int outk, const lik_plaid_docs_t* d, const int32_t* codes, const uint8_t* res, int norm,
+                  uint16_t* out, int64_t out_stride, int64_t ntok, hipStream_t s) {
+  switch (d->centroid_dtype) {
+    case LIK_BF16: return launch_decode_cd<LPT, EK_BF16>(outk, d, codes, res, norm, out, out_stride, ntok, s);
+    case LIK_F16: return launch_decode_cd<LPT, EK_F16>(outk, d, codes, res, norm, out, out_stride, ntok, s);
+    case LIK_F32: return launch_decode_cd<LPT, EK_F32>(outk, d, codes, res, norm, out, out_stride, ntok, s);
+    default: return LIK_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace lik
+
+using namespace lik;
+
+extern "C" int lik_plaid_decode(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end, uint32_t flags,
+                                int32_t out_dtype, void* out, int64_t out_stride, lik_stream_t stream) {
+  if (!docs || tok_begin < 0 || tok_end < tok_begin) return LIK_ERR_INVALID;
+  if (docs->nbits != 2 && docs->nbits != 4 && docs->nbits != 8) return LIK_ERR_INVALID;
+  if (docs->dim <= 0 || docs->dim % 8 != 0) return LIK_ERR_INVALID;
+  if (docs->n_buckets < 1 || docs->n_buckets > 256 || !docs->bucket_weights) return LIK_ERR_INVALID;
+  if (out_dtype != LIK_BF16 && out_dtype != LIK_F16) return LIK_ERR_UNSUPPORTED;
+  if (docs->res_stride_tok * 8 < (int64_t)docs->dim * docs->nbits) return LIK_ERR_INVALID;
+  if (out_stride < docs->dim || (out_stride * 2) % 16 != 0 || ((uintptr_t)out) % 16 != 0) return LIK_ERR_UNSUPPORTED;
+  const int64_t ntok = tok_end - tok_begin;
+  if (ntok == 0) return LIK_OK;
+  if (!out || !docs->codes || !docs->residuals || !docs->centroids || docs->n_centroids < 1) return LIK_ERR_INVALID;
+  const int ceb = docs->centroid_dtype == LIK_F32 ? 4 : 2;
+  if (((uintptr_t)docs->centroids) % 16 != 0 || (docs->cent_stride * ceb) % 16 != 0) return LIK_ERR_UNSUPPORTED;
+  if (((uintptr_t)docs->residuals) % 8 != 0 || docs->res_stride_tok % docs->nbits != 0) return LIK_ERR_UNSUPPORTED;
+  if (ntok > (int64_t)0x7fffffff * 8) return LIK_ERR_UNSUPPORTED;
+  const int32_t* codes = docs->codes + tok_begin;
+  const uint8_t* res = docs->residuals + tok_begin * docs->res_stride_tok;
+  const int norm = (flags & LIK_NORMALIZE) ? 1 : 0;
+  const int outk = out_dtype == LIK_F16 ? EK_F16 : EK_BF16;
+  uint16_t* o = (uint16_t*)out;
+  hipStream_t s = (hipStream_t)stream;
+  // lane group per token = padded dim / 8 (the fused kernel's row reduction width)
+  if (docs->dim <= 64) return launch_decode<8>(outk, docs, codes, res, norm, o, out_stride, ntok, s);
+  if (docs->dim <= 128) return launch_decode<16>(outk, docs, codes, res, norm, o, out_stride, ntok, s);
+  if (docs->dim <= 256) return launch_decode<32>(outk, docs, codes, res, norm, o, out_stride, ntok, s);
+  return LIK_ERR_UNSUPPORTED;
+}

@@ -25,6 +25,7 @@ LIK_ERR_LAUNCH = -4
 LIK_BF16, LIK_F16, LIK_F32, LIK_FP8_E4M3 = 0, 1, 2, 3
 LIK_NORMALIZE = 1
 LIK_KD_LAYOUT = 2
+LIK_NORMALIZE_Q = 4
 
 _ERRORS = {
     LIK_ERR_INVALID: "invalid argument",
@@ -39,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "lik_maxsim_workspace_size",
     "lik_maxsim_pairs",
     "lik_plaid_maxsim",
+    "lik_plaid_decode",
     "lik_plaid_approx_score",
     "lik_topk_merge",
     "lik_version",
@@ -125,6 +127,8 @@ def load() -> ctypes.CDLL:
     lib.lik_maxsim_pairs.restype = ctypes.c_int
     lib.lik_plaid_maxsim.argtypes = [P(LikSeqs), P(LikPlaidDocs), ctypes.c_uint32, _p, _i64, _i64, _p]
     lib.lik_plaid_maxsim.restype = ctypes.c_int
+    lib.lik_plaid_decode.argtypes = [P(LikPlaidDocs), _i64, _i64, ctypes.c_uint32, _i32, _p, _i64, _p]
+    lib.lik_plaid_decode.restype = ctypes.c_int
     lib.lik_plaid_approx_score.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _p]
     lib.lik_plaid_approx_score.restype = ctypes.c_int
     lib.lik_topk_merge.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_int, _p, _p,

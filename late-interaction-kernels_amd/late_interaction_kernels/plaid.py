@@ -234,8 +234,103 @@ def maxsim_residual_varlen(
             codes = codes_flat.contiguous().to(torch.int32)
             docs = _plaid_docs(codes, residuals_flat, centroids, bw, nbits, d, cu=cu, n=Nd,
                                max_len=int(max_seqlen_d or 0))
-            _plaid_launch(_prep_q(Q), docs, normalize, out)
+            Qp = _prep_q(Q)
+            if _use_decode_route(Nq, Lq):
+                cu_host = cu.cpu()  # the route's one device->host sync: chunk token bounds
+                j0 = 0
+                buf = None
+                while j0 < Nd:
+                    t0 = int(cu_host[j0])
+                    # largest doc range from j0 whose tokens fit the decode budget (at least one doc)
+                    j1 = int(torch.searchsorted(cu_host, t0 + _DECODE_TOKENS, right=True)) - 1
+                    j1 = min(max(j1, j0 + 1), Nd)
+                    buf = _decoded_chunk_scores(Qp, docs, cu, j0, j1, t0, int(cu_host[j1]), normalize,
+                                                out[:, j0:j1], buf)
+                    j0 = j1
+            else:
+                _plaid_launch(Qp, docs, normalize, out)
     return out.squeeze(0) if q_squeeze else out
+
+
+# Decode-once route. The fused kernel decodes each document once per
+# 512-token query block (column group); with many query tokens that repeats
+# the decode work, so above this size each doc chunk is decoded once into
+# HBM (lik_plaid_decode) and scored by the dense MaxSim kernel. Both routes
+# produce bitwise the same bf16/fp16 rows and the same scores.
+_DECODE_ROUTE_MIN_QTOK = 2048
+_DECODE_TOKENS = 1 << 20  # tokens decoded per chunk (256 MB of bf16 rows at d = 128)
+
+
+def _use_decode_route(Nq: int, Lq: int) -> bool:
+    return Nq * Lq >= _DECODE_ROUTE_MIN_QTOK
+
+
+def decode_residual_tokens(
+    codes_flat: torch.Tensor,
+    residuals_flat: torch.Tensor,
+    centroids: torch.Tensor,
+    bucket_weights: torch.Tensor,
+    nbits: int,
+    *,
+    normalize: bool = True,
+    dtype: torch.dtype = torch.bfloat16,
+) -> torch.Tensor:
+    """Decode PLAID tokens to ``[T, d]`` rows: ``centroids[code] + bucket_weights[field]``
+    per feature (little-endian fields, reference.py:124-139, 164-167), L2-normalised
+    when ``normalize``, rounded once to ``dtype`` (bf16 or fp16)."""
+    _check_nbits(nbits)
+    if codes_flat.dim() != 1 or residuals_flat.dim() != 2 or residuals_flat.shape[0] != codes_flat.shape[0]:
+        raise ValueError("codes_flat must be [T] and residuals_flat [T, packed_dim]")
+    if dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("dtype must be torch.bfloat16 or torch.float16")
+    _lib.require_gpu(codes_flat, residuals_flat, centroids, bucket_weights)
+    d = centroids.shape[-1]
+    residuals_flat, centroids, bw = _prep_index(residuals_flat, centroids, bucket_weights, nbits, d)
+    codes = codes_flat.contiguous().to(torch.int32)
+    T = codes.shape[0]
+    out = torch.empty(T, d, device=codes.device, dtype=dtype)
+    if T:
+        docs = _plaid_docs(codes, residuals_flat, centroids, bw, nbits, d, n=0, max_len=0)
+        _decode_into(docs, 0, T, normalize, out)
+    return out
+
+
+def _decode_into(docs: _lib.LikPlaidDocs, t0: int, t1: int, normalize: bool, out: torch.Tensor) -> None:
+    lib = _lib.load()
+    with torch.cuda.device(out.device):
+        rc = lib.lik_plaid_decode(
+            ctypes.byref(docs), t0, t1, _lib.LIK_NORMALIZE if normalize else 0, _lib.DTYPE_CODE[out.dtype],
+            out.data_ptr(), out.stride(0), _lib.stream_of(out),
+        )
+    _lib.check(rc, "lik_plaid_decode")
+
+
+def _decoded_chunk_scores(Qp, docs, cu, j0: int, j1: int, t0: int, t1: int, normalize: bool,
+                          out: torch.Tensor, buf: torch.Tensor | None) -> torch.Tensor:
+    """Scores of docs [j0, j1) (tokens [t0, t1)) into ``out`` ([Nq, j1-j0] view):
+    decode the chunk once, then dense packed MaxSim with query-only normalise.
+    Returns the decode buffer for reuse."""
+    d = Qp.shape[-1]
+    ntok = t1 - t0
+    if buf is None or buf.shape[0] < ntok or buf.dtype != Qp.dtype:
+        buf = torch.empty(max(ntok, 1), d, device=Qp.device, dtype=Qp.dtype)
+    if ntok == 0:
+        out.zero_()
+        return buf
+    _decode_into(docs, t0, t1, normalize, buf)
+    cu_rel = cu[j0 : j1 + 1] - t0
+    Nq, Lq, _ = Qp.shape
+    qs = _lib.seqs(Qp, n=Nq, length=Lq, stride_n=Qp.stride(0), stride_l=Qp.stride(1))
+    ds = _lib.seqs(buf, n=j1 - j0, length=0, stride_l=buf.stride(0), cu=cu_rel)
+    flags = _lib.LIK_NORMALIZE_Q if normalize else 0
+    lib = _lib.load()
+    nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
+    ws = _lib.workspace(nbytes, Qp.device)
+    with torch.cuda.device(Qp.device):
+        rc = lib.lik_maxsim(ctypes.byref(qs), ctypes.byref(ds), flags, 1.0, out.data_ptr(), out.stride(0),
+                            out.stride(1), _lib.ptr(ws), nbytes, _lib.stream_of(out))
+    _lib.check(rc, "lik_maxsim")
+    return buf
 
 
 def retrieve_residual_varlen(
@@ -276,17 +371,37 @@ def retrieve_residual_varlen(
         raise ValueError(f"chunk must be positive, got {chunk}")
     run_s = run_i = None
     with torch.no_grad():
-        for start in range(0, Nd, cs):
-            end = min(start + cs, Nd)
-            s = maxsim_residual_varlen(Q, codes_flat, residuals_flat, cu[start : end + 1], centroids,
-                                       bucket_weights, nbits, normalize=normalize)
-            run_s, run_i = topk_update(s, start, run_s, run_i, k, largest)
+        if _use_decode_route(Nq, Q.shape[1]) and Q.shape[1] > 0:
+            # decode-once route: one sync for the chunks' token bounds, one
+            # decode buffer reused by every chunk
+            _check_nbits(nbits)
+            _lib.require_gpu(Q, codes_flat, residuals_flat, cu_seqlens_d, centroids, bucket_weights)
+            d = Q.shape[-1]
+            res, cent, bw = _prep_index(residuals_flat, centroids, bucket_weights, nbits, d)
+            codes = codes_flat.contiguous().to(torch.int32)
+            docs = _plaid_docs(codes, res, cent, bw, nbits, d, cu=cu, n=Nd, max_len=0)
+            Qp = _prep_q(Q)
+            bounds = cu[list(range(0, Nd, cs)) + [Nd]].tolist()
+            buf = None
+            scores = torch.empty(Nq, cs, device=Q.device, dtype=torch.float32)
+            for c, start in enumerate(range(0, Nd, cs)):
+                end = min(start + cs, Nd)
+                s = scores[:, : end - start]
+                buf = _decoded_chunk_scores(Qp, docs, cu, start, end, bounds[c], bounds[c + 1], normalize, s, buf)
+                run_s, run_i = topk_update(s, start, run_s, run_i, k, largest)
+        else:
+            for start in range(0, Nd, cs):
+                end = min(start + cs, Nd)
+                s = maxsim_residual_varlen(Q, codes_flat, residuals_flat, cu[start : end + 1], centroids,
+                                           bucket_weights, nbits, normalize=normalize)
+                run_s, run_i = topk_update(s, start, run_s, run_i, k, largest)
     if q_squeeze:
         return run_s[0], run_i[0]
     return run_s, run_i
 
 
 __all__ = [
+    "decode_residual_tokens",
     "plaid_approx_score",
     "maxsim_residual",
     "maxsim_residual_varlen",

@@ -62,6 +62,28 @@ def test_fp8_per_token_and_masks():
     assert rel_err(got, O.maxsim(Q.numpy(), D.numpy(), qm.numpy(), dm.numpy())) < 3e-2
 
 
+def test_fp8_per_token_after_other_kernels():
+    """Regression: the per-row-scale epilogue must not read stale LDS on its
+    first iteration. Interleave other MaxSim launches (which leave negative
+    values in LDS) with one-doc-per-workgroup per-token fp8 calls."""
+    from late_interaction_kernels import maxsim
+    from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_token
+
+    _case("fp8 per-token interleaved")
+    g = torch.Generator().manual_seed(9)
+    Q = torch.randn(2, 32, 128, generator=g)
+    D = torch.randn(5, 40, 128, generator=g)
+    Qf, sq = quantize_fp8_per_token(Q.cuda())
+    Df, sd = quantize_fp8_per_token(D.cuda())
+    ref = O.maxsim(_np(Qf) * sq.cpu().numpy()[..., None], _np(Df) * sd.cpu().numpy()[..., None])
+    other_q = -torch.rand(64, 32, 128, device="cuda").to(torch.bfloat16)
+    other_d = torch.rand(300, 64, 128, device="cuda").to(torch.bfloat16)
+    for _ in range(4):
+        maxsim(other_q, other_d, normalize=True)
+        got = _np(maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd))
+        assert rel_err(got, ref) < 2e-3
+
+
 def _index(Nd, max_Ld, d, n_cent, nbits, seed, cdtype=torch.float32):
     g = torch.Generator().manual_seed(seed)
     cent = (torch.randn(n_cent, d, generator=g) * 0.3)

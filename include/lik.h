@@ -93,6 +93,38 @@ int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float o
 size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags);
 
 /*
+ * Training forward: lik_maxsim (out_scale 1) that also writes, for every
+ * (query i, doc j, query token s), the index of the doc token that wins the
+ * max: argmax[(i * docs + j) * Q->len + s], docs = D->n (cross product) or
+ * D->n / Q->n (LIK_KD_LAYOUT); ties go to the lowest doc-token index, and -1
+ * marks a row with no valid doc token (it contributes 0). bf16 / f16 / f32
+ * padded or packed docs; same masks, flags and workspace as lik_maxsim.
+ * Replaces forward.py:_run_forward with save_argmax=True
+ * (forward.py:160-182, autograd.py:169-181).
+ */
+int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float* out,
+                      int64_t out_stride_q, int64_t out_stride_d, int32_t* argmax, void* workspace,
+                      size_t workspace_bytes, lik_stream_t stream);
+
+/*
+ * Backward: given grad[i * grad_ld + j] = dL/dscore[i, j] and the argmax of
+ * lik_maxsim_argmax, writes fp32 grad_q [Q->n, Q->len, dim] and grad_d
+ * [D->n, D->len, dim] (every element written; rows that win nothing get 0).
+ * Q and D padded (no cu_seqlens / lengths); Q->mask (keep flags) zeroes the
+ * masked query tokens' terms; a doc mask acts only through the argmax.
+ * With LIK_NORMALIZE the gradients are taken through x / max(||x||, 1e-12)
+ * and the caller passes lik_maxsim_backward_workspace_size() bytes.
+ * Deterministic: fixed summation order, no atomics.
+ * Replaces backward/unified.py:maxsim_backward_unified and
+ * backward/lowmem.py:maxsim_backward_lowmem (+ the normalise Jacobian of
+ * autograd.py:211-225).
+ */
+int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q, const lik_seqs_t* D,
+                        const int32_t* argmax, uint32_t flags, float* grad_q, float* grad_d, void* workspace,
+                        size_t workspace_bytes, lik_stream_t stream);
+size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags);
+
+/*
  * Pair-list scoring: out[p] = MaxSim(Q_{pair_q[p]}, D_{pair_d[p]}).
  * Replaces score_pairs.py:_scatter_forward / _scatter_fwd_kernel
  * (score_pairs.py:33, launcher score_pairs.py:318).

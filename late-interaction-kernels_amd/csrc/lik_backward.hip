@@ -1,0 +1,316 @@
+// MaxSim backward for gfx950: gradients of the scores with respect to the
+// (unnormalised) query and document token embeddings, from the argmax the
+// training forward saved.
+//
+// score[i,j] = sum_s qm[i,s] * <Qh[i,s], Dh[j, a(i,j,s)]>, a = argmax (or -1:
+// no valid doc token, the row contributes 0), Xh = X / max(||X||, 1e-12) when
+// normalising, else X. With G = dL/dscore:
+//   dL/dQh[i,s] = qm[i,s] * sum_j G[i,j] * Dh[j, a(i,j,s)]
+//   dL/dDh[j,t] = sum_{i,s : a(i,j,s) = t} qm[i,s] * G[i,j] * Qh[i,s]
+// and through the normalisation dL/dX = (dL/dXh - <dL/dXh, Xh> Xh) / max(||X||, 1e-12).
+// This is the math of the reference's backward (backward/unified.py:27-88,
+// autograd.py:183-229); the kernels are our own:
+//
+// * grad_q_kernel: one wavefront per query token (i, s); lanes own d/64
+//   embedding dims. The argmax and G entries of 64 docs are loaded at once
+//   (one per lane) and walked in doc order, so the sum order is fixed.
+// * grad_d_kernel: one wavefront per (doc j, block of RB doc tokens) with an
+//   LDS accumulator of RB rows. It scans the (i, s) pairs in order, 64 query
+//   tokens per ballot; each pair whose winner falls in the block adds its
+//   scaled query row to that accumulator row. No atomics: every lane updates
+//   only its own dims, in scan order, so grad_D is bitwise deterministic.
+// Both apply the normalisation Jacobian to the finished row in registers.
+#include "lik_common.h"
+
+namespace lik {
+
+template <int EK>
+__device__ __forceinline__ float load_elem(const char* row, int e) {
+  if constexpr (EK == EK_BF16) return __uint_as_float((uint32_t)(*(const uint16_t*)(row + 2 * e)) << 16);
+  else if constexpr (EK == EK_F16) return f16_to_f32(*(const uint16_t*)(row + 2 * e));
+  else return *(const float*)(row + 4 * e);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+struct BwdParams {
+  const float* grad;  // [Nq, ld_g]
+  int64_t ld_g;
+  const char* q;      // Q rows: q + i*q_sn + s*q_sl (bytes)
+  int64_t q_sn, q_sl;
+  const char* d;      // D rows: d + j*d_sn + t*d_sl (bytes)
+  int64_t d_sn, d_sl;
+  const int32_t* amax;  // [Nq * ndoc_pg, Lq]
+  const int8_t* qmask;  // [Nq, Lq] keep flags, or null
+  int64_t qm_sn, qm_sl;
+  const float* qinv;  // [Nq * Lq] inverse norms (normalise), else null
+  const float* dinv;  // [Nd * Ld]
+  float* gq;          // [Nq, Lq, dim] fp32
+  float* gd;          // [Nd, Ld, dim] fp32
+  int64_t nq, lq, nd, ld;
+  int64_t ndoc_pg;    // docs per query: Nd (cross product) or K (KD layout)
+  int kd;
+  int dim;
+};
+
+// inv[r] = 1 / max(||row r||, 1e-12) for rows r = i*L + t of a [n, L, dim] tensor.
+template <int EK>
+__global__ void __launch_bounds__(256) row_invnorm_kernel(const char* x, int64_t sn, int64_t sl, int64_t n,
+                                                          int64_t L, int dim, float* inv) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= n * L) return;
+  const char* row = x + (r / L) * sn + (r % L) * sl;
+  float ss = 0.f;
+  for (int e = 0; e < dim; ++e) {
+    const float v = load_elem<EK>(row, e);
+    ss = fmaf(v, v, ss);
+  }
+  inv[r] = inv_norm(ss);
+}
+
+template <int EK, int DPL>
+__global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  if (w >= bp.nq * bp.lq) return;
+  const int64_t i = w / bp.lq, s = w % bp.lq;
+  const int64_t j0 = bp.kd ? i * bp.ndoc_pg : 0;
+  const int32_t* am = bp.amax + (i * bp.ndoc_pg) * bp.lq + s;
+  const float* g = bp.grad + i * bp.ld_g;
+  float acc[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) acc[k] = 0.f;
+  for (int64_t c0 = 0; c0 < bp.ndoc_pg; c0 += 64) {
+    const int64_t jl = c0 + lane;
+    const int av = jl < bp.ndoc_pg ? am[jl * bp.lq] : -1;
+    const float gv = jl < bp.ndoc_pg ? g[jl] : 0.f;
+    float sv = gv;
+    if (bp.dinv && av >= 0) sv *= bp.dinv[(j0 + jl) * bp.ld + av];
+    uint64_t bal = __ballot(av >= 0 && gv != 0.f);
+    while (bal) {
+      const int l = __builtin_ctzll(bal);
+      bal &= bal - 1;
+      const int a = __builtin_amdgcn_readlane(av, l);
+      const float sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), l));
+      const char* row = bp.d + (j0 + c0 + l) * bp.d_sn + (int64_t)a * bp.d_sl;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const int e = lane * DPL + k;
+        if (e < bp.dim) acc[k] = fmaf(sc, load_elem<EK>(row, e), acc[k]);
+      }
+    }
+  }
+  const bool keep = !bp.qmask || bp.qmask[i * bp.qm_sn + s * bp.qm_sl] != 0;
+  if (bp.qinv) {
+    const float qi = bp.qinv[w];
+    const char* qrow = bp.q + i * bp.q_sn + s * bp.q_sl;
+    float xh[DPL], dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      const int e = lane * DPL + k;
+      xh[k] = e < bp.dim ? load_elem<EK>(qrow, e) * qi : 0.f;
+      dot = fmaf(acc[k], xh[k], dot);
+    }
+    dot = wave_sum(dot);
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) acc[k] = (acc[k] - dot * xh[k]) * qi;
+  }
+  float* out = bp.gq + w * bp.dim;
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) {
+    const int e = lane * DPL + k;
+    if (e < bp.dim) out[e] = keep ? acc[k] : 0.f;
+  }
+}
+
+// RB doc rows per wavefront, RB * 64 * DPL floats of LDS accumulator (16 KB).
+template <int EK, int DPL>
+__global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
+  constexpr int RB = 64 / DPL < 32 ? 64 / DPL : 32;
+  __shared__ float s_acc[RB][64 * DPL];
+  const int lane = threadIdx.x;
+  const int64_t nrb = (bp.ld + RB - 1) / RB;
+  const int64_t j = blockIdx.x / nrb;
+  const int64_t t0 = (blockIdx.x % nrb) * RB;
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) s_acc[r][lane * DPL + k] = 0.f;
+  const int64_t jl = bp.kd ? j % bp.ndoc_pg : j;
+  const int64_t i_begin = bp.kd ? j / bp.ndoc_pg : 0;
+  const int64_t i_end = bp.kd ? i_begin + 1 : bp.nq;
+  for (int64_t i = i_begin; i < i_end; ++i) {
+    const float gij = bp.grad[i * bp.ld_g + jl];
+    if (gij == 0.f) continue;
+    const int32_t* am = bp.amax + (i * bp.ndoc_pg + jl) * bp.lq;
+    for (int64_t s0 = 0; s0 < bp.lq; s0 += 64) {
+      const int64_t s = s0 + lane;
+      int a = s < bp.lq ? am[s] : -1;
+      if (a >= 0 && bp.qmask && bp.qmask[i * bp.qm_sn + s * bp.qm_sl] == 0) a = -1;
+      float sc = gij;
+      if (bp.qinv && a >= 0) sc *= bp.qinv[i * bp.lq + s];
+      uint64_t bal = __ballot(a >= t0 && a < t0 + RB);
+      while (bal) {
+        const int l = __builtin_ctzll(bal);
+        bal &= bal - 1;
+        const int r = __builtin_amdgcn_readlane(a, l) - (int)t0;
+        const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
+        const char* qrow = bp.q + i * bp.q_sn + (s0 + l) * bp.q_sl;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) {
+          const int e = lane * DPL + k;
+          if (e < bp.dim) s_acc[r][e] = fmaf(c, load_elem<EK>(qrow, e), s_acc[r][e]);
+        }
+      }
+    }
+  }
+  // finished rows: normalisation Jacobian, then store
+  for (int r = 0; r < RB; ++r) {
+    const int64_t t = t0 + r;
+    if (t >= bp.ld) break;
+    float gh[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) gh[k] = s_acc[r][lane * DPL + k];
+    if (bp.dinv) {
+      const float di = bp.dinv[j * bp.ld + t];
+      const char* drow = bp.d + j * bp.d_sn + t * bp.d_sl;
+      float xh[DPL], dot = 0.f;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const int e = lane * DPL + k;
+        xh[k] = e < bp.dim ? load_elem<EK>(drow, e) * di : 0.f;
+        dot = fmaf(gh[k], xh[k], dot);
+      }
+      dot = wave_sum(dot);
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) gh[k] = (gh[k] - dot * xh[k]) * di;
+    }
+    float* out = bp.gd + (j * bp.ld + t) * bp.dim;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      const int e = lane * DPL + k;
+      if (e < bp.dim) out[e] = gh[k];
+    }
+  }
+}
+
+template <int EK, int DPL>
+int launch_bwd(const BwdParams& bp, hipStream_t s) {
+  constexpr int RB = 64 / DPL < 32 ? 64 / DPL : 32;
+  const int64_t nw = bp.nq * bp.lq;
+  if (nw > 0) {
+    hipLaunchKernelGGL((grad_q_kernel<EK, DPL>), dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, s, bp);
+    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+  }
+  const int64_t nb = bp.nd * ((bp.ld + RB - 1) / RB);
+  if (nb > 0) {
+    hipLaunchKernelGGL((grad_d_kernel<EK, DPL>), dim3((unsigned)nb), dim3(64), 0, s, bp);
+    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+  }
+  return LIK_OK;
+}
+
+template <int EK>
+int launch_bwd_dpl(const BwdParams& bp, hipStream_t s) {
+  if (bp.dim <= 64) return launch_bwd<EK, 1>(bp, s);
+  if (bp.dim <= 128) return launch_bwd<EK, 2>(bp, s);
+  if (bp.dim <= 256) return launch_bwd<EK, 4>(bp, s);
+  if (bp.dim <= 512) return launch_bwd<EK, 8>(bp, s);
+  return LIK_ERR_UNSUPPORTED;
+}
+
+template <int EK>
+int launch_invnorm(const char* x, int64_t sn, int64_t sl, int64_t n, int64_t L, int dim, float* inv, hipStream_t s) {
+  const int64_t rows = n * L;
+  if (rows == 0) return LIK_OK;
+  hipLaunchKernelGGL((row_invnorm_kernel<EK>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, x, sn, sl, n, L,
+                     dim, inv);
+  return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+}
+
+int elem_size(int dt) { return dt == LIK_F32 ? 4 : 2; }
+
+}  // namespace lik
+
+using namespace lik;
+
+extern "C" {
+
+size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
+  if (!Q || !D || !(flags & LIK_NORMALIZE)) return 0;
+  return (size_t)(Q->n * Q->len + D->n * D->len) * sizeof(float) + 256;
+}
+
+int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q, const lik_seqs_t* D,
+                        const int32_t* argmax, uint32_t flags, float* grad_q, float* grad_d, void* workspace,
+                        size_t workspace_bytes, lik_stream_t stream) {
+  if (!Q || !D) return LIK_ERR_INVALID;
+  if (Q->dtype != D->dtype || Q->dim != D->dim || Q->dim <= 0) return LIK_ERR_INVALID;
+  if (Q->dtype != LIK_BF16 && Q->dtype != LIK_F16 && Q->dtype != LIK_F32) return LIK_ERR_UNSUPPORTED;
+  if (Q->cu_seqlens || D->cu_seqlens || Q->lengths || D->lengths || D->mask || Q->token_scale || D->token_scale)
+    return LIK_ERR_UNSUPPORTED;  // padded layout; doc masks act through the forward's argmax
+  if (Q->n < 0 || D->n < 0 || Q->len < 0 || D->len < 0) return LIK_ERR_INVALID;
+  if (Q->dim > 512) return LIK_ERR_UNSUPPORTED;
+  const bool kd = (flags & LIK_KD_LAYOUT) != 0;
+  if (kd && (Q->n == 0 || D->n % Q->n != 0)) return LIK_ERR_INVALID;
+  if (Q->n == 0 || D->n == 0) return LIK_OK;
+  if (!grad || !argmax || !grad_q || !grad_d || !Q->data || !D->data) return LIK_ERR_INVALID;
+  hipStream_t s = (hipStream_t)stream;
+  const int eb = elem_size(Q->dtype);
+  BwdParams bp{};
+  bp.grad = grad;
+  bp.ld_g = grad_ld;
+  bp.q = (const char*)Q->data;
+  bp.q_sn = Q->stride_n * eb;
+  bp.q_sl = Q->stride_l * eb;
+  bp.d = (const char*)D->data;
+  bp.d_sn = D->stride_n * eb;
+  bp.d_sl = D->stride_l * eb;
+  bp.amax = argmax;
+  bp.qmask = Q->mask;
+  bp.qm_sn = Q->mask_stride_n;
+  bp.qm_sl = Q->mask_stride_l;
+  bp.gq = grad_q;
+  bp.gd = grad_d;
+  bp.nq = Q->n;
+  bp.lq = Q->len;
+  bp.nd = D->n;
+  bp.ld = D->len;
+  bp.kd = kd ? 1 : 0;
+  bp.ndoc_pg = kd ? D->n / Q->n : D->n;
+  bp.dim = Q->dim;
+  int rc;
+  if (flags & LIK_NORMALIZE) {
+    const size_t need = lik_maxsim_backward_workspace_size(Q, D, flags);
+    if (!workspace || workspace_bytes < need) return LIK_ERR_WORKSPACE;
+    float* qinv = (float*)workspace;
+    float* dinv = qinv + Q->n * Q->len;
+    bp.qinv = qinv;
+    bp.dinv = dinv;
+    switch (Q->dtype) {
+      case LIK_BF16:
+        if ((rc = launch_invnorm<EK_BF16>(bp.q, bp.q_sn, bp.q_sl, Q->n, Q->len, Q->dim, qinv, s)) != LIK_OK) return rc;
+        rc = launch_invnorm<EK_BF16>(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, D->dim, dinv, s);
+        break;
+      case LIK_F16:
+        if ((rc = launch_invnorm<EK_F16>(bp.q, bp.q_sn, bp.q_sl, Q->n, Q->len, Q->dim, qinv, s)) != LIK_OK) return rc;
+        rc = launch_invnorm<EK_F16>(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, D->dim, dinv, s);
+        break;
+      default:
+        if ((rc = launch_invnorm<EK_F32>(bp.q, bp.q_sn, bp.q_sl, Q->n, Q->len, Q->dim, qinv, s)) != LIK_OK) return rc;
+        rc = launch_invnorm<EK_F32>(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, D->dim, dinv, s);
+    }
+    if (rc != LIK_OK) return rc;
+  }
+  switch (Q->dtype) {
+    case LIK_BF16: return launch_bwd_dpl<EK_BF16>(bp, s);
+    case LIK_F16: return launch_bwd_dpl<EK_F16>(bp, s);
+    default: return launch_bwd_dpl<EK_F32>(bp, s);
+  }
+}
+
+}  // extern "C"

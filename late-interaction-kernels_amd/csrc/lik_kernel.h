@@ -44,7 +44,8 @@ constexpr int kRMax = 512;  // docs per workgroup (host caps R)
 // FEAT: features compiled in (a cleared bit removes the code path; the host
 // picks an instantiation whose bits cover the call): F_MASK doc mask,
 // F_TS per-token doc scale, F_NORM L2 normalise, F_CU packed docs.
-enum { F_MASK = 1, F_TS = 2, F_NORM = 4, F_CU = 8, F_ALL = 15 };
+// F_ARGMAX (training forward): also write each (query token, doc) winner's doc-token index.
+enum { F_MASK = 1, F_TS = 2, F_NORM = 4, F_CU = 8, F_ALL = 15, F_ARGMAX = 16 };
 
 template <int EK, int DPAD, int W, int NSUB, int SRC, int CD, int FEAT>
 __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
@@ -258,6 +259,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   };
   struct Desc {
     int nv;       // valid rows of the tile (0..32)
+    int t;        // tile index within its doc
     int k;        // doc index within the workgroup's range
     bool docend;  // last tile of its doc
     bool holes;   // doc has a mask with holes (dense)
@@ -290,6 +292,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     const int rem = c.len - c.t * 32;
     d.nv = rem >= 32 ? 32 : (rem > 0 ? rem : 0);
     d.k = c.k;
+    d.t = c.t;
     d.docend = c.len > 0 && rem <= 32;
     d.holes = c.holes;
     d.tok = c.off + (int64_t)c.t * 32;
@@ -510,9 +513,11 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   constexpr int NACC = (W == 8 && NSUB >= 4) ? 1 : 2;
   f32x16 acc[NACC][NSUB];
   float m[NSUB];
+  int mi[NSUB];  // F_ARGMAX: doc-token index of m (-1: no valid token yet)
 #pragma unroll
   for (int sub = 0; sub < NSUB; ++sub) {
     m[sub] = NEG_INF;
+    mi[sub] = -1;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[NACC - 1][sub][e] = NEG_INF;
   }
@@ -602,9 +607,28 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     }
   };
 
-  // Running max over the rows of the previous tile (accumulator set P).
-  auto epilogue = [&](auto PP, int rslot) {
+  // Running max over the rows of the previous tile (accumulator set P),
+  // whose first row is doc token `row0`.
+  auto epilogue = [&](auto PP, int rslot, int row0) {
     constexpr int P = NACC == 2 ? decltype(PP)::value : 0;
+    if constexpr ((FEAT & F_ARGMAX) != 0) {
+      // rows are visited in increasing index order and only a strictly larger
+      // value replaces the winner: ties keep the lowest doc-token index
+      const int r0 = row0 + 4 * h;
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float v = acc[P][sub][4 * j + e];
+            const bool up = v > m[sub];
+            m[sub] = up ? v : m[sub];
+            mi[sub] = up ? r0 + 8 * j + e : mi[sub];
+          }
+      (void)rslot;
+      return;
+    }
     if constexpr (kRowScaleEpi) {
       if (row_scale) {
         f32x4 sc[4];
@@ -629,6 +653,29 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   // The previous tile was the last of doc k: park the per-column maxima.
   auto doc_end = [&](int k) {
     const int sl = nend % NSLOT;
+    if constexpr ((FEAT & F_ARGMAX) != 0) {
+      // winner over lanes l, l^32 (larger value; equal values: lower index),
+      // written to argmax[(q * docs + j) * Lq + token]
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) {
+        const auto sv = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
+        const auto si = __builtin_amdgcn_permlane32_swap((uint32_t)mi[sub], (uint32_t)mi[sub], false, false);
+        const float v0 = __uint_as_float(sv[0]), v1 = __uint_as_float(sv[1]);
+        const int i0 = (int)si[0], i1 = (int)si[1];
+        const bool take1 = v1 > v0 || (v1 == v0 && (unsigned)i1 < (unsigned)i0);
+        const int win = take1 ? i1 : i0;
+        const int col = (wv * NSUB + sub) * 32 + l32;
+        const int ul = col / p.LU;
+        if (h == 0 && p.amax && !p.pair_q && ul < p.QPG) {
+          const int64_t u = g * p.QPG + ul;
+          const int64_t q = u / p.nc;
+          const int64_t tok = (u - q * p.nc) * p.LU + (col - ul * p.LU);
+          if (u < p.nunits && tok < p.amax_ld)
+            p.amax[(q * p.ndocs_pg + jl0 + k) * p.amax_ld + tok] = __builtin_isfinite(fmaxf(v0, v1)) ? win : -1;
+        }
+        mi[sub] = -1;
+      }
+    }
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
@@ -723,9 +770,9 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     const Desc qn = produce(cur);
     if constexpr (NACC == 2) {
       mma_tile(IP{}, IP{}, buf_x);
-      epilogue(IQ{}, (i + 3) & 3);
+      epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
     } else {
-      epilogue(IQ{}, (i + 3) & 3);
+      epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
       mma_tile(IP{}, IP{}, buf_x);
     }
     if constexpr (kPrefetchA) load_a(IQ{}, buf_a);

@@ -72,6 +72,12 @@ __global__ void __launch_bounds__(256) doc_extent_kernel(const int8_t* mask, int
   }
 }
 
+// a[i] = v for i < n (used to mark argmax entries "no winner" before a training forward).
+__global__ void __launch_bounds__(256) fill_i32_kernel(int32_t* a, int64_t n, int32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) a[i] = v;
+}
+
 // out[q, j] = sum_c part[q*nc + c, j], c ascending.
 __global__ void __launch_bounds__(256) unit_sum_kernel(const float* part, int64_t nq, int nc, int64_t nd,
                                                        float* out, int64_t osq, int64_t osd) {
@@ -244,6 +250,14 @@ int pick_R(int64_t ngroups, int64_t ndocs) {
 }
 
 int launch_dense(int dt, const Plan& pl, const Params& p, int64_t nb, hipStream_t s) {
+  if (p.amax) {
+    switch (dt) {
+      case LIK_BF16: return launch_dense_train_bf16(pl, p, nb, s);
+      case LIK_F16: return launch_dense_train_f16(pl, p, nb, s);
+      case LIK_F32: return launch_dense_train_f32(pl, p, nb, s);
+      default: return LIK_ERR_UNSUPPORTED;
+    }
+  }
   switch (dt) {
     case LIK_BF16: return launch_dense_bf16(pl, p, nb, s);
     case LIK_F16: return launch_dense_f16(pl, p, nb, s);
@@ -353,9 +367,28 @@ size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint3
   return ws_layout(Q, D, flags, pl).total;
 }
 
+static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
+                       int64_t out_stride_q, int64_t out_stride_d, int32_t* argmax, void* workspace,
+                       size_t workspace_bytes, lik_stream_t stream);
+
 int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
                int64_t out_stride_q, int64_t out_stride_d, void* workspace, size_t workspace_bytes,
                lik_stream_t stream) {
+  return maxsim_impl(Q, D, flags, out_scale, out, out_stride_q, out_stride_d, nullptr, workspace, workspace_bytes,
+                     stream);
+}
+
+int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float* out, int64_t out_stride_q,
+                      int64_t out_stride_d, int32_t* argmax, void* workspace, size_t workspace_bytes,
+                      lik_stream_t stream) {
+  if (!argmax && Q && D && Q->n > 0 && D->n > 0) return LIK_ERR_INVALID;
+  if (Q && (Q->dtype == LIK_FP8_E4M3 || Q->token_scale || (D && D->token_scale))) return LIK_ERR_UNSUPPORTED;
+  return maxsim_impl(Q, D, flags, 1.0f, out, out_stride_q, out_stride_d, argmax, workspace, workspace_bytes, stream);
+}
+
+static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
+                       int64_t out_stride_q, int64_t out_stride_d, int32_t* argmax, void* workspace,
+                       size_t workspace_bytes, lik_stream_t stream) {
   int rc;
   if ((rc = check_seqs(Q)) != LIK_OK) return rc;
   if ((rc = check_seqs(D)) != LIK_OK) return rc;
@@ -383,6 +416,16 @@ int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float o
   p.ngroups = pl.ngroups;
   p.kd_K = kd ? D->n / Q->n : 0;
   p.ndocs_pg = kd ? p.kd_K : D->n;
+  if (argmax) {
+    // entries no doc-end reaches (empty docs) stay -1
+    const int64_t na = Q->n * p.ndocs_pg * Q->len;
+    if (na > 0) {
+      hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, s, argmax, na, -1);
+      if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+    }
+    p.amax = argmax;
+    p.amax_ld = Q->len;
+  }
 
   char* ws = (char*)workspace;
   if (wl.need_extent) {

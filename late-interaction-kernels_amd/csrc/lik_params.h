@@ -55,6 +55,8 @@ struct Params {
   float out_scale;
   float* out;
   int64_t osq, osd;
+  int32_t* amax;    // training forward: winner doc-token index per (query, doc, query token), or null
+  int64_t amax_ld;  // query tokens per (query, doc) row of amax (the padded Lq)
 };
 
 enum { SRC_DENSE = 0, SRC_PLAID = 1 };
@@ -106,6 +108,10 @@ int launch_dense_f16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s)
 int launch_dense_f32(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 int launch_dense_fp8(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 int launch_plaid_bf16(int cd, const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
+// training forward (argmax output), lik_inst_train_*.hip
+int launch_dense_train_bf16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
+int launch_dense_train_f16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
+int launch_dense_train_f32(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 int launch_plaid_f16(int cd, const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 
 }  // namespace lik

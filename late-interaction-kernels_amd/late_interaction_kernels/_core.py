@@ -101,6 +101,82 @@ def dense_maxsim(
     return out
 
 
+def dense_maxsim_train(
+    Q: torch.Tensor,
+    D: torch.Tensor,
+    q_mask: torch.Tensor | None,
+    d_mask: torch.Tensor | None,
+    *,
+    normalize: bool,
+    kd: bool,
+):
+    """Training forward: scores plus the saved state the backward needs.
+
+    Returns ``(scores, argmax, Qp, Dp, qm)``: ``argmax`` is ``[Nq * docs, Lq]``
+    int32 (winning doc-token index, -1 for rows without a valid doc token);
+    ``Qp`` / ``Dp`` are the kernel-ready (16-byte-row) copies of Q and D and
+    ``qm`` the int8 query mask.
+    """
+    _lib.require_gpu(Q, D, q_mask, d_mask)
+    Nq, Lq, _ = Q.shape
+    Nd, Ld, _ = D.shape
+    docs = (Nd // Nq if Nq else 0) if kd else Nd
+    out = torch.empty(Nq, docs, device=Q.device, dtype=torch.float32)
+    argmax = torch.full((Nq * docs, Lq), -1, device=Q.device, dtype=torch.int32)
+    Qp = _lib.prepare_tokens(Q.detach())
+    Dp = _lib.prepare_tokens(D.detach())
+    qm = _mask_i8(q_mask, (Nq, Lq))
+    if Nq == 0 or docs == 0 or Lq == 0 or Ld == 0:
+        return out.zero_(), argmax, Qp, Dp, qm
+    dm = _mask_i8(d_mask, (Nd, Ld))
+    qs = _lib.seqs(Qp, n=Nq, length=Lq, stride_n=Qp.stride(0), stride_l=Qp.stride(1), mask=qm,
+                   mask_strides=(qm.stride(0), qm.stride(1)) if qm is not None else (0, 0))
+    ds = _lib.seqs(Dp, n=Nd, length=Ld, stride_n=Dp.stride(0), stride_l=Dp.stride(1), mask=dm,
+                   mask_strides=(dm.stride(0), dm.stride(1)) if dm is not None else (0, 0))
+    flags = (_lib.LIK_NORMALIZE if normalize else 0) | (_lib.LIK_KD_LAYOUT if kd else 0)
+    lib = _lib.load()
+    nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
+    ws = _lib.workspace(nbytes, Q.device)
+    with torch.cuda.device(Q.device):
+        rc = lib.lik_maxsim_argmax(ctypes.byref(qs), ctypes.byref(ds), flags, out.data_ptr(), out.stride(0),
+                                   out.stride(1), argmax.data_ptr(), _lib.ptr(ws), nbytes, _lib.stream_of(out))
+    _lib.check(rc, "lik_maxsim_argmax")
+    return out, argmax, Qp, Dp, qm
+
+
+def maxsim_backward(
+    grad: torch.Tensor,
+    Qp: torch.Tensor,
+    Dp: torch.Tensor,
+    argmax: torch.Tensor,
+    qm: torch.Tensor | None,
+    *,
+    normalize: bool,
+    kd: bool,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 ``(grad_Q [Nq, Lq, dp], grad_D [Nd, Ld, dp])`` for upstream ``grad`` [Nq, docs]."""
+    Nq, Lq, dp = Qp.shape
+    Nd, Ld, _ = Dp.shape
+    gq = torch.zeros(Nq, Lq, dp, device=Qp.device, dtype=torch.float32)
+    gd = torch.zeros(Nd, Ld, dp, device=Dp.device, dtype=torch.float32)
+    if Nq == 0 or Nd == 0 or Lq == 0 or Ld == 0:
+        return gq, gd
+    g = grad.to(torch.float32).contiguous()
+    qs = _lib.seqs(Qp, n=Nq, length=Lq, stride_n=Qp.stride(0), stride_l=Qp.stride(1), mask=qm,
+                   mask_strides=(qm.stride(0), qm.stride(1)) if qm is not None else (0, 0))
+    ds = _lib.seqs(Dp, n=Nd, length=Ld, stride_n=Dp.stride(0), stride_l=Dp.stride(1))
+    flags = (_lib.LIK_NORMALIZE if normalize else 0) | (_lib.LIK_KD_LAYOUT if kd else 0)
+    lib = _lib.load()
+    nbytes = lib.lik_maxsim_backward_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
+    ws = _lib.workspace(nbytes, Qp.device)
+    with torch.cuda.device(Qp.device):
+        rc = lib.lik_maxsim_backward(g.data_ptr(), g.stride(0), ctypes.byref(qs), ctypes.byref(ds), argmax.data_ptr(),
+                                     flags, gq.data_ptr(), gd.data_ptr(), _lib.ptr(ws), nbytes,
+                                     _lib.stream_of(gq))
+    _lib.check(rc, "lik_maxsim_backward")
+    return gq, gd
+
+
 def packed_maxsim(
     Q_packed: torch.Tensor,
     D_packed: torch.Tensor,

@@ -38,6 +38,9 @@ _ERRORS = {
 EXPORTED_SYMBOLS = (
     "lik_maxsim",
     "lik_maxsim_workspace_size",
+    "lik_maxsim_argmax",
+    "lik_maxsim_backward",
+    "lik_maxsim_backward_workspace_size",
     "lik_maxsim_pairs",
     "lik_plaid_maxsim",
     "lik_plaid_decode",
@@ -123,6 +126,14 @@ def load() -> ctypes.CDLL:
     lib.lik_maxsim.restype = ctypes.c_int
     lib.lik_maxsim_workspace_size.argtypes = [P(LikSeqs), P(LikSeqs), ctypes.c_uint32]
     lib.lik_maxsim_workspace_size.restype = ctypes.c_size_t
+    lib.lik_maxsim_argmax.argtypes = [P(LikSeqs), P(LikSeqs), ctypes.c_uint32, _p, _i64, _i64, _p, _p,
+                                      ctypes.c_size_t, _p]
+    lib.lik_maxsim_argmax.restype = ctypes.c_int
+    lib.lik_maxsim_backward.argtypes = [_p, _i64, P(LikSeqs), P(LikSeqs), _p, ctypes.c_uint32, _p, _p, _p,
+                                        ctypes.c_size_t, _p]
+    lib.lik_maxsim_backward.restype = ctypes.c_int
+    lib.lik_maxsim_backward_workspace_size.argtypes = [P(LikSeqs), P(LikSeqs), ctypes.c_uint32]
+    lib.lik_maxsim_backward_workspace_size.restype = ctypes.c_size_t
     lib.lik_maxsim_pairs.argtypes = [P(LikSeqs), P(LikSeqs), _p, _p, _i64, ctypes.c_uint32, _p, _p]
     lib.lik_maxsim_pairs.restype = ctypes.c_int
     lib.lik_plaid_maxsim.argtypes = [P(LikSeqs), P(LikPlaidDocs), ctypes.c_uint32, _p, _i64, _i64, _p]

@@ -5,9 +5,12 @@ Signatures and dispatch follow the reference's ``autograd.py:356-501``:
 2-D inputs squeeze the matching output dim, masks are ``True`` = keep.
 All scoring runs in the gfx950 HIP kernels of liblik_hip.so.
 
-This build is forward (inference) only. The reference's ``backward=``
-strategies are accepted for signature compatibility and validated, but a
-call that needs gradients raises ``NotImplementedError``.
+Gradients: when Q or D requires grad (and grad mode is on), the training
+forward saves each winner's doc-token index and the backward runs the
+deterministic HIP gradient kernels (``lik_maxsim_backward``). The
+reference's ``backward="unified" | "lowmem"`` strategies both map to that
+one implementation (atomic-free, bitwise reproducible); the argument is
+validated for compatibility.
 """
 
 from __future__ import annotations
@@ -17,7 +20,7 @@ import warnings
 
 import torch
 
-from ._core import dense_maxsim, unify_dtype
+from ._core import dense_maxsim, dense_maxsim_train, maxsim_backward, unify_dtype
 
 _VALID_METHODS = ("auto", "unified", "lowmem")
 
@@ -59,12 +62,49 @@ def _maybe_warn_unnormalized(Q: torch.Tensor) -> None:
 
 
 def _no_grad_guard(*ts: torch.Tensor) -> None:
+    """Packed / padded entry points are inference-only in this build."""
     if torch.is_grad_enabled() and any(t.requires_grad for t in ts):
         raise NotImplementedError(
-            "late_interaction_kernels (MI355X build) implements the MaxSim forward only; "
-            "gradients are not available yet. Call under torch.no_grad() / inference_mode() "
-            "or detach the inputs."
+            "late_interaction_kernels (MI355X build): gradients are implemented for maxsim / "
+            "maxsim_pairs (incl. KD layout); this packed entry point is inference-only. Call under "
+            "torch.no_grad() / inference_mode() or use maxsim on padded tensors."
         )
+
+
+def _needs_grad(*ts: torch.Tensor) -> bool:
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
+class _MaxSimFn(torch.autograd.Function):
+    """Fused MaxSim with saved argmax (reference autograd.py:169-229)."""
+
+    @staticmethod
+    def forward(ctx, Q, D, q_mask, d_mask, normalize, kd):
+        scores, argmax, Qp, Dp, qm = dense_maxsim_train(Q, D, q_mask, d_mask, normalize=normalize, kd=kd)
+        ctx.save_for_backward(Qp, Dp, argmax, qm)
+        ctx.normalize = normalize
+        ctx.kd = kd
+        ctx.shapes = (Q.shape, D.shape)
+        ctx.dtypes = (Q.dtype, D.dtype)
+        ctx.mark_non_differentiable(argmax)
+        return scores
+
+    @staticmethod
+    def backward(ctx, grad_scores):
+        Qp, Dp, argmax, qm = ctx.saved_tensors
+        gq, gd = maxsim_backward(grad_scores, Qp, Dp, argmax, qm, normalize=ctx.normalize, kd=ctx.kd)
+        (qshape, dshape), (qdt, ddt) = ctx.shapes, ctx.dtypes
+        gq = gq[..., : qshape[-1]].to(qdt) if ctx.needs_input_grad[0] else None
+        gd = gd[..., : dshape[-1]].to(ddt) if ctx.needs_input_grad[1] else None
+        return gq, gd, None, None, None, None
+
+
+def _score(Q, D, q_mask, d_mask, *, normalize: bool, kd: bool = False) -> torch.Tensor:
+    if _needs_grad(Q, D):
+        if Q.dtype == torch.float64 or D.dtype == torch.float64:
+            raise TypeError("maxsim gradients support fp16 / bf16 / fp32 inputs")
+        return _MaxSimFn.apply(Q, D, q_mask, d_mask, normalize, kd)
+    return dense_maxsim(Q, D, q_mask, d_mask, normalize=normalize, kd=kd)
 
 
 def _resolve_method(backward: str | None) -> str:
@@ -94,11 +134,10 @@ def _maxsim_kd(Q, D, q_mask, d_mask, *, normalize: bool) -> torch.Tensor:
             f"d_mask must be [Nq={Nq}, K={K}, Ld={Ld}] for KD layout; got {tuple(d_mask.shape)}."
         )
     _validate_devices(Q, D, q_mask, d_mask)
-    _no_grad_guard(Q, D)
     Q, D = unify_dtype(Q, D)
     D_flat = D.reshape(Nq * K, Ld, d_d)
     dm = d_mask.reshape(Nq * K, Ld) if d_mask is not None else None
-    return dense_maxsim(Q, D_flat, q_mask, dm, normalize=normalize, kd=True)
+    return _score(Q, D_flat, q_mask, dm, normalize=normalize, kd=True)
 
 
 def maxsim(
@@ -150,11 +189,10 @@ def maxsim(
             f"vs D.shape[-1]={D.shape[-1]}."
         )
     _validate_devices(Q, D, q_mask, d_mask)
-    _no_grad_guard(Q, D)
     if not normalize:
         _maybe_warn_unnormalized(Q)
     Q, D = unify_dtype(Q, D)
-    scores = dense_maxsim(Q, D, q_mask, d_mask, normalize=normalize)
+    scores = _score(Q, D, q_mask, d_mask, normalize=normalize)
     if q_was_2d and d_was_2d:
         return scores.reshape(())
     if q_was_2d:

@@ -18,6 +18,7 @@ bucket, so corrupt indices cannot fault.
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -237,16 +238,10 @@ def maxsim_residual_varlen(
             Qp = _prep_q(Q)
             if _use_decode_route(Nq, Lq):
                 cu_host = cu.cpu()  # the route's one device->host sync: chunk token bounds
-                j0 = 0
                 buf = None
-                while j0 < Nd:
-                    t0 = int(cu_host[j0])
-                    # largest doc range from j0 whose tokens fit the decode budget (at least one doc)
-                    j1 = int(torch.searchsorted(cu_host, t0 + _DECODE_TOKENS, right=True)) - 1
-                    j1 = min(max(j1, j0 + 1), Nd)
-                    buf = _decoded_chunk_scores(Qp, docs, cu, j0, j1, t0, int(cu_host[j1]), normalize,
-                                                out[:, j0:j1], buf)
-                    j0 = j1
+                for j0, j1 in _token_chunks(cu_host, 0, Nd):
+                    buf = _decoded_chunk_scores(Qp, docs, cu, j0, j1, int(cu_host[j0]), int(cu_host[j1]),
+                                                normalize, out[:, j0:j1], buf)
             else:
                 _plaid_launch(Qp, docs, normalize, out)
     return out.squeeze(0) if q_squeeze else out
@@ -261,7 +256,24 @@ _DECODE_ROUTE_MIN_QTOK = 2048
 _DECODE_TOKENS = 1 << 20  # tokens decoded per chunk (256 MB of bf16 rows at d = 128)
 
 
+def _token_chunks(cu_host: torch.Tensor, j0: int, j1: int):
+    """Split docs [j0, j1) into consecutive ranges of at most _DECODE_TOKENS
+    tokens each (a longer single doc forms its own range)."""
+    while j0 < j1:
+        t0 = int(cu_host[j0])
+        e = int(torch.searchsorted(cu_host, t0 + _DECODE_TOKENS, right=True)) - 1
+        e = min(max(e, j0 + 1), j1)
+        yield j0, e
+        j0 = e
+
+
 def _use_decode_route(Nq: int, Lq: int) -> bool:
+    """``LIK_PLAID_ROUTE=fused|decode`` forces a route; otherwise by query-token count."""
+    forced = os.environ.get("LIK_PLAID_ROUTE", "auto")
+    if forced == "fused":
+        return False
+    if forced == "decode":
+        return True
     return Nq * Lq >= _DECODE_ROUTE_MIN_QTOK
 
 
@@ -381,13 +393,15 @@ def retrieve_residual_varlen(
             codes = codes_flat.contiguous().to(torch.int32)
             docs = _plaid_docs(codes, res, cent, bw, nbits, d, cu=cu, n=Nd, max_len=0)
             Qp = _prep_q(Q)
-            bounds = cu[list(range(0, Nd, cs)) + [Nd]].tolist()
+            cu_host = cu.cpu()  # the route's one device->host sync: decode chunk bounds
             buf = None
             scores = torch.empty(Nq, cs, device=Q.device, dtype=torch.float32)
-            for c, start in enumerate(range(0, Nd, cs)):
+            for start in range(0, Nd, cs):
                 end = min(start + cs, Nd)
                 s = scores[:, : end - start]
-                buf = _decoded_chunk_scores(Qp, docs, cu, start, end, bounds[c], bounds[c + 1], normalize, s, buf)
+                for j0, j1 in _token_chunks(cu_host, start, end):
+                    buf = _decoded_chunk_scores(Qp, docs, cu, j0, j1, int(cu_host[j0]), int(cu_host[j1]), normalize,
+                                                s[:, j0 - start : j1 - start], buf)
                 run_s, run_i = topk_update(s, start, run_s, run_i, k, largest)
         else:
             for start in range(0, Nd, cs):

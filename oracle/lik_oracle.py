@@ -31,6 +31,10 @@ Pinning (how each function is checked, see tests/test_oracle.py):
   plaid_approx_score
       - brute force loop, empty docs -> 0, padding invariance
         (tests/test_reference_cpu.py:25-47).
+  maxsim_argmax / maxsim_grads
+      - argmax against a pure-Python scan (first index of the max, -1 for an
+        all-masked doc); gradients against central finite differences of
+        maxsim() (away from ties) with and without normalise, masks, KD.
 """
 
 from __future__ import annotations
@@ -104,6 +108,68 @@ def maxsim(Q, D, q_mask=None, d_mask=None, *, normalize=False, dtype=np.float64,
     if d2:
         return out[:, 0]
     return out
+
+
+def maxsim_argmax(Q, D, d_mask=None, *, normalize=False, kd=False):
+    """Winner doc-token index per (query i, doc j, query token s) -> int [Nq * docs, Lq]
+    (reference forward.py:160-182 with save_argmax): the lowest index among the
+    maximal scores over valid doc tokens, -1 when doc j has no valid token.
+    Cross product: docs = Nd; KD (kd=True, D [Nq*K, Ld, d]): query i scores docs
+    [i*K, (i+1)*K). float64 scores."""
+    Q = np.asarray(Q, dtype=np.float64)
+    D = np.asarray(D, dtype=np.float64)
+    if normalize:
+        Q, D = _normalize(Q), _normalize(D)
+    Nq, Lq, _ = Q.shape
+    Nd, Ld, _ = D.shape
+    docs = Nd // Nq if kd else Nd
+    dm = np.ones((Nd, Ld), bool) if d_mask is None else np.broadcast_to(np.asarray(d_mask, bool), (Nd, Ld))
+    out = np.full((Nq * docs, Lq), -1, dtype=np.int64)
+    for i in range(Nq):
+        for jl in range(docs):
+            j = i * docs + jl if kd else jl
+            if not dm[j].any():
+                continue
+            S = Q[i] @ D[j].T  # [Lq, Ld]
+            S = np.where(dm[j][None, :], S, NEG_INF)
+            out[i * docs + jl] = S.argmax(axis=1)  # numpy argmax: first (lowest) index of the max
+    return out
+
+
+def maxsim_grads(G, Q, D, argmax, q_mask=None, *, normalize=False, kd=False):
+    """Gradients of L = sum_ij G[i,j] * score[i,j] w.r.t. Q and D given the winners
+    (reference backward/unified.py:27-88 plus the normalise Jacobian of
+    autograd.py:211-225, with F.normalize's eps 1e-12):
+      dL/dQh[i,s] = qm[i,s] sum_j G[i,j] Dh[j, a(i,j,s)]
+      dL/dDh[j,t] = sum_{i,s: a(i,j,s)=t} qm[i,s] G[i,j] Qh[i,s]
+      dL/dX = (dL/dXh - <dL/dXh, Xh> Xh) / max(||X||, 1e-12).  float64."""
+    G = np.asarray(G, dtype=np.float64)
+    Q = np.asarray(Q, dtype=np.float64)
+    D = np.asarray(D, dtype=np.float64)
+    Nq, Lq, d = Q.shape
+    Nd, Ld, _ = D.shape
+    docs = Nd // Nq if kd else Nd
+    am = np.asarray(argmax).reshape(Nq, docs, Lq)
+    qm = np.ones((Nq, Lq), bool) if q_mask is None else np.broadcast_to(np.asarray(q_mask, bool), (Nq, Lq))
+    qn = np.maximum(np.sqrt((Q * Q).sum(-1, keepdims=True)), 1e-12)
+    dn = np.maximum(np.sqrt((D * D).sum(-1, keepdims=True)), 1e-12)
+    Qh, Dh = (Q / qn, D / dn) if normalize else (Q, D)
+    gQh = np.zeros_like(Q)
+    gDh = np.zeros_like(D)
+    for i in range(Nq):
+        for jl in range(docs):
+            j = i * docs + jl if kd else jl
+            for s in range(Lq):
+                t = am[i, jl, s]
+                if t < 0 or not qm[i, s]:
+                    continue
+                gQh[i, s] += G[i, jl] * Dh[j, t]
+                gDh[j, t] += G[i, jl] * Qh[i, s]
+    if not normalize:
+        return gQh, gDh
+    gQ = (gQh - (gQh * Qh).sum(-1, keepdims=True) * Qh) / qn
+    gD = (gDh - (gDh * Dh).sum(-1, keepdims=True) * Dh) / dn
+    return gQ, gD
 
 
 def maxsim_kd(Q, D, q_mask=None, d_mask=None, *, normalize=False, dtype=np.float64):

@@ -106,15 +106,17 @@ def test_decode_route_matches_fused_bitwise(monkeypatch, budget):
     assert rel_err(routed.cpu().numpy(), ref) < 1e-2
 
 
-def test_retrieve_decode_route(monkeypatch):
+@pytest.mark.parametrize("budget,chunk", [(1 << 20, 256), (300, 256), (700, None)])
+def test_retrieve_decode_route(monkeypatch, budget, chunk):
     from late_interaction_kernels import plaid
 
-    _case("retrieve decode route")
+    _case(f"retrieve decode route budget={budget} chunk={chunk}")
     cent, bw, codes, res, cu = _varlen_index(900, 60, 2, 21)
     Q = torch.randn(70, 32, 128).to(torch.bfloat16).cuda()  # 2240 query tokens: decode route
     args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), 2)
     assert plaid._use_decode_route(70, 32)
-    s, i = plaid.retrieve_residual_varlen(Q, *args, 50, chunk=256)
+    monkeypatch.setattr(plaid, "_DECODE_TOKENS", budget)
+    s, i = plaid.retrieve_residual_varlen(Q, *args, 50, chunk=chunk)
     monkeypatch.setattr(plaid, "_DECODE_ROUTE_MIN_QTOK", 1 << 30)
     full = plaid.maxsim_residual_varlen(Q, *args)  # fused route
     ws, wi = O.topk_stable(full.cpu().numpy(), 50)

@@ -245,3 +245,83 @@ def test_oracle_plaid_approx():
     # padding beyond the length does not matter
     codes2 = codes.copy(); codes2[1, 3:] = 0
     np.testing.assert_allclose(O.plaid_approx_score(qcs, codes2, lens)[1], got[1])
+
+
+# --------------------------------------------------------------------------- #
+# gradients (training backward)                                               #
+# --------------------------------------------------------------------------- #
+
+
+def _brute_argmax(Q, D, dm):
+    Nq, Lq, _ = Q.shape
+    Nd, Ld, _ = D.shape
+    out = []
+    for i in range(Nq):
+        for j in range(Nd):
+            row = []
+            for s in range(Lq):
+                best, bi = None, -1
+                for t in range(Ld):
+                    if not dm[j, t]:
+                        continue
+                    v = float(np.dot(Q[i, s], D[j, t]))
+                    if best is None or v > best:
+                        best, bi = v, t
+                row.append(bi)
+            out.append(row)
+    return np.array(out)
+
+
+def test_oracle_argmax_matches_scan_and_ties():
+    rng = np.random.default_rng(4)
+    Q = rng.standard_normal((2, 3, 5))
+    D = rng.standard_normal((3, 6, 5))
+    D[1, 4] = D[1, 2]  # exact tie: the lower index wins
+    dm = np.ones((3, 6), bool)
+    dm[2] = False  # all-masked doc -> -1
+    dm[0, 1] = False
+    got = O.maxsim_argmax(Q, D, dm)
+    assert np.array_equal(got, _brute_argmax(Q, D, dm))
+    assert (got.reshape(2, 3, 3)[:, 2] == -1).all()
+    assert not (got.reshape(2, 3, 3)[:, 1] == 4).any()
+
+
+@pytest.mark.parametrize("normalize", [False, True])
+@pytest.mark.parametrize("kd", [False, True])
+def test_oracle_grads_match_finite_differences(normalize, kd):
+    rng = np.random.default_rng(11 + normalize + 2 * kd)
+    Nq, Lq, d, Ld = 2, 3, 4, 5
+    Nd = Nq * 2 if kd else 3
+    Q = rng.standard_normal((Nq, Lq, d))
+    D = rng.standard_normal((Nd, Ld, d))
+    qm = np.ones((Nq, Lq), bool)
+    qm[1, 2] = False
+    dm = np.ones((Nd, Ld), bool)
+    dm[0, 3] = False
+    docs = Nd // Nq if kd else Nd
+    G = rng.standard_normal((Nq, docs))
+
+    def loss(Qx, Dx):
+        if kd:
+            sc = O.maxsim_kd(Qx, Dx.reshape(Nq, docs, Ld, d), qm, dm.reshape(Nq, docs, Ld), normalize=normalize)
+        else:
+            sc = O.maxsim(Qx, Dx, qm, dm, normalize=normalize)
+        return float((G * sc).sum())
+
+    am = O.maxsim_argmax(Q, D, dm, normalize=normalize, kd=kd)
+    gQ, gD = O.maxsim_grads(G, Q, D, am, qm, normalize=normalize, kd=kd)
+    eps = 1e-6
+    for X, gX, which in ((Q, gQ, 0), (D, gD, 1)):
+        num = np.zeros_like(X)
+        it = np.nditer(X, flags=["multi_index"])
+        for _ in it:
+            idx = it.multi_index
+            Xp, Xm = X.copy(), X.copy()
+            Xp[idx] += eps
+            Xm[idx] -= eps
+            fp = loss(Xp, D) if which == 0 else loss(Q, Xp)
+            fm = loss(Xm, D) if which == 0 else loss(Q, Xm)
+            num[idx] = (fp - fm) / (2 * eps)
+        np.testing.assert_allclose(gX, num, rtol=1e-5, atol=1e-6)
+    assert np.all(gQ[1, 2] == 0)  # masked query token
+    assert np.all(gD[0, 3] == 0)  # masked doc token

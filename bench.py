@@ -462,6 +462,60 @@ def wl_ref_shapes(args):
             "roofline": None}
 
 
+# The reference's published training step times (forward + backward, bf16,
+# H100, best of its two backward paths; docs/benchmarks.md:329-335).
+REF_TRAIN = [
+    ("pylate-text B256 Lq32 Ld300", 256, 256, 32, 300, None, 2.10),
+    ("colpali B128 Lq32 Ld1030", 128, 128, 32, 1030, None, 1.38),
+    ("colpali-neg B128xn8", 128, None, 32, 1030, 8, 0.71),
+    ("colpali-neg B256xn16", 256, None, 32, 1030, 16, 1.37),
+    ("longq B64 Lq1030 Ld1030", 64, 64, 1030, 1030, None, 5.6),
+]
+
+
+def wl_train_shapes(args):
+    """Forward + backward (maxsim(...).sum().backward(), normalize=True, bf16)
+    per training shape of the reference, next to its published time.
+    ``value`` = geometric mean speedup."""
+    import torch
+
+    from late_interaction_kernels import maxsim
+
+    g = torch.Generator(device="cuda").manual_seed(6)
+    rows = []
+    for name, B, Nd, Lq, Ld, K, ref_ms in REF_TRAIN:
+        Q = _normed((B, Lq, 128), g, torch.bfloat16).requires_grad_()
+        D = (_normed((B, K, Ld, 128), g, torch.bfloat16) if K else _normed((Nd, Ld, 128), g, torch.bfloat16))
+        D.requires_grad_()
+
+        def step():
+            Q.grad = None
+            D.grad = None
+            maxsim(Q, D, normalize=True).sum().backward()
+
+        for _ in range(3):
+            step()
+        _sync()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        n = 10
+        a.record()
+        for _ in range(n):
+            step()
+        b.record()
+        _sync()
+        ms = a.elapsed_time(b) / n
+        rows.append({"shape": name, "ms": round(ms, 4), "ref_h100_ms": ref_ms, "speedup": round(ref_ms / ms, 2)})
+        del Q, D
+    gm = math.exp(sum(math.log(r["speedup"]) for r in rows) / len(rows))
+    return {"metric": "training fwd+bwd speedup over the reference's published H100 step times (geomean)",
+            "value": round(gm, 2), "unit": "x", "ms_per_step": round(sum(r["ms"] for r in rows), 4),
+            "dtype": "bf16",
+            "config": {"workload": "reference training shapes (docs/benchmarks.md:329-335), normalize=True",
+                       "shapes": rows},
+            "roofline": None}
+
+
 def wl_hbm_copy(args):
     """Calibration: a plain 2 GiB device copy (torch's copy kernel). Its GB/s is the
     achievable HBM rate on this box, and its rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -496,6 +550,7 @@ WORKLOADS = {
     "hbm_copy": wl_hbm_copy,
     "plaid_q1": wl_plaid_q1,
     "ref_shapes": wl_ref_shapes,
+    "train_shapes": wl_train_shapes,
     "plaid_decode": wl_plaid_decode,
     "inbatch": wl_inbatch,
     "inbatch_norm": lambda a: wl_inbatch(a, normalize=True),

@@ -107,9 +107,10 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
                       size_t workspace_bytes, lik_stream_t stream);
 
 /*
- * Backward: given grad[i * grad_ld + j] = dL/dscore[i, j] and the argmax of
- * lik_maxsim_argmax, writes fp32 grad_q [Q->n, Q->len, dim] and grad_d
- * [D->n, D->len, dim] (every element written; rows that win nothing get 0).
+ * Backward: given grad[i * grad_ld + j] = dL/dscore[i, j] (fp32) and the
+ * argmax of lik_maxsim_argmax, writes grad_q [Q->n, Q->len, dim] and grad_d
+ * [D->n, D->len, dim], contiguous, in the dtype of Q and D (accumulated in
+ * fp32; every element written, rows that win nothing get 0).
  * Q and D padded (no cu_seqlens / lengths); Q->mask (keep flags) zeroes the
  * masked query tokens' terms; a doc mask acts only through the argmax.
  * With LIK_NORMALIZE the gradients are taken through x / max(||x||, 1e-12)
@@ -120,7 +121,7 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
  * autograd.py:211-225).
  */
 int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q, const lik_seqs_t* D,
-                        const int32_t* argmax, uint32_t flags, float* grad_q, float* grad_d, void* workspace,
+                        const int32_t* argmax, uint32_t flags, void* grad_q, void* grad_d, void* workspace,
                         size_t workspace_bytes, lik_stream_t stream);
 size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags);
 

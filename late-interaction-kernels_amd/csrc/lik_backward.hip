@@ -37,6 +37,9 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+template <int EK>
+constexpr int sizeof_ek() { return EK == EK_F32 ? 4 : 2; }
+
 struct BwdParams {
   const float* grad;  // [Nq, ld_g]
   int64_t ld_g;
@@ -49,27 +52,43 @@ struct BwdParams {
   int64_t qm_sn, qm_sl;
   const float* qinv;  // [Nq * Lq] inverse norms (normalise), else null
   const float* dinv;  // [Nd * Ld]
-  float* gq;          // [Nq, Lq, dim] fp32
-  float* gd;          // [Nd, Ld, dim] fp32
+  char* gq;           // [Nq, Lq, dim] in the input dtype
+  char* gd;           // [Nd, Ld, dim] in the input dtype
   int64_t nq, lq, nd, ld;
   int64_t ndoc_pg;    // docs per query: Nd (cross product) or K (KD layout)
   int kd;
   int dim;
 };
 
-// inv[r] = 1 / max(||row r||, 1e-12) for rows r = i*L + t of a [n, L, dim] tensor.
-template <int EK>
+// inv[r] = 1 / max(||row r||, 1e-12) for rows r = i*L + t of a [n, L, dim]
+// tensor: LPR lanes per row, each summing 16-byte chunks, then an xor-shuffle
+// reduction over the row's lanes (coalesced: a row is read as contiguous chunks).
+template <int EK, int LPR>
 __global__ void __launch_bounds__(256) row_invnorm_kernel(const char* x, int64_t sn, int64_t sl, int64_t n,
                                                           int64_t L, int dim, float* inv) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= n * L) return;
-  const char* row = x + (r / L) * sn + (r % L) * sl;
+  constexpr int EPC = EK == EK_F32 ? 4 : 8;  // elements per 16-byte chunk
+  const int64_t r = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
+  const int c0 = threadIdx.x % LPR;
+  const bool ok = r < n * L;
   float ss = 0.f;
-  for (int e = 0; e < dim; ++e) {
-    const float v = load_elem<EK>(row, e);
-    ss = fmaf(v, v, ss);
+  if (ok) {
+    const char* row = x + (r / L) * sn + (r % L) * sl;
+    for (int c = c0; c * EPC < dim; c += LPR) {
+      const u32x4 v = *(const u32x4*)(row + (int64_t)c * 16);
+      ss += chunk_sumsq<EK>(v);
+    }
   }
-  inv[r] = inv_norm(ss);
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
+  if (ok && c0 == 0) inv[r] = inv_norm(ss);
+}
+
+// Store a gradient value in the input dtype.
+template <int EK>
+__device__ __forceinline__ void store_elem(char* row, int e, float v) {
+  if constexpr (EK == EK_BF16) *(uint16_t*)(row + 2 * e) = (uint16_t)f32_to_bf16_bits(v);
+  else if constexpr (EK == EK_F16) *(uint16_t*)(row + 2 * e) = (uint16_t)f32_to_f16_bits(v);
+  else *(float*)(row + 4 * e) = v;
 }
 
 template <int EK, int DPL>
@@ -119,11 +138,11 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
 #pragma unroll
     for (int k = 0; k < DPL; ++k) acc[k] = (acc[k] - dot * xh[k]) * qi;
   }
-  float* out = bp.gq + w * bp.dim;
+  char* out = bp.gq + w * bp.dim * (int64_t)sizeof_ek<EK>();
 #pragma unroll
   for (int k = 0; k < DPL; ++k) {
     const int e = lane * DPL + k;
-    if (e < bp.dim) out[e] = keep ? acc[k] : 0.f;
+    if (e < bp.dim) store_elem<EK>(out, e, keep ? acc[k] : 0.f);
   }
 }
 
@@ -143,6 +162,7 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
   const int64_t jl = bp.kd ? j % bp.ndoc_pg : j;
   const int64_t i_begin = bp.kd ? j / bp.ndoc_pg : 0;
   const int64_t i_end = bp.kd ? i_begin + 1 : bp.nq;
+  uint32_t touched = 0;  // rows of the block that received a contribution (wave-uniform)
   for (int64_t i = i_begin; i < i_end; ++i) {
     const float gij = bp.grad[i * bp.ld_g + jl];
     if (gij == 0.f) continue;
@@ -158,6 +178,7 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
         const int l = __builtin_ctzll(bal);
         bal &= bal - 1;
         const int r = __builtin_amdgcn_readlane(a, l) - (int)t0;
+        touched |= 1u << r;
         const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
         const char* qrow = bp.q + i * bp.q_sn + (s0 + l) * bp.q_sl;
 #pragma unroll
@@ -172,6 +193,15 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
   for (int r = 0; r < RB; ++r) {
     const int64_t t = t0 + r;
     if (t >= bp.ld) break;
+    char* out = bp.gd + (j * bp.ld + t) * bp.dim * (int64_t)sizeof_ek<EK>();
+    if (!((touched >> r) & 1u)) {  // no winner in this row: zero gradient, no D read
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        const int e = lane * DPL + k;
+        if (e < bp.dim) store_elem<EK>(out, e, 0.f);
+      }
+      continue;
+    }
     float gh[DPL];
 #pragma unroll
     for (int k = 0; k < DPL; ++k) gh[k] = s_acc[r][lane * DPL + k];
@@ -189,11 +219,10 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
 #pragma unroll
       for (int k = 0; k < DPL; ++k) gh[k] = (gh[k] - dot * xh[k]) * di;
     }
-    float* out = bp.gd + (j * bp.ld + t) * bp.dim;
 #pragma unroll
     for (int k = 0; k < DPL; ++k) {
       const int e = lane * DPL + k;
-      if (e < bp.dim) out[e] = gh[k];
+      if (e < bp.dim) store_elem<EK>(out, e, gh[k]);
     }
   }
 }
@@ -225,10 +254,11 @@ int launch_bwd_dpl(const BwdParams& bp, hipStream_t s) {
 
 template <int EK>
 int launch_invnorm(const char* x, int64_t sn, int64_t sl, int64_t n, int64_t L, int dim, float* inv, hipStream_t s) {
+  constexpr int LPR = 16;  // lanes per row
   const int64_t rows = n * L;
   if (rows == 0) return LIK_OK;
-  hipLaunchKernelGGL((row_invnorm_kernel<EK>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, x, sn, sl, n, L,
-                     dim, inv);
+  hipLaunchKernelGGL((row_invnorm_kernel<EK, LPR>), dim3((unsigned)((rows * LPR + 255) / 256)), dim3(256), 0, s, x,
+                     sn, sl, n, L, dim, inv);
   return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
 }
 
@@ -246,7 +276,7 @@ size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t*
 }
 
 int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q, const lik_seqs_t* D,
-                        const int32_t* argmax, uint32_t flags, float* grad_q, float* grad_d, void* workspace,
+                        const int32_t* argmax, uint32_t flags, void* grad_q, void* grad_d, void* workspace,
                         size_t workspace_bytes, lik_stream_t stream) {
   if (!Q || !D) return LIK_ERR_INVALID;
   if (Q->dtype != D->dtype || Q->dim != D->dim || Q->dim <= 0) return LIK_ERR_INVALID;
@@ -274,8 +304,12 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   bp.qmask = Q->mask;
   bp.qm_sn = Q->mask_stride_n;
   bp.qm_sl = Q->mask_stride_l;
-  bp.gq = grad_q;
-  bp.gd = grad_d;
+  bp.gq = (char*)grad_q;
+  bp.gd = (char*)grad_d;
+  // 16-byte row chunks for the norm kernel
+  if (((uintptr_t)Q->data) % 16 || ((uintptr_t)D->data) % 16 || (Q->dim * eb) % 16 || bp.q_sl % 16 || bp.d_sl % 16 ||
+      bp.q_sn % 16 || bp.d_sn % 16)
+    return LIK_ERR_UNSUPPORTED;
   bp.nq = Q->n;
   bp.lq = Q->len;
   bp.nd = D->n;

@@ -361,10 +361,16 @@ int lik_timing_end(double* total_ms, int64_t* launches) {
 
 size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
   if (check_seqs(Q) != LIK_OK || check_seqs(D) != LIK_OK) return 0;
-  Plan pl;
+  // the plan may use min_w 1 or 4 (normalise / training forward): cover both
   const bool kd = (flags & LIK_KD_LAYOUT) != 0;
-  if (make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl) != LIK_OK) return 0;
-  return ws_layout(Q, D, flags, pl).total;
+  size_t total = 0;
+  for (int min_w : {1, 4}) {
+    Plan pl;
+    if (make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w) != LIK_OK) return 0;
+    const size_t t = ws_layout(Q, D, flags, pl).total;
+    total = t > total ? t : total;
+  }
+  return total;
 }
 
 static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
@@ -400,7 +406,10 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
   hipStream_t s = (hipStream_t)stream;
 
   Plan pl;
-  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl)) != LIK_OK) return rc;
+  // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: spread
+  // it over at least 4 waves even when the query block fits one wave's columns
+  const int min_w = ((flags & LIK_NORMALIZE) || argmax) ? 4 : 1;
+  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w)) != LIK_OK) return rc;
   const WsLayout wl = ws_layout(Q, D, flags, pl);
   if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return LIK_ERR_WORKSPACE;
 

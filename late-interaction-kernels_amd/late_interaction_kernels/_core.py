@@ -154,13 +154,13 @@ def maxsim_backward(
     normalize: bool,
     kd: bool,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """fp32 ``(grad_Q [Nq, Lq, dp], grad_D [Nd, Ld, dp])`` for upstream ``grad`` [Nq, docs]."""
+    """``(grad_Q [Nq, Lq, dp], grad_D [Nd, Ld, dp])`` in the input dtype for upstream ``grad`` [Nq, docs]."""
     Nq, Lq, dp = Qp.shape
     Nd, Ld, _ = Dp.shape
-    gq = torch.zeros(Nq, Lq, dp, device=Qp.device, dtype=torch.float32)
-    gd = torch.zeros(Nd, Ld, dp, device=Dp.device, dtype=torch.float32)
     if Nq == 0 or Nd == 0 or Lq == 0 or Ld == 0:
-        return gq, gd
+        return torch.zeros_like(Qp), torch.zeros_like(Dp)
+    gq = torch.empty(Nq, Lq, dp, device=Qp.device, dtype=Qp.dtype)  # every element is written
+    gd = torch.empty(Nd, Ld, dp, device=Dp.device, dtype=Dp.dtype)
     g = grad.to(torch.float32).contiguous()
     qs = _lib.seqs(Qp, n=Nq, length=Lq, stride_n=Qp.stride(0), stride_l=Qp.stride(1), mask=qm,
                    mask_strides=(qm.stride(0), qm.stride(1)) if qm is not None else (0, 0))

@@ -186,6 +186,17 @@ int lik_plaid_decode(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t to
                      int32_t out_dtype, void* out, int64_t out_stride, lik_stream_t stream);
 
 /*
+ * Reverse the bit order inside each of nbytes bytes (in may equal out; both
+ * 4-byte aligned). Converts ColBERTv2 / fast-plaid residual bytes (each code's
+ * bits least-significant first, packed most-significant-bit first by
+ * numpy.packbits) to the little-endian field layout the PLAID kernels read.
+ * Replaces the byte_reversed_bits_map lookup of fast-plaid's decompressor
+ * (noted at benchmarks/plaid/bench_decompress_maxsim.py:144-149), applied
+ * once at index load instead of per decode.
+ */
+int lik_residual_reverse_bits(const uint8_t* in, uint8_t* out, int64_t nbytes, lik_stream_t stream);
+
+/*
  * PLAID approximate (centroid-only) score: out[b] = sum_{s<Lq} max_{t<len_b} qcs[codes[b,t], s],
  * with out-of-range codes clamped to centroid 0 and an empty doc scoring 0.
  * Replaces plaid.py:plaid_approx_score (plaid.py:82-136, kernel plaid.py:28-79).

@@ -113,9 +113,33 @@ int launch_decode(int outk, const lik_plaid_docs_t* d, const int32_t* codes, con
   }
 }
 
+// out[i] = in[i] with its 8 bits reversed, 4 bytes per thread: reversing a
+// 32-bit word and swapping its bytes back reverses the bits inside each byte.
+__global__ void __launch_bounds__(256) reverse_bits_kernel(const uint8_t* in, uint8_t* out, int64_t n) {
+  const int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t b = w * 4;
+  if (b + 4 <= n) {
+    const uint32_t v = *(const uint32_t*)(in + b);
+    *(uint32_t*)(out + b) = __builtin_bswap32(__builtin_bitreverse32(v));
+  } else {
+    for (int64_t i = b; i < n; ++i) out[i] = __builtin_bitreverse8(in[i]);
+  }
+}
+
 }  // namespace lik
 
 using namespace lik;
+
+extern "C" int lik_residual_reverse_bits(const uint8_t* in, uint8_t* out, int64_t nbytes, lik_stream_t stream) {
+  if (nbytes < 0 || (nbytes > 0 && (!in || !out))) return LIK_ERR_INVALID;
+  if (((uintptr_t)in) % 4 || ((uintptr_t)out) % 4) return LIK_ERR_UNSUPPORTED;
+  if (nbytes == 0) return LIK_OK;
+  const int64_t words = (nbytes + 3) / 4;
+  if ((words + 255) / 256 > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(reverse_bits_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, (hipStream_t)stream, in,
+                     out, nbytes);
+  return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+}
 
 extern "C" int lik_plaid_decode(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end, uint32_t flags,
                                 int32_t out_dtype, void* out, int64_t out_stride, lik_stream_t stream) {

@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "lik_plaid_maxsim",
     "lik_plaid_decode",
     "lik_plaid_approx_score",
+    "lik_residual_reverse_bits",
     "lik_topk_merge",
     "lik_version",
     "lik_timing_begin",
@@ -140,6 +141,8 @@ def load() -> ctypes.CDLL:
     lib.lik_plaid_maxsim.restype = ctypes.c_int
     lib.lik_plaid_decode.argtypes = [P(LikPlaidDocs), _i64, _i64, ctypes.c_uint32, _i32, _p, _i64, _p]
     lib.lik_plaid_decode.restype = ctypes.c_int
+    lib.lik_residual_reverse_bits.argtypes = [_p, _p, _i64, _p]
+    lib.lik_residual_reverse_bits.restype = ctypes.c_int
     lib.lik_plaid_approx_score.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _p]
     lib.lik_plaid_approx_score.restype = ctypes.c_int
     lib.lik_topk_merge.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_int, _p, _p,

@@ -31,6 +31,9 @@ Pinning (how each function is checked, see tests/test_oracle.py):
   plaid_approx_score
       - brute force loop, empty docs -> 0, padding invariance
         (tests/test_reference_cpu.py:25-47).
+  pack_residuals_colbert / reverse_bits_bytes
+      - reversing the bits of every byte of the ColBERT / fast-plaid encoding
+        gives exactly pack_residuals (our little-endian layout); hand bytes.
   maxsim_argmax / maxsim_grads
       - argmax against a pure-Python scan (first index of the max, -1 for an
         all-masked doc); gradients against central finite differences of
@@ -268,6 +271,26 @@ def pack_residuals(bucket_codes, nbits: int) -> np.ndarray:
     for f in range(d):
         out[..., f // cpb] |= bc[..., f] << ((f % cpb) * nbits)
     return out.astype(np.uint8)
+
+
+def pack_residuals_colbert(bucket_codes, nbits: int) -> np.ndarray:
+    """The on-disk residual encoding of ColBERTv2 / fast-plaid (third-party; not in
+    the reference tree, whose loader reads these files at
+    benchmarks/plaid/bench_fastplaid_e2e.py:75-140 and whose decoder notes the
+    byte-reversed bit map at benchmarks/plaid/bench_decompress_maxsim.py:144-149):
+    each code contributes its nbits bits least-significant first, and the bit
+    stream is packed with numpy.packbits (first bit -> most significant bit)."""
+    bc = np.asarray(bucket_codes, dtype=np.int64)
+    bits = (bc[..., None] >> np.arange(nbits)) & 1  # [..., d, nbits], LSB first
+    flat = bits.reshape(bc.shape[:-1] + (-1,)).astype(np.uint8)
+    return np.packbits(flat, axis=-1)
+
+
+def reverse_bits_bytes(b) -> np.ndarray:
+    """Reverse the bit order of every byte (b7..b0 -> b0..b7)."""
+    b = np.asarray(b, dtype=np.uint8)
+    return np.unpackbits(b[..., None], axis=-1)[..., ::-1].reshape(b.shape + (8,)).dot(
+        1 << np.arange(7, -1, -1)).astype(np.uint8)
 
 
 def decode_residual_tokens(codes, residuals, centroids, bucket_weights, nbits: int, dtype=np.float64):

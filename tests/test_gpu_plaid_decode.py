@@ -122,3 +122,57 @@ def test_retrieve_decode_route(monkeypatch, budget, chunk):
     ws, wi = O.topk_stable(full.cpu().numpy(), 50)
     np.testing.assert_array_equal(i.cpu().numpy(), wi)
     np.testing.assert_array_equal(s.cpu().numpy(), ws)
+
+
+def _write_fastplaid_index(path, nbits, merged, seed=3):
+    """A small index directory in fast-plaid's on-disk format (ColBERTv2 bit packing)."""
+    import json
+    import os
+
+    rng = np.random.default_rng(seed)
+    d, n_cent = 128, 40
+    doclens = [rng.integers(1, 30, 25).tolist(), rng.integers(1, 30, 17).tolist()]
+    cent = rng.standard_normal((n_cent, d)).astype(np.float32)
+    bw = np.linspace(-0.2, 0.2, 2**nbits).astype(np.float32)
+    codes = [rng.integers(0, n_cent, sum(dl)).astype(np.int64) for dl in doclens]
+    bcodes = [rng.integers(0, 2**nbits, (sum(dl), d)) for dl in doclens]
+    os.makedirs(path, exist_ok=True)
+    with open(os.path.join(path, "metadata.json"), "w") as f:
+        json.dump({"nbits": nbits, "num_chunks": 2}, f)
+    np.save(os.path.join(path, "centroids.npy"), cent)
+    np.save(os.path.join(path, "bucket_weights.npy"), bw)
+    for i, dl in enumerate(doclens):
+        with open(os.path.join(path, f"doclens.{i}.json"), "w") as f:
+            json.dump(dl, f)
+    packed = [O.pack_residuals_colbert(b, nbits) for b in bcodes]
+    if merged:
+        np.save(os.path.join(path, "merged_codes.npy"), np.concatenate(codes + [np.zeros(3, np.int64)]))
+        np.save(os.path.join(path, "merged_residuals.npy"), np.concatenate(packed + [np.zeros((3, d * nbits // 8), np.uint8)]))
+    else:
+        for i in range(2):
+            np.save(os.path.join(path, f"codes.{i}.npy"), codes[i])
+            np.save(os.path.join(path, f"residuals.{i}.npy"), packed[i])
+    return sum(doclens, []), cent, bw, np.concatenate(codes), np.concatenate(bcodes)
+
+
+@pytest.mark.parametrize("nbits", [2, 4])
+@pytest.mark.parametrize("merged", [False, True])
+def test_fastplaid_index_loader(tmp_path, nbits, merged):
+    from late_interaction_kernels.plaid import maxsim_residual_varlen
+    from late_interaction_kernels.plaid_index import load_fastplaid_index
+
+    _case(f"fast-plaid loader nbits={nbits} merged={merged}")
+    doclens, cent, bw, codes, bcodes = _write_fastplaid_index(str(tmp_path), nbits, merged)
+    idx = load_fastplaid_index(str(tmp_path), centroid_dtype=torch.float32)
+    T = sum(doclens)
+    assert idx["n_docs"] == len(doclens) and idx["total_tokens"] == T and idx["nbits"] == nbits
+    np.testing.assert_array_equal(idx["codes_flat"].cpu().numpy(), codes)
+    # residuals converted to the kernels' little-endian field layout, bit for bit
+    np.testing.assert_array_equal(idx["residuals_flat"].cpu().numpy(), O.pack_residuals(bcodes, nbits))
+    np.testing.assert_array_equal(idx["cu_seqlens_d"].cpu().numpy(), np.concatenate([[0], np.cumsum(doclens)]))
+    Q = torch.randn(3, 32, 128).to(torch.bfloat16).cuda()
+    got = maxsim_residual_varlen(Q, idx["codes_flat"], idx["residuals_flat"], idx["cu_seqlens_d"], idx["centroids"],
+                                 idx["bucket_weights"], nbits)
+    ref = O.maxsim_residual_varlen(Q.float().cpu().numpy(), codes, O.pack_residuals(bcodes, nbits),
+                                   idx["cu_seqlens_d"].cpu().numpy(), cent, bw, nbits)
+    assert rel_err(got.cpu().numpy(), ref) < 1e-2

@@ -325,3 +325,20 @@ def test_oracle_grads_match_finite_differences(normalize, kd):
         np.testing.assert_allclose(gX, num, rtol=1e-5, atol=1e-6)
     assert np.all(gQ[1, 2] == 0)  # masked query token
     assert np.all(gD[0, 3] == 0)  # masked doc token
+
+
+@pytest.mark.parametrize("nbits", [2, 4, 8])
+def test_oracle_colbert_encoding_is_bit_reversed_little_endian(nbits):
+    rng = np.random.default_rng(nbits)
+    codes = rng.integers(0, 2**nbits, (7, 128))
+    colbert = O.pack_residuals_colbert(codes, nbits)
+    assert colbert.shape == (7, 128 * nbits // 8)
+    np.testing.assert_array_equal(O.reverse_bits_bytes(colbert), O.pack_residuals(codes, nbits))
+    np.testing.assert_array_equal(O.unpack_residuals(O.reverse_bits_bytes(colbert), nbits, 128), codes)
+
+
+def test_oracle_colbert_encoding_hand_bytes():
+    # nbits=2, codes [1, 2, 3, 0]: bits LSB-first 10 01 11 00 -> packbits 0b10011100
+    assert O.pack_residuals_colbert(np.array([[1, 2, 3, 0]]), 2)[0, 0] == 0b10011100
+    assert O.reverse_bits_bytes(np.array([0b10011100]))[0] == 0b00111001
+    assert O.reverse_bits_bytes(np.array([0x01, 0x80, 0xF0]).astype(np.uint8)).tolist() == [0x80, 0x01, 0x0F]

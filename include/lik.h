@@ -73,6 +73,7 @@ typedef struct {
 #define LIK_NORMALIZE 1u /* per-token L2 normalise Q and D (F.normalize, eps 1e-12) */
 #define LIK_KD_LAYOUT 2u /* D holds n = Nq*K docs; query i scores docs [i*K, (i+1)*K) */
 #define LIK_NORMALIZE_Q 4u /* normalise query tokens only (docs already unit rows, e.g. decoded PLAID) */
+#define LIK_NORMALIZE_D 8u /* normalise doc tokens only (queries pre-normalised, e.g. a projection head) */
 
 /*
  * score[i, j] = out_scale * sum_{s valid in Q_i} max_{t valid in D_j} <Q_i[s], D_j[t]>
@@ -111,10 +112,12 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
  * argmax of lik_maxsim_argmax, writes grad_q [Q->n, Q->len, dim] and grad_d
  * [D->n, D->len, dim], contiguous, in the dtype of Q and D (accumulated in
  * fp32; every element written, rows that win nothing get 0).
- * Q and D padded (no cu_seqlens / lengths); Q->mask (keep flags) zeroes the
- * masked query tokens' terms; a doc mask acts only through the argmax.
- * With LIK_NORMALIZE the gradients are taken through x / max(||x||, 1e-12)
- * and the caller passes lik_maxsim_backward_workspace_size() bytes.
+ * Q padded; D padded, or packed (cu_seqlens) when grad_d is null (only
+ * grad_q is computed then); Q->mask (keep flags) zeroes the masked query
+ * tokens' terms; doc masks / lengths act only through the argmax. With
+ * LIK_NORMALIZE (both sides), LIK_NORMALIZE_Q or LIK_NORMALIZE_D the
+ * gradients are taken through x / max(||x||, 1e-12) on those sides and the
+ * caller passes lik_maxsim_backward_workspace_size() bytes.
  * Deterministic: fixed summation order, no atomics.
  * Replaces backward/unified.py:maxsim_backward_unified and
  * backward/lowmem.py:maxsim_backward_lowmem (+ the normalise Jacobian of

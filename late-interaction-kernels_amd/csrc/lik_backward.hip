@@ -45,8 +45,9 @@ struct BwdParams {
   int64_t ld_g;
   const char* q;      // Q rows: q + i*q_sn + s*q_sl (bytes)
   int64_t q_sn, q_sl;
-  const char* d;      // D rows: d + j*d_sn + t*d_sl (bytes)
+  const char* d;      // D rows: d + j*d_sn + t*d_sl, or d + (d_cu[j] + t)*d_sl when packed (bytes)
   int64_t d_sn, d_sl;
+  const int32_t* d_cu;
   const int32_t* amax;  // [Nq * ndoc_pg, Lq]
   const int8_t* qmask;  // [Nq, Lq] keep flags, or null
   int64_t qm_sn, qm_sl;
@@ -108,14 +109,15 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
     const int av = jl < bp.ndoc_pg ? am[jl * bp.lq] : -1;
     const float gv = jl < bp.ndoc_pg ? g[jl] : 0.f;
     float sv = gv;
-    if (bp.dinv && av >= 0) sv *= bp.dinv[(j0 + jl) * bp.ld + av];
+    if (bp.dinv && av >= 0) sv *= bp.dinv[(j0 + jl) * bp.ld + av];  // dinv only for padded docs
     uint64_t bal = __ballot(av >= 0 && gv != 0.f);
     while (bal) {
       const int l = __builtin_ctzll(bal);
       bal &= bal - 1;
       const int a = __builtin_amdgcn_readlane(av, l);
       const float sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), l));
-      const char* row = bp.d + (j0 + c0 + l) * bp.d_sn + (int64_t)a * bp.d_sl;
+      const int64_t jg = j0 + c0 + l;
+      const char* row = bp.d_cu ? bp.d + ((int64_t)bp.d_cu[jg] + a) * bp.d_sl : bp.d + jg * bp.d_sn + (int64_t)a * bp.d_sl;
 #pragma unroll
       for (int k = 0; k < DPL; ++k) {
         const int e = lane * DPL + k;
@@ -235,7 +237,7 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
     hipLaunchKernelGGL((grad_q_kernel<EK, DPL>), dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, s, bp);
     if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
   }
-  const int64_t nb = bp.nd * ((bp.ld + RB - 1) / RB);
+  const int64_t nb = bp.gd ? bp.nd * ((bp.ld + RB - 1) / RB) : 0;
   if (nb > 0) {
     hipLaunchKernelGGL((grad_d_kernel<EK, DPL>), dim3((unsigned)nb), dim3(64), 0, s, bp);
     if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
@@ -270,9 +272,15 @@ using namespace lik;
 
 extern "C" {
 
+static bool bwd_norm_q(uint32_t f) { return (f & (LIK_NORMALIZE | LIK_NORMALIZE_Q)) != 0; }
+static bool bwd_norm_d(uint32_t f) { return (f & (LIK_NORMALIZE | LIK_NORMALIZE_D)) != 0; }
+
 size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
-  if (!Q || !D || !(flags & LIK_NORMALIZE)) return 0;
-  return (size_t)(Q->n * Q->len + D->n * D->len) * sizeof(float) + 256;
+  if (!Q || !D) return 0;
+  size_t n = 0;
+  if (bwd_norm_q(flags)) n += (size_t)(Q->n * Q->len);
+  if (bwd_norm_d(flags)) n += (size_t)(D->n * D->len);
+  return n ? n * sizeof(float) + 256 : 0;
 }
 
 int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q, const lik_seqs_t* D,
@@ -281,14 +289,15 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   if (!Q || !D) return LIK_ERR_INVALID;
   if (Q->dtype != D->dtype || Q->dim != D->dim || Q->dim <= 0) return LIK_ERR_INVALID;
   if (Q->dtype != LIK_BF16 && Q->dtype != LIK_F16 && Q->dtype != LIK_F32) return LIK_ERR_UNSUPPORTED;
-  if (Q->cu_seqlens || D->cu_seqlens || Q->lengths || D->lengths || D->mask || Q->token_scale || D->token_scale)
-    return LIK_ERR_UNSUPPORTED;  // padded layout; doc masks act through the forward's argmax
+  if (Q->cu_seqlens || Q->lengths || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
+  // doc masks / lengths act through the forward's argmax; packed docs only for grad_q
+  if (D->cu_seqlens && (grad_d || bwd_norm_d(flags))) return LIK_ERR_UNSUPPORTED;
   if (Q->n < 0 || D->n < 0 || Q->len < 0 || D->len < 0) return LIK_ERR_INVALID;
   if (Q->dim > 512) return LIK_ERR_UNSUPPORTED;
   const bool kd = (flags & LIK_KD_LAYOUT) != 0;
   if (kd && (Q->n == 0 || D->n % Q->n != 0)) return LIK_ERR_INVALID;
   if (Q->n == 0 || D->n == 0) return LIK_OK;
-  if (!grad || !argmax || !grad_q || !grad_d || !Q->data || !D->data) return LIK_ERR_INVALID;
+  if (!grad || !argmax || !grad_q || !Q->data || !D->data) return LIK_ERR_INVALID;
   hipStream_t s = (hipStream_t)stream;
   const int eb = elem_size(Q->dtype);
   BwdParams bp{};
@@ -300,6 +309,7 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   bp.d = (const char*)D->data;
   bp.d_sn = D->stride_n * eb;
   bp.d_sl = D->stride_l * eb;
+  bp.d_cu = D->cu_seqlens;
   bp.amax = argmax;
   bp.qmask = Q->mask;
   bp.qm_sn = Q->mask_stride_n;
@@ -318,27 +328,24 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   bp.ndoc_pg = kd ? D->n / Q->n : D->n;
   bp.dim = Q->dim;
   int rc;
-  if (flags & LIK_NORMALIZE) {
-    const size_t need = lik_maxsim_backward_workspace_size(Q, D, flags);
-    if (!workspace || workspace_bytes < need) return LIK_ERR_WORKSPACE;
-    float* qinv = (float*)workspace;
-    float* dinv = qinv + Q->n * Q->len;
-    bp.qinv = qinv;
-    bp.dinv = dinv;
+  const size_t need = lik_maxsim_backward_workspace_size(Q, D, flags);
+  if (need && (!workspace || workspace_bytes < need)) return LIK_ERR_WORKSPACE;
+  float* wsf = (float*)workspace;
+  auto invnorm = [&](const char* x, int64_t sn, int64_t sl, int64_t n, int64_t L, float* inv) {
     switch (Q->dtype) {
-      case LIK_BF16:
-        if ((rc = launch_invnorm<EK_BF16>(bp.q, bp.q_sn, bp.q_sl, Q->n, Q->len, Q->dim, qinv, s)) != LIK_OK) return rc;
-        rc = launch_invnorm<EK_BF16>(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, D->dim, dinv, s);
-        break;
-      case LIK_F16:
-        if ((rc = launch_invnorm<EK_F16>(bp.q, bp.q_sn, bp.q_sl, Q->n, Q->len, Q->dim, qinv, s)) != LIK_OK) return rc;
-        rc = launch_invnorm<EK_F16>(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, D->dim, dinv, s);
-        break;
-      default:
-        if ((rc = launch_invnorm<EK_F32>(bp.q, bp.q_sn, bp.q_sl, Q->n, Q->len, Q->dim, qinv, s)) != LIK_OK) return rc;
-        rc = launch_invnorm<EK_F32>(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, D->dim, dinv, s);
+      case LIK_BF16: return launch_invnorm<EK_BF16>(x, sn, sl, n, L, Q->dim, inv, s);
+      case LIK_F16: return launch_invnorm<EK_F16>(x, sn, sl, n, L, Q->dim, inv, s);
+      default: return launch_invnorm<EK_F32>(x, sn, sl, n, L, Q->dim, inv, s);
     }
-    if (rc != LIK_OK) return rc;
+  };
+  if (bwd_norm_q(flags)) {
+    bp.qinv = wsf;
+    wsf += Q->n * Q->len;
+    if ((rc = invnorm(bp.q, bp.q_sn, bp.q_sl, Q->n, Q->len, wsf - Q->n * Q->len)) != LIK_OK) return rc;
+  }
+  if (bwd_norm_d(flags)) {
+    bp.dinv = wsf;
+    if ((rc = invnorm(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, wsf)) != LIK_OK) return rc;
   }
   switch (Q->dtype) {
     case LIK_BF16: return launch_bwd_dpl<EK_BF16>(bp, s);

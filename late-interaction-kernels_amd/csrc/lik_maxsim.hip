@@ -275,6 +275,11 @@ int launch_plaid(int dt, int cd, const Plan& pl, const Params& p, int64_t nb, hi
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Params::normalize bits from the API flags: bit 0 queries, bit 1 docs.
+int norm_bits(uint32_t flags) {
+  return ((flags & (LIK_NORMALIZE | LIK_NORMALIZE_Q)) ? 1 : 0) | ((flags & (LIK_NORMALIZE | LIK_NORMALIZE_D)) ? 2 : 0);
+}
+
 // Launch timing, a measurement aid that is off unless lik_timing_begin() was
 // called: the tile-kernel launch of each scoring call (the one that scores
 // the mask-free docs, i.e. all of them unless a mask has holes) is bracketed
@@ -408,7 +413,7 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
   Plan pl;
   // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: spread
   // it over at least 4 waves even when the query block fits one wave's columns
-  const int min_w = ((flags & LIK_NORMALIZE) || argmax) ? 4 : 1;
+  const int min_w = ((norm_bits(flags) & 2) || argmax) ? 4 : 1;
   if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w)) != LIK_OK) return rc;
   const WsLayout wl = ws_layout(Q, D, flags, pl);
   if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return LIK_ERR_WORKSPACE;
@@ -416,7 +421,7 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
   Params p{};
   p.q = to_dev(*Q);
   p.d = to_dev(*D);
-  p.normalize = (flags & LIK_NORMALIZE) ? 3 : ((flags & LIK_NORMALIZE_Q) ? 1 : 0);
+  p.normalize = norm_bits(flags);
   p.out_scale = out_scale;
   p.nunits = pl.nunits;
   p.nc = pl.nc;
@@ -502,7 +507,7 @@ int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pa
   Params p{};
   p.q = to_dev(*Q);
   p.d = to_dev(*D);
-  p.normalize = (flags & LIK_NORMALIZE) ? 3 : ((flags & LIK_NORMALIZE_Q) ? 1 : 0);
+  p.normalize = norm_bits(flags);
   p.out_scale = 1.f;
   p.pair_q = pair_q;
   p.pair_d = pair_d;
@@ -567,7 +572,7 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   p.pl.bw = docs->bucket_weights;
   p.pl.nb = docs->n_buckets;
   p.pl.nbits = docs->nbits;
-  p.normalize = (flags & LIK_NORMALIZE) ? 3 : ((flags & LIK_NORMALIZE_Q) ? 1 : 0);
+  p.normalize = norm_bits(flags);
   p.out_scale = 1.f;
   p.nunits = pl.nunits;
   p.nc = 1;

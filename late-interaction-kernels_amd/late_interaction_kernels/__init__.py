@@ -9,11 +9,12 @@ A drop-in for the ``late_interaction_kernels`` Python API::
 
 Every op runs hand-written HIP kernels (bf16/fp16/fp8 MFMA, fused
 normalise/mask/PLAID decode, fused top-k merge) from ``_lib/liblik_hip.so``
-on the current HIP stream. Inputs must be ROCm GPU tensors; the MaxSim
-forward (inference) path is implemented, gradients are not.
+on the current HIP stream. Inputs must be ROCm GPU tensors. ``maxsim``,
+``maxsim_pairs``, the PLAID scorers (in Q) and ``fused_head.maxsim_from_hidden``
+are differentiable: an argmax-saving forward plus a deterministic HIP backward.
 
 Submodules mirror the reference: ``score_pairs``, ``padded``, ``plaid``,
-``fp8``, ``varlen``, ``topk``, ``retrieve``.
+``fp8``, ``varlen``, ``topk``, ``retrieve``, ``fused_head``, ``plaid_index``.
 """
 
 from importlib.metadata import PackageNotFoundError

@@ -57,6 +57,7 @@ def dense_maxsim(
     d_mask: torch.Tensor | None = None,
     *,
     normalize: bool = False,
+    norm: int | None = None,
     kd: bool = False,
     q_lengths: torch.Tensor | None = None,
     d_lengths: torch.Tensor | None = None,
@@ -96,7 +97,9 @@ def dense_maxsim(
         mask_strides=(dm.stride(0), dm.stride(1)) if dm is not None else (0, 0),
         token_scale=dsc, scale_strides=(dsc.stride(0), dsc.stride(1)) if dsc is not None else (0, 0),
     )
-    flags = (_lib.LIK_NORMALIZE if normalize else 0) | (_lib.LIK_KD_LAYOUT if kd else 0)
+    if norm is None:
+        norm = 3 if normalize else 0
+    flags = _lib.norm_flags(norm) | (_lib.LIK_KD_LAYOUT if kd else 0)
     _launch(qs, ds, flags, out_scale, out, Q.device)
     return out
 
@@ -107,10 +110,11 @@ def dense_maxsim_train(
     q_mask: torch.Tensor | None,
     d_mask: torch.Tensor | None,
     *,
-    normalize: bool,
+    norm: int,
     kd: bool,
 ):
     """Training forward: scores plus the saved state the backward needs.
+    ``norm`` is a bitmask: 1 normalises query tokens, 2 doc tokens.
 
     Returns ``(scores, argmax, Qp, Dp, qm)``: ``argmax`` is ``[Nq * docs, Lq]``
     int32 (winning doc-token index, -1 for rows without a valid doc token);
@@ -133,7 +137,7 @@ def dense_maxsim_train(
                    mask_strides=(qm.stride(0), qm.stride(1)) if qm is not None else (0, 0))
     ds = _lib.seqs(Dp, n=Nd, length=Ld, stride_n=Dp.stride(0), stride_l=Dp.stride(1), mask=dm,
                    mask_strides=(dm.stride(0), dm.stride(1)) if dm is not None else (0, 0))
-    flags = (_lib.LIK_NORMALIZE if normalize else 0) | (_lib.LIK_KD_LAYOUT if kd else 0)
+    flags = _lib.norm_flags(norm) | (_lib.LIK_KD_LAYOUT if kd else 0)
     lib = _lib.load()
     nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
     ws = _lib.workspace(nbytes, Q.device)
@@ -151,7 +155,7 @@ def maxsim_backward(
     argmax: torch.Tensor,
     qm: torch.Tensor | None,
     *,
-    normalize: bool,
+    norm: int,
     kd: bool,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``(grad_Q [Nq, Lq, dp], grad_D [Nd, Ld, dp])`` in the input dtype for upstream ``grad`` [Nq, docs]."""
@@ -165,7 +169,7 @@ def maxsim_backward(
     qs = _lib.seqs(Qp, n=Nq, length=Lq, stride_n=Qp.stride(0), stride_l=Qp.stride(1), mask=qm,
                    mask_strides=(qm.stride(0), qm.stride(1)) if qm is not None else (0, 0))
     ds = _lib.seqs(Dp, n=Nd, length=Ld, stride_n=Dp.stride(0), stride_l=Dp.stride(1))
-    flags = (_lib.LIK_NORMALIZE if normalize else 0) | (_lib.LIK_KD_LAYOUT if kd else 0)
+    flags = _lib.norm_flags(norm) | (_lib.LIK_KD_LAYOUT if kd else 0)
     lib = _lib.load()
     nbytes = lib.lik_maxsim_backward_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
     ws = _lib.workspace(nbytes, Qp.device)

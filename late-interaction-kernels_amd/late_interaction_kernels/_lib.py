@@ -26,6 +26,12 @@ LIK_BF16, LIK_F16, LIK_F32, LIK_FP8_E4M3 = 0, 1, 2, 3
 LIK_NORMALIZE = 1
 LIK_KD_LAYOUT = 2
 LIK_NORMALIZE_Q = 4
+LIK_NORMALIZE_D = 8
+
+
+def norm_flags(norm: int) -> int:
+    """API flag for a normalise bitmask (1: query tokens, 2: doc tokens)."""
+    return {0: 0, 1: LIK_NORMALIZE_Q, 2: LIK_NORMALIZE_D, 3: LIK_NORMALIZE}[norm]
 
 _ERRORS = {
     LIK_ERR_INVALID: "invalid argument",

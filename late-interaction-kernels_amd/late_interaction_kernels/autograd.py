@@ -79,10 +79,10 @@ class _MaxSimFn(torch.autograd.Function):
     """Fused MaxSim with saved argmax (reference autograd.py:169-229)."""
 
     @staticmethod
-    def forward(ctx, Q, D, q_mask, d_mask, normalize, kd):
-        scores, argmax, Qp, Dp, qm = dense_maxsim_train(Q, D, q_mask, d_mask, normalize=normalize, kd=kd)
+    def forward(ctx, Q, D, q_mask, d_mask, norm, kd):
+        scores, argmax, Qp, Dp, qm = dense_maxsim_train(Q, D, q_mask, d_mask, norm=norm, kd=kd)
         ctx.save_for_backward(Qp, Dp, argmax, qm)
-        ctx.normalize = normalize
+        ctx.norm = norm
         ctx.kd = kd
         ctx.shapes = (Q.shape, D.shape)
         ctx.dtypes = (Q.dtype, D.dtype)
@@ -92,19 +92,21 @@ class _MaxSimFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_scores):
         Qp, Dp, argmax, qm = ctx.saved_tensors
-        gq, gd = maxsim_backward(grad_scores, Qp, Dp, argmax, qm, normalize=ctx.normalize, kd=ctx.kd)
+        gq, gd = maxsim_backward(grad_scores, Qp, Dp, argmax, qm, norm=ctx.norm, kd=ctx.kd)
         (qshape, dshape), (qdt, ddt) = ctx.shapes, ctx.dtypes
         gq = gq[..., : qshape[-1]].to(qdt) if ctx.needs_input_grad[0] else None
         gd = gd[..., : dshape[-1]].to(ddt) if ctx.needs_input_grad[1] else None
         return gq, gd, None, None, None, None
 
 
-def _score(Q, D, q_mask, d_mask, *, normalize: bool, kd: bool = False) -> torch.Tensor:
+def _score(Q, D, q_mask, d_mask, *, normalize: bool | int, kd: bool = False) -> torch.Tensor:
+    """``normalize``: bool (both sides) or a bitmask (1: query tokens, 2: doc tokens)."""
+    norm = (3 if normalize else 0) if isinstance(normalize, bool) else int(normalize)
     if _needs_grad(Q, D):
         if Q.dtype == torch.float64 or D.dtype == torch.float64:
             raise TypeError("maxsim gradients support fp16 / bf16 / fp32 inputs")
-        return _MaxSimFn.apply(Q, D, q_mask, d_mask, normalize, kd)
-    return dense_maxsim(Q, D, q_mask, d_mask, normalize=normalize, kd=kd)
+        return _MaxSimFn.apply(Q, D, q_mask, d_mask, norm, kd)
+    return dense_maxsim(Q, D, q_mask, d_mask, norm=norm, kd=kd)
 
 
 def _resolve_method(backward: str | None) -> str:

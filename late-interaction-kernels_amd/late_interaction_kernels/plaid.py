@@ -10,7 +10,10 @@
 A token's embedding is ``centroids[code] + bucket_weights[b_f]`` per feature
 ``f``, where ``b_f`` is the ``nbits``-bit field ``f`` of the packed residual
 row, little-endian within each byte (``reference.py:124-139``). Decode,
-normalise and MaxSim are one kernel: the decoded tile only ever lives in LDS.
+normalise and MaxSim are one kernel (the decoded tile only lives in LDS), or,
+for large query batches, a decode pass followed by the dense MaxSim kernel.
+Gradients flow into Q (codes / residuals are integers; centroids and bucket
+weights are treated as frozen, as in the reference).
 Out-of-range centroid codes are clamped to 0 and bucket codes to the last
 bucket, so corrupt indices cannot fault.
 """
@@ -161,7 +164,7 @@ def maxsim_residual(
         bucket_weights: ``[2**nbits]`` fp32.
         nbits: 2, 4 or 8.
     Returns:
-        ``[Nq, Nd]`` fp32 (``[Nd]`` for 2-D Q). Inference only.
+        ``[Nq, Nd]`` fp32 (``[Nd]`` for 2-D Q). Differentiable in ``Q``.
     """
     _check_nbits(nbits)
     if codes.dim() != 2:
@@ -171,12 +174,15 @@ def maxsim_residual(
     q_squeeze = Q.dim() == 2
     if q_squeeze:
         Q = Q.unsqueeze(0)
-    if torch.is_grad_enabled() and Q.requires_grad:
-        raise NotImplementedError("maxsim_residual: gradients are not available in the MI355X build")
     _lib.require_gpu(Q, codes, residuals, doc_lengths, centroids, bucket_weights)
     Nq, Lq, d = Q.shape
     Nd, L = codes.shape
     residuals, centroids, bw = _prep_index(residuals, centroids, bucket_weights, nbits, d)
+    if torch.is_grad_enabled() and Q.requires_grad and Nq and Nd and Lq and L:
+        lens = doc_lengths.contiguous().to(torch.int32)
+        out = _residual_with_q_grad(Q, codes.reshape(-1), residuals.reshape(Nd * L, -1), centroids, bw, nbits,
+                                    lengths=lens, Nd=Nd, L=L, normalize=normalize)
+        return out.squeeze(0) if q_squeeze else out
     out = torch.empty(Nq, Nd, device=Q.device, dtype=torch.float32)
     if Nq and Nd:
         if Lq == 0 or L == 0:
@@ -218,8 +224,6 @@ def maxsim_residual_varlen(
         raise ValueError("residuals_flat must be 2-D [total_d_tokens, packed_dim]")
     if cu_seqlens_d.dim() != 1:
         raise ValueError("cu_seqlens_d must be 1-D [Nd + 1]")
-    if torch.is_grad_enabled() and Q.requires_grad:
-        raise NotImplementedError("maxsim_residual_varlen is inference-only")
     _lib.require_gpu(Q, codes_flat, residuals_flat, cu_seqlens_d, centroids, bucket_weights)
     Nq, Lq, d = Q.shape
     residuals_flat, centroids, bw = _prep_index(residuals_flat, centroids, bucket_weights, nbits, d)
@@ -227,6 +231,10 @@ def maxsim_residual_varlen(
     Nd = cu.numel() - 1
     if max_seqlen_d is not None:
         assert_max_seqlen_covers(cu, int(max_seqlen_d), "max_seqlen_d")
+    if torch.is_grad_enabled() and Q.requires_grad and Nq and Nd > 0 and Lq and codes_flat.numel():
+        out = _residual_with_q_grad(Q, codes_flat, residuals_flat, centroids, bw, nbits, cu=cu, Nd=Nd, L=0,
+                                    normalize=normalize)
+        return out.squeeze(0) if q_squeeze else out
     out = torch.empty(Nq, max(Nd, 0), device=Q.device, dtype=torch.float32)
     if Nq and Nd > 0:
         if Lq == 0 or codes_flat.numel() == 0:
@@ -305,6 +313,73 @@ def decode_residual_tokens(
         docs = _plaid_docs(codes, residuals_flat, centroids, bw, nbits, d, n=0, max_len=0)
         _decode_into(docs, 0, T, normalize, out)
     return out
+
+
+class _ResidualQGradFn(torch.autograd.Function):
+    """PLAID MaxSim differentiable in Q only (reference plaid.py:518-616): codes and
+    residuals are integers, centroids / bucket weights frozen. Forward decodes the
+    docs once (lik_plaid_decode) and runs the argmax-saving MaxSim on the decoded
+    rows; backward runs the grad_Q kernel against the same rows."""
+
+    @staticmethod
+    def forward(ctx, Q, docs_tuple, cu, lengths, Nd, L, normalize):
+        codes, residuals, centroids, bw, nbits = docs_tuple
+        Qp = _lib.prepare_tokens(Q.detach())
+        Nq, Lq, d = Qp.shape
+        T = codes.shape[0]
+        docs = _plaid_docs(codes, residuals, centroids, bw, nbits, d, n=0, max_len=0)
+        dec = torch.empty(max(T, 1), d, device=Q.device, dtype=Qp.dtype)
+        if T:
+            _decode_into(docs, 0, T, normalize, dec)
+        qs = _lib.seqs(Qp, n=Nq, length=Lq, stride_n=Qp.stride(0), stride_l=Qp.stride(1))
+        if cu is not None:
+            ds = _lib.seqs(dec, n=Nd, length=0, stride_l=dec.stride(0), cu=cu)
+        else:
+            ds = _lib.seqs(dec, n=Nd, length=L, stride_n=L * dec.stride(0), stride_l=dec.stride(0), lengths=lengths)
+        flags = _lib.LIK_NORMALIZE_Q if normalize else 0
+        out = torch.empty(Nq, Nd, device=Q.device, dtype=torch.float32)
+        argmax = torch.full((Nq * Nd, Lq), -1, device=Q.device, dtype=torch.int32)
+        lib = _lib.load()
+        nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
+        ws = _lib.workspace(nbytes, Q.device)
+        with torch.cuda.device(Q.device):
+            rc = lib.lik_maxsim_argmax(ctypes.byref(qs), ctypes.byref(ds), flags, out.data_ptr(), out.stride(0),
+                                       out.stride(1), argmax.data_ptr(), _lib.ptr(ws), nbytes, _lib.stream_of(out))
+        _lib.check(rc, "lik_maxsim_argmax")
+        ctx.save_for_backward(Qp, dec, argmax, cu, lengths)
+        ctx.meta = (Nd, L, normalize, Q.shape[-1], Q.dtype)
+        ctx.mark_non_differentiable(argmax)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_scores):
+        Qp, dec, argmax, cu, lengths = ctx.saved_tensors
+        Nd, L, normalize, d_in, qdt = ctx.meta
+        Nq, Lq, d = Qp.shape
+        g = grad_scores.to(torch.float32).contiguous()
+        qs = _lib.seqs(Qp, n=Nq, length=Lq, stride_n=Qp.stride(0), stride_l=Qp.stride(1))
+        if cu is not None:
+            ds = _lib.seqs(dec, n=Nd, length=0, stride_l=dec.stride(0), cu=cu)
+        else:
+            ds = _lib.seqs(dec, n=Nd, length=L, stride_n=L * dec.stride(0), stride_l=dec.stride(0), lengths=lengths)
+        flags = _lib.LIK_NORMALIZE_Q if normalize else 0
+        gq = torch.empty_like(Qp)
+        lib = _lib.load()
+        nbytes = lib.lik_maxsim_backward_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
+        ws = _lib.workspace(nbytes, Qp.device)
+        with torch.cuda.device(Qp.device):
+            rc = lib.lik_maxsim_backward(g.data_ptr(), g.stride(0), ctypes.byref(qs), ctypes.byref(ds),
+                                         argmax.data_ptr(), flags, gq.data_ptr(), None, _lib.ptr(ws), nbytes,
+                                         _lib.stream_of(gq))
+        _lib.check(rc, "lik_maxsim_backward")
+        return gq[..., :d_in].to(qdt), None, None, None, None, None, None
+
+
+def _residual_with_q_grad(Q, codes_flat, residuals, centroids, bw, nbits, *, cu=None, lengths=None, Nd, L,
+                          normalize):
+    Qc = Q.to(torch.float16 if Q.dtype == torch.float16 else torch.bfloat16)  # differentiable cast
+    codes = codes_flat.contiguous().to(torch.int32)
+    return _ResidualQGradFn.apply(Qc, (codes, residuals, centroids, bw, nbits), cu, lengths, Nd, L, normalize)
 
 
 def _decode_into(docs: _lib.LikPlaidDocs, t0: int, t1: int, normalize: bool, out: torch.Tensor) -> None:

@@ -73,8 +73,8 @@ def load_fastplaid_index(
     centroids_np = _npy(os.path.join(index_path, "centroids.npy"))
     d = int(d or centroids_np.shape[1])
     packed_dim = (d * nbits + 7) // 8
-    centroids = torch.from_numpy(np.ascontiguousarray(centroids_np)).to(device=device, dtype=centroid_dtype)
-    bucket_weights = torch.from_numpy(np.ascontiguousarray(_npy(os.path.join(index_path, "bucket_weights.npy"))))
+    centroids = torch.from_numpy(np.array(centroids_np, copy=True)).to(device=device, dtype=centroid_dtype)
+    bucket_weights = torch.from_numpy(np.array(_npy(os.path.join(index_path, "bucket_weights.npy")), copy=True))
     bucket_weights = bucket_weights.to(device=device, dtype=torch.float32)
 
     doc_lens: list[int] = []
@@ -102,7 +102,7 @@ def load_fastplaid_index(
         raise ValueError(f"index holds {codes_all.shape[0]} codes / {res_all.shape[0]} residual rows "
                          f"for {total} document tokens")
     codes_flat = torch.from_numpy(np.ascontiguousarray(codes_all[:total]).astype(np.int32, copy=False)).to(device)
-    res_raw = torch.from_numpy(np.ascontiguousarray(res_all[:total]).astype(np.uint8, copy=False)).to(device)
+    res_raw = torch.from_numpy(np.array(res_all[:total], dtype=np.uint8, copy=True)).to(device)
     residuals_flat = reverse_residual_bits(res_raw).view(total, packed_dim)
 
     doc_lengths = torch.tensor(doc_lens, device=device, dtype=torch.int64)

@@ -75,7 +75,7 @@ def test_argmax_and_grads_match_oracle(dtype, tol, gap, normalize, kd):
     Nq, Lq, d, Ld = 5, 24, 64, 50
     Nd = Nq * 3 if kd else 7
     Q, D, qm, dm = _inputs(Nq, Nd, Lq, Ld, d, dtype, 7 + normalize + 2 * kd)
-    scores, am, Qp, Dp, qmi = dense_maxsim_train(Q.cuda(), D.cuda(), qm.cuda(), dm.cuda(), normalize=normalize, kd=kd)
+    scores, am, Qp, Dp, qmi = dense_maxsim_train(Q.cuda(), D.cuda(), qm.cuda(), dm.cuda(), norm=3 if normalize else 0, kd=kd)
     ref_am = O.maxsim_argmax(_np(Q), _np(D), dm.numpy(), normalize=normalize, kd=kd)
     got_am = am.cpu().numpy()
     sep = _separated(Q, D, dm, normalize, kd, gap)
@@ -85,7 +85,7 @@ def test_argmax_and_grads_match_oracle(dtype, tol, gap, normalize, kd):
     assert np.array_equal(got_am[sep], ref_am[sep])
     assert np.array_equal(got_am == -1, ref_am == -1)
     G = torch.randn(Nq, docs)
-    gq, gd = maxsim_backward(G.cuda(), Qp, Dp, am, qmi, normalize=normalize, kd=kd)
+    gq, gd = maxsim_backward(G.cuda(), Qp, Dp, am, qmi, norm=3 if normalize else 0, kd=kd)
     rq, rd = O.maxsim_grads(G.numpy(), _np(Q), _np(D), got_am, qm.numpy(), normalize=normalize, kd=kd)
     assert rel_err(_np(gq), rq) < tol
     assert rel_err(_np(gd), rd) < tol

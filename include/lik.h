@@ -111,17 +111,19 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
  * Backward: given grad[i * grad_ld + j] = dL/dscore[i, j] (fp32) and the
  * argmax of lik_maxsim_argmax, writes grad_q [Q->n, Q->len, dim] and grad_d
  * [D->n, D->len, dim], contiguous, in the dtype of Q and D (accumulated in
- * fp32; every element written, rows that win nothing get 0).
- * Q padded; D padded, or packed (cu_seqlens) when grad_d is null (only
- * grad_q is computed then); Q->mask (keep flags) zeroes the masked query
- * tokens' terms; doc masks / lengths act only through the argmax. With
+ * fp32; every element written, rows that win nothing get 0). grad_d may be
+ * null (only grad_q is computed). Either side may be packed (cu_seqlens,
+ * ->len = longest sequence): its gradient is then [rows, dim] indexed like
+ * the packed input, and only rows cu[0] .. cu[n] are written. Q->mask (keep
+ * flags) zeroes the masked query tokens' terms; doc masks / lengths act only
+ * through the argmax. A packed side cannot be normalised here. With
  * LIK_NORMALIZE (both sides), LIK_NORMALIZE_Q or LIK_NORMALIZE_D the
  * gradients are taken through x / max(||x||, 1e-12) on those sides and the
  * caller passes lik_maxsim_backward_workspace_size() bytes.
  * Deterministic: fixed summation order, no atomics.
  * Replaces backward/unified.py:maxsim_backward_unified and
  * backward/lowmem.py:maxsim_backward_lowmem (+ the normalise Jacobian of
- * autograd.py:211-225).
+ * autograd.py:211-225), and varlen.py:143-263 for packed inputs.
  */
 int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q, const lik_seqs_t* D,
                         const int32_t* argmax, uint32_t flags, void* grad_q, void* grad_d, void* workspace,

@@ -19,6 +19,10 @@
 //   tokens per ballot; each pair whose winner falls in the block adds its
 //   scaled query row to that accumulator row. No atomics: every lane updates
 //   only its own dims, in scan order, so grad_D is bitwise deterministic.
+//   Packed docs (cu_seqlens): a block is RB consecutive packed rows and may
+//   span several docs; it scans each of them in doc order.
+// Packed queries: the wave of (i, s) exits when s is past query i's length;
+// rows are addressed through cu_q (reference varlen.py:143-263).
 // Both apply the normalisation Jacobian to the finished row in registers.
 #include "lik_common.h"
 
@@ -43,8 +47,9 @@ constexpr int sizeof_ek() { return EK == EK_F32 ? 4 : 2; }
 struct BwdParams {
   const float* grad;  // [Nq, ld_g]
   int64_t ld_g;
-  const char* q;      // Q rows: q + i*q_sn + s*q_sl (bytes)
+  const char* q;      // Q rows: q + i*q_sn + s*q_sl, or q + (q_cu[i] + s)*q_sl when packed (bytes)
   int64_t q_sn, q_sl;
+  const int32_t* q_cu;
   const char* d;      // D rows: d + j*d_sn + t*d_sl, or d + (d_cu[j] + t)*d_sl when packed (bytes)
   int64_t d_sn, d_sl;
   const int32_t* d_cu;
@@ -53,9 +58,9 @@ struct BwdParams {
   int64_t qm_sn, qm_sl;
   const float* qinv;  // [Nq * Lq] inverse norms (normalise), else null
   const float* dinv;  // [Nd * Ld]
-  char* gq;           // [Nq, Lq, dim] in the input dtype
-  char* gd;           // [Nd, Ld, dim] in the input dtype
-  int64_t nq, lq, nd, ld;
+  char* gq;           // [Nq, Lq, dim] (packed: [rows, dim]) in the input dtype
+  char* gd;           // [Nd, Ld, dim] (packed: [rows, dim]) in the input dtype
+  int64_t nq, lq, nd, ld;  // lq / ld: padded lengths, or the longest sequence when packed
   int64_t ndoc_pg;    // docs per query: Nd (cross product) or K (KD layout)
   int kd;
   int dim;
@@ -98,6 +103,12 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
   const int64_t w = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
   if (w >= bp.nq * bp.lq) return;
   const int64_t i = w / bp.lq, s = w % bp.lq;
+  int64_t qr = w;  // storage row of token (i, s)
+  if (bp.q_cu) {
+    const int64_t q0 = bp.q_cu[i];
+    if (s >= (int64_t)bp.q_cu[i + 1] - q0) return;
+    qr = q0 + s;
+  }
   const int64_t j0 = bp.kd ? i * bp.ndoc_pg : 0;
   const int32_t* am = bp.amax + (i * bp.ndoc_pg) * bp.lq + s;
   const float* g = bp.grad + i * bp.ld_g;
@@ -127,8 +138,8 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
   }
   const bool keep = !bp.qmask || bp.qmask[i * bp.qm_sn + s * bp.qm_sl] != 0;
   if (bp.qinv) {
-    const float qi = bp.qinv[w];
-    const char* qrow = bp.q + i * bp.q_sn + s * bp.q_sl;
+    const float qi = bp.qinv[qr];
+    const char* qrow = bp.q_cu ? bp.q + qr * bp.q_sl : bp.q + i * bp.q_sn + s * bp.q_sl;
     float xh[DPL], dot = 0.f;
 #pragma unroll
     for (int k = 0; k < DPL; ++k) {
@@ -140,7 +151,7 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
 #pragma unroll
     for (int k = 0; k < DPL; ++k) acc[k] = (acc[k] - dot * xh[k]) * qi;
   }
-  char* out = bp.gq + w * bp.dim * (int64_t)sizeof_ek<EK>();
+  char* out = bp.gq + qr * bp.dim * (int64_t)sizeof_ek<EK>();
 #pragma unroll
   for (int k = 0; k < DPL; ++k) {
     const int e = lane * DPL + k;
@@ -149,53 +160,93 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
 }
 
 // RB doc rows per wavefront, RB * 64 * DPL floats of LDS accumulator (16 KB).
+// Padded docs: block b is rows [t0, t0 + RB) of doc b / nrb. Packed docs: block
+// b is storage rows [cu[0] + b*RB, +RB), each doc overlapping it scanned in turn.
 template <int EK, int DPL>
 __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
   constexpr int RB = 64 / DPL < 32 ? 64 / DPL : 32;
   __shared__ float s_acc[RB][64 * DPL];
   const int lane = threadIdx.x;
-  const int64_t nrb = (bp.ld + RB - 1) / RB;
-  const int64_t j = blockIdx.x / nrb;
-  const int64_t t0 = (blockIdx.x % nrb) * RB;
 #pragma unroll
   for (int r = 0; r < RB; ++r)
 #pragma unroll
     for (int k = 0; k < DPL; ++k) s_acc[r][lane * DPL + k] = 0.f;
-  const int64_t jl = bp.kd ? j % bp.ndoc_pg : j;
-  const int64_t i_begin = bp.kd ? j / bp.ndoc_pg : 0;
-  const int64_t i_end = bp.kd ? i_begin + 1 : bp.nq;
   uint32_t touched = 0;  // rows of the block that received a contribution (wave-uniform)
-  for (int64_t i = i_begin; i < i_end; ++i) {
-    const float gij = bp.grad[i * bp.ld_g + jl];
-    if (gij == 0.f) continue;
-    const int32_t* am = bp.amax + (i * bp.ndoc_pg + jl) * bp.lq;
-    for (int64_t s0 = 0; s0 < bp.lq; s0 += 64) {
-      const int64_t s = s0 + lane;
-      int a = s < bp.lq ? am[s] : -1;
-      if (a >= 0 && bp.qmask && bp.qmask[i * bp.qm_sn + s * bp.qm_sl] == 0) a = -1;
-      float sc = gij;
-      if (bp.qinv && a >= 0) sc *= bp.qinv[i * bp.lq + s];
-      uint64_t bal = __ballot(a >= t0 && a < t0 + RB);
-      while (bal) {
-        const int l = __builtin_ctzll(bal);
-        bal &= bal - 1;
-        const int r = __builtin_amdgcn_readlane(a, l) - (int)t0;
-        touched |= 1u << r;
-        const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
-        const char* qrow = bp.q + i * bp.q_sn + (s0 + l) * bp.q_sl;
+
+  // Add the contributions of doc j whose winner a lies in [wlo, wlo + n) to
+  // accumulator rows off + (a - wlo).
+  auto scan_doc = [&](int64_t j, int64_t wlo, int n, int off) {
+    const int64_t jl = bp.kd ? j % bp.ndoc_pg : j;
+    const int64_t i_begin = bp.kd ? j / bp.ndoc_pg : 0;
+    const int64_t i_end = bp.kd ? i_begin + 1 : bp.nq;
+    for (int64_t i = i_begin; i < i_end; ++i) {
+      const float gij = bp.grad[i * bp.ld_g + jl];
+      if (gij == 0.f) continue;
+      const int32_t* am = bp.amax + (i * bp.ndoc_pg + jl) * bp.lq;
+      int64_t qlen = bp.lq, qbase = 0;
+      if (bp.q_cu) {
+        qbase = bp.q_cu[i];
+        qlen = (int64_t)bp.q_cu[i + 1] - qbase;
+      }
+      for (int64_t s0 = 0; s0 < qlen; s0 += 64) {
+        const int64_t s = s0 + lane;
+        int a = s < qlen ? am[s] : -1;
+        if (a >= 0 && bp.qmask && bp.qmask[i * bp.qm_sn + s * bp.qm_sl] == 0) a = -1;
+        float sc = gij;
+        if (bp.qinv && a >= 0) sc *= bp.qinv[bp.q_cu ? qbase + s : i * bp.lq + s];
+        uint64_t bal = __ballot(a >= wlo && a < wlo + n);
+        while (bal) {
+          const int l = __builtin_ctzll(bal);
+          bal &= bal - 1;
+          const int r = off + __builtin_amdgcn_readlane(a, l) - (int)wlo;
+          touched |= 1u << r;
+          const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
+          const char* qrow = bp.q_cu ? bp.q + (qbase + s0 + l) * bp.q_sl : bp.q + i * bp.q_sn + (s0 + l) * bp.q_sl;
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) {
-          const int e = lane * DPL + k;
-          if (e < bp.dim) s_acc[r][e] = fmaf(c, load_elem<EK>(qrow, e), s_acc[r][e]);
+          for (int k = 0; k < DPL; ++k) {
+            const int e = lane * DPL + k;
+            if (e < bp.dim) s_acc[r][e] = fmaf(c, load_elem<EK>(qrow, e), s_acc[r][e]);
+          }
         }
       }
     }
+  };
+
+  int nrows;         // rows of this block
+  int64_t out_row0;  // storage row of accumulator row 0
+  int64_t j_pad = 0, t0 = 0;
+  if (bp.d_cu) {
+    const int64_t base = bp.d_cu[0], endr = bp.d_cu[bp.nd];
+    const int64_t r0 = base + (int64_t)blockIdx.x * RB;
+    if (r0 >= endr) return;
+    nrows = (int)(endr - r0 < RB ? endr - r0 : RB);
+    out_row0 = r0;
+    // first doc whose rows reach past r0: largest j with cu[j] <= r0 (binary search)
+    int64_t lo = 0, hi = bp.nd;  // invariant: cu[lo] <= r0 < cu[hi]
+    while (hi - lo > 1) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (bp.d_cu[mid] <= r0) lo = mid;
+      else hi = mid;
+    }
+    for (int64_t j = lo; j < bp.nd; ++j) {
+      const int64_t c0 = bp.d_cu[j], c1 = bp.d_cu[j + 1];
+      if (c0 >= r0 + nrows) break;
+      const int64_t a0 = r0 > c0 ? r0 : c0;  // overlap [a0, a1) in storage rows
+      const int64_t a1 = c1 < r0 + nrows ? c1 : r0 + nrows;
+      if (a1 > a0) scan_doc(j, a0 - c0, (int)(a1 - a0), (int)(a0 - r0));
+    }
+  } else {
+    const int64_t nrb = (bp.ld + RB - 1) / RB;
+    j_pad = blockIdx.x / nrb;
+    t0 = (blockIdx.x % nrb) * RB;
+    nrows = (int)(bp.ld - t0 < RB ? bp.ld - t0 : RB);
+    out_row0 = j_pad * bp.ld + t0;
+    scan_doc(j_pad, t0, nrows, 0);
   }
-  // finished rows: normalisation Jacobian, then store
-  for (int r = 0; r < RB; ++r) {
-    const int64_t t = t0 + r;
-    if (t >= bp.ld) break;
-    char* out = bp.gd + (j * bp.ld + t) * bp.dim * (int64_t)sizeof_ek<EK>();
+
+  // finished rows: normalisation Jacobian (padded docs only), then store
+  for (int r = 0; r < nrows; ++r) {
+    char* out = bp.gd + (out_row0 + r) * bp.dim * (int64_t)sizeof_ek<EK>();
     if (!((touched >> r) & 1u)) {  // no winner in this row: zero gradient, no D read
 #pragma unroll
       for (int k = 0; k < DPL; ++k) {
@@ -208,8 +259,9 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
 #pragma unroll
     for (int k = 0; k < DPL; ++k) gh[k] = s_acc[r][lane * DPL + k];
     if (bp.dinv) {
-      const float di = bp.dinv[j * bp.ld + t];
-      const char* drow = bp.d + j * bp.d_sn + t * bp.d_sl;
+      const int64_t t = t0 + r;
+      const float di = bp.dinv[j_pad * bp.ld + t];
+      const char* drow = bp.d + j_pad * bp.d_sn + t * bp.d_sl;
       float xh[DPL], dot = 0.f;
 #pragma unroll
       for (int k = 0; k < DPL; ++k) {
@@ -237,7 +289,9 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
     hipLaunchKernelGGL((grad_q_kernel<EK, DPL>), dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, s, bp);
     if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
   }
-  const int64_t nb = bp.gd ? bp.nd * ((bp.ld + RB - 1) / RB) : 0;
+  // packed docs: sum of lengths <= nd * ld, so nd * ld / RB blocks cover them
+  const int64_t nb = !bp.gd ? 0 : bp.d_cu ? (bp.nd * bp.ld + RB - 1) / RB : bp.nd * ((bp.ld + RB - 1) / RB);
+  if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
   if (nb > 0) {
     hipLaunchKernelGGL((grad_d_kernel<EK, DPL>), dim3((unsigned)nb), dim3(64), 0, s, bp);
     if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
@@ -289,9 +343,11 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   if (!Q || !D) return LIK_ERR_INVALID;
   if (Q->dtype != D->dtype || Q->dim != D->dim || Q->dim <= 0) return LIK_ERR_INVALID;
   if (Q->dtype != LIK_BF16 && Q->dtype != LIK_F16 && Q->dtype != LIK_F32) return LIK_ERR_UNSUPPORTED;
-  if (Q->cu_seqlens || Q->lengths || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
-  // doc masks / lengths act through the forward's argmax; packed docs only for grad_q
-  if (D->cu_seqlens && (grad_d || bwd_norm_d(flags))) return LIK_ERR_UNSUPPORTED;
+  if (Q->lengths || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
+  // doc masks / lengths act through the forward's argmax; a packed side is
+  // never normalised here (its row count is only known on the device)
+  if ((Q->cu_seqlens && bwd_norm_q(flags)) || (D->cu_seqlens && bwd_norm_d(flags))) return LIK_ERR_UNSUPPORTED;
+  if (D->cu_seqlens && (flags & LIK_KD_LAYOUT)) return LIK_ERR_INVALID;
   if (Q->n < 0 || D->n < 0 || Q->len < 0 || D->len < 0) return LIK_ERR_INVALID;
   if (Q->dim > 512) return LIK_ERR_UNSUPPORTED;
   const bool kd = (flags & LIK_KD_LAYOUT) != 0;
@@ -306,6 +362,7 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   bp.q = (const char*)Q->data;
   bp.q_sn = Q->stride_n * eb;
   bp.q_sl = Q->stride_l * eb;
+  bp.q_cu = Q->cu_seqlens;
   bp.d = (const char*)D->data;
   bp.d_sn = D->stride_n * eb;
   bp.d_sl = D->stride_l * eb;

@@ -212,6 +212,49 @@ def packed_maxsim(
     return out
 
 
+def packed_maxsim_train(Q_packed, D_packed, cu_q, cu_d, max_q: int, max_d: int):
+    """Training forward on packed Q and D: ``(scores [Nq, Nd], argmax [Nq*Nd, max_q], Qp, Dp)``."""
+    _lib.require_gpu(Q_packed, D_packed, cu_q, cu_d)
+    Nq = cu_q.numel() - 1
+    Nd = cu_d.numel() - 1
+    out = torch.zeros(max(Nq, 0), max(Nd, 0), device=Q_packed.device, dtype=torch.float32)
+    argmax = torch.full((max(Nq, 0) * max(Nd, 0), max(max_q, 0)), -1, device=Q_packed.device, dtype=torch.int32)
+    Qp = _lib.prepare_tokens(Q_packed.detach())
+    Dp = _lib.prepare_tokens(D_packed.detach())
+    if Nq <= 0 or Nd <= 0 or max_q <= 0 or Q_packed.shape[0] == 0 or D_packed.shape[0] == 0:
+        return out, argmax, Qp, Dp
+    qs = _lib.seqs(Qp, n=Nq, length=max_q, stride_l=Qp.stride(0), cu=cu_q)
+    ds = _lib.seqs(Dp, n=Nd, length=max(int(max_d), 0), stride_l=Dp.stride(0), cu=cu_d)
+    lib = _lib.load()
+    nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), 0)
+    ws = _lib.workspace(nbytes, Q_packed.device)
+    with torch.cuda.device(Q_packed.device):
+        rc = lib.lik_maxsim_argmax(ctypes.byref(qs), ctypes.byref(ds), 0, out.data_ptr(), out.stride(0),
+                                   out.stride(1), argmax.data_ptr(), _lib.ptr(ws), nbytes, _lib.stream_of(out))
+    _lib.check(rc, "lik_maxsim_argmax")
+    return out, argmax, Qp, Dp
+
+
+def packed_backward(grad, Qp, Dp, cu_q, cu_d, argmax, max_q: int, max_d: int, *, need_d: bool = True):
+    """Gradients of packed MaxSim: ``(grad_Q [rows_q, dp], grad_D [rows_d, dp] or None)`` in the input dtype.
+    Rows outside ``cu[0] .. cu[-1]`` are zero."""
+    Nq = cu_q.numel() - 1
+    Nd = cu_d.numel() - 1
+    gq = torch.zeros_like(Qp)
+    gd = torch.zeros_like(Dp) if need_d else None
+    if Nq <= 0 or Nd <= 0 or max_q <= 0 or Qp.shape[0] == 0 or Dp.shape[0] == 0:
+        return gq, gd
+    g = grad.to(torch.float32).contiguous()
+    qs = _lib.seqs(Qp, n=Nq, length=max_q, stride_l=Qp.stride(0), cu=cu_q)
+    ds = _lib.seqs(Dp, n=Nd, length=max(int(max_d), 0), stride_l=Dp.stride(0), cu=cu_d)
+    lib = _lib.load()
+    with torch.cuda.device(Qp.device):
+        rc = lib.lik_maxsim_backward(g.data_ptr(), g.stride(0), ctypes.byref(qs), ctypes.byref(ds), argmax.data_ptr(),
+                                     0, gq.data_ptr(), _lib.ptr(gd), None, 0, _lib.stream_of(gq))
+    _lib.check(rc, "lik_maxsim_backward")
+    return gq, gd
+
+
 def _launch(qs, ds, flags: int, out_scale: float, out: torch.Tensor, device: torch.device) -> None:
     lib = _lib.load()
     nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)

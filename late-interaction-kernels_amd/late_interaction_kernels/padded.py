@@ -15,7 +15,7 @@ from dataclasses import dataclass
 import torch
 
 from ._core import dense_maxsim, unify_dtype
-from .autograd import _no_grad_guard
+from .autograd import _needs_grad, _score
 
 
 @dataclass(frozen=True)
@@ -128,10 +128,17 @@ def maxsim_padded(
             raise ValueError("lengths must all be > 0")
         if bool((ql > Lq).any()) or bool((dl > Ld).any()):
             raise ValueError("a length exceeds the padded extent")
-    _no_grad_guard(queries, documents)
     Q, D = unify_dtype(queries, documents)
     if B == 0 or C == 0:
         return torch.zeros(B, C, device=queries.device, dtype=torch.float32)
+    if _needs_grad(queries, documents):
+        # training: the KD layout with length masks through the argmax forward
+        # and the deterministic backward (the reference's pair-list backward,
+        # score_pairs.py:344-420, computes the same gradients)
+        dev = queries.device
+        qm = torch.arange(Lq, device=dev)[None, :] < query_lengths.to(dev).reshape(B, 1)
+        dm = torch.arange(Ld, device=dev)[None, :] < doc_lengths.to(dev).reshape(B * C, 1)
+        return _score(Q, D.reshape(B * C, Ld, d), qm, dm, normalize=False, kd=True)
     return dense_maxsim(
         Q,
         D.reshape(B * C, Ld, d),

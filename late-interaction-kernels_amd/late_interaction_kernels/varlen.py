@@ -1,11 +1,34 @@
-"""``maxsim_varlen``: MaxSim on packed (cu_seqlens) inputs (reference varlen.py:452-493)."""
+"""``maxsim_varlen``: MaxSim on packed (cu_seqlens) inputs (reference varlen.py:452-493),
+differentiable in both inputs (reference varlen.py:136-263, 372-449): an
+argmax-saving forward and the deterministic HIP backward on packed rows."""
 
 from __future__ import annotations
 
 import torch
 
-from ._core import assert_max_seqlen_covers, packed_maxsim, seqlen_max, unify_dtype
-from .autograd import _no_grad_guard
+from ._core import (assert_max_seqlen_covers, packed_backward, packed_maxsim, packed_maxsim_train, seqlen_max,
+                    unify_dtype)
+from .autograd import _needs_grad
+
+
+class _MaxSimVarlenFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, Q, D, cu_q, cu_d, max_q, max_d):
+        scores, argmax, Qp, Dp = packed_maxsim_train(Q, D, cu_q, cu_d, max_q, max_d)
+        ctx.save_for_backward(Qp, Dp, cu_q, cu_d, argmax)
+        ctx.meta = (max_q, max_d, Q.shape[-1], Q.dtype, D.dtype)
+        ctx.mark_non_differentiable(argmax)
+        return scores
+
+    @staticmethod
+    def backward(ctx, grad_scores):
+        Qp, Dp, cu_q, cu_d, argmax = ctx.saved_tensors
+        max_q, max_d, d, qdt, ddt = ctx.meta
+        gq, gd = packed_backward(grad_scores, Qp, Dp, cu_q, cu_d, argmax, max_q, max_d,
+                                 need_d=ctx.needs_input_grad[1])
+        gq = gq[:, :d].to(qdt) if ctx.needs_input_grad[0] else None
+        gd = gd[:, :d].to(ddt) if gd is not None else None
+        return gq, gd, None, None, None, None
 
 
 def maxsim_varlen(
@@ -16,7 +39,7 @@ def maxsim_varlen(
     max_seqlen_q: int | None = None,
     max_seqlen_d: int | None = None,
 ) -> torch.Tensor:
-    """MaxSim on packed (no-padding) inputs.
+    """MaxSim on packed (no-padding) inputs. Autograd-aware.
 
     Args:
         Q_packed: ``[sum(Lq_i), d]`` fp16 / bf16 / fp32.
@@ -48,7 +71,6 @@ def maxsim_varlen(
             f"Q_packed and D_packed must share the embedding dim; got "
             f"Q_packed.shape[1]={Q_packed.shape[1]} vs D_packed.shape[1]={D_packed.shape[1]}."
         )
-    _no_grad_guard(Q_packed, D_packed)
     cu_q = cu_seqlens_q.to(torch.int32).contiguous()
     cu_d = cu_seqlens_d.to(torch.int32).contiguous()
     if max_seqlen_q is None:
@@ -58,6 +80,12 @@ def maxsim_varlen(
     if max_seqlen_d is not None:
         assert_max_seqlen_covers(cu_d, int(max_seqlen_d), "max_seqlen_d")
     Qp, Dp = unify_dtype(Q_packed, D_packed)
+    if _needs_grad(Q_packed, D_packed):
+        if Qp.dtype == torch.float64:
+            raise TypeError("maxsim_varlen gradients support fp16 / bf16 / fp32 inputs")
+        # the backward's grid over packed doc rows is sized by the longest doc
+        max_d = seqlen_max(cu_d) if max_seqlen_d is None else int(max_seqlen_d)
+        return _MaxSimVarlenFn.apply(Qp, Dp, cu_q, cu_d, int(max_seqlen_q), max_d)
     return packed_maxsim(Qp, Dp, cu_q, cu_d, int(max_seqlen_q), int(max_seqlen_d or 0))
 
 

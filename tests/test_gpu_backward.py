@@ -178,3 +178,90 @@ def test_pairs_kd_and_long_query_grads():
                torch.ones(3, 40, dtype=torch.bool, device="cuda"), True).sum().backward()
     assert rel_err(_np(Q.grad), _np(Qr.grad)) < 1e-3
     assert rel_err(_np(D.grad), _np(Dr.grad)) < 1e-3
+
+
+def _varlen_ref(Qp, Dp, cu_q, cu_d):
+    """fp32 autograd loop: scores[i, j] = sum_s max_t <Q_i[s], D_j[t]>, empty -> 0 (reference.py:213-245)."""
+    Nq, Nd = len(cu_q) - 1, len(cu_d) - 1
+    rows = []
+    for i in range(Nq):
+        Qi = Qp[cu_q[i] : cu_q[i + 1]]
+        cols = []
+        for j in range(Nd):
+            Dj = Dp[cu_d[j] : cu_d[j + 1]]
+            if Qi.shape[0] == 0 or Dj.shape[0] == 0:
+                cols.append(Qp.sum() * 0)
+            else:
+                cols.append((Qi @ Dj.T).max(-1).values.sum())
+        rows.append(torch.stack(cols))
+    return torch.stack(rows)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-3), (torch.bfloat16, 2e-2)])
+def test_varlen_grads(dtype, tol):
+    from late_interaction_kernels import maxsim_varlen
+
+    _case(f"varlen grads {dtype}")
+    g = torch.Generator().manual_seed(9)
+    # short docs (several per 32-row block), an empty doc, docs spanning blocks, an empty query
+    ld = torch.tensor([3, 1, 0, 70, 5, 2, 33, 1, 64, 4, 9, 31])
+    lq = torch.tensor([7, 0, 32, 19, 40])
+    cu_d = torch.cat([torch.zeros(1, dtype=torch.long), ld.cumsum(0)]).to(torch.int32)
+    cu_q = torch.cat([torch.zeros(1, dtype=torch.long), lq.cumsum(0)]).to(torch.int32)
+    Q = torch.randn(int(lq.sum()), 96, generator=g).to(dtype)
+    D = torch.randn(int(ld.sum()), 96, generator=g).to(dtype)
+    G = torch.randn(len(lq), len(ld), generator=g)
+    Qc = Q.cuda().requires_grad_()
+    Dc = D.cuda().requires_grad_()
+    s = maxsim_varlen(Qc, Dc, cu_q.cuda(), cu_d.cuda())
+    (s * G.cuda()).sum().backward()
+    Qr = Q.float().cuda().requires_grad_()
+    Dr = D.float().cuda().requires_grad_()
+    sr = _varlen_ref(Qr, Dr, cu_q.tolist(), cu_d.tolist())
+    (sr * G.cuda()).sum().backward()
+    assert Qc.grad.dtype == dtype and Dc.grad.dtype == dtype
+    assert rel_err(_np(s), _np(sr)) < tol
+    assert rel_err(_np(Qc.grad), _np(Qr.grad)) < tol
+    assert rel_err(_np(Dc.grad), _np(Dr.grad)) < tol
+    # inference path gives the same scores; a second backward is bitwise identical
+    with torch.no_grad():
+        s0 = maxsim_varlen(Q.cuda(), D.cuda(), cu_q.cuda(), cu_d.cuda())
+    assert torch.equal(s.detach(), s0)
+    g1 = (Qc.grad.clone(), Dc.grad.clone())
+    Qc.grad = None
+    Dc.grad = None
+    (maxsim_varlen(Qc, Dc, cu_q.cuda(), cu_d.cuda(), max_seqlen_q=40, max_seqlen_d=70) * G.cuda()).sum().backward()
+    assert torch.equal(Qc.grad, g1[0]) and torch.equal(Dc.grad, g1[1])
+
+
+def test_padded_grads():
+    from late_interaction_kernels import maxsim_padded
+
+    _case("maxsim_padded grads")
+    g = torch.Generator().manual_seed(12)
+    B, C, Lq, Ld, d = 4, 3, 20, 30, 64
+    Q = torch.randn(B, Lq, d, generator=g)
+    D = torch.randn(B, C, Ld, d, generator=g)
+    ql = torch.tensor([20, 5, 0, 13])
+    dl = torch.randint(0, Ld + 1, (B, C), generator=g)
+    dl[0, 0] = 0
+    dl[1, 2] = Ld
+    Qc = Q.cuda().requires_grad_()
+    Dc = D.cuda().requires_grad_()
+    s = maxsim_padded(Qc, Dc, ql.cuda(), dl.cuda())
+    G = torch.randn(B, C, generator=g).cuda()
+    (s * G).sum().backward()
+    Qr = Q.cuda().requires_grad_()
+    Dr = D.cuda().requires_grad_()
+    ref = []
+    for b in range(B):
+        row = []
+        for c in range(C):
+            qi, dj = Qr[b, : ql[b]], Dr[b, c, : dl[b, c]]
+            row.append((qi @ dj.T).max(-1).values.sum() if len(qi) and len(dj) else Qr.sum() * 0)
+        ref.append(torch.stack(row))
+    sr = torch.stack(ref)
+    (sr * G).sum().backward()
+    assert rel_err(_np(s), _np(sr)) < 1e-4
+    assert rel_err(_np(Qc.grad), _np(Qr.grad)) < 1e-3
+    assert rel_err(_np(Dc.grad), _np(Dr.grad)) < 1e-3

@@ -140,6 +140,33 @@ int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pa
                      lik_stream_t stream);
 
 /*
+ * Training forward of pair-list scoring: lik_maxsim_pairs that also writes
+ * argmax[p * Q->len + s] (winning doc-token index of query token s in pair
+ * p, ties to the lowest index, -1 where the pair has no valid doc token).
+ * bf16 / f16 / f32. Replaces score_pairs.py:_scatter_forward(save_argmax=True).
+ */
+int lik_maxsim_pairs_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q,
+                            const int32_t* pair_d, int64_t num_pairs, uint32_t flags, float* out,
+                            int32_t* argmax, lik_stream_t stream);
+
+/*
+ * Backward of pair-list scoring: grad[p] = dL/dout[p] (fp32) and the argmax
+ * of lik_maxsim_pairs_argmax give grad_q and grad_d laid out like Q and D
+ * (padded [n, len, dim] or packed [rows, dim], contiguous, input dtype;
+ * grad_d may be null). Pairs with an out-of-range index contribute nothing.
+ * No normalise, no KD flag. Needs lik_maxsim_pairs_backward_workspace_size()
+ * bytes of workspace (each query's and each doc's pair list, built on the
+ * device with a stable radix sort). Deterministic, no atomics.
+ * Replaces score_pairs.py:344-420 (_MaxSimScorePairsFn.backward and its
+ * grad kernels).
+ */
+int lik_maxsim_pairs_backward(const float* grad, const lik_seqs_t* Q, const lik_seqs_t* D,
+                              const int32_t* pair_q, const int32_t* pair_d, int64_t num_pairs,
+                              const int32_t* argmax, uint32_t flags, void* grad_q, void* grad_d,
+                              void* workspace, size_t workspace_bytes, lik_stream_t stream);
+size_t lik_maxsim_pairs_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, int64_t num_pairs);
+
+/*
  * PLAID compressed documents: token t of doc j has centroid code
  * codes[tok] and packed residual bytes residuals[tok*res_stride + 0..packed_dim),
  * tok = cu_seqlens[j] + t (packed) or j*codes_stride_n + t (padded, with

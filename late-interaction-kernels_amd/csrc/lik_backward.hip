@@ -23,8 +23,14 @@
 //   span several docs; it scans each of them in doc order.
 // Packed queries: the wave of (i, s) exits when s is past query i's length;
 // rows are addressed through cu_q (reference varlen.py:143-263).
+// Pair lists (reference score_pairs.py:344-420): the score units are pairs p =
+// (pair_q[p], pair_d[p]) instead of the (i, j) grid. The host builds, with a
+// stable radix sort, each query's and each doc's pair list in increasing p;
+// grad_q walks query i's list, grad_d doc j's list, so the order is fixed.
 // Both apply the normalisation Jacobian to the finished row in registers.
 #include "lik_common.h"
+
+#include <hipcub/hipcub.hpp>
 
 namespace lik {
 
@@ -62,6 +68,13 @@ struct BwdParams {
   char* gd;           // [Nd, Ld, dim] (packed: [rows, dim]) in the input dtype
   int64_t nq, lq, nd, ld;  // lq / ld: padded lengths, or the longest sequence when packed
   int64_t ndoc_pg;    // docs per query: Nd (cross product) or K (KD layout)
+  // pair lists (null outside pair mode): grad / argmax rows are indexed by pair
+  const int32_t* pair_q;
+  const int32_t* pair_d;
+  const int32_t* q_ptr;   // [nq + 1] offsets into q_list
+  const int32_t* q_list;  // pairs grouped by query, increasing within a query
+  const int32_t* d_ptr;   // [nd + 1]
+  const int32_t* d_list;
   int kd;
   int dim;
 };
@@ -110,24 +123,40 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
     qr = q0 + s;
   }
   const int64_t j0 = bp.kd ? i * bp.ndoc_pg : 0;
-  const int32_t* am = bp.amax + (i * bp.ndoc_pg) * bp.lq + s;
-  const float* g = bp.grad + i * bp.ld_g;
+  // units of query i: docs jl < ndoc_pg, or its pairs q_list[u0 .. u0 + nu)
+  int64_t nu = bp.ndoc_pg, u0 = 0;
+  if (bp.q_ptr) {
+    u0 = bp.q_ptr[i];
+    nu = (int64_t)bp.q_ptr[i + 1] - u0;
+  }
   float acc[DPL];
 #pragma unroll
   for (int k = 0; k < DPL; ++k) acc[k] = 0.f;
-  for (int64_t c0 = 0; c0 < bp.ndoc_pg; c0 += 64) {
+  for (int64_t c0 = 0; c0 < nu; c0 += 64) {
     const int64_t jl = c0 + lane;
-    const int av = jl < bp.ndoc_pg ? am[jl * bp.lq] : -1;
-    const float gv = jl < bp.ndoc_pg ? g[jl] : 0.f;
+    int av = -1, jd = 0;
+    float gv = 0.f;
+    if (jl < nu) {
+      if (bp.q_ptr) {
+        const int64_t pr = bp.q_list[u0 + jl];
+        av = bp.amax[pr * bp.lq + s];
+        gv = bp.grad[pr];
+        jd = bp.pair_d[pr];
+      } else {
+        av = bp.amax[(i * bp.ndoc_pg + jl) * bp.lq + s];
+        gv = bp.grad[i * bp.ld_g + jl];
+        jd = (int)(j0 + jl);
+      }
+    }
     float sv = gv;
-    if (bp.dinv && av >= 0) sv *= bp.dinv[(j0 + jl) * bp.ld + av];  // dinv only for padded docs
+    if (bp.dinv && av >= 0) sv *= bp.dinv[(int64_t)jd * bp.ld + av];  // dinv only for padded docs
     uint64_t bal = __ballot(av >= 0 && gv != 0.f);
     while (bal) {
       const int l = __builtin_ctzll(bal);
       bal &= bal - 1;
       const int a = __builtin_amdgcn_readlane(av, l);
       const float sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), l));
-      const int64_t jg = j0 + c0 + l;
+      const int64_t jg = __builtin_amdgcn_readlane(jd, l);
       const char* row = bp.d_cu ? bp.d + ((int64_t)bp.d_cu[jg] + a) * bp.d_sl : bp.d + jg * bp.d_sn + (int64_t)a * bp.d_sl;
 #pragma unroll
       for (int k = 0; k < DPL; ++k) {
@@ -176,13 +205,28 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
   // Add the contributions of doc j whose winner a lies in [wlo, wlo + n) to
   // accumulator rows off + (a - wlo).
   auto scan_doc = [&](int64_t j, int64_t wlo, int n, int off) {
+    // units of doc j: queries i (grid / KD), or its pairs d_list[u_begin .. u_end)
     const int64_t jl = bp.kd ? j % bp.ndoc_pg : j;
-    const int64_t i_begin = bp.kd ? j / bp.ndoc_pg : 0;
-    const int64_t i_end = bp.kd ? i_begin + 1 : bp.nq;
-    for (int64_t i = i_begin; i < i_end; ++i) {
-      const float gij = bp.grad[i * bp.ld_g + jl];
+    int64_t u_begin = bp.kd ? j / bp.ndoc_pg : 0;
+    int64_t u_end = bp.kd ? u_begin + 1 : bp.nq;
+    if (bp.d_ptr) {
+      u_begin = bp.d_ptr[j];
+      u_end = bp.d_ptr[j + 1];
+    }
+    for (int64_t u = u_begin; u < u_end; ++u) {
+      int64_t i, arow;
+      float gij;
+      if (bp.d_ptr) {
+        arow = bp.d_list[u];
+        i = bp.pair_q[arow];
+        gij = bp.grad[arow];
+      } else {
+        i = u;
+        arow = i * bp.ndoc_pg + jl;
+        gij = bp.grad[i * bp.ld_g + jl];
+      }
       if (gij == 0.f) continue;
-      const int32_t* am = bp.amax + (i * bp.ndoc_pg + jl) * bp.lq;
+      const int32_t* am = bp.amax + arow * bp.lq;
       int64_t qlen = bp.lq, qbase = 0;
       if (bp.q_cu) {
         qbase = bp.q_cu[i];
@@ -320,6 +364,68 @@ int launch_invnorm(const char* x, int64_t sn, int64_t sl, int64_t n, int64_t L, 
 
 int elem_size(int dt) { return dt == LIK_F32 ? 4 : 2; }
 
+// Sort keys of the pair lists: key = owner (query or doc) index, or n (sorted
+// last, in no list) for a pair with an out-of-range index; vals = pair index.
+__global__ void __launch_bounds__(256) pair_keys_kernel(const int32_t* pair_q, const int32_t* pair_d, int64_t np,
+                                                        int64_t nq, int64_t nd, int32_t* kq, int32_t* kd,
+                                                        int32_t* iota) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= np) return;
+  const int32_t q = pair_q[p], d = pair_d[p];
+  const bool ok = q >= 0 && q < nq && d >= 0 && d < nd;
+  kq[p] = ok ? q : (int32_t)nq;
+  kd[p] = ok ? d : (int32_t)nd;
+  iota[p] = (int32_t)p;
+}
+
+// ptr[k] = first position of key >= k in the sorted keys, k = 0 .. n.
+__global__ void __launch_bounds__(256) bucket_ptr_kernel(const int32_t* sorted, int64_t np, int64_t n, int32_t* ptr) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k > n) return;
+  int64_t lo = 0, hi = np;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (sorted[mid] < k) lo = mid + 1;
+    else hi = mid;
+  }
+  ptr[k] = (int32_t)lo;
+}
+
+struct PairWs {
+  size_t kq, kd, iota, ks, qlist, dlist, qptr, dptr, temp, temp_bytes, total;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static int end_bit_for(int64_t n) {
+  int b = 1;
+  while (b < 31 && ((int64_t)1 << b) <= n) ++b;
+  return b;
+}
+
+static PairWs pair_ws_layout(int64_t np, int64_t nq, int64_t nd) {
+  PairWs w{};
+  size_t o = 0;
+  const size_t a = align256((size_t)np * 4);
+  w.kq = o; o += a;
+  w.kd = o; o += a;
+  w.iota = o; o += a;
+  w.ks = o; o += a;
+  w.qlist = o; o += a;
+  w.dlist = o; o += a;
+  w.qptr = o; o += align256((size_t)(nq + 1) * 4);
+  w.dptr = o; o += align256((size_t)(nd + 1) * 4);
+  size_t tb = 0;
+  hipcub::DeviceRadixSort::SortPairs(nullptr, tb, (const int32_t*)nullptr, (int32_t*)nullptr,
+                                     (const int32_t*)nullptr, (int32_t*)nullptr, (int)np, 0,
+                                     end_bit_for(nq > nd ? nq : nd));
+  w.temp = o;
+  w.temp_bytes = tb;
+  o += align256(tb);
+  w.total = o + 256;
+  return w;
+}
+
 }  // namespace lik
 
 using namespace lik;
@@ -328,6 +434,11 @@ extern "C" {
 
 static bool bwd_norm_q(uint32_t f) { return (f & (LIK_NORMALIZE | LIK_NORMALIZE_Q)) != 0; }
 static bool bwd_norm_d(uint32_t f) { return (f & (LIK_NORMALIZE | LIK_NORMALIZE_D)) != 0; }
+
+size_t lik_maxsim_pairs_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, int64_t num_pairs) {
+  if (!Q || !D || num_pairs <= 0 || Q->n < 0 || D->n < 0) return 0;
+  return pair_ws_layout(num_pairs, Q->n, D->n).total;
+}
 
 size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
   if (!Q || !D) return 0;
@@ -404,6 +515,84 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
     bp.dinv = wsf;
     if ((rc = invnorm(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, wsf)) != LIK_OK) return rc;
   }
+  switch (Q->dtype) {
+    case LIK_BF16: return launch_bwd_dpl<EK_BF16>(bp, s);
+    case LIK_F16: return launch_bwd_dpl<EK_F16>(bp, s);
+    default: return launch_bwd_dpl<EK_F32>(bp, s);
+  }
+}
+
+int lik_maxsim_pairs_backward(const float* grad, const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q,
+                              const int32_t* pair_d, int64_t num_pairs, const int32_t* argmax, uint32_t flags,
+                              void* grad_q, void* grad_d, void* workspace, size_t workspace_bytes,
+                              lik_stream_t stream) {
+  if (!Q || !D || num_pairs < 0) return LIK_ERR_INVALID;
+  if (Q->dtype != D->dtype || Q->dim != D->dim || Q->dim <= 0) return LIK_ERR_INVALID;
+  if (Q->dtype != LIK_BF16 && Q->dtype != LIK_F16 && Q->dtype != LIK_F32) return LIK_ERR_UNSUPPORTED;
+  if (Q->lengths || D->lengths || Q->token_scale || D->token_scale || D->mask) return LIK_ERR_UNSUPPORTED;
+  if (flags & (LIK_NORMALIZE | LIK_NORMALIZE_Q | LIK_NORMALIZE_D | LIK_KD_LAYOUT)) return LIK_ERR_UNSUPPORTED;
+  if (Q->dim > 512) return LIK_ERR_UNSUPPORTED;
+  if (Q->n < 0 || D->n < 0 || Q->len < 0 || D->len < 0) return LIK_ERR_INVALID;
+  if (num_pairs > 0x7fffffffLL || Q->n > 0x7ffffffeLL || D->n > 0x7ffffffeLL) return LIK_ERR_UNSUPPORTED;
+  if (num_pairs == 0 || Q->n == 0 || D->n == 0) return LIK_OK;
+  if (!grad || !pair_q || !pair_d || !argmax || !grad_q || !Q->data || !D->data) return LIK_ERR_INVALID;
+  const int eb = elem_size(Q->dtype);
+  if (((uintptr_t)Q->data) % 16 || ((uintptr_t)D->data) % 16 || (Q->dim * eb) % 16 || (Q->stride_l * eb) % 16 ||
+      (D->stride_l * eb) % 16 || (Q->stride_n * eb) % 16 || (D->stride_n * eb) % 16)
+    return LIK_ERR_UNSUPPORTED;
+  const PairWs w = pair_ws_layout(num_pairs, Q->n, D->n);
+  if (!workspace || workspace_bytes < w.total) return LIK_ERR_WORKSPACE;
+  char* ws = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  if ((size_t)(ws - (char*)workspace) + w.total - 256 > workspace_bytes) return LIK_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  auto I = [&](size_t off) { return (int32_t*)(ws + off); };
+  const unsigned pb = (unsigned)((num_pairs + 255) / 256);
+  hipLaunchKernelGGL(pair_keys_kernel, dim3(pb), dim3(256), 0, s, pair_q, pair_d, num_pairs, Q->n, D->n, I(w.kq),
+                     I(w.kd), I(w.iota));
+  if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+  const int eb_bits = end_bit_for(Q->n > D->n ? Q->n : D->n);
+  // stable LSD radix sort: pairs of one owner keep increasing pair order
+  struct Pass { size_t key, list, ptr; int64_t n; } passes[2] = {{w.kq, w.qlist, w.qptr, Q->n},
+                                                               {w.kd, w.dlist, w.dptr, D->n}};
+  for (const Pass& ps : passes) {
+    size_t tb = w.temp_bytes;
+    if (hipcub::DeviceRadixSort::SortPairs(ws + w.temp, tb, I(ps.key), I(w.ks), I(w.iota), I(ps.list),
+                                           (int)num_pairs, 0, eb_bits, s) != hipSuccess)
+      return LIK_ERR_LAUNCH;
+    hipLaunchKernelGGL(bucket_ptr_kernel, dim3((unsigned)((ps.n + 1 + 255) / 256)), dim3(256), 0, s, I(w.ks),
+                       num_pairs, ps.n, I(ps.ptr));
+    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+  }
+  BwdParams bp{};
+  bp.grad = grad;
+  bp.ld_g = 1;
+  bp.q = (const char*)Q->data;
+  bp.q_sn = Q->stride_n * eb;
+  bp.q_sl = Q->stride_l * eb;
+  bp.q_cu = Q->cu_seqlens;
+  bp.d = (const char*)D->data;
+  bp.d_sn = D->stride_n * eb;
+  bp.d_sl = D->stride_l * eb;
+  bp.d_cu = D->cu_seqlens;
+  bp.amax = argmax;
+  bp.qmask = Q->mask;
+  bp.qm_sn = Q->mask_stride_n;
+  bp.qm_sl = Q->mask_stride_l;
+  bp.gq = (char*)grad_q;
+  bp.gd = (char*)grad_d;
+  bp.nq = Q->n;
+  bp.lq = Q->len;
+  bp.nd = D->n;
+  bp.ld = D->len;
+  bp.kd = 0;
+  bp.ndoc_pg = 0;
+  bp.dim = Q->dim;
+  bp.pair_q = pair_q;
+  bp.pair_d = pair_d;
+  bp.q_ptr = I(w.qptr);
+  bp.q_list = I(w.qlist);
+  bp.d_ptr = I(w.dptr);
+  bp.d_list = I(w.dlist);
   switch (Q->dtype) {
     case LIK_BF16: return launch_bwd_dpl<EK_BF16>(bp, s);
     case LIK_F16: return launch_bwd_dpl<EK_F16>(bp, s);

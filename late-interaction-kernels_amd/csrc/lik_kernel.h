@@ -655,7 +655,8 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     const int sl = nend % NSLOT;
     if constexpr ((FEAT & F_ARGMAX) != 0) {
       // winner over lanes l, l^32 (larger value; equal values: lower index),
-      // written to argmax[(q * docs + j) * Lq + token]
+      // written to argmax[(q * docs + j) * Lq + token] (pair mode: unit g is
+      // the pair, one doc: argmax[pair * Lq + token])
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
         const auto sv = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
@@ -666,7 +667,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
         const int win = take1 ? i1 : i0;
         const int col = (wv * NSUB + sub) * 32 + l32;
         const int ul = col / p.LU;
-        if (h == 0 && p.amax && !p.pair_q && ul < p.QPG) {
+        if (h == 0 && p.amax && ul < p.QPG) {
           const int64_t u = g * p.QPG + ul;
           const int64_t q = u / p.nc;
           const int64_t tok = (u - q * p.nc) * p.LU + (col - ul * p.LU);

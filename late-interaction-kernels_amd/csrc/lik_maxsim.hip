@@ -492,8 +492,8 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
   return LIK_OK;
 }
 
-int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, const int32_t* pair_d,
-                     int64_t num_pairs, uint32_t flags, float* out, lik_stream_t stream) {
+static int pairs_impl(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, const int32_t* pair_d,
+                      int64_t num_pairs, uint32_t flags, float* out, int32_t* argmax, lik_stream_t stream) {
   int rc;
   if ((rc = check_seqs(Q)) != LIK_OK) return rc;
   if ((rc = check_seqs(D)) != LIK_OK) return rc;
@@ -502,9 +502,20 @@ int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pa
   if (D->mask || (flags & LIK_KD_LAYOUT)) return LIK_ERR_INVALID;
   if (num_pairs == 0) return LIK_OK;
   Plan pl;
-  if ((rc = make_plan(Q->dtype, Q->dim, 1, Q->len, true, pl)) != LIK_OK) return rc;
+  if ((rc = make_plan(Q->dtype, Q->dim, 1, Q->len, true, pl, argmax ? 4 : 1)) != LIK_OK) return rc;
   if (pl.nc != 1) return LIK_ERR_UNSUPPORTED;
+  hipStream_t s = (hipStream_t)stream;
   Params p{};
+  if (argmax) {
+    if (Q->dtype == LIK_FP8_E4M3 || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
+    const int64_t na = num_pairs * Q->len;  // pairs with no winner stay -1
+    if (na > 0) {
+      hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, s, argmax, na, -1);
+      if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+    }
+    p.amax = argmax;
+    p.amax_ld = Q->len;
+  }
   p.q = to_dev(*Q);
   p.d = to_dev(*D);
   p.normalize = norm_bits(flags);
@@ -523,7 +534,18 @@ int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pa
   p.out = out;
   p.osq = 1;
   p.osd = 0;
-  return timed_launch((hipStream_t)stream, [&] { return launch_dense(Q->dtype, pl, p, num_pairs, (hipStream_t)stream); });
+  return timed_launch(s, [&] { return launch_dense(Q->dtype, pl, p, num_pairs, s); });
+}
+
+int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, const int32_t* pair_d,
+                     int64_t num_pairs, uint32_t flags, float* out, lik_stream_t stream) {
+  return pairs_impl(Q, D, pair_q, pair_d, num_pairs, flags, out, nullptr, stream);
+}
+
+int lik_maxsim_pairs_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, const int32_t* pair_d,
+                            int64_t num_pairs, uint32_t flags, float* out, int32_t* argmax, lik_stream_t stream) {
+  if (num_pairs > 0 && !argmax) return LIK_ERR_INVALID;
+  return pairs_impl(Q, D, pair_q, pair_d, num_pairs, flags, out, argmax, stream);
 }
 
 int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t flags, float* out,

@@ -300,6 +300,48 @@ def pairs_maxsim(
     return out
 
 
+def pairs_maxsim_train(Q_packed, D_packed, cu_q, cu_d, pair_q, pair_d, max_q: int, max_d: int):
+    """Pair-list training forward: ``(scores [P], argmax [P, max_q], Qp, Dp)``."""
+    _lib.require_gpu(Q_packed, D_packed, cu_q, cu_d, pair_q, pair_d)
+    P = pair_q.numel()
+    out = torch.zeros(P, device=Q_packed.device, dtype=torch.float32)
+    argmax = torch.full((P, max(max_q, 0)), -1, device=Q_packed.device, dtype=torch.int32)
+    Qp = _lib.prepare_tokens(Q_packed.detach())
+    Dp = _lib.prepare_tokens(D_packed.detach())
+    if P == 0 or max_q <= 0 or Q_packed.shape[0] == 0 or D_packed.shape[0] == 0:
+        return out, argmax, Qp, Dp
+    qs = _lib.seqs(Qp, n=cu_q.numel() - 1, length=max_q, stride_l=Qp.stride(0), cu=cu_q)
+    ds = _lib.seqs(Dp, n=cu_d.numel() - 1, length=max(int(max_d), 0), stride_l=Dp.stride(0), cu=cu_d)
+    lib = _lib.load()
+    with torch.cuda.device(Q_packed.device):
+        rc = lib.lik_maxsim_pairs_argmax(ctypes.byref(qs), ctypes.byref(ds), pair_q.data_ptr(), pair_d.data_ptr(), P,
+                                         0, out.data_ptr(), argmax.data_ptr(), _lib.stream_of(out))
+    _lib.check(rc, "lik_maxsim_pairs_argmax")
+    return out, argmax, Qp, Dp
+
+
+def pairs_backward(grad, Qp, Dp, cu_q, cu_d, pair_q, pair_d, argmax, max_q: int, max_d: int, *,
+                   need_d: bool = True):
+    """Gradients of pair-list MaxSim: ``(grad_Q [rows_q, dp], grad_D [rows_d, dp] or None)``."""
+    P = pair_q.numel()
+    gq = torch.zeros_like(Qp)
+    gd = torch.zeros_like(Dp) if need_d else None
+    if P == 0 or max_q <= 0 or Qp.shape[0] == 0 or Dp.shape[0] == 0:
+        return gq, gd
+    g = grad.to(torch.float32).contiguous()
+    qs = _lib.seqs(Qp, n=cu_q.numel() - 1, length=max_q, stride_l=Qp.stride(0), cu=cu_q)
+    ds = _lib.seqs(Dp, n=cu_d.numel() - 1, length=max(int(max_d), 0), stride_l=Dp.stride(0), cu=cu_d)
+    lib = _lib.load()
+    nbytes = lib.lik_maxsim_pairs_backward_workspace_size(ctypes.byref(qs), ctypes.byref(ds), P)
+    ws = _lib.workspace(nbytes, Qp.device)
+    with torch.cuda.device(Qp.device):
+        rc = lib.lik_maxsim_pairs_backward(g.data_ptr(), ctypes.byref(qs), ctypes.byref(ds), pair_q.data_ptr(),
+                                           pair_d.data_ptr(), P, argmax.data_ptr(), 0, gq.data_ptr(), _lib.ptr(gd),
+                                           _lib.ptr(ws), nbytes, _lib.stream_of(gq))
+    _lib.check(rc, "lik_maxsim_pairs_backward")
+    return gq, gd
+
+
 def seqlen_max(cu: torch.Tensor) -> int:
     """Longest sequence in ``cu_seqlens`` (one device->host sync)."""
     if cu.numel() <= 1:

@@ -48,6 +48,9 @@ EXPORTED_SYMBOLS = (
     "lik_maxsim_backward",
     "lik_maxsim_backward_workspace_size",
     "lik_maxsim_pairs",
+    "lik_maxsim_pairs_argmax",
+    "lik_maxsim_pairs_backward",
+    "lik_maxsim_pairs_backward_workspace_size",
     "lik_plaid_maxsim",
     "lik_plaid_decode",
     "lik_plaid_approx_score",
@@ -143,6 +146,13 @@ def load() -> ctypes.CDLL:
     lib.lik_maxsim_backward_workspace_size.restype = ctypes.c_size_t
     lib.lik_maxsim_pairs.argtypes = [P(LikSeqs), P(LikSeqs), _p, _p, _i64, ctypes.c_uint32, _p, _p]
     lib.lik_maxsim_pairs.restype = ctypes.c_int
+    lib.lik_maxsim_pairs_argmax.argtypes = [P(LikSeqs), P(LikSeqs), _p, _p, _i64, ctypes.c_uint32, _p, _p, _p]
+    lib.lik_maxsim_pairs_argmax.restype = ctypes.c_int
+    lib.lik_maxsim_pairs_backward.argtypes = [_p, P(LikSeqs), P(LikSeqs), _p, _p, _i64, _p, ctypes.c_uint32, _p, _p,
+                                              _p, ctypes.c_size_t, _p]
+    lib.lik_maxsim_pairs_backward.restype = ctypes.c_int
+    lib.lik_maxsim_pairs_backward_workspace_size.argtypes = [P(LikSeqs), P(LikSeqs), _i64]
+    lib.lik_maxsim_pairs_backward_workspace_size.restype = ctypes.c_size_t
     lib.lik_plaid_maxsim.argtypes = [P(LikSeqs), P(LikPlaidDocs), ctypes.c_uint32, _p, _i64, _i64, _p]
     lib.lik_plaid_maxsim.restype = ctypes.c_int
     lib.lik_plaid_decode.argtypes = [P(LikPlaidDocs), _i64, _i64, ctypes.c_uint32, _i32, _p, _i64, _p]

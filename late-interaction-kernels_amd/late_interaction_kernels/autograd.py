@@ -61,16 +61,6 @@ def _maybe_warn_unnormalized(Q: torch.Tensor) -> None:
         )
 
 
-def _no_grad_guard(*ts: torch.Tensor) -> None:
-    """Packed / padded entry points are inference-only in this build."""
-    if torch.is_grad_enabled() and any(t.requires_grad for t in ts):
-        raise NotImplementedError(
-            "late_interaction_kernels (MI355X build): gradients are implemented for maxsim / "
-            "maxsim_pairs (incl. KD layout); this packed entry point is inference-only. Call under "
-            "torch.no_grad() / inference_mode() or use maxsim on padded tensors."
-        )
-
-
 def _needs_grad(*ts: torch.Tensor) -> bool:
     return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
 

@@ -265,3 +265,44 @@ def test_padded_grads():
     assert rel_err(_np(s), _np(sr)) < 1e-4
     assert rel_err(_np(Qc.grad), _np(Qr.grad)) < 1e-3
     assert rel_err(_np(Dc.grad), _np(Dr.grad)) < 1e-3
+
+
+def test_score_pairs_grads():
+    from late_interaction_kernels.score_pairs import score_pairs_packed
+
+    _case("score_pairs grads")
+    g = torch.Generator().manual_seed(21)
+    lq = torch.tensor([12, 0, 30, 7, 25, 3])
+    ld = torch.tensor([40, 2, 0, 17, 33, 5, 64, 1])
+    cu_q = torch.cat([torch.zeros(1, dtype=torch.long), lq.cumsum(0)]).to(torch.int32)
+    cu_d = torch.cat([torch.zeros(1, dtype=torch.long), ld.cumsum(0)]).to(torch.int32)
+    # duplicates, a query in many pairs, a doc in many pairs, an out-of-range pair
+    pq = torch.tensor([0, 2, 2, 3, 4, 4, 4, 5, 1, 2, 0, 3, 2, 4, 9])
+    pd = torch.tensor([0, 3, 3, 6, 1, 6, 4, 7, 0, 2, 6, 6, 6, 5, 0])
+    Q = torch.randn(int(lq.sum()), 64, generator=g)
+    D = torch.randn(int(ld.sum()), 64, generator=g)
+    G = torch.randn(len(pq), generator=g).cuda()
+    Qc = Q.cuda().requires_grad_()
+    Dc = D.cuda().requires_grad_()
+    s = score_pairs_packed(Qc, Dc, cu_q.cuda(), cu_d.cuda(), pq.cuda(), pd.cuda())
+    (s * G).sum().backward()
+    Qr = Q.cuda().requires_grad_()
+    Dr = D.cuda().requires_grad_()
+    ref = []
+    for a, b in zip(pq.tolist(), pd.tolist()):
+        if a >= len(lq) or b >= len(ld) or lq[a] == 0 or ld[b] == 0:
+            ref.append(Qr.sum() * 0)
+            continue
+        qi = Qr[cu_q[a] : cu_q[a + 1]]
+        dj = Dr[cu_d[b] : cu_d[b + 1]]
+        ref.append((qi @ dj.T).max(-1).values.sum())
+    sr = torch.stack(ref)
+    (sr * G).sum().backward()
+    assert rel_err(_np(s), _np(sr)) < 1e-4
+    assert rel_err(_np(Qc.grad), _np(Qr.grad)) < 1e-3
+    assert rel_err(_np(Dc.grad), _np(Dr.grad)) < 1e-3
+    g1 = (Qc.grad.clone(), Dc.grad.clone())
+    Qc.grad = None
+    Dc.grad = None
+    (score_pairs_packed(Qc, Dc, cu_q.cuda(), cu_d.cuda(), pq.cuda(), pd.cuda()) * G).sum().backward()
+    assert torch.equal(Qc.grad, g1[0]) and torch.equal(Dc.grad, g1[1])

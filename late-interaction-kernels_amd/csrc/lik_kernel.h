@@ -47,8 +47,21 @@ constexpr int kRMax = 512;  // docs per workgroup (host caps R)
 // F_ARGMAX (training forward): also write each (query token, doc) winner's doc-token index.
 enum { F_MASK = 1, F_TS = 2, F_NORM = 4, F_CU = 8, F_ALL = 15, F_ARGMAX = 16 };
 
+// Four-wave workgroups of 4 column blocks per wave (dense bf16 / fp16
+// scoring without masks, normalisation or argmax, which would not fit) are
+// held to 256 registers so that two workgroups share each CU: their
+// barriers are independent, so one workgroup's per-tile bookkeeping and
+// barrier wait are covered by the other's MFMAs.
+template <int EK, int W, int NSUB, int SRC, int FEAT>
+constexpr bool two_wg_per_cu() {
+  return W == 4 && NSUB == 4 && SRC == SRC_DENSE && (EK == EK_BF16 || EK == EK_F16) &&
+         (FEAT & (F_ARGMAX | F_NORM | F_TS | F_MASK)) == 0;
+}
+
 template <int EK, int DPAD, int W, int NSUB, int SRC, int CD, int FEAT>
-__global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
+__global__ void __launch_bounds__(W * 64)
+    __attribute__((amdgpu_waves_per_eu(two_wg_per_cu<EK, W, NSUB, SRC, FEAT>() ? 2 : 1)))
+    maxsim_kernel(const Params p) {
   using T = KT<EK, DPAD>;
   constexpr int NT = W * 64;
   constexpr int COLS = W * NSUB * 32;
@@ -191,7 +204,11 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   // ---------------- query block -> B fragments in VGPRs ----------------
   u32x4 bq[NSUB][KS][FV];
   u32x4 bql[T::SPLIT ? NSUB : 1][T::SPLIT ? KS : 1];
-  float qsc[NSUB];
+  // Per-column query scale (normalise, fp8 token scales). Padding and masked
+  // query columns have zero fragments, so their maxima are 0 (or non-finite,
+  // which scores 0) without a scale: kernels with neither feature keep none.
+  constexpr bool kQsc = SRC == SRC_PLAID || (FEAT & (F_NORM | F_TS)) != 0;
+  float qsc[kQsc ? NSUB : 1];
 #pragma unroll
   for (int sub = 0; sub < NSUB; ++sub) {
     const int col = (wv * NSUB + sub) * 32 + l32;
@@ -241,7 +258,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     ss += __shfl_xor(ss, 32);
     float sc = f_norm_q ? inv_norm(ss) : 1.f;
     if (valid && p.q.ts) sc *= p.q.ts[q * p.q.tsn + tok * p.q.tsl];
-    qsc[sub] = valid ? sc : 0.f;
+    if constexpr (kQsc) qsc[sub] = valid ? sc : 0.f;
   }
 
 
@@ -503,14 +520,20 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
 
   // ---------------- compute pieces ----------------
   // Accumulators: set P holds tile i (MFMA in flight), set 1-P holds tile i-1
-  // (epilogue), so one wave overlaps tile i's MFMAs with tile i-1's max. Row
-  // masking is folded into the MFMA C operand: the first k-step of a tile
-  // adds `bias` (0 for valid rows, -inf for rows past the doc end or
-  // dropped by the mask), so the epilogue is a plain running max.
+  // (epilogue), so one wave overlaps tile i's MFMAs with tile i-1's max.
   // Two accumulator sets unless they do not fit in 256 registers next to the
-  // query fragments (8 waves x 4 blocks): then one set, the epilogue runs
-  // before the tile's MFMAs and the SIMD's second wave covers the gap.
-  constexpr int NACC = (W == 8 && NSUB >= 4) ? 1 : 2;
+  // query fragments (4 blocks per wave with two waves per SIMD): then one
+  // set, the epilogue runs before the tile's MFMAs and the SIMD's other
+  // wave covers the gap.
+  constexpr bool kTwoWg = two_wg_per_cu<EK, W, NSUB, SRC, FEAT>();
+  constexpr int NACC = ((W == 8 && NSUB >= 4) || kTwoWg) ? 1 : 2;
+  // Row masking. With two sets it is folded into the MFMA C operand: the
+  // first k-step of a tile adds `bias` (0 for valid rows, -inf for rows past
+  // the doc end or dropped by the mask), so the epilogue is a plain running
+  // max. In the 256-register two-workgroup kernel the 16 bias registers do
+  // not fit: tiles start from 0 and the epilogue sets invalid rows to -inf,
+  // in partial tiles only.
+  constexpr bool kBiasC = !kTwoWg;
   f32x16 acc[NACC][NSUB];
   float m[NSUB];
   int mi[NSUB];  // F_ARGMAX: doc-token index of m (-1: no valid token yet)
@@ -525,6 +548,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
 #pragma unroll
   for (int e = 0; e < 16; ++e) bias[e] = 0.f;
   uint32_t bias_bits = 0xffffffffu;
+  uint32_t vb_cur = 0xffffffffu, vb_prev = 0xffffffffu;  // row-valid bits of tiles i, i-1 (no bias)
   // accumulator element e of lane (h, l32) is doc row 8*(e/4) + 4*h + e%4
   auto set_bias = [&](uint32_t vb) {
 #pragma unroll
@@ -536,7 +560,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   // LDS one iteration ahead of their MFMAs into register set S. For large
   // embedding dims the two sets would not fit next to the query fragments,
   // so the MFMA loop reads them from the tile's LDS buffer instead.
-  constexpr bool kPrefetchA = KS * FV <= 8;
+  constexpr bool kPrefetchA = KS * FV <= 8 && !kTwoWg;
   u32x4 af[kPrefetchA ? 2 : 1][KS][FV];
   u32x4 afl[kPrefetchA ? 2 : 1][T::SPLIT ? KS : 1];
   auto load_a = [&](auto SS, int buf) {
@@ -564,7 +588,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
       }
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
-        f32x16 c = ks == 0 ? bias : acc[P][sub];
+        f32x16 c = ks == 0 ? (kBiasC ? bias : f32x16{}) : acc[P][sub];
         c = mfma32<EK>(c, af[S][ks], bq[sub][ks]);
         if constexpr (T::SPLIT) {
           c = mfma32<EK>(c, af[S][ks], &bql[sub][ks]);
@@ -611,6 +635,17 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
   // whose first row is doc token `row0`.
   auto epilogue = [&](auto PP, int rslot, int row0) {
     constexpr int P = NACC == 2 ? decltype(PP)::value : 0;
+    if constexpr (!kBiasC) {
+      // rows of tile i-1 that are not valid: -inf before the max
+      if (vb_prev != 0xffffffffu) {
+        const uint32_t vh = vb_prev >> (4 * h);
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (!((vh >> (8 * (e >> 2) + (e & 3))) & 1u)) acc[P][sub][e] = NEG_INF;
+      }
+    }
     if constexpr ((FEAT & F_ARGMAX) != 0) {
       // rows are visited in increasing index order and only a strictly larger
       // value replaces the winner: ties keep the lowest doc-token index
@@ -681,7 +716,7 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
     for (int sub = 0; sub < NSUB; ++sub) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
       const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over lanes l, l^32
-      if (h == 0) s_colb[sl][(wv * NSUB + sub) * 32 + l32] = __builtin_isfinite(mm) ? mm * qsc[sub] : 0.f;
+      if (h == 0) s_colb[sl][(wv * NSUB + sub) * 32 + l32] = __builtin_isfinite(mm) ? (kQsc ? mm * qsc[kQsc ? sub : 0] : mm) : 0.f;
       m[sub] = NEG_INF;
     }
     if (tid == 0) s_slotk[sl] = k;
@@ -764,7 +799,12 @@ __global__ void __launch_bounds__(W * 64) maxsim_kernel(const Params p) {
         if (q0.holes) vb &= vw0;
       }
       vb = __builtin_amdgcn_readfirstlane(vb);
-      if (vb != bias_bits) set_bias(vb);
+      if constexpr (kBiasC) {
+        if (vb != bias_bits) set_bias(vb);
+      } else {
+        vb_prev = vb_cur;
+        vb_cur = vb;
+      }
     }
     // one block: MFMA tile i, read A of tile i+1, max of tile i-1, commit
     // tile i+2, fetch tile i+4

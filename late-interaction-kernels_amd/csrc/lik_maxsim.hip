@@ -178,7 +178,8 @@ int check_seqs(const lik_seqs_t* s) {
 // Choose the column block, Lq chunking and grouping for `nq` queries of
 // (max) length `lq`. `one_query_per_group` is true when each query owns its
 // documents (KD / pairs).
-int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group, Plan& pl, int min_w = 1) {
+int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group, Plan& pl, int min_w = 1,
+              bool prefer_two_wg = false) {
   pl.dpad = pick_dpad(dt, dim);
   if (pl.dpad < 0) return LIK_ERR_UNSUPPORTED;
   const int nsmax = max_nsub(dt, pl.dpad);
@@ -200,6 +201,13 @@ int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group,
   if (best < 0) return LIK_ERR_UNSUPPORTED;
   pl.W = kCfgs[best].W;
   pl.NSUB = kCfgs[best].NSUB;
+  // Dense bf16 / fp16 scoring: the equally wide 4 x 4 block runs two
+  // workgroups per CU (the kernel caps it at 256 registers), which measures
+  // faster than one 8-wave workgroup.
+  if (prefer_two_wg && pl.W == 8 && pl.NSUB == 2 && nsmax >= 4 && min_w <= 4 && (dt == LIK_BF16 || dt == LIK_F16)) {
+    pl.W = 4;
+    pl.NSUB = 4;
+  }
   // LIK_CFG="W,NSUB" forces a column-block configuration (tuning aid).
   if (const char* e = getenv("LIK_CFG")) {
     int w = 0, ns = 0;
@@ -371,7 +379,7 @@ size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint3
   size_t total = 0;
   for (int min_w : {1, 4}) {
     Plan pl;
-    if (make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w) != LIK_OK) return 0;
+    if (make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, norm_bits(flags) == 0) != LIK_OK) return 0;
     const size_t t = ws_layout(Q, D, flags, pl).total;
     total = t > total ? t : total;
   }
@@ -414,7 +422,8 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
   // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: spread
   // it over at least 4 waves even when the query block fits one wave's columns
   const int min_w = ((norm_bits(flags) & 2) || argmax) ? 4 : 1;
-  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w)) != LIK_OK) return rc;
+  const bool two_wg = argmax == nullptr && norm_bits(flags) == 0 && !Q->token_scale && !D->token_scale;
+  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, two_wg)) != LIK_OK) return rc;
   const WsLayout wl = ws_layout(Q, D, flags, pl);
   if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return LIK_ERR_WORKSPACE;
 

@@ -170,7 +170,7 @@ __global__ void __launch_bounds__(W * 64)
     s_dlen[k] = skip ? 0 : ((int32_t)L | (holes ? (int32_t)0x80000000 : 0));
     if (L == 0 && !skip) {
       for (int t = 0; t < p.QPG; ++t)
-        if (float* o = s_outp[t]) o[k * p.osd] = 0.f;
+        if (float* o = s_outp[t]) ((__attribute__((address_space(1))) float*)o)[k * p.osd] = 0.f;
     }
   }
   __syncthreads();
@@ -317,7 +317,13 @@ __global__ void __launch_bounds__(W * 64)
   };
 
   // ---------------- staging: fetch (global -> VGPR ring) and commit (-> LDS) ----------------
-  u32x4 st[2][NCH][NCV];
+  // Staging registers of fetched tiles. Two slots (tile i+4 is fetched while
+  // tile i+3's data is in flight) unless registers are capped at 256 for two
+  // workgroups per CU: then one slot, tile i+3 fetched after tile i+2 is
+  // committed (the other workgroup covers the shorter load lead).
+  constexpr bool kTwoWg = two_wg_per_cu<EK, W, NSUB, SRC, FEAT>();
+  constexpr bool kOneSlot = kTwoWg;
+  u32x4 st[kOneSlot ? 1 : 2][NCH][NCV];
   uint32_t sm[SRC == SRC_DENSE ? 2 : 1];          // dense + mask: the tile's row-validity word
   float sts[SRC == SRC_DENSE ? 2 : 1][NCH];       // dense fp8: token scale per row
   uint32_t sb0[SRC == SRC_PLAID ? 2 : 1][NCH];    // PLAID: residual bits (low)
@@ -362,7 +368,7 @@ __global__ void __launch_bounds__(W * 64)
   // the doc end and padding chunks are out of range and read as 0).
   auto fetch_dense = [&](auto SS, const Cur& c, const Desc& d) {
     if constexpr (SRC == SRC_DENSE) {
-      constexpr int S = decltype(SS)::value;
+      constexpr int S = kOneSlot ? 0 : decltype(SS)::value;
       // one doc spans < 4 GiB (checked on the host), so 32-bit math is exact
       const uint32_t span = (uint32_t)(c.len > 1 ? c.len - 1 : 0) * (uint32_t)p.d.sl_b + (uint32_t)(p.d.dim * T::IN_B);
       const __amdgpu_buffer_rsrc_t rd = make_rsrc(p.d.data + c.off, span);
@@ -434,7 +440,7 @@ __global__ void __launch_bounds__(W * 64)
   // to the MFMA type); PLAID rows are decoded, normalised and rounded. Rows
   // past the tile's valid ones are written as zeros.
   auto commit = [&](auto SS, const Desc& d, int buf, int rslot) {
-    constexpr int S = decltype(SS)::value;
+    constexpr int S = kOneSlot ? 0 : decltype(SS)::value;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int row = (tid + i * NT) / SCPR, cc = lcc[i];
@@ -525,7 +531,6 @@ __global__ void __launch_bounds__(W * 64)
   // query fragments (4 blocks per wave with two waves per SIMD): then one
   // set, the epilogue runs before the tile's MFMAs and the SIMD's other
   // wave covers the gap.
-  constexpr bool kTwoWg = two_wg_per_cu<EK, W, NSUB, SRC, FEAT>();
   constexpr int NACC = ((W == 8 && NSUB >= 4) || kTwoWg) ? 1 : 2;
   // Row masking. With two sets it is folded into the MFMA C operand: the
   // first k-step of a tile adds `bias` (0 for valid rows, -inf for rows past
@@ -578,6 +583,25 @@ __global__ void __launch_bounds__(W * 64)
     constexpr int P = NACC == 2 ? decltype(PP)::value : 0;
     constexpr int S = kPrefetchA ? decltype(SS)::value : 0;
     const char* A = s_tile[buf][0] + l32 * T::ROW_B + h * T::HALF_B;
+    if constexpr (kTwoWg) {
+      // A fragments from LDS inside the tile, two k-steps ahead of their
+      // MFMAs (three rotating registers). The fences keep LDS reads and
+      // MFMAs in this order and let other instructions move across them.
+      constexpr int kFence = 0x2 | 0x4 | 0x10 | 0x20 | 0x40 | 0x200 | 0x400;
+      u32x4 a3[3];
+      a3[0] = *(const u32x4*)(A);
+      if constexpr (KS > 1) a3[1] = *(const u32x4*)(A + T::FRAG_B);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 2 < KS) a3[(ks + 2) % 3] = *(const u32x4*)(A + (ks + 2) * T::FRAG_B);
+        __builtin_amdgcn_sched_barrier(kFence);
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub)
+          acc[P][sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[P][sub], &a3[ks % 3], bq[sub][ks]);
+        __builtin_amdgcn_sched_barrier(kFence);
+      }
+      return;
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if constexpr (!kPrefetchA) {
@@ -627,7 +651,9 @@ __global__ void __launch_bounds__(W * 64)
       } else {
         for (int j = 0; j < p.LU; ++j) sum += cv[j];
       }
-      orow[s_slotk[sl] * p.osd] = sum * p.out_scale;
+      // global (not generic) store: a flat store would also count in the LDS
+      // wait counter and force full waits on the A-fragment reads
+      ((__attribute__((address_space(1))) float*)orow)[s_slotk[sl] * p.osd] = sum * p.out_scale;
     }
   };
 
@@ -728,7 +754,8 @@ __global__ void __launch_bounds__(W * 64)
   using I1 = std::integral_constant<int, 1>;
   // Pipeline at iteration i: MFMA tile i (A fragments already in registers),
   // read tile i+1's A fragments from LDS, max of tile i-1, commit tile i+2 to
-  // LDS, fetch tile i+4 (PLAID: data of tile i+4, codes of tile i+5).
+  // LDS, fetch tile i+4 (PLAID: data of tile i+4, codes of tile i+5; one
+  // staging slot: tile i+3).
   // Descriptor queue: qm1 = tile i-1, q0 = i, q1 = i+1, q2 = i+2, q3 = i+3
   // (PLAID also q4 = i+4); the cursor produces the newest tile.
   Cur cur;
@@ -737,7 +764,20 @@ __global__ void __launch_bounds__(W * 64)
   // mask words of tiles i, i+1, i+2 (dense + mask; taken from the staged loads at commit)
   uint32_t vw0 = 0xffffffffu, vw1 = 0xffffffffu, vw2 = 0xffffffffu;
   q0 = produce(cur);
-  if constexpr (SRC == SRC_DENSE) {
+  if constexpr (SRC == SRC_DENSE && kOneSlot) {
+    // one staging slot: tiles 0 and 1 committed, tile 2 in flight (the
+    // cursor runs three tiles ahead of the MFMA)
+    fetch_dense(I0{}, cur, q0);
+    cur_adv(cur);
+    commit(I0{}, q0, 0, 0);
+    q1 = produce(cur);
+    fetch_dense(I0{}, cur, q1);
+    cur_adv(cur);
+    commit(I0{}, q1, 1, 1);
+    q2 = produce(cur);
+    fetch_dense(I0{}, cur, q2);
+    cur_adv(cur);
+  } else if constexpr (SRC == SRC_DENSE) {
     fetch_dense(I0{}, cur, q0);
     cur_adv(cur);
     q1 = produce(cur);
@@ -820,7 +860,7 @@ __global__ void __launch_bounds__(W * 64)
     commit(IP{}, q2, buf_c, (i + 2) & 3);
     if constexpr (SRC == SRC_DENSE && (FEAT & F_MASK) != 0) vw2 = sm[P];
     if constexpr (SRC == SRC_DENSE) {
-      fetch_dense(IP{}, cur, qn);  // tile i+4 into slot (i+4)%2
+      fetch_dense(IP{}, cur, qn);  // tile i+4 into slot (i+4)%2 (one slot: tile i+3, after the commit)
     } else {
       fetch_plaid(IP{}, q4);       // tile i+4, codes from slot (i+4)%2
       fetch_codes(IQ{}, qn);       // codes of tile i+5 into slot (i+5)%2
@@ -851,10 +891,13 @@ __global__ void __launch_bounds__(W * 64)
     qm1 = q0;
     q0 = q1;
     q1 = q2;
-    q2 = q3;
-    if constexpr (SRC == SRC_DENSE) {
+    if constexpr (SRC == SRC_DENSE && kOneSlot) {
+      q2 = qn;
+    } else if constexpr (SRC == SRC_DENSE) {
+      q2 = q3;
       q3 = qn;
     } else {
+      q2 = q3;
       q3 = q4;
       q4 = qn;
     }

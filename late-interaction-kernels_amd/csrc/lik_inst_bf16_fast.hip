@@ -16,6 +16,9 @@ int launch_dense_bf16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s
     case F_MASK | F_NORM: return launch_cfg<EK_BF16, 128, SRC_DENSE, 0, F_MASK | F_NORM>(pl, p, nb, s);
     case F_CU: return launch_cfg<EK_BF16, 128, SRC_DENSE, 0, F_CU>(pl, p, nb, s);
     case F_CU | F_NORM: return launch_cfg<EK_BF16, 128, SRC_DENSE, 0, F_CU | F_NORM>(pl, p, nb, s);
+    case F_NORMQ: return launch_cfg<EK_BF16, 128, SRC_DENSE, 0, F_NORMQ>(pl, p, nb, s);
+    case F_MASK | F_NORMQ: return launch_cfg<EK_BF16, 128, SRC_DENSE, 0, F_MASK | F_NORMQ>(pl, p, nb, s);
+    case F_CU | F_NORMQ: return launch_cfg<EK_BF16, 128, SRC_DENSE, 0, F_CU | F_NORMQ>(pl, p, nb, s);
       default: break;
     }
   }

@@ -45,7 +45,9 @@ constexpr int kRMax = 512;  // docs per workgroup (host caps R)
 // picks an instantiation whose bits cover the call): F_MASK doc mask,
 // F_TS per-token doc scale, F_NORM L2 normalise, F_CU packed docs.
 // F_ARGMAX (training forward): also write each (query token, doc) winner's doc-token index.
-enum { F_MASK = 1, F_TS = 2, F_NORM = 4, F_CU = 8, F_ALL = 15, F_ARGMAX = 16 };
+// F_NORM: normalise query and / or doc tokens (runtime bits); F_NORMQ:
+// normalise query tokens only (prologue code, nothing in the tile loop).
+enum { F_MASK = 1, F_TS = 2, F_NORM = 4, F_CU = 8, F_ALL = 15, F_ARGMAX = 16, F_NORMQ = 32 };
 
 // Four-wave workgroups of 4 column blocks per wave (dense bf16 / fp16
 // scoring without masks, normalisation or argmax, which would not fit) are
@@ -95,7 +97,7 @@ __global__ void __launch_bounds__(W * 64)
   const bool f_mask = (FEAT & F_MASK) && p.d.mask != nullptr;
   const bool f_ts = (FEAT & F_TS) && p.d.ts != nullptr;
   // p.normalize: bit 0 normalises query tokens, bit 1 doc tokens
-  const bool f_norm_q = (SRC == SRC_PLAID || (FEAT & F_NORM)) && (p.normalize & 1);
+  const bool f_norm_q = (SRC == SRC_PLAID || (FEAT & (F_NORM | F_NORMQ))) && (p.normalize & 1);
   const bool f_norm = (SRC == SRC_PLAID || (FEAT & F_NORM)) && (p.normalize & 2);
   const bool f_cu = (FEAT & F_CU) && p.d.cu != nullptr;
   const int tid = threadIdx.x;
@@ -207,7 +209,7 @@ __global__ void __launch_bounds__(W * 64)
   // Per-column query scale (normalise, fp8 token scales). Padding and masked
   // query columns have zero fragments, so their maxima are 0 (or non-finite,
   // which scores 0) without a scale: kernels with neither feature keep none.
-  constexpr bool kQsc = SRC == SRC_PLAID || (FEAT & (F_NORM | F_TS)) != 0;
+  constexpr bool kQsc = SRC == SRC_PLAID || (FEAT & (F_NORM | F_NORMQ | F_TS)) != 0;
   float qsc[kQsc ? NSUB : 1];
 #pragma unroll
   for (int sub = 0; sub < NSUB; ++sub) {
@@ -964,7 +966,8 @@ int launch_dpad(const Plan& pl, const Params& p, int64_t nb, hipStream_t s) {
 
 // Features a call needs (FEAT bits).
 inline int needed_feat(const Params& p) {
-  return (p.d.mask ? F_MASK : 0) | (p.d.ts ? F_TS : 0) | (p.normalize ? F_NORM : 0) | (p.d.cu ? F_CU : 0);
+  return (p.d.mask ? F_MASK : 0) | (p.d.ts ? F_TS : 0) |
+         ((p.normalize & 2) ? F_NORM : (p.normalize & 1) ? F_NORMQ : 0) | (p.d.cu ? F_CU : 0);
 }
 
 }  // namespace lik

@@ -78,6 +78,38 @@ __global__ void __launch_bounds__(256) fill_i32_kernel(int32_t* a, int64_t n, in
   if (i < n) a[i] = v;
 }
 
+// Doc-token normalisation ahead of the tile kernel: out[j, t] = D[j, t] /
+// max(||D[j, t]||, 1e-12), rounded once to the input type, into a contiguous
+// [n, L, dim] buffer. LPR lanes per row (the row's 16-byte chunks, zeros past
+// dim), each summing its chunk's squares in element order, then an xor-
+// shuffle over the row's lanes: the arithmetic of the tile kernel's commit,
+// so the rows are bitwise those it would have normalised in LDS.
+template <int EK, int LPR>
+__global__ void __launch_bounds__(256) norm_rows_kernel(const char* x, int64_t sn, int64_t sl, int64_t n, int64_t L,
+                                                        int dim, char* out) {
+  constexpr int EPC = 8;  // bf16 / fp16 elements per chunk
+  const int64_t r = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
+  const int cc = threadIdx.x % LPR;
+  const bool ok = r < n * L;
+  const bool live = ok && cc * EPC < dim;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (live) v = *(const u32x4*)(x + (r / L) * sn + (r % L) * sl + (int64_t)cc * 16);
+  float ss = chunk_sumsq<EK>(v);
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
+  const float sc = inv_norm(ss);
+  if (!live) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (EK == EK_BF16)
+      v[e] = f32_to_bf16_bits(bf16lo_to_f32(v[e]) * sc) | (f32_to_bf16_bits(bf16hi_to_f32(v[e]) * sc) << 16);
+    else
+      v[e] = f32_to_f16_bits(f16_to_f32((uint16_t)(v[e] & 0xffffu)) * sc) |
+             (f32_to_f16_bits(f16_to_f32((uint16_t)(v[e] >> 16)) * sc) << 16);
+  }
+  *(u32x4*)(out + r * (int64_t)dim * 2 + (int64_t)cc * 16) = v;
+}
+
 // out[q, j] = sum_c part[q*nc + c, j], c ascending.
 __global__ void __launch_bounds__(256) unit_sum_kernel(const float* part, int64_t nq, int nc, int64_t nd,
                                                        float* out, int64_t osq, int64_t osd) {
@@ -317,13 +349,42 @@ int timed_launch(hipStream_t s, F&& launch) {
 }
 
 struct WsLayout {
-  size_t extent_off = 0, holes_off = 0, tbits_off = 0, part_off = 0, total = 0;
-  bool need_extent = false, need_part = false;
+  size_t extent_off = 0, holes_off = 0, tbits_off = 0, part_off = 0, dnorm_off = 0, total = 0;
+  bool need_extent = false, need_part = false, need_dnorm = false;
 };
 
-WsLayout ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, const Plan& pl) {
+// Doc tokens are normalised once, ahead of the tile kernel, when several
+// workgroups would each normalise every doc tile (cross-product scoring with
+// more than one query group, padded bf16 / fp16 docs, no training forward):
+// the kernel then only normalises its query block.
+bool prenorm_docs(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool argmax, const Plan& pl) {
+  return (norm_bits(flags) & 2) && !argmax && !(flags & LIK_KD_LAYOUT) && !D->cu_seqlens && pl.ngroups > 1 &&
+         (Q->dtype == LIK_BF16 || Q->dtype == LIK_F16) && D->len > 0;
+}
+
+// The plan of a scoring call: the two-workgroup 4 x 4 block is preferred when
+// the tile loop does no doc-side work (no doc normalise left in the kernel,
+// no argmax, no token scales).
+int plan_call(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool argmax, Plan& pl, bool& prenorm) {
+  const bool kd = (flags & LIK_KD_LAYOUT) != 0;
+  const int min_w = ((norm_bits(flags) & 2) || argmax) ? 4 : 1;
+  const bool plain = !argmax && !Q->token_scale && !D->token_scale;
+  int rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, plain);
+  if (rc != LIK_OK) return rc;
+  prenorm = prenorm_docs(Q, D, flags, argmax, pl);
+  if ((norm_bits(flags) & 2) && !prenorm && plain)  // docs normalised in the kernel: no 4 x 4 preference
+    rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, false);
+  return rc;
+}
+
+WsLayout ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, const Plan& pl, bool prenorm) {
   WsLayout w;
   size_t off = 0;
+  if (prenorm) {
+    w.need_dnorm = true;
+    w.dnorm_off = off;
+    off = align256(off + (size_t)D->n * (size_t)D->len * (size_t)D->dim * 2);
+  }
   if (D->mask) {
     w.need_extent = true;
     w.extent_off = off;
@@ -374,13 +435,13 @@ int lik_timing_end(double* total_ms, int64_t* launches) {
 
 size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
   if (check_seqs(Q) != LIK_OK || check_seqs(D) != LIK_OK) return 0;
-  // the plan may use min_w 1 or 4 (normalise / training forward): cover both
-  const bool kd = (flags & LIK_KD_LAYOUT) != 0;
+  // the same size serves the scoring call and the training forward
   size_t total = 0;
-  for (int min_w : {1, 4}) {
+  for (bool argmax : {false, true}) {
     Plan pl;
-    if (make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, norm_bits(flags) == 0) != LIK_OK) return 0;
-    const size_t t = ws_layout(Q, D, flags, pl).total;
+    bool prenorm = false;
+    if (plan_call(Q, D, flags, argmax, pl, prenorm) != LIK_OK) return 0;
+    const size_t t = ws_layout(Q, D, flags, pl, prenorm).total;
     total = t > total ? t : total;
   }
   return total;
@@ -418,19 +479,52 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
   if (Q->n == 0 || D->n == 0) return LIK_OK;
   hipStream_t s = (hipStream_t)stream;
 
+  // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: the
+  // plan spreads it over at least 4 waves, or the docs are normalised once
+  // ahead of the tile kernel
   Plan pl;
-  // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: spread
-  // it over at least 4 waves even when the query block fits one wave's columns
-  const int min_w = ((norm_bits(flags) & 2) || argmax) ? 4 : 1;
-  const bool two_wg = argmax == nullptr && norm_bits(flags) == 0 && !Q->token_scale && !D->token_scale;
-  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, two_wg)) != LIK_OK) return rc;
-  const WsLayout wl = ws_layout(Q, D, flags, pl);
+  bool prenorm = false;
+  if ((rc = plan_call(Q, D, flags, argmax != nullptr, pl, prenorm)) != LIK_OK) return rc;
+  const WsLayout wl = ws_layout(Q, D, flags, pl, prenorm);
   if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return LIK_ERR_WORKSPACE;
 
   Params p{};
   p.q = to_dev(*Q);
   p.d = to_dev(*D);
   p.normalize = norm_bits(flags);
+  char* ws = (char*)workspace;
+  if (wl.need_dnorm) {
+    // normalised copy of the docs, contiguous [n, len, dim]; the tile kernel
+    // then normalises only its query block
+    char* dn = ws + wl.dnorm_off;
+    const int eb = elem_bytes(D->dtype);
+    const int64_t rows = D->n * D->len;
+    const int lpr = pl.dpad * eb / 16;  // the tile kernel's chunks per row
+    const unsigned nblk = (unsigned)((rows * lpr + 255) / 256);
+    const char* dx = (const char*)D->data;
+    const int64_t sn = D->stride_n * eb, sl = D->stride_l * eb;
+    if ((rc = timed_launch(s, [&] {
+           auto go = [&](auto kern) {
+             hipLaunchKernelGGL(kern, dim3(nblk), dim3(256), 0, s, dx, sn, sl, D->n, D->len, D->dim, dn);
+             return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+           };
+           if (D->dtype == LIK_BF16) {
+             if (lpr == 8) return go(norm_rows_kernel<EK_BF16, 8>);
+             if (lpr == 16) return go(norm_rows_kernel<EK_BF16, 16>);
+             if (lpr == 32) return go(norm_rows_kernel<EK_BF16, 32>);
+             return go(norm_rows_kernel<EK_BF16, 64>);
+           }
+           if (lpr == 8) return go(norm_rows_kernel<EK_F16, 8>);
+           if (lpr == 16) return go(norm_rows_kernel<EK_F16, 16>);
+           if (lpr == 32) return go(norm_rows_kernel<EK_F16, 32>);
+           return go(norm_rows_kernel<EK_F16, 64>);
+         })) != LIK_OK)
+      return rc;
+    p.d.data = dn;
+    p.d.sn_b = D->len * (int64_t)D->dim * eb;
+    p.d.sl_b = (int64_t)D->dim * eb;
+    p.normalize &= 1;
+  }
   p.out_scale = out_scale;
   p.nunits = pl.nunits;
   p.nc = pl.nc;
@@ -450,7 +544,6 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
     p.amax_ld = Q->len;
   }
 
-  char* ws = (char*)workspace;
   if (wl.need_extent) {
     p.extent = (const int32_t*)(ws + wl.extent_off);
     p.holes = (const uint8_t*)(ws + wl.holes_off);

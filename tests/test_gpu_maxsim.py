@@ -298,3 +298,23 @@ def test_cuda_graph_capture_replay():
         assert torch.equal(out, eager)
         _ = maxsim(Q[:2], D[:5], normalize=True)  # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_doc_prenormalise_matches_in_kernel(dtype):
+    """Several query groups (20 queries) normalise the docs once ahead of the
+    tile kernel; one group (16 queries) normalises them inside it. Same
+    rounding, same MFMA order, same per-query summation order (a query's
+    place in its group is the same): the first 16 rows are bitwise equal."""
+    from late_interaction_kernels import maxsim
+
+    _case(f"prenorm {dtype}")
+    g = torch.Generator().manual_seed(31)
+    Q = (torch.randn(20, 32, 128, generator=g) * 3).to(dtype).cuda()
+    D = (torch.randn(37, 75, 128, generator=g) * 0.2).to(dtype).cuda()
+    dm = (torch.arange(75)[None] < torch.randint(1, 76, (37,), generator=g)[:, None]).cuda()
+    allq = maxsim(Q, D, d_mask=dm, normalize=True)
+    first = maxsim(Q[:16], D, d_mask=dm, normalize=True)
+    assert torch.equal(allq[:16], first)
+    ref = O.maxsim(_np(Q), _np(D), None, dm.cpu().numpy(), normalize=True)
+    assert rel_err(_np(allq), ref) < TOL[dtype]

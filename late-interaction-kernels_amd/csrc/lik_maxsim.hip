@@ -674,6 +674,47 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   // centroid rows are gathered with 32-bit byte offsets
   if (docs->n_centroids * docs->cent_stride * ceb >= (int64_t)1 << 32) return LIK_ERR_UNSUPPORTED;
 
+  // A few queries (up to 4 of <= 32 tokens): one wavefront per (query, doc
+  // range) decodes straight into its MFMA fragments (the tile kernel is
+  // latency-bound here).
+  const int sdp = pick_dpad(Q->dtype, Q->dim);
+  const char* se = getenv("LIK_PLAID_STREAM");
+  if (Q->n <= 4 && Q->len >= 1 && Q->len <= 32 && (sdp == 64 || sdp == 128) && docs->res_stride_tok % 4 == 0 &&
+      !(se && se[0] == '0')) {
+    Params p{};
+    p.q = to_dev(*Q);
+    p.pl.codes = docs->codes;
+    p.pl.res = docs->residuals;
+    p.pl.cu = docs->cu_seqlens;
+    p.pl.lengths = docs->lengths;
+    p.pl.n = docs->n;
+    p.pl.L = docs->max_len;
+    p.pl.codes_sn = docs->codes_stride_n;
+    p.pl.res_st = docs->res_stride_tok;
+    p.pl.cent = (const char*)docs->centroids;
+    p.pl.cent_sb = docs->cent_stride * ceb;
+    p.pl.ncent = docs->n_centroids;
+    p.pl.bw = docs->bucket_weights;
+    p.pl.nb = docs->n_buckets;
+    p.pl.nbits = docs->nbits;
+    p.normalize = norm_bits(flags);
+    p.out_scale = 1.f;
+    p.out = out;
+    p.osq = out_stride_q;
+    p.osd = out_stride_d;
+    p.LU = (int)Q->len;
+    const int nsub = 1;  // one query per wavefront
+    p.ngroups = (Q->n + nsub - 1) / nsub;
+    // ~16k wavefronts over the corpus, at most 512 docs each
+    int64_t R = (docs->n + 16383) / 16384;
+    p.R = (int)(R < 1 ? 1 : (R > 512 ? 512 : R));
+    p.NR = (docs->n + p.R - 1) / p.R;
+    const int ek = Q->dtype == LIK_F16 ? EK_F16 : EK_BF16;
+    const int cdk = docs->centroid_dtype == LIK_F32 ? EK_F32 : (docs->centroid_dtype == LIK_F16 ? EK_F16 : EK_BF16);
+    hipStream_t s = (hipStream_t)stream;
+    return timed_launch(s, [&] { return launch_plaid_stream(ek, cdk, sdp, nsub, p, s); });
+  }
+
   Plan pl;
   // PLAID tiles carry the decode VALU work: at least 4 waves share each tile
   // even when the query block would fit one wave's columns.

@@ -1,0 +1,366 @@
+// PLAID residual MaxSim for a few queries (up to 4 of <= 32 tokens) on
+// gfx950: one wavefront streams a range of documents for one query on its
+// own, no LDS tile ring and no barriers in the loop.
+//
+// With a handful of query columns the tile kernel's per-tile work is mostly
+// the decode and its latency chain (code -> centroid row -> decode -> MFMA);
+// a workgroup walking thousands of tiles behind one barrier each is latency
+// bound. Here each lane decodes the half row that is its own MFMA A fragment
+// (lane (l32, h): doc token l32 of the tile, embedding elements
+// [h*DPAD/2, (h+1)*DPAD/2)), the two halves' squared norms meet through one
+// permlane32 swap, and the fragments go straight to the MFMA. Codes are
+// loaded two tiles ahead and centroid rows / residual bytes one tile ahead
+// (two staging sets), and several waves per SIMD cover the rest.
+//
+// The arithmetic is the decode kernel's (lik_plaid_decode.hip), element for
+// element: emb = centroid + bucket weight in fp32, per 8-element chunk a fma
+// chain of squares, chunk sums combined in the xor-tree order of a row's
+// lanes, x / max(||x||, 1e-12) rounded once. The bucket weights of all fields
+// of a residual byte come from one LDS table entry (byte -> values).
+// Reference: plaid.py:684-963 (fused residual MaxSim), reference.py:124-179.
+#include "lik_kernel.h"
+
+namespace lik {
+
+// Occupancy target: the latency chain is covered by the other waves of the
+// SIMD, so registers are capped: 3 waves per SIMD at d <= 64, 2 at d = 128
+// (query fragments, two staging sets of centroid rows and residual bytes,
+// one accumulator; more waves would spill).
+template <int EK, int DPAD, int CD, int NBITS, int NSUB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >= 128 ? 2 : 3)))
+    plaid_stream_kernel(const Params p) {
+  using T = KT<EK, DPAD>;
+  constexpr int KS = T::KSTEPS;           // 8-element chunks per lane (= MFMA k-steps)
+  constexpr int HALF = DPAD / 2;          // elements per lane
+  constexpr int CSZ = CD == EK_F32 ? 4 : 2;
+  constexpr int CVL = HALF * CSZ / 16;    // 16-byte centroid loads per lane
+  constexpr int RBL = HALF * NBITS / 8;   // residual bytes per lane
+  constexpr int RVL = RBL / 4;            // residual dwords per lane
+  constexpr int FPB = 8 / NBITS;          // fields per residual byte
+  static_assert(RBL % 4 == 0, "residual half rows are whole dwords");
+  constexpr float NEG_INF = -__builtin_huge_valf();
+
+  __shared__ __attribute__((aligned(16))) float s_lut[256 * FPB];
+  for (int i = threadIdx.x; i < 256 * FPB; i += 256) {
+    const int v = i / FPB, k = i % FPB;
+    uint32_t bc = ((uint32_t)v >> (k * NBITS)) & ((1u << NBITS) - 1u);
+    bc = bc < (uint32_t)p.pl.nb ? bc : (uint32_t)(p.pl.nb - 1);
+    s_lut[i] = p.pl.bw[bc];
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  // wave index, uniform (so is everything the doc cursor derives from it)
+  const int64_t wv = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t g = wv / p.NR, r = wv - g * p.NR;
+  if (g >= p.ngroups) return;  // wave-uniform, after the only barrier
+
+  // ---- query block: NSUB queries, token l32 of query g*NSUB+sub in column l32 ----
+  u32x4 bq[NSUB][KS];
+  float qsc[NSUB];
+  const bool f_norm_q = (p.normalize & 1) != 0;
+  const bool f_norm_d = (p.normalize & 2) != 0;
+#pragma unroll
+  for (int sub = 0; sub < NSUB; ++sub) {
+    const int64_t q = g * NSUB + sub;
+    const bool valid = q < p.q.n && l32 < seq_len(p.q, q);
+    const char* rowp = valid ? seq_row0(p.q, q) + (int64_t)l32 * p.q.sl_b : nullptr;
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int e = h * HALF + ks * 8;
+      bq[sub][ks] = (valid && e < p.q.dim) ? *(const u32x4*)(rowp + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
+      if (f_norm_q) ss += chunk_sumsq<EK>(bq[sub][ks]);
+    }
+    ss += __shfl_xor(ss, 32);
+    qsc[sub] = valid ? (f_norm_q ? inv_norm(ss) : 1.f) : 0.f;
+  }
+
+  // ---- documents [j0, j1) as a stream of 32-token tiles ----
+  const int64_t j0 = r * p.R;
+  const int64_t j1 = j0 + p.R < p.pl.n ? j0 + p.R : p.pl.n;
+  auto dlen = [&](int64_t j) -> int64_t { return doc_len<SRC_PLAID>(p, j); };
+  auto dtok = [&](int64_t j) -> int64_t { return p.pl.cu ? (int64_t)p.pl.cu[j] : j * p.pl.codes_sn; };
+  auto store = [&](int64_t j, int sub, float v) {
+    const int64_t q = g * NSUB + sub;
+    if (q < p.q.n)
+      ((__attribute__((address_space(1))) float*)p.out)[q * p.osq + j * p.osd] = v;
+  };
+  // tile descriptor (wave-uniform); j = -1: past the range
+  struct Tile {
+    int64_t j, tok;
+    int t, nv;
+  };
+  // descriptors are wave-uniform by construction; say so, so the buffer
+  // descriptors built from them live in scalar registers
+  auto uni64 = [](int64_t x) -> int64_t {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+  auto uni = [&](const Tile& t) -> Tile {
+    return Tile{uni64(t.j), uni64(t.tok), __builtin_amdgcn_readfirstlane(t.t), __builtin_amdgcn_readfirstlane(t.nv)};
+  };
+  // first non-empty doc at or after j (empty docs score 0 on the way)
+  auto open_doc = [&](int64_t j) -> Tile {
+    while (j < j1) {
+      const int64_t len = dlen(j);
+      if (len > 0) return uni(Tile{j, dtok(j), 0, (int)(len < 32 ? len : 32)});
+      if (lane < NSUB) store(j, lane, 0.f);
+      ++j;
+    }
+    return Tile{-1, 0, 0, 0};
+  };
+  auto next_tile = [&](const Tile& c) -> Tile {
+    if (c.j < 0) return c;
+    const int64_t len = dlen(c.j);
+    const int64_t start = (int64_t)(c.t + 1) * 32;
+    if (start < len) {
+      const int64_t rem = len - start;
+      return uni(Tile{c.j, c.tok + 32, c.t + 1, (int)(rem < 32 ? rem : 32)});
+    }
+    return open_doc(c.j + 1);
+  };
+
+  const __amdgpu_buffer_rsrc_t rcent = make_rsrc(p.pl.cent, sat_u32(p.pl.ncent * p.pl.cent_sb));
+  auto load_code = [&](const Tile& d) -> int32_t {
+    if (d.j < 0) return 0;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.pl.codes + d.tok, (uint32_t)d.nv * 4u);
+    return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, l32 < d.nv ? (uint32_t)l32 * 4u : kOOB, 0, 0);
+  };
+  struct Stage {
+    u32x4 c[CVL];
+    uint32_t rw[RVL];
+  };
+  auto load_data = [&](const Tile& d, int32_t code, Stage& st) {
+    const bool ok = d.j >= 0 && l32 < d.nv;
+    int64_t cd = code;
+    cd = (cd < 0 || cd >= p.pl.ncent) ? 0 : cd;
+    const uint32_t coff = ok ? (uint32_t)(cd * p.pl.cent_sb) + (uint32_t)(h * HALF * CSZ) : kOOB;
+#pragma unroll
+    for (int v = 0; v < CVL; ++v) st.c[v] = __builtin_amdgcn_raw_buffer_load_b128(rcent, coff == kOOB ? kOOB : coff + 16u * v, 0, 0);
+    const __amdgpu_buffer_rsrc_t rres =
+        make_rsrc(p.pl.res + (d.j >= 0 ? d.tok : 0) * p.pl.res_st, ok ? sat_u32((int64_t)d.nv * p.pl.res_st) : 0u);
+    const uint32_t roff = ok ? (uint32_t)l32 * (uint32_t)p.pl.res_st + (uint32_t)(h * RBL) : kOOB;
+#pragma unroll
+    for (int v = 0; v < RVL; ++v)
+      st.rw[v] = __builtin_amdgcn_raw_buffer_load_b32(rres, roff == kOOB ? kOOB : roff + 4u * v, 0, 0);
+  };
+
+  f32x16 acc[NSUB];
+  float m[NSUB];
+#pragma unroll
+  for (int sub = 0; sub < NSUB; ++sub) m[sub] = NEG_INF;
+
+  // decode tile d from st into A fragments, MFMA, running max; doc end: score.
+  // Two passes over the lane's half row (the norm needs all of it before any
+  // element is scaled): squares first, then the same fp32 values again,
+  // scaled, rounded and fed to the MFMA chunk by chunk.
+  auto cent_chunk = [&](const Stage& st, int ks, float* cv) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int ei = ks * 8 + e;  // element of this lane's half
+      if constexpr (CD == EK_F32) cv[e] = __uint_as_float(st.c[ei >> 2][ei & 3]);
+      else if constexpr (CD == EK_BF16)
+        cv[e] = (ei & 1) ? bf16hi_to_f32(st.c[ei >> 3][(ei >> 1) & 3]) : bf16lo_to_f32(st.c[ei >> 3][(ei >> 1) & 3]);
+      else {
+        const uint32_t w = st.c[ei >> 3][(ei >> 1) & 3];
+        cv[e] = f16_to_f32((uint16_t)((ei & 1) ? (w >> 16) : (w & 0xffffu)));
+      }
+    }
+  };
+  // bucket weights of chunk ks's 8 fields: 8 / FPB residual bytes, one LDS entry each
+  auto bw_chunk = [&](const Stage& st, int ks, float* bw) {
+#pragma unroll
+    for (int b = 0; b < 8 / FPB; ++b) {
+      const int byte_i = (ks * 8) / FPB + b;
+      const uint32_t byv = (st.rw[byte_i >> 2] >> ((byte_i & 3) * 8)) & 0xffu;
+      if constexpr (FPB == 4) {
+        const f32x4 t = *(const f32x4*)&s_lut[byv * 4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bw[b * 4 + k] = t[k];
+      } else if constexpr (FPB == 2) {
+        const float2 t = *(const float2*)&s_lut[byv * 2];
+        bw[b * 2] = t.x;
+        bw[b * 2 + 1] = t.y;
+      } else {
+        bw[b] = s_lut[byv];
+      }
+    }
+  };
+  auto compute = [&](const Tile& d, const Stage& st) {
+    float cs[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      float cv[8], bw[8];
+      cent_chunk(st, ks, cv);
+      bw_chunk(st, ks, bw);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (h * HALF + ks * 8 + e) < p.q.dim ? cv[e] + bw[e] : 0.f;
+        ss = fmaf(x, x, ss);
+      }
+      cs[ks] = ss;
+    }
+    // chunk sums in the xor-tree order of the decode kernel's row lanes:
+    // pairs, then pairs of pairs, ... within the half, then across halves
+#pragma unroll
+    for (int w = 1; w < KS; w <<= 1)
+#pragma unroll
+      for (int c = 0; c < KS; c += 2 * w) cs[c] = cs[c] + cs[c + w];
+    float ss = cs[0];
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    const float sc = f_norm_d ? inv_norm(ss) : 1.f;
+    // The second pass recomputes the first pass's values on purpose: opaque
+    // copies of the staged words keep the compiler from holding all 128
+    // intermediate values live between the passes instead.
+    Stage s2;
+#pragma unroll
+    for (int v = 0; v < CVL; ++v) {
+      s2.c[v] = st.c[v];
+      asm volatile("" : "+v"(s2.c[v]));
+    }
+#pragma unroll
+    for (int v = 0; v < RVL; ++v) {
+      s2.rw[v] = st.rw[v];
+      asm volatile("" : "+v"(s2.rw[v]));
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      float cv[8], bw[8];
+      cent_chunk(s2, ks, cv);
+      bw_chunk(s2, ks, bw);
+      u32x4 af;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int e0 = h * HALF + ks * 8 + 2 * k;
+        const float x0 = e0 < p.q.dim ? cv[2 * k] + bw[2 * k] : 0.f;
+        const float x1 = e0 + 1 < p.q.dim ? cv[2 * k + 1] + bw[2 * k + 1] : 0.f;
+        if constexpr (EK == EK_F16)
+          af[k] = f32_to_f16_bits(x0 * sc) | (f32_to_f16_bits(x1 * sc) << 16);
+        else
+          af[k] = f32_to_bf16_bits(x0 * sc) | (f32_to_bf16_bits(x1 * sc) << 16);
+      }
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) acc[sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[sub], &af, &bq[sub][ks]);
+    }
+    // running max over the tile's valid rows (row of element e: 8*(e/4) + 4h + e%4)
+    if (d.nv == 32) {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m[sub] = fmaxf(m[sub], acc[sub][e]);
+    } else {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (8 * (e >> 2) + 4 * h + (e & 3) < d.nv) m[sub] = fmaxf(m[sub], acc[sub][e]);
+    }
+    if ((int64_t)(d.t + 1) * 32 >= dlen(d.j)) {
+      // doc end: column maxima over both halves, scaled, summed over the
+      // query's tokens in column order
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
+        const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        const float v = __builtin_isfinite(mm) ? mm * qsc[sub] : 0.f;
+        auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
+        // the tile kernel's flush order: that kernel puts up to 4 queries of
+        // <= 32 tokens in one group, query q at place q, and its sum starts at
+        // 4-column chunk q % (Lq / 4) and wraps
+        float s = 0.f;
+        if ((p.LU & 3) == 0) {
+          const int nv4 = p.LU >> 2;
+          int c = (int)((g * NSUB + sub) % nv4);
+          for (int j = 0; j < nv4; ++j) {
+            s += col(4 * c);
+            s += col(4 * c + 1);
+            s += col(4 * c + 2);
+            s += col(4 * c + 3);
+            c = (c + 1 == nv4) ? 0 : c + 1;
+          }
+        } else {
+          for (int c = 0; c < p.LU; ++c) s += col(c);
+        }
+        if (lane == 0) store(d.j, sub, s * p.out_scale);
+        m[sub] = NEG_INF;
+      }
+    }
+  };
+
+  // pipeline: compute tile c, data of tile c+1 in flight, code of tile c+2 in flight
+  Tile tc = open_doc(j0);
+  Tile t1 = next_tile(tc);
+  Stage sa, sb;
+  const int32_t code_c = load_code(tc);
+  load_data(tc, code_c, sa);
+  int32_t code1 = load_code(t1);
+  while (tc.j >= 0) {
+    Tile t2 = next_tile(t1);
+    load_data(t1, code1, sb);
+    int32_t code2 = load_code(t2);
+    compute(tc, sa);
+    tc = t1;
+    t1 = t2;
+    code1 = code2;
+    if (tc.j < 0) break;
+    t2 = next_tile(t1);
+    load_data(t1, code1, sa);
+    code2 = load_code(t2);
+    compute(tc, sb);
+    tc = t1;
+    t1 = t2;
+    code1 = code2;
+  }
+}
+
+template <int EK, int DPAD, int CD, int NBITS>
+int launch_stream_nsub(int nsub, const Params& p, int64_t nblocks, hipStream_t s) {
+  if (nsub != 1) return LIK_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((plaid_stream_kernel<EK, DPAD, CD, NBITS, 1>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+  return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+}
+
+template <int EK, int DPAD, int CD>
+int launch_stream_nbits(int nbits, int nsub, const Params& p, int64_t nblocks, hipStream_t s) {
+  switch (nbits) {
+    case 2: return launch_stream_nsub<EK, DPAD, CD, 2>(nsub, p, nblocks, s);
+    case 4: return launch_stream_nsub<EK, DPAD, CD, 4>(nsub, p, nblocks, s);
+    case 8: return launch_stream_nsub<EK, DPAD, CD, 8>(nsub, p, nblocks, s);
+    default: return LIK_ERR_UNSUPPORTED;
+  }
+}
+
+template <int EK, int DPAD>
+int launch_stream_cd(int cd, int nbits, int nsub, const Params& p, int64_t nblocks, hipStream_t s) {
+  switch (cd) {
+    case EK_BF16: return launch_stream_nbits<EK, DPAD, EK_BF16>(nbits, nsub, p, nblocks, s);
+    case EK_F16: return launch_stream_nbits<EK, DPAD, EK_F16>(nbits, nsub, p, nblocks, s);
+    case EK_F32: return launch_stream_nbits<EK, DPAD, EK_F32>(nbits, nsub, p, nblocks, s);
+    default: return LIK_ERR_UNSUPPORTED;
+  }
+}
+
+// Launch the stream kernel: p.ngroups query groups of nsub queries, p.NR doc
+// ranges of p.R docs each, one wavefront per (group, range), 4 per block.
+int launch_plaid_stream(int ek, int cd, int dpad, int nsub, const Params& p, hipStream_t s) {
+  const int64_t waves = p.ngroups * p.NR;
+  const int64_t nblocks = (waves + 3) / 4;
+  if (nblocks > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  const int nbits = p.pl.nbits;
+  if (ek == EK_BF16) {
+    if (dpad == 64) return launch_stream_cd<EK_BF16, 64>(cd, nbits, nsub, p, nblocks, s);
+    if (dpad == 128) return launch_stream_cd<EK_BF16, 128>(cd, nbits, nsub, p, nblocks, s);
+  } else {
+    if (dpad == 64) return launch_stream_cd<EK_F16, 64>(cd, nbits, nsub, p, nblocks, s);
+    if (dpad == 128) return launch_stream_cd<EK_F16, 128>(cd, nbits, nsub, p, nblocks, s);
+  }
+  return LIK_ERR_UNSUPPORTED;
+}
+
+}  // namespace lik

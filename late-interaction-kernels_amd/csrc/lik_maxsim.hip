@@ -680,7 +680,7 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   const int sdp = pick_dpad(Q->dtype, Q->dim);
   const char* se = getenv("LIK_PLAID_STREAM");
   if (Q->n <= 4 && Q->len >= 1 && Q->len <= 32 && (sdp == 64 || sdp == 128) && docs->res_stride_tok % 4 == 0 &&
-      !(se && se[0] == '0')) {
+      docs->centroid_dtype != LIK_F32 && !(se && se[0] == '0')) {
     Params p{};
     p.q = to_dev(*Q);
     p.pl.codes = docs->codes;

@@ -26,7 +26,8 @@ namespace lik {
 // SIMD, so registers are capped: 3 waves per SIMD at d <= 64, 2 at d = 128
 // (query fragments, two staging sets of centroid rows and residual bytes,
 // one accumulator; more waves would spill).
-template <int EK, int DPAD, int CD, int NBITS, int NSUB>
+// FULLD: the embedding dim is DPAD (no padding elements to zero).
+template <int EK, int DPAD, int CD, int NBITS, int NSUB, bool FULLD>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >= 128 ? 2 : 3)))
     plaid_stream_kernel(const Params p) {
   using T = KT<EK, DPAD>;
@@ -198,7 +199,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = (h * HALF + ks * 8 + e) < p.q.dim ? cv[e] + bw[e] : 0.f;
+        const float x = (FULLD || (h * HALF + ks * 8 + e) < p.q.dim) ? cv[e] + bw[e] : 0.f;
         ss = fmaf(x, x, ss);
       }
       cs[ks] = ss;
@@ -238,12 +239,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int e0 = h * HALF + ks * 8 + 2 * k;
-        const float x0 = e0 < p.q.dim ? cv[2 * k] + bw[2 * k] : 0.f;
-        const float x1 = e0 + 1 < p.q.dim ? cv[2 * k + 1] + bw[2 * k + 1] : 0.f;
+        const float x0 = (FULLD || e0 < p.q.dim) ? cv[2 * k] + bw[2 * k] : 0.f;
+        const float x1 = (FULLD || e0 + 1 < p.q.dim) ? cv[2 * k + 1] + bw[2 * k + 1] : 0.f;
+        // bf16: one packed round-to-nearest-even conversion per pair (the
+        // fp16 pair conversion would round toward zero: keep the scalar one)
         if constexpr (EK == EK_F16)
           af[k] = f32_to_f16_bits(x0 * sc) | (f32_to_f16_bits(x1 * sc) << 16);
         else
-          af[k] = f32_to_bf16_bits(x0 * sc) | (f32_to_bf16_bits(x1 * sc) << 16);
+          af[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0 * sc, x1 * sc}, bf16x2));
       }
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) acc[sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[sub], &af, &bq[sub][ks]);
@@ -322,7 +325,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
 template <int EK, int DPAD, int CD, int NBITS>
 int launch_stream_nsub(int nsub, const Params& p, int64_t nblocks, hipStream_t s) {
   if (nsub != 1) return LIK_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((plaid_stream_kernel<EK, DPAD, CD, NBITS, 1>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+  if (p.q.dim == DPAD)
+    hipLaunchKernelGGL((plaid_stream_kernel<EK, DPAD, CD, NBITS, 1, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((plaid_stream_kernel<EK, DPAD, CD, NBITS, 1, false>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
   return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
 }
 
@@ -341,7 +347,6 @@ int launch_stream_cd(int cd, int nbits, int nsub, const Params& p, int64_t nbloc
   switch (cd) {
     case EK_BF16: return launch_stream_nbits<EK, DPAD, EK_BF16>(nbits, nsub, p, nblocks, s);
     case EK_F16: return launch_stream_nbits<EK, DPAD, EK_F16>(nbits, nsub, p, nblocks, s);
-    case EK_F32: return launch_stream_nbits<EK, DPAD, EK_F32>(nbits, nsub, p, nblocks, s);
     default: return LIK_ERR_UNSUPPORTED;
   }
 }

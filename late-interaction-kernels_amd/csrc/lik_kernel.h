@@ -77,14 +77,26 @@ __global__ void __launch_bounds__(W * 64)
   constexpr float NEG_INF = -__builtin_huge_valf();
   static_assert(SRC == SRC_DENSE || (!T::SPLIT && EK != EK_FP8), "PLAID computes in bf16/f16");
 
-  // tile j lives in LDS buffer j % 3: tile i is being multiplied (from
-  // registers), tile i+1's A fragments are being read, tile i+2 is being written
-  __shared__ __attribute__((aligned(16))) char s_tile[3][T::NARR][T::TILE_B];
+  // Direct global -> LDS tile loads (buffer_load ... lds) in the two-workgroup
+  // kernel with 256-byte rows: no staging registers, no LDS writes of staged
+  // data. A DMA instruction writes 64 x 16 bytes contiguously, so those tiles
+  // are unpadded with a XOR swizzle (16-byte chunk c of row r at slot
+  // c ^ (r & 15)), which keeps the A-fragment reads conflict-free; they cycle
+  // through 4 buffers (tile i multiplied, tiles i+1 .. i+3 landing).
+  constexpr bool kDMA = two_wg_per_cu<EK, W, NSUB, SRC, FEAT>() && DPAD * T::CB == 256;
+  // otherwise tile j lives in LDS buffer j % 3: tile i is being multiplied
+  // (from registers), tile i+1's A fragments are being read, tile i+2 is
+  // being written
+  constexpr int NBUF = kDMA ? 4 : 3;
+  constexpr int TBYTES = kDMA ? 32 * 256 : T::TILE_B;
+  __shared__ __attribute__((aligned(16))) char s_tile[NBUF][T::NARR][TBYTES];
   __shared__ __attribute__((aligned(16))) float s_rs[4][32];  // fp8 per-row scale of tile j in slot j % 4
   // Finished documents: per-column maxima (already scaled, 0 for invalid
-  // columns) of the last 16 docs and their local indices. A half (8 docs) is
-  // summed per unit and written out one iteration after it fills.
-  constexpr int NSLOT = 16;
+  // columns) of the last NSLOT docs and their local indices. A half is summed
+  // per unit and written out one iteration after it fills. (16 slots; 8 in the
+  // DMA kernel, whose fourth tile buffer takes the LDS.)
+  constexpr int NSLOT = kDMA ? 8 : 16;
+  constexpr int HSLOT = NSLOT / 2;
   __shared__ __attribute__((aligned(16))) float s_colb[NSLOT][COLS];
   __shared__ int s_slotk[NSLOT];
   __shared__ float s_bw[SRC == SRC_PLAID ? 256 : 1];
@@ -342,8 +354,10 @@ __global__ void __launch_bounds__(W * 64)
   int lcc[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    const int c = tid + i * NT;
-    const int row = c / SCPR, cc = c % SCPR;
+    // DMA: chunk i of this lane is LDS slot (wave * NCH + i) * 64 + lane,
+    // i.e. row slot / 16 and global chunk (slot % 16) ^ (row & 15)
+    const int c = kDMA ? (wv * NCH + i) * 64 + lane : tid + i * NT;
+    const int row = c / SCPR, cc = kDMA ? ((c % SCPR) ^ (row & 15)) : c % SCPR;
     const bool inr = FULLCH || c < 32 * SCPR;
     lcc[i] = cc;
     if constexpr (SRC == SRC_DENSE) {
@@ -368,6 +382,38 @@ __global__ void __launch_bounds__(W * 64)
 
   // Dense: token data of the cursor's current tile into slot S (rows past
   // the doc end and padding chunks are out of range and read as 0).
+  // DMA fetch of tile d straight into LDS buffer buf (two-workgroup kernel).
+  // Issued as inline asm: the compiler treats a DMA write as aliasing every
+  // later LDS read and would wait for all DMA before each A-fragment read;
+  // here the ordering is explicit (the step-end wait and barrier). M0 (the
+  // LDS destination) is saved and restored around the load.
+  auto fetch_dma = [&](const Cur& c, const Desc& d, int buf) {
+    if constexpr (kDMA) {
+      const uint32_t span = (uint32_t)(c.len > 1 ? c.len - 1 : 0) * (uint32_t)p.d.sl_b + (uint32_t)(p.d.dim * T::IN_B);
+      const uint64_t base = (uint64_t)(p.d.data + c.off);
+      // raw buffer descriptor: base, stride 0, num_records = span, untyped 32-bit format
+      const u32x4 desc = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
+                          (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu),
+                          (uint32_t)__builtin_amdgcn_readfirstlane(span), 0x00020000u};
+      const uint32_t toff = (uint32_t)c.t * 32u * (uint32_t)p.d.sl_b;
+      const int wu = __builtin_amdgcn_readfirstlane(wv);
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(s_tile[buf][0] + (wu * NCH + i) * 1024));
+        const uint32_t voff = lrow[i] < d.nv ? loff[i] + toff : kOOB;
+        uint32_t saved;
+        asm volatile(
+            "s_mov_b32 %0, m0\n\t"
+            "s_mov_b32 m0, %1\n\t"
+            "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+            "s_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(lds), "v"(voff), "s"(desc)
+            : "memory");
+      }
+    }
+  };
   auto fetch_dense = [&](auto SS, const Cur& c, const Desc& d) {
     if constexpr (SRC == SRC_DENSE) {
       constexpr int S = kOneSlot ? 0 : decltype(SS)::value;
@@ -590,12 +636,20 @@ __global__ void __launch_bounds__(W * 64)
       // MFMAs (three rotating registers). The fences keep LDS reads and
       // MFMAs in this order and let other instructions move across them.
       constexpr int kFence = 0x2 | 0x4 | 0x10 | 0x20 | 0x40 | 0x200 | 0x400;
+      // A fragment k-step ks of this lane: logical chunk h * KS + ks of row
+      // l32 (DMA layout: at slot chunk ^ (l32 & 15) of a 256-byte row)
+      auto afrag = [&](int ks) -> const u32x4* {
+        if constexpr (kDMA)
+          return (const u32x4*)(s_tile[buf][0] + l32 * 256 + (((h * KS + ks) ^ (l32 & 15)) * 16));
+        else
+          return (const u32x4*)(A + ks * T::FRAG_B);
+      };
       u32x4 a3[3];
-      a3[0] = *(const u32x4*)(A);
-      if constexpr (KS > 1) a3[1] = *(const u32x4*)(A + T::FRAG_B);
+      a3[0] = *afrag(0);
+      if constexpr (KS > 1) a3[1] = *afrag(1);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 2 < KS) a3[(ks + 2) % 3] = *(const u32x4*)(A + (ks + 2) * T::FRAG_B);
+        if (ks + 2 < KS) a3[(ks + 2) % 3] = *afrag(ks + 2);
         __builtin_amdgcn_sched_barrier(kFence);
 #pragma unroll
         for (int sub = 0; sub < NSUB; ++sub)
@@ -766,7 +820,21 @@ __global__ void __launch_bounds__(W * 64)
   // mask words of tiles i, i+1, i+2 (dense + mask; taken from the staged loads at commit)
   uint32_t vw0 = 0xffffffffu, vw1 = 0xffffffffu, vw2 = 0xffffffffu;
   q0 = produce(cur);
-  if constexpr (SRC == SRC_DENSE && kOneSlot) {
+  if constexpr (SRC == SRC_DENSE && kDMA) {
+    // tiles 0, 1, 2 into buffers 0, 1, 2; the cursor runs three tiles ahead
+    // of the MFMA
+    fetch_dma(cur, q0, 0);
+    cur_adv(cur);
+    q1 = produce(cur);
+    fetch_dma(cur, q1, 1);
+    cur_adv(cur);
+    q2 = produce(cur);
+    fetch_dma(cur, q2, 2);
+    cur_adv(cur);
+    // tile 0 landed before the barrier (tiles 1 and 2, 2 * NCH younger
+    // instructions, may still be in flight: the first step's end waits)
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  } else if constexpr (SRC == SRC_DENSE && kOneSlot) {
     // one staging slot: tiles 0 and 1 committed, tile 2 in flight (the
     // cursor runs three tiles ahead of the MFMA)
     fetch_dense(I0{}, cur, q0);
@@ -830,7 +898,7 @@ __global__ void __launch_bounds__(W * 64)
     using IP = std::integral_constant<int, P>;
     using IQ = std::integral_constant<int, 1 - P>;
     if (flush_half >= 0) {
-      flush(flush_half * 8, 8);
+      flush(flush_half * HSLOT, HSLOT);
       flush_half = -1;
     }
     {
@@ -851,17 +919,20 @@ __global__ void __launch_bounds__(W * 64)
     // one block: MFMA tile i, read A of tile i+1, max of tile i-1, commit
     // tile i+2, fetch tile i+4
     const Desc qn = produce(cur);
+    const int bx = kDMA ? (i & 3) : buf_x;
     if constexpr (NACC == 2) {
-      mma_tile(IP{}, IP{}, buf_x);
+      mma_tile(IP{}, IP{}, bx);
       epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
     } else {
       epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
-      mma_tile(IP{}, IP{}, buf_x);
+      mma_tile(IP{}, IP{}, bx);
     }
     if constexpr (kPrefetchA) load_a(IQ{}, buf_a);
-    commit(IP{}, q2, buf_c, (i + 2) & 3);
+    if constexpr (!kDMA) commit(IP{}, q2, buf_c, (i + 2) & 3);
     if constexpr (SRC == SRC_DENSE && (FEAT & F_MASK) != 0) vw2 = sm[P];
-    if constexpr (SRC == SRC_DENSE) {
+    if constexpr (SRC == SRC_DENSE && kDMA) {
+      fetch_dma(cur, qn, (i + 3) & 3);  // tile i+3 straight into its LDS buffer
+    } else if constexpr (SRC == SRC_DENSE) {
       fetch_dense(IP{}, cur, qn);  // tile i+4 into slot (i+4)%2 (one slot: tile i+3, after the commit)
     } else {
       fetch_plaid(IP{}, q4);       // tile i+4, codes from slot (i+4)%2
@@ -888,7 +959,7 @@ __global__ void __launch_bounds__(W * 64)
     }
     if (i >= 1 && qm1.docend) {
       doc_end(qm1.k);
-      if ((nend & 7) == 0) flush_half = ((nend >> 3) - 1) & 1;
+      if ((nend % HSLOT) == 0) flush_half = ((nend / HSLOT) - 1) & 1;
     }
     qm1 = q0;
     q0 = q1;
@@ -908,7 +979,17 @@ __global__ void __launch_bounds__(W * 64)
     buf_x = buf_a;
     buf_a = buf_a == 2 ? 0 : buf_a + 1;
     buf_c = buf_c == 2 ? 0 : buf_c + 1;
-    __syncthreads();
+    if constexpr (kDMA) {
+      // Tile i+1 must have landed before any wave reads it: this wave's DMA
+      // of tile i+1 is older than those of tiles i+2 and i+3 (2 * NCH
+      // instructions), and loads complete in order. The barrier has no
+      // memory fence (a fence would wait for all DMA); the clobber keeps the
+      // compiler from moving LDS accesses across it.
+      static_assert(NCH == 2, "vmcnt below assumes 2 DMA instructions per wave and tile");
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+      __syncthreads();
+    }
   };
   // iterations 0..ntiles: iteration ntiles only finishes tile ntiles-1 (its
   // MFMA, commit and fetch work on empty tiles and are discarded)
@@ -919,8 +1000,10 @@ __global__ void __launch_bounds__(W * 64)
     if (i + 2 > ntiles) break;
   }
   // remaining finished docs: the due half (if any) and the partial half
-  if (flush_half >= 0) flush(flush_half * 8, 8);
-  if (nend & 7) flush(nend & ~7, nend & 7);
+  if (flush_half >= 0) flush(flush_half * HSLOT, HSLOT);
+  if (nend % HSLOT) flush(nend - nend % HSLOT, nend % HSLOT);
+  // no DMA may still be writing this workgroup's LDS when it exits
+  if constexpr (kDMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 template <int EK, int DPAD, int W, int NSUB, int SRC, int CD, int FEAT>
 int launch_one(const Params& p, int64_t nblocks, hipStream_t s) {

@@ -56,13 +56,19 @@ enum { F_MASK = 1, F_TS = 2, F_NORM = 4, F_CU = 8, F_ALL = 15, F_ARGMAX = 16, F_
 // barrier wait are covered by the other's MFMAs.
 template <int EK, int W, int NSUB, int SRC, int FEAT>
 constexpr bool two_wg_per_cu() {
-  return W == 4 && NSUB == 4 && SRC == SRC_DENSE && (EK == EK_BF16 || EK == EK_F16) &&
+  return W == 4 && NSUB == 4 && SRC == SRC_DENSE && (EK == EK_BF16 || EK == EK_F16 || EK == EK_FP8) &&
          (FEAT & (F_ARGMAX | F_NORM | F_TS | F_MASK)) == 0;
+}
+// Workgroups per CU of those kernels (fp8 would nearly fit three, but spills
+// at 168 VGPRs and measures slower).
+template <int EK, int W, int NSUB, int SRC, int FEAT>
+constexpr int wg_per_cu() {
+  return two_wg_per_cu<EK, W, NSUB, SRC, FEAT>() ? 2 : 1;
 }
 
 template <int EK, int DPAD, int W, int NSUB, int SRC, int CD, int FEAT>
 __global__ void __launch_bounds__(W * 64)
-    __attribute__((amdgpu_waves_per_eu(two_wg_per_cu<EK, W, NSUB, SRC, FEAT>() ? 2 : 1)))
+    __attribute__((amdgpu_waves_per_eu(wg_per_cu<EK, W, NSUB, SRC, FEAT>())))
     maxsim_kernel(const Params p) {
   using T = KT<EK, DPAD>;
   constexpr int NT = W * 64;
@@ -644,16 +650,21 @@ __global__ void __launch_bounds__(W * 64)
         else
           return (const u32x4*)(A + ks * T::FRAG_B);
       };
-      u32x4 a3[3];
-      a3[0] = *afrag(0);
-      if constexpr (KS > 1) a3[1] = *afrag(1);
+      u32x4 a3[3][FV];
+      auto lda = [&](int slot, int ks) {
+        const u32x4* src = afrag(ks);
+#pragma unroll
+        for (int v = 0; v < FV; ++v) a3[slot][v] = src[v];
+      };
+      lda(0, 0);
+      if constexpr (KS > 1) lda(1, 1);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 2 < KS) a3[(ks + 2) % 3] = *afrag(ks + 2);
+        if (ks + 2 < KS) lda((ks + 2) % 3, ks + 2);
         __builtin_amdgcn_sched_barrier(kFence);
 #pragma unroll
         for (int sub = 0; sub < NSUB; ++sub)
-          acc[P][sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[P][sub], &a3[ks % 3], bq[sub][ks]);
+          acc[P][sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[P][sub], a3[ks % 3], bq[sub][ks]);
         __builtin_amdgcn_sched_barrier(kFence);
       }
       return;

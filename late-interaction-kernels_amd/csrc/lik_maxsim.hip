@@ -240,6 +240,11 @@ int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group,
     pl.W = 4;
     pl.NSUB = 4;
   }
+  // fp8: 4 x 4 at two workgroups per CU beats the one-workgroup 8 x 4
+  if (prefer_two_wg && pl.W == 8 && pl.NSUB == 4 && min_w <= 4 && dt == LIK_FP8_E4M3) {
+    pl.W = 4;
+    pl.NSUB = 4;
+  }
   // LIK_CFG="W,NSUB" forces a column-block configuration (tuning aid).
   if (const char* e = getenv("LIK_CFG")) {
     int w = 0, ns = 0;

@@ -253,6 +253,22 @@ int lik_topk_merge(const float* scores, int64_t rows, int64_t n, int64_t ld, int
                    int64_t prev_ld, int64_t k, int largest, float* out_scores, int64_t* out_idx,
                    int64_t out_ld, lik_stream_t stream);
 
+/*
+ * Top-k of rows of any width: the same selection and tie rule as
+ * lik_topk_merge, but n is unbounded (idx_base + n < 2^32). Rows wider than
+ * 4096 scores are reduced as a tree of workgroups (4096-score slices, then
+ * merges of k-key lists) in a workspace of
+ * lik_topk_select_workspace_size(rows, n, k) bytes (0 when n <= 4096).
+ * Replaces topk.py:41-86 / retrieve.py:278-305 for an unchunked call
+ * (chunk=None): one selection over all Nd scores per query instead of a
+ * sequence of per-chunk merges.
+ */
+size_t lik_topk_select_workspace_size(int64_t rows, int64_t n, int64_t k);
+int lik_topk_select(const float* scores, int64_t rows, int64_t n, int64_t ld, int64_t idx_base,
+                    const float* prev_scores, const int64_t* prev_idx, int64_t prev_k,
+                    int64_t prev_ld, int64_t k, int largest, float* out_scores, int64_t* out_idx,
+                    int64_t out_ld, void* workspace, size_t workspace_bytes, lik_stream_t stream);
+
 /* Library version string and the gfx target it was built for. */
 const char* lik_version(void);
 

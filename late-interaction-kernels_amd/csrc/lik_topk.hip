@@ -1,13 +1,21 @@
-// Chunked top-k merge and PLAID approximate scoring for gfx950.
+// Top-k selection and PLAID approximate scoring for gfx950.
 //
 // Top-k: each (score, index) candidate becomes one 64-bit key
 //   key = order(score) << 32 | ~index
 // where order() is the monotone float->uint32 map (descending scores map to
 // descending keys; for largest=False the score part is complemented). Keys
-// are unique, and "larger key" == "better score, then lower index", so the k
-// best candidates are exactly the k largest keys. One workgroup per row finds
-// the k-th largest key by an 8-pass MSB-first radix select over LDS-resident
-// keys (256-bin histograms), compacts the winners and bitonic-sorts them.
+// are unique and never 0 (indices stay below 2^32 - 1), and "larger key" ==
+// "better score, then lower index", so the k best candidates are exactly the
+// k largest keys and any grouping of the candidates selects the same set.
+//
+// One workgroup selects the kk largest of up to TK_MAX_KEYS LDS-resident keys
+// by an 8-pass MSB-first radix select (256-bin histograms), compacts the
+// winners and bitonic-sorts them. A row wider than one workgroup's share is
+// reduced as a tree: level 0 gives each TK_MAX_N-score slice of a row its own
+// workgroup, which writes its k best keys (0-padded) to a workspace; each
+// further level merges up to TK_MAX_KEYS / k such lists per workgroup, and the
+// level with one group left writes scores and indices. The running list
+// (prev_*) joins slice 0 at level 0.
 // This replaces topk.py:41-86 / retrieve.py:278-305 (torch.topk + cat +
 // gather per chunk) and pins the tie order torch.topk leaves unspecified.
 #include "lik_common.h"
@@ -15,7 +23,7 @@
 namespace lik {
 
 constexpr int TK_THREADS = 256;
-constexpr int TK_MAX_N = 4096;  // new candidates per call
+constexpr int TK_MAX_N = 4096;  // scores per level-0 group
 constexpr int TK_MAX_K = 1024;
 constexpr int TK_MAX_KEYS = TK_MAX_N + TK_MAX_K;
 
@@ -34,102 +42,147 @@ __device__ __forceinline__ uint64_t make_key(float s, uint32_t idx, int largest)
   return ((uint64_t)o << 32) | (uint64_t)(~idx);
 }
 
-__global__ void __launch_bounds__(TK_THREADS)
-    topk_merge_kernel(const float* __restrict__ scores, int64_t n, int64_t ld, int64_t idx_base,
-                      const float* prev_s, const int64_t* prev_i, int64_t pk, int64_t pld, int64_t k,
-                      int largest, float* out_s, int64_t* out_i, int64_t old) {
+struct TopkArgs {
+  // level 0: scores [rows, n] (row stride ld), doc index = idx_base + column
+  const float* scores;
+  int64_t n, ld, idx_base;
+  const float* prev_s;
+  const int64_t* prev_i;
+  int64_t pk, pld;
+  // later levels: per row nin keys (lists of k) at keys_in + row * nin
+  const uint64_t* keys_in;
+  int64_t nin;
+  int64_t k;
+  int largest;
+  int groups;        // groups per row at this level
+  int64_t per_group; // scores (level 0) or keys (later levels) per group
+  // output: keys_out + (row * groups + g) * k when groups > 1, else scores/indices
+  uint64_t* keys_out;
+  float* out_s;
+  int64_t* out_i;
+  int64_t old;
+};
+
+template <bool FROM_KEYS>
+__global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(TopkArgs a) {
   __shared__ uint64_t s_keys[TK_MAX_KEYS];
   __shared__ uint64_t s_sel[TK_MAX_K];
   __shared__ uint32_t s_hist[256];
   __shared__ uint64_t s_prefix, s_pmask;
-  __shared__ int s_kk, s_done, s_cnt;
+  __shared__ int s_kk, s_done, s_cnt, s_real;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int64_t row = blockIdx.x;
-  const int total = (int)(pk + n);
+  const int64_t row = blockIdx.x / a.groups;
+  const int g = (int)(blockIdx.x - row * a.groups);
+  if (tid == 0) s_real = 0;
+  __syncthreads();
 
-  for (int i = tid; i < total; i += TK_THREADS) {
-    uint64_t key;
-    if (i < pk) {
-      key = make_key(prev_s[row * pld + i], (uint32_t)prev_i[row * pld + i], largest);
-    } else {
-      const int64_t c = i - pk;
-      key = make_key(scores[row * ld + c], (uint32_t)(idx_base + c), largest);
+  int total;
+  if (!FROM_KEYS) {
+    const int64_t c0 = (int64_t)g * a.per_group;
+    const int64_t nn = min(a.per_group, a.n - c0);
+    const int pk = g == 0 ? (int)a.pk : 0;
+    total = pk + (int)nn;
+    for (int i = tid; i < total; i += TK_THREADS) {
+      uint64_t key;
+      if (i < pk) {
+        key = make_key(a.prev_s[row * a.pld + i], (uint32_t)a.prev_i[row * a.pld + i], a.largest);
+      } else {
+        const int64_t c = c0 + (i - pk);
+        key = make_key(a.scores[row * a.ld + c], (uint32_t)(a.idx_base + c), a.largest);
+      }
+      s_keys[i] = key;
     }
-    s_keys[i] = key;
+    if (tid == 0) s_real = total;
+  } else {
+    const int64_t c0 = (int64_t)g * a.per_group;
+    total = (int)min(a.per_group, a.nin - c0);
+    const uint64_t* src = a.keys_in + row * a.nin + c0;
+    for (int i0 = 0; i0 < total; i0 += TK_THREADS) {
+      const int i = i0 + tid;
+      const uint64_t key = i < total ? src[i] : 0;
+      if (i < total) s_keys[i] = key;
+      const uint64_t nz = __ballot(key != 0);
+      if (lane == 0 && nz) atomicAdd(&s_real, __popcll(nz));
+    }
   }
   if (tid == 0) {
     s_prefix = 0;
     s_pmask = 0;
-    s_kk = (int)k;
     s_done = 0;
     s_cnt = 0;
   }
   __syncthreads();
+  const int kk_sel = (int)min(a.k, (int64_t)s_real);
+  if (tid == 0) s_kk = kk_sel;
+  __syncthreads();
 
-  for (int pass = 0; pass < 8; ++pass) {
-    const int shift = 56 - 8 * pass;
-    s_hist[tid] = 0;  // TK_THREADS == 256 bins
-    __syncthreads();
+  if (kk_sel > 0) {
+    for (int pass = 0; pass < 8; ++pass) {
+      const int shift = 56 - 8 * pass;
+      s_hist[tid] = 0;  // TK_THREADS == 256 bins
+      __syncthreads();
+      const uint64_t prefix = s_prefix, pmask = s_pmask;
+      for (int i = tid; i < total; i += TK_THREADS) {
+        const uint64_t key = s_keys[i];
+        if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (wv == 0) {
+        // lane l owns bins 255-4l .. 252-4l (descending); find the bin holding
+        // the kk-th largest remaining key with a wavefront inclusive scan.
+        uint32_t c[4], local = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c[j] = s_hist[255 - 4 * lane - j];
+          local += c[j];
+        }
+        uint32_t incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t v = __shfl_up(incl, o);
+          if (lane >= o) incl += v;
+        }
+        const uint32_t excl = incl - local;
+        const uint32_t kk = (uint32_t)s_kk;
+        if (excl < kk && kk <= incl) {
+          uint32_t cum = excl;
+          int bin = 0;
+          uint32_t rem = 0, cnt = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (cnt == 0 && cum + c[j] >= kk) {
+              bin = 255 - 4 * lane - j;
+              rem = kk - cum;
+              cnt = c[j];
+            }
+            cum += c[j];
+          }
+          s_prefix = prefix | ((uint64_t)bin << shift);
+          s_pmask = pmask | ((uint64_t)0xffu << shift);
+          s_kk = (int)rem;
+          s_done = (cnt == rem) ? 1 : 0;
+        }
+      }
+      __syncthreads();
+      if (s_done) break;
+    }
+
+    // winners: (key & pmask) >= prefix; exactly kk_sel of them (keys are
+    // unique and the kk_sel-th largest is a real key, above every 0 pad)
     const uint64_t prefix = s_prefix, pmask = s_pmask;
     for (int i = tid; i < total; i += TK_THREADS) {
       const uint64_t key = s_keys[i];
-      if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    if (wv == 0) {
-      // lane l owns bins 255-4l .. 252-4l (descending); find the bin holding
-      // the kk-th largest remaining key with a wavefront inclusive scan.
-      uint32_t c[4], local = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = s_hist[255 - 4 * lane - j];
-        local += c[j];
+      if ((key & pmask) >= prefix) {
+        const int pos = atomicAdd(&s_cnt, 1);
+        if (pos < TK_MAX_K) s_sel[pos] = key;
       }
-      uint32_t incl = local;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o);
-        if (lane >= o) incl += v;
-      }
-      const uint32_t excl = incl - local;
-      const uint32_t kk = (uint32_t)s_kk;
-      if (excl < kk && kk <= incl) {
-        uint32_t cum = excl;
-        int bin = 0;
-        uint32_t rem = 0, cnt = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (cnt == 0 && cum + c[j] >= kk) {
-            bin = 255 - 4 * lane - j;
-            rem = kk - cum;
-            cnt = c[j];
-          }
-          cum += c[j];
-        }
-        s_prefix = prefix | ((uint64_t)bin << shift);
-        s_pmask = pmask | ((uint64_t)0xffu << shift);
-        s_kk = (int)rem;
-        s_done = (cnt == rem) ? 1 : 0;
-      }
-    }
-    __syncthreads();
-    if (s_done) break;
-  }
-
-  // winners: (key & pmask) >= prefix; exactly k of them
-  const uint64_t prefix = s_prefix, pmask = s_pmask;
-  for (int i = tid; i < total; i += TK_THREADS) {
-    const uint64_t key = s_keys[i];
-    if ((key & pmask) >= prefix) {
-      const int pos = atomicAdd(&s_cnt, 1);
-      if (pos < TK_MAX_K) s_sel[pos] = key;
     }
   }
   __syncthreads();
   int P = 1;
-  while (P < k) P <<= 1;
-  for (int i = (int)k + tid; i < P; i += TK_THREADS) s_sel[i] = 0;
+  while (P < kk_sel) P <<= 1;
+  for (int i = kk_sel + tid; i < P; i += TK_THREADS) s_sel[i] = 0;
   __syncthreads();
   // bitonic sort, descending
   for (int size = 2; size <= P; size <<= 1) {
@@ -138,24 +191,41 @@ __global__ void __launch_bounds__(TK_THREADS)
         const int lo = 2 * i - (i & (stride - 1));
         const int hi = lo + stride;
         const bool desc = (lo & size) == 0;
-        const uint64_t a = s_sel[lo], b = s_sel[hi];
-        if ((a < b) == desc) {
-          s_sel[lo] = b;
-          s_sel[hi] = a;
+        const uint64_t x = s_sel[lo], y = s_sel[hi];
+        if ((x < y) == desc) {
+          s_sel[lo] = y;
+          s_sel[hi] = x;
         }
       }
       __syncthreads();
     }
   }
-  for (int i = tid; i < k; i += TK_THREADS) {
-    const uint64_t key = s_sel[i];
-    uint32_t o = (uint32_t)(key >> 32);
-    if (!largest) o = ~o;
-    out_s[row * old + i] = order_float(o);
-    out_i[row * old + i] = (int64_t)(uint32_t)(~(uint32_t)key);
+  if (a.keys_out) {
+    uint64_t* dst = a.keys_out + ((int64_t)blockIdx.x) * a.k;
+    for (int i = tid; i < a.k; i += TK_THREADS) dst[i] = i < kk_sel ? s_sel[i] : 0;
+  } else {
+    for (int i = tid; i < kk_sel; i += TK_THREADS) {
+      const uint64_t key = s_sel[i];
+      uint32_t o = (uint32_t)(key >> 32);
+      if (!a.largest) o = ~o;
+      a.out_s[row * a.old + i] = order_float(o);
+      a.out_i[row * a.old + i] = (int64_t)(uint32_t)(~(uint32_t)key);
+    }
   }
 }
 
+// Tree shape for one call: level-0 groups, lists merged per later group, and
+// the workspace (two ping-pong key buffers of rows * groups0 * k keys).
+struct TopkPlan {
+  int64_t g0, merge, ws_bytes;
+};
+inline TopkPlan topk_plan(int64_t rows, int64_t n, int64_t k) {
+  TopkPlan t;
+  t.g0 = n <= TK_MAX_N ? 1 : (n + TK_MAX_N - 1) / TK_MAX_N;
+  t.merge = k > 0 ? TK_MAX_KEYS / k : 1;
+  t.ws_bytes = t.g0 > 1 ? 2 * rows * t.g0 * k * (int64_t)sizeof(uint64_t) : 0;
+  return t;
+}
 // PLAID approximate score, plaid.py:28-79 semantics: one wavefront per doc,
 // lane s < Lq keeps the running max of qcs[code, s] over the doc's tokens.
 __global__ void __launch_bounds__(256)
@@ -192,23 +262,85 @@ using namespace lik;
 
 extern "C" {
 
-int lik_topk_merge(const float* scores, int64_t rows, int64_t n, int64_t ld, int64_t idx_base,
-                   const float* prev_scores, const int64_t* prev_idx, int64_t prev_k, int64_t prev_ld,
-                   int64_t k, int largest, float* out_scores, int64_t* out_idx, int64_t out_ld,
-                   lik_stream_t stream) {
+static int topk_validate(const float* scores, int64_t rows, int64_t n, int64_t idx_base, const float* prev_scores,
+                         const int64_t* prev_idx, int64_t prev_k, int64_t k, float* out_scores, int64_t* out_idx) {
   if (rows < 0 || n < 0 || prev_k < 0 || k < 0) return LIK_ERR_INVALID;
   if (rows == 0 || k == 0) return LIK_OK;
-  if (n > TK_MAX_N || k > TK_MAX_K || prev_k > TK_MAX_K) return LIK_ERR_UNSUPPORTED;
+  if (k > TK_MAX_K || prev_k > TK_MAX_K) return LIK_ERR_UNSUPPORTED;
   if (k > prev_k + n) return LIK_ERR_INVALID;
   if (n > 0 && !scores) return LIK_ERR_INVALID;
   if (prev_k > 0 && (!prev_scores || !prev_idx)) return LIK_ERR_INVALID;
   if (!out_scores || !out_idx) return LIK_ERR_INVALID;
   if (idx_base < 0 || idx_base + n > 0xffffffffLL) return LIK_ERR_UNSUPPORTED;
-  if (rows > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(topk_merge_kernel, dim3((unsigned)rows), dim3(TK_THREADS), 0, (hipStream_t)stream, scores,
-                     n, ld, idx_base, prev_scores, prev_idx, prev_k, prev_ld, k, largest, out_scores, out_idx,
-                     out_ld);
+  return 1;
+}
+
+static int topk_run(const float* scores, int64_t rows, int64_t n, int64_t ld, int64_t idx_base,
+                    const float* prev_scores, const int64_t* prev_idx, int64_t prev_k, int64_t prev_ld, int64_t k,
+                    int largest, float* out_scores, int64_t* out_idx, int64_t out_ld, void* ws, hipStream_t st) {
+  const TopkPlan t = topk_plan(rows, n, k);
+  if (rows * t.g0 > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  TopkArgs a{};
+  a.scores = scores;
+  a.n = n;
+  a.ld = ld;
+  a.idx_base = idx_base;
+  a.prev_s = prev_scores;
+  a.prev_i = prev_idx;
+  a.pk = prev_k;
+  a.pld = prev_ld;
+  a.k = k;
+  a.largest = largest;
+  a.groups = (int)t.g0;
+  a.per_group = TK_MAX_N;
+  a.out_s = out_scores;
+  a.out_i = out_idx;
+  a.old = out_ld;
+  uint64_t* bufs[2] = {(uint64_t*)ws, ws ? (uint64_t*)ws + rows * t.g0 * k : nullptr};
+  a.keys_out = t.g0 > 1 ? bufs[0] : nullptr;
+  hipLaunchKernelGGL(topk_select_kernel<false>, dim3((unsigned)(rows * t.g0)), dim3(TK_THREADS), 0, st, a);
+  int64_t lists = t.g0;
+  int cur = 0;
+  while (lists > 1) {
+    const int64_t groups = (lists + t.merge - 1) / t.merge;
+    a.keys_in = bufs[cur];
+    a.nin = lists * k;
+    a.groups = (int)groups;
+    a.per_group = t.merge * k;
+    a.keys_out = groups > 1 ? bufs[cur ^ 1] : nullptr;
+    hipLaunchKernelGGL(topk_select_kernel<true>, dim3((unsigned)(rows * groups)), dim3(TK_THREADS), 0, st, a);
+    lists = groups;
+    cur ^= 1;
+  }
   return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+}
+
+int lik_topk_merge(const float* scores, int64_t rows, int64_t n, int64_t ld, int64_t idx_base,
+                   const float* prev_scores, const int64_t* prev_idx, int64_t prev_k, int64_t prev_ld,
+                   int64_t k, int largest, float* out_scores, int64_t* out_idx, int64_t out_ld,
+                   lik_stream_t stream) {
+  const int v = topk_validate(scores, rows, n, idx_base, prev_scores, prev_idx, prev_k, k, out_scores, out_idx);
+  if (v != 1) return v;
+  if (n > TK_MAX_N) return LIK_ERR_UNSUPPORTED;
+  return topk_run(scores, rows, n, ld, idx_base, prev_scores, prev_idx, prev_k, prev_ld, k, largest, out_scores,
+                  out_idx, out_ld, nullptr, (hipStream_t)stream);
+}
+
+size_t lik_topk_select_workspace_size(int64_t rows, int64_t n, int64_t k) {
+  if (rows < 0 || n < 0 || k < 0) return 0;
+  return (size_t)topk_plan(rows, n, k).ws_bytes;
+}
+
+int lik_topk_select(const float* scores, int64_t rows, int64_t n, int64_t ld, int64_t idx_base,
+                    const float* prev_scores, const int64_t* prev_idx, int64_t prev_k, int64_t prev_ld, int64_t k,
+                    int largest, float* out_scores, int64_t* out_idx, int64_t out_ld, void* workspace,
+                    size_t workspace_bytes, lik_stream_t stream) {
+  const int v = topk_validate(scores, rows, n, idx_base, prev_scores, prev_idx, prev_k, k, out_scores, out_idx);
+  if (v != 1) return v;
+  const TopkPlan t = topk_plan(rows, n, k);
+  if (t.ws_bytes > 0 && (!workspace || workspace_bytes < (size_t)t.ws_bytes)) return LIK_ERR_WORKSPACE;
+  return topk_run(scores, rows, n, ld, idx_base, prev_scores, prev_idx, prev_k, prev_ld, k, largest, out_scores,
+                  out_idx, out_ld, workspace, (hipStream_t)stream);
 }
 
 int lik_plaid_approx_score(const float* qcs, int64_t n_centroids, int64_t lq, int64_t qcs_stride_c,

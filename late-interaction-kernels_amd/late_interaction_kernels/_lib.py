@@ -56,6 +56,8 @@ EXPORTED_SYMBOLS = (
     "lik_plaid_approx_score",
     "lik_residual_reverse_bits",
     "lik_topk_merge",
+    "lik_topk_select",
+    "lik_topk_select_workspace_size",
     "lik_version",
     "lik_timing_begin",
     "lik_timing_end",
@@ -164,6 +166,11 @@ def load() -> ctypes.CDLL:
     lib.lik_topk_merge.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_int, _p, _p,
                                    _i64, _p]
     lib.lik_topk_merge.restype = ctypes.c_int
+    lib.lik_topk_select.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_int, _p, _p,
+                                    _i64, _p, ctypes.c_size_t, _p]
+    lib.lik_topk_select.restype = ctypes.c_int
+    lib.lik_topk_select_workspace_size.argtypes = [_i64, _i64, _i64]
+    lib.lik_topk_select_workspace_size.restype = ctypes.c_size_t
     lib.lik_version.argtypes = []
     lib.lik_version.restype = ctypes.c_char_p
     lib.lik_timing_begin.argtypes = []

@@ -1,7 +1,8 @@
 """Chunked top-k MaxSim (reference topk.py:12-91), with a fused HIP merge.
 
 Each document chunk is scored by the MaxSim kernel into a ``[Nq, chunk]``
-buffer, then ``lik_topk_merge`` folds it into the running ``[Nq, k]`` list.
+buffer, then ``lik_topk_select`` folds it into the running ``[Nq, k]`` list
+in one call, however wide the chunk (a tree of workgroups for wide rows).
 Ties are broken by the lower document index, so chunked and unchunked calls
 return identical results (torch.topk leaves tie order unspecified).
 """
@@ -15,7 +16,6 @@ import torch
 from . import _lib
 from ._core import dense_maxsim, unify_dtype
 
-TOPK_MAX_N = 4096  # new candidates per merge call
 TOPK_MAX_K = 1024  # largest k the fused merge handles
 
 
@@ -49,22 +49,23 @@ def topk_update(
         return _merge_sorted_fallback(s_all, i_all, min(k, s_all.shape[-1]), largest)
     lib = _lib.load()
     cs = chunk_scores.contiguous() if chunk_scores.stride(-1) != 1 else chunk_scores
-    for c0 in range(0, n, TOPK_MAX_N):
-        nn = min(TOPK_MAX_N, n - c0)
-        pk = 0 if run_s is None else run_s.shape[-1]
-        kk = min(k, pk + nn)
-        out_s = torch.empty(R, kk, device=dev, dtype=torch.float32)
-        out_i = torch.empty(R, kk, device=dev, dtype=torch.int64)
-        sub = cs[:, c0 : c0 + nn]
-        with torch.cuda.device(dev):
-            rc = lib.lik_topk_merge(
-                sub.data_ptr(), R, nn, cs.stride(0), idx_base + c0,
-                _lib.ptr(run_s), _lib.ptr(run_i), pk, run_s.stride(0) if run_s is not None else 0,
-                kk, 1 if largest else 0, out_s.data_ptr(), out_i.data_ptr(), kk, _lib.stream_of(out_s),
-            )
-        _lib.check(rc, "lik_topk_merge")
-        run_s, run_i = out_s, out_i
-    return run_s, run_i
+    pk = 0 if run_s is None else run_s.shape[-1]
+    kk = min(k, pk + n)
+    out_s = torch.empty(R, kk, device=dev, dtype=torch.float32)
+    out_i = torch.empty(R, kk, device=dev, dtype=torch.int64)
+    if R == 0 or kk == 0:
+        return out_s, out_i
+    nws = lib.lik_topk_select_workspace_size(R, n, kk)
+    ws = torch.empty(nws, device=dev, dtype=torch.uint8) if nws else None
+    with torch.cuda.device(dev):
+        rc = lib.lik_topk_select(
+            cs.data_ptr(), R, n, cs.stride(0), idx_base,
+            _lib.ptr(run_s), _lib.ptr(run_i), pk, run_s.stride(0) if run_s is not None else 0,
+            kk, 1 if largest else 0, out_s.data_ptr(), out_i.data_ptr(), kk, _lib.ptr(ws), nws,
+            _lib.stream_of(out_s),
+        )
+    _lib.check(rc, "lik_topk_select")
+    return out_s, out_i
 
 
 def maxsim_topk(

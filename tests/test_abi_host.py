@@ -74,6 +74,14 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     rc = lib.lik_maxsim(ctypes.byref(ok), ctypes.byref(ok), 0, ctypes.c_float(1.0), None, 0, 0, None, 0, None)
     assert rc == _lib.LIK_OK
     assert lib.lik_topk_merge(None, 4, 8, 8, 0, None, None, 0, 0, 2048, 1, None, None, 0, None) != _lib.LIK_OK
+    # tree select: no workspace up to 4096 scores a row, two ping-pong key
+    # buffers of rows * ceil(n / 4096) * k keys above
+    L = _lib.load()
+    assert L.lik_topk_select_workspace_size(8, 4096, 100) == 0
+    assert L.lik_topk_select_workspace_size(2, 4097, 100) == 2 * 2 * 2 * 100 * 8
+    assert L.lik_topk_select_workspace_size(1, 1 << 20, 100) == 2 * 256 * 100 * 8
+    rc = L.lik_topk_select(1, 1, 1 << 20, 1 << 20, 0, None, None, 0, 0, 100, 1, 1, 1, 100, None, 0, None)
+    assert rc == _lib.LIK_ERR_WORKSPACE
 
 
 def test_value_errors_match_the_reference_contract():

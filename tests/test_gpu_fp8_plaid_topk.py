@@ -171,7 +171,8 @@ def test_plaid_empty_corpus():
 
 @pytest.mark.parametrize("largest", [True, False])
 @pytest.mark.parametrize("n,k,chunk", [(100, 10, None), (5000, 100, 4096), (9000, 1000, 2048), (37, 37, 5),
-                                       (300, 7, 1)])
+                                       (300, 7, 1), (300000, 100, None), (70000, 1000, None), (20001, 1, None),
+                                       (50000, 64, 20000), (4097, 4097 - 4096, 4096)])
 def test_topk_merge_bit_exact(largest, n, k, chunk):
     from late_interaction_kernels.topk import topk_update
 
@@ -188,6 +189,35 @@ def test_topk_merge_bit_exact(largest, n, k, chunk):
     ws, wi = O.topk_stable(s.numpy(), k, largest=largest)
     np.testing.assert_array_equal(run_i.cpu().numpy(), wi)
     np.testing.assert_array_equal(run_s.cpu().numpy(), ws)
+
+
+def test_topk_merge_entry_point():
+    """lik_topk_merge keeps its one-workgroup-per-row contract (n <= 4096)."""
+    from late_interaction_kernels import _lib
+
+    _case("topk merge entry point")
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(5)
+    prev = torch.sort(torch.randint(0, 20, (3, 50), generator=g).float(), dim=-1, descending=True).values
+    prev_i = torch.arange(10000, 10050).expand(3, 50).contiguous()
+    s = torch.randint(0, 20, (3, 4096), generator=g).float()
+    out_s = torch.empty(3, 80, device="cuda")
+    out_i = torch.empty(3, 80, device="cuda", dtype=torch.int64)
+    ps, pi, sc = prev.cuda(), prev_i.cuda(), s.cuda()
+    rc = lib.lik_topk_merge(sc.data_ptr(), 3, 4096, 4096, 0, ps.data_ptr(), pi.data_ptr(), 50, 50, 80, 1,
+                            out_s.data_ptr(), out_i.data_ptr(), 80, _lib.stream_of(out_s))
+    assert rc == _lib.LIK_OK
+    rc = lib.lik_topk_merge(sc.data_ptr(), 3, 4097, 4096, 0, None, None, 0, 0, 80, 1,
+                            out_s.data_ptr(), out_i.data_ptr(), 80, _lib.stream_of(out_s))
+    assert rc == _lib.LIK_ERR_UNSUPPORTED
+    torch.cuda.synchronize()
+    all_s = torch.cat([prev, s], -1).numpy()
+    all_i = torch.cat([prev_i, torch.arange(4096).expand(3, 4096)], -1).numpy()
+    # stable order on (score desc, index asc)
+    for r in range(3):
+        order = np.lexsort((all_i[r], -all_s[r]))[:80]
+        np.testing.assert_array_equal(out_i[r].cpu().numpy(), all_i[r][order])
+        np.testing.assert_array_equal(out_s[r].cpu().numpy(), all_s[r][order])
 
 
 def test_retrieve_matches_oracle_on_gpu_scores():

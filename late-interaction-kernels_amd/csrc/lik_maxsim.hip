@@ -710,6 +710,14 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
     p.LU = (int)Q->len;
     const int nsub = 1;  // one query per wavefront
     p.ngroups = (Q->n + nsub - 1) / nsub;
+    // LDS-gather variant: 16-byte aligned residual rows, a residual tile no
+    // larger than the padded rows' (LIK_PLAID_STREAM=1 keeps the per-lane
+    // variant, a tuning aid)
+    {
+      const int64_t rsb = (int64_t)sdp * docs->nbits / 8, nr = (32 * rsb + 1023) / 1024;
+      p.gather = ((uintptr_t)docs->residuals) % 16 == 0 && docs->res_stride_tok % 16 == 0 &&
+                 32 * docs->res_stride_tok <= nr * 1024 && !(se && se[0] == '1');
+    }
     // ~16k wavefronts over the corpus, at most 512 docs each
     int64_t R = (docs->n + 16383) / 16384;
     p.R = (int)(R < 1 ? 1 : (R > 512 ? 512 : R));

@@ -51,6 +51,7 @@ struct Params {
   int R;             // docs per workgroup
   int64_t NR;        // doc ranges per group
   int xcd_map;
+  int gather;     // PLAID stream kernel: LDS-gather variant
   int normalize;  // bit 0: L2-normalise query tokens; bit 1: doc tokens
   float out_scale;
   float* out;

@@ -322,9 +322,314 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   }
 }
 
+// Gather variant of the stream kernel (same arithmetic, bitwise the same
+// scores). Centroid rows and residual bytes go straight from memory into a
+// per-wave LDS stage (buffer_load ... lds), 16 lanes per 256-byte row, so
+// one load instruction covers 4 whole rows (8 cache lines) instead of 64 half
+// rows in 64 lines; the address path, not the memory, bounded the per-lane
+// gathers. Each 16-byte chunk of row R sits at slot chunk ^ (R % LPR) so
+// that a lane's fragment reads (row l32, chunk h*KS + ks) spread over all
+// banks. The decoded fp32 half row stays in VGPRs (no staging registers
+// now), so the decode runs once. Two LDS stages per wave: the gather of tile
+// c+1 is in flight while tile c is decoded and scored.
+//
+// Waits are explicit: the compiler does not count the inline-asm gathers,
+// so every iteration starts with vmcnt(0) (stage c and code c+1 landed;
+// this wave issued nothing since) and lgkmcnt(0) (tile c-1's LDS reads are
+// done before its stage is overwritten). Doc scores are stored one
+// iteration late, after that wait, so a store never holds up a gather.
+template <int EK, int DPAD, int CD, int NBITS, bool FULLD>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+    plaid_gather_kernel(const Params p) {
+  using T = KT<EK, DPAD>;
+  constexpr int KS = T::KSTEPS;            // 8-element chunks per lane (= MFMA k-steps)
+  constexpr int HALF = DPAD / 2;
+  constexpr int RB = DPAD * 2;             // centroid row bytes (bf16 / fp16)
+  constexpr int LPR = RB / 16;             // gather lanes per row
+  constexpr int RPI = 64 / LPR;            // rows per gather instruction
+  constexpr int NI = 32 / RPI;             // centroid gather instructions per tile
+  constexpr int RSB = DPAD * NBITS / 8;    // residual bytes per (padded) row
+  constexpr int NR = (32 * RSB + 1023) / 1024;  // residual gather instructions per tile
+  constexpr int RBL = HALF * NBITS / 8;    // residual bytes per lane
+  constexpr int RVL = RBL / 4;
+  constexpr int FPB = 8 / NBITS;
+  constexpr int CBYTES = 32 * RB;
+  constexpr int STB = CBYTES + NR * 1024;  // one stage: 32 centroid rows + residual tile
+  static_assert(RBL % 4 == 0 && CD != EK_F32, "gather layout");
+  constexpr float NEG_INF = -__builtin_huge_valf();
+
+  __shared__ __attribute__((aligned(16))) float s_lut[256 * FPB];
+  __shared__ __attribute__((aligned(1024))) char s_st[4][2][STB];
+  for (int i = threadIdx.x; i < 256 * FPB; i += 256) {
+    const int v = i / FPB, k = i % FPB;
+    uint32_t bc = ((uint32_t)v >> (k * NBITS)) & ((1u << NBITS) - 1u);
+    bc = bc < (uint32_t)p.pl.nb ? bc : (uint32_t)(p.pl.nb - 1);
+    s_lut[i] = p.pl.bw[bc];
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wl = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t wv = (int64_t)blockIdx.x * 4 + wl;
+  const int64_t g = wv / p.NR, r = wv - g * p.NR;
+  if (g >= p.ngroups) return;  // wave-uniform, after the only barrier
+
+  // ---- query: token l32 of query g in column l32 ----
+  u32x4 bq[KS];
+  float qsc;
+  const bool f_norm_q = (p.normalize & 1) != 0;
+  const bool f_norm_d = (p.normalize & 2) != 0;
+  {
+    const bool valid = g < p.q.n && l32 < seq_len(p.q, g);
+    const char* rowp = valid ? seq_row0(p.q, g) + (int64_t)l32 * p.q.sl_b : nullptr;
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int e = h * HALF + ks * 8;
+      bq[ks] = (valid && e < p.q.dim) ? *(const u32x4*)(rowp + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
+      if (f_norm_q) ss += chunk_sumsq<EK>(bq[ks]);
+    }
+    ss += __shfl_xor(ss, 32);
+    qsc = valid ? (f_norm_q ? inv_norm(ss) : 1.f) : 0.f;
+  }
+
+  const int64_t j0 = r * p.R;
+  const int64_t j1 = j0 + p.R < p.pl.n ? j0 + p.R : p.pl.n;
+  auto dlen = [&](int64_t j) -> int64_t { return doc_len<SRC_PLAID>(p, j); };
+  auto dtok = [&](int64_t j) -> int64_t { return p.pl.cu ? (int64_t)p.pl.cu[j] : j * p.pl.codes_sn; };
+  auto store = [&](int64_t j, float v) {
+    if (g < p.q.n) ((__attribute__((address_space(1))) float*)p.out)[g * p.osq + j * p.osd] = v;
+  };
+  struct Tile {
+    int64_t j, tok;
+    int t, nv;
+  };
+  auto uni64 = [](int64_t x) -> int64_t {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
+  auto uni = [&](const Tile& t) -> Tile {
+    return Tile{uni64(t.j), uni64(t.tok), __builtin_amdgcn_readfirstlane(t.t), __builtin_amdgcn_readfirstlane(t.nv)};
+  };
+  auto open_doc = [&](int64_t j) -> Tile {
+    while (j < j1) {
+      const int64_t len = dlen(j);
+      if (len > 0) return uni(Tile{j, dtok(j), 0, (int)(len < 32 ? len : 32)});
+      if (lane == 0) store(j, 0.f);
+      ++j;
+    }
+    return Tile{-1, 0, 0, 0};
+  };
+  auto next_tile = [&](const Tile& c) -> Tile {
+    if (c.j < 0) return c;
+    const int64_t len = dlen(c.j);
+    const int64_t start = (int64_t)(c.t + 1) * 32;
+    if (start < len) {
+      const int64_t rem = len - start;
+      return uni(Tile{c.j, c.tok + 32, c.t + 1, (int)(rem < 32 ? rem : 32)});
+    }
+    return open_doc(c.j + 1);
+  };
+  auto load_code = [&](const Tile& d) -> int32_t {
+    if (d.j < 0) return 0;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.pl.codes + d.tok, (uint32_t)d.nv * 4u);
+    return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, l32 < d.nv ? (uint32_t)l32 * 4u : kOOB, 0, 0);
+  };
+  auto rsrc_words = [](const void* base, uint32_t nbytes) -> u32x4 {
+    const uint64_t b = (uint64_t)base;
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu),
+                 (uint32_t)__builtin_amdgcn_readfirstlane(nbytes), 0x00020000u};
+  };
+  const u32x4 dcent = rsrc_words(p.pl.cent, sat_u32(p.pl.ncent * p.pl.cent_sb));
+  auto lds_addr = [&](int st, int off) -> uint32_t {
+    return (uint32_t)__builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_st[wl][st][0]) + (uint32_t)off);
+  };
+  auto dma = [&](uint32_t lds, uint32_t voff, const u32x4& desc) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(desc)
+        : "memory");
+  };
+  // gather tile d (codes in lanes l32) into stage st
+  auto gather = [&](const Tile& d, int32_t code, int st) {
+    if (d.j < 0) return;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = i * RPI + lane / LPR;
+      const int chunk = (lane % LPR) ^ (row % LPR);
+      int64_t cd = __builtin_amdgcn_ds_bpermute(row * 4, code);
+      cd = (cd < 0 || cd >= p.pl.ncent) ? 0 : cd;
+      const uint32_t voff = row < d.nv ? (uint32_t)(cd * p.pl.cent_sb) + (uint32_t)(chunk * 16) : kOOB;
+      dma(lds_addr(st, i * 1024), voff, dcent);
+    }
+    const u32x4 dres = rsrc_words(p.pl.res + d.tok * p.pl.res_st, (uint32_t)d.nv * (uint32_t)p.pl.res_st);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) dma(lds_addr(st, CBYTES + i * 1024), (uint32_t)(i * 1024 + lane * 16), dres);
+  };
+
+  float m = NEG_INF;
+  int64_t pend_j = -1;
+  float pend_v = 0.f;
+
+  auto compute = [&](const Tile& d, int st) {
+    const char* stage = &s_st[wl][st][0];
+    uint32_t rw[RVL];
+    {
+      const char* rp = stage + CBYTES + l32 * (int)p.pl.res_st + h * RBL;
+      if constexpr (RVL % 4 == 0) {
+#pragma unroll
+        for (int v = 0; v < RVL / 4; ++v) {
+          const u32x4 t = *(const u32x4*)(rp + 16 * v);
+          rw[4 * v] = t[0]; rw[4 * v + 1] = t[1]; rw[4 * v + 2] = t[2]; rw[4 * v + 3] = t[3];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < RVL / 2; ++v) {
+          const uint2 t = *(const uint2*)(rp + 8 * v);
+          rw[2 * v] = t.x; rw[2 * v + 1] = t.y;
+        }
+      }
+    }
+    float x[KS][8];
+    float cs[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cc = h * KS + ks;
+      const u32x4 cw = *(const u32x4*)(stage + l32 * RB + ((cc ^ (l32 % LPR)) * 16));
+      float bw[8];
+#pragma unroll
+      for (int b = 0; b < 8 / FPB; ++b) {
+        const int byte_i = (ks * 8) / FPB + b;
+        const uint32_t byv = (rw[byte_i >> 2] >> ((byte_i & 3) * 8)) & 0xffu;
+        if constexpr (FPB == 4) {
+          const f32x4 t = *(const f32x4*)&s_lut[byv * 4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) bw[b * 4 + k] = t[k];
+        } else if constexpr (FPB == 2) {
+          const float2 t = *(const float2*)&s_lut[byv * 2];
+          bw[b * 2] = t.x;
+          bw[b * 2 + 1] = t.y;
+        } else {
+          bw[b] = s_lut[byv];
+        }
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = cw[e >> 1];
+        float c;
+        if constexpr (CD == EK_BF16) c = (e & 1) ? bf16hi_to_f32(w) : bf16lo_to_f32(w);
+        else c = f16_to_f32((uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu)));
+        const float xv = (FULLD || (h * HALF + ks * 8 + e) < p.q.dim) ? c + bw[e] : 0.f;
+        x[ks][e] = xv;
+        ss = fmaf(xv, xv, ss);
+      }
+      cs[ks] = ss;
+    }
+#pragma unroll
+    for (int w = 1; w < KS; w <<= 1)
+#pragma unroll
+      for (int c = 0; c < KS; c += 2 * w) cs[c] = cs[c] + cs[c + w];
+    float ss = cs[0];
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    const float sc = f_norm_d ? inv_norm(ss) : 1.f;
+    f32x16 acc;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 af;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float x0 = x[ks][2 * k] * sc, x1 = x[ks][2 * k + 1] * sc;
+        if constexpr (EK == EK_F16)
+          af[k] = f32_to_f16_bits(x0) | (f32_to_f16_bits(x1) << 16);
+        else
+          af[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, bf16x2));
+      }
+      acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &af, &bq[ks]);
+    }
+    if (d.nv == 32) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) m = fmaxf(m, acc[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (8 * (e >> 2) + 4 * h + (e & 3) < d.nv) m = fmaxf(m, acc[e]);
+    }
+    if ((int64_t)(d.t + 1) * 32 >= dlen(d.j)) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+      const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const float v = __builtin_isfinite(mm) ? mm * qsc : 0.f;
+      auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
+      // the tile kernel's flush order (query g at place g of its group of 4:
+      // the sum starts at 4-column chunk g % (Lq / 4) and wraps)
+      float s = 0.f;
+      if ((p.LU & 3) == 0) {
+        const int nv4 = p.LU >> 2;
+        int c = (int)(g % nv4);
+        for (int j = 0; j < nv4; ++j) {
+          s += col(4 * c);
+          s += col(4 * c + 1);
+          s += col(4 * c + 2);
+          s += col(4 * c + 3);
+          c = (c + 1 == nv4) ? 0 : c + 1;
+        }
+      } else {
+        for (int c = 0; c < p.LU; ++c) s += col(c);
+      }
+      pend_j = d.j;
+      pend_v = s * p.out_scale;
+      m = NEG_INF;
+    }
+  };
+
+  Tile tc = open_doc(j0);
+  Tile t1 = next_tile(tc);
+  const int32_t code_c = load_code(tc);
+  int32_t code1 = load_code(t1);
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(code1) : : "memory");
+  gather(tc, code_c, 0);
+  int st = 0;
+  while (tc.j >= 0) {
+    const Tile t2 = next_tile(t1);
+    // stage st (tile tc) and code1 have landed; tile tc-1's LDS reads are done
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : "+v"(code1) : : "memory");
+    if (pend_j >= 0) {
+      if (lane == 0) store(pend_j, pend_v);
+      pend_j = -1;
+    }
+    gather(t1, code1, st ^ 1);
+    code1 = load_code(t2);
+    compute(tc, st);
+    tc = t1;
+    t1 = t2;
+    st ^= 1;
+  }
+  if (pend_j >= 0 && lane == 0) store(pend_j, pend_v);
+  // no gather may still be writing this wave's LDS when it exits
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 template <int EK, int DPAD, int CD, int NBITS>
 int launch_stream_nsub(int nsub, const Params& p, int64_t nblocks, hipStream_t s) {
   if (nsub != 1) return LIK_ERR_UNSUPPORTED;
+  if (p.gather) {
+    if (p.q.dim == DPAD)
+      hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, false>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+  }
   if (p.q.dim == DPAD)
     hipLaunchKernelGGL((plaid_stream_kernel<EK, DPAD, CD, NBITS, 1, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
   else

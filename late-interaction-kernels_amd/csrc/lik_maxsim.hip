@@ -716,7 +716,8 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
     {
       const int64_t rsb = (int64_t)sdp * docs->nbits / 8, nr = (32 * rsb + 1023) / 1024;
       p.gather = ((uintptr_t)docs->residuals) % 16 == 0 && docs->res_stride_tok % 16 == 0 &&
-                 32 * docs->res_stride_tok <= nr * 1024 && !(se && se[0] == '1');
+                 32 * docs->res_stride_tok <= nr * 1024 &&
+                 docs->n_centroids * docs->cent_stride * ceb <= (int64_t)kInvRow && !(se && se[0] == '1');
     }
     // ~16k wavefronts over the corpus, at most 512 docs each
     int64_t R = (docs->n + 16383) / 16384;

@@ -60,6 +60,10 @@ struct Params {
   int64_t amax_ld;  // query tokens per (query, doc) row of amax (the padded Lq)
 };
 
+// PLAID gather kernel: byte offset given to a row past the tile end; the
+// host routes only centroid tables smaller than this to that kernel
+constexpr uint32_t kInvRow = 0xfff00000u;
+
 enum { SRC_DENSE = 0, SRC_PLAID = 1 };
 
 __device__ __forceinline__ int64_t seq_len(const SeqDev& s, int64_t i) {

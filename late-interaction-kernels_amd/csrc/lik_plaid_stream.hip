@@ -330,16 +330,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
 // gathers. Each 16-byte chunk of row R sits at slot chunk ^ (R % LPR) so
 // that a lane's fragment reads (row l32, chunk h*KS + ks) spread over all
 // banks. The decoded fp32 half row stays in VGPRs (no staging registers
-// now), so the decode runs once. Two LDS stages per wave: the gather of tile
-// c+1 is in flight while tile c is decoded and scored.
+// now), so the decode runs once. One LDS stage per wave: tile c is read out
+// of it into registers first, then the gather of tile c+1 overwrites it and
+// is in flight while tile c is decoded and scored (9 KB of LDS per wave at
+// d = 128, 3 waves per SIMD).
 //
 // Waits are explicit: the compiler does not count the inline-asm gathers,
-// so every iteration starts with vmcnt(0) (stage c and code c+1 landed;
-// this wave issued nothing since) and lgkmcnt(0) (tile c-1's LDS reads are
-// done before its stage is overwritten). Doc scores are stored one
-// iteration late, after that wait, so a store never holds up a gather.
+// so every iteration starts with vmcnt(0) (tile c and code c+1 landed; this
+// wave issued nothing since), and the gather of tile c+1 waits for
+// lgkmcnt(0) (tile c's LDS reads done). Doc scores are stored one iteration
+// late, after the first wait, so a store never holds up a gather.
 template <int EK, int DPAD, int CD, int NBITS, bool FULLD>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >= 128 ? 3 : 4)))
     plaid_gather_kernel(const Params p) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;            // 8-element chunks per lane (= MFMA k-steps)
@@ -359,7 +361,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   constexpr float NEG_INF = -__builtin_huge_valf();
 
   __shared__ __attribute__((aligned(16))) float s_lut[256 * FPB];
-  __shared__ __attribute__((aligned(1024))) char s_st[4][2][STB];
+  __shared__ __attribute__((aligned(1024))) char s_st[4][STB];
   for (int i = threadIdx.x; i < 256 * FPB; i += 256) {
     const int v = i / FPB, k = i % FPB;
     uint32_t bc = ((uint32_t)v >> (k * NBITS)) & ((1u << NBITS) - 1u);
@@ -442,10 +444,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
                  (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu),
                  (uint32_t)__builtin_amdgcn_readfirstlane(nbytes), 0x00020000u};
   };
-  const u32x4 dcent = rsrc_words(p.pl.cent, sat_u32(p.pl.ncent * p.pl.cent_sb));
-  auto lds_addr = [&](int st, int off) -> uint32_t {
+  // rows past the tile's end get offset kInvRow (+ chunk), at or beyond the
+  // table's record count (the host keeps tables below kInvRow bytes)
+  const u32x4 dcent = rsrc_words(p.pl.cent, (uint32_t)(p.pl.ncent * p.pl.cent_sb));
+  auto lds_addr = [&](int off) -> uint32_t {
     return (uint32_t)__builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_st[wl][st][0]) + (uint32_t)off);
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_st[wl][0]) + (uint32_t)off);
   };
   auto dma = [&](uint32_t lds, uint32_t voff, const u32x4& desc) {
     uint32_t saved;
@@ -458,52 +462,66 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
         : "s"(lds), "v"(voff), "s"(desc)
         : "memory");
   };
-  // gather tile d (codes in lanes l32) into stage st
-  auto gather = [&](const Tile& d, int32_t code, int st) {
+  // gather tile d (code of row l32 in lane l32) into this wave's stage, once
+  // the stage's previous contents have been read (lgkmcnt(0))
+  auto gather = [&](const Tile& d, int32_t code) {
     if (d.j < 0) return;
+    int64_t cd = code;
+    cd = (cd < 0 || cd >= p.pl.ncent) ? 0 : cd;
+    const uint32_t rowoff = l32 < d.nv ? (uint32_t)cd * (uint32_t)p.pl.cent_sb : kInvRow;
+    uint32_t voff[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int row = i * RPI + lane / LPR;
       const int chunk = (lane % LPR) ^ (row % LPR);
-      int64_t cd = __builtin_amdgcn_ds_bpermute(row * 4, code);
-      cd = (cd < 0 || cd >= p.pl.ncent) ? 0 : cd;
-      const uint32_t voff = row < d.nv ? (uint32_t)(cd * p.pl.cent_sb) + (uint32_t)(chunk * 16) : kOOB;
-      dma(lds_addr(st, i * 1024), voff, dcent);
+      voff[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(row * 4, (int)rowoff) + (uint32_t)(chunk * 16);
     }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < NI; ++i) dma(lds_addr(i * 1024), voff[i], dcent);
     const u32x4 dres = rsrc_words(p.pl.res + d.tok * p.pl.res_st, (uint32_t)d.nv * (uint32_t)p.pl.res_st);
 #pragma unroll
-    for (int i = 0; i < NR; ++i) dma(lds_addr(st, CBYTES + i * 1024), (uint32_t)(i * 1024 + lane * 16), dres);
+    for (int i = 0; i < NR; ++i) dma(lds_addr(CBYTES + i * 1024), (uint32_t)(i * 1024 + lane * 16), dres);
   };
 
   float m = NEG_INF;
   int64_t pend_j = -1;
   float pend_v = 0.f;
 
-  auto compute = [&](const Tile& d, int st) {
-    const char* stage = &s_st[wl][st][0];
+  // tile data of this wave's stage into registers
+  struct Regs {
+    u32x4 cw[KS];
     uint32_t rw[RVL];
-    {
-      const char* rp = stage + CBYTES + l32 * (int)p.pl.res_st + h * RBL;
-      if constexpr (RVL % 4 == 0) {
+  };
+  auto read_stage = [&](Regs& rg) {
+    const char* stage = &s_st[wl][0];
+    const char* rp = stage + CBYTES + l32 * (int)p.pl.res_st + h * RBL;
+    if constexpr (RVL % 4 == 0) {
 #pragma unroll
-        for (int v = 0; v < RVL / 4; ++v) {
-          const u32x4 t = *(const u32x4*)(rp + 16 * v);
-          rw[4 * v] = t[0]; rw[4 * v + 1] = t[1]; rw[4 * v + 2] = t[2]; rw[4 * v + 3] = t[3];
-        }
-      } else {
+      for (int v = 0; v < RVL / 4; ++v) {
+        const u32x4 t = *(const u32x4*)(rp + 16 * v);
+        rg.rw[4 * v] = t[0]; rg.rw[4 * v + 1] = t[1]; rg.rw[4 * v + 2] = t[2]; rg.rw[4 * v + 3] = t[3];
+      }
+    } else {
 #pragma unroll
-        for (int v = 0; v < RVL / 2; ++v) {
-          const uint2 t = *(const uint2*)(rp + 8 * v);
-          rw[2 * v] = t.x; rw[2 * v + 1] = t.y;
-        }
+      for (int v = 0; v < RVL / 2; ++v) {
+        const uint2 t = *(const uint2*)(rp + 8 * v);
+        rg.rw[2 * v] = t.x; rg.rw[2 * v + 1] = t.y;
       }
     }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int cc = h * KS + ks;
+      rg.cw[ks] = *(const u32x4*)(stage + l32 * RB + ((cc ^ (l32 % LPR)) * 16));
+    }
+  };
+  auto compute = [&](const Tile& d, const Regs& rg) {
+    const uint32_t* rw = rg.rw;
     float x[KS][8];
     float cs[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const int cc = h * KS + ks;
-      const u32x4 cw = *(const u32x4*)(stage + l32 * RB + ((cc ^ (l32 % LPR)) * 16));
+      const u32x4 cw = rg.cw[ks];
       float bw[8];
 #pragma unroll
       for (int b = 0; b < 8 / FPB; ++b) {
@@ -598,22 +616,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
   const int32_t code_c = load_code(tc);
   int32_t code1 = load_code(t1);
   asm volatile("s_waitcnt vmcnt(0)" : "+v"(code1) : : "memory");
-  gather(tc, code_c, 0);
-  int st = 0;
+  gather(tc, code_c);
   while (tc.j >= 0) {
     const Tile t2 = next_tile(t1);
-    // stage st (tile tc) and code1 have landed; tile tc-1's LDS reads are done
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : "+v"(code1) : : "memory");
+    // tile tc's gather and code1 have landed
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(code1) : : "memory");
     if (pend_j >= 0) {
       if (lane == 0) store(pend_j, pend_v);
       pend_j = -1;
     }
-    gather(t1, code1, st ^ 1);
+    Regs rg;
+    read_stage(rg);
+    gather(t1, code1);
     code1 = load_code(t2);
-    compute(tc, st);
+    compute(tc, rg);
     tc = t1;
     t1 = t2;
-    st ^= 1;
   }
   if (pend_j >= 0 && lane == 0) store(pend_j, pend_v);
   // no gather may still be writing this wave's LDS when it exits

@@ -67,6 +67,16 @@ __device__ __forceinline__ f32x16 mfma32(const f32x16& c, const u32x4* a, const 
   }
 }
 
+// c + a.lo * b.lo + a.hi * b.hi on packed 16-bit pairs, fp32 accumulate.
+template <int EK>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  if constexpr (EK == EK_F16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), c, false);
+}
+
 __device__ __forceinline__ float bf16lo_to_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi_to_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

@@ -710,14 +710,19 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
     p.LU = (int)Q->len;
     const int nsub = 1;  // one query per wavefront
     p.ngroups = (Q->n + nsub - 1) / nsub;
-    // LDS-gather variant: 16-byte aligned residual rows, a residual tile no
-    // larger than the padded rows' (LIK_PLAID_STREAM=1 keeps the per-lane
-    // variant, a tuning aid)
+    // LDS-gather variants need 16-byte aligned residual rows and a residual
+    // tile no larger than the padded rows'. Centroids of the query's type take
+    // the split form (q.c + q.r, norm from its parts: within bf16 / fp16
+    // rounding of the decode route, not bitwise equal to it); others the
+    // exact decode. LIK_PLAID_STREAM=1 / =2 force the per-lane / the exact
+    // gather variant (tuning and parity aids).
     {
       const int64_t rsb = (int64_t)sdp * docs->nbits / 8, nr = (32 * rsb + 1023) / 1024;
-      p.gather = ((uintptr_t)docs->residuals) % 16 == 0 && docs->res_stride_tok % 16 == 0 &&
-                 32 * docs->res_stride_tok <= nr * 1024 &&
-                 docs->n_centroids * docs->cent_stride * ceb <= (int64_t)kInvRow && !(se && se[0] == '1');
+      const bool lds_ok = ((uintptr_t)docs->residuals) % 16 == 0 && docs->res_stride_tok % 16 == 0 &&
+                          32 * docs->res_stride_tok <= nr * 1024 &&
+                          docs->n_centroids * docs->cent_stride * ceb <= (int64_t)kInvRow;
+      const bool same_type = docs->centroid_dtype == Q->dtype;
+      p.gather = !lds_ok || (se && se[0] == '1') ? 0 : (same_type && !(se && se[0] == '2') ? 2 : 1);
     }
     // ~16k wavefronts over the corpus, at most 512 docs each
     int64_t R = (docs->n + 16383) / 16384;

@@ -340,8 +340,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
 // wave issued nothing since), and the gather of tile c+1 waits for
 // lgkmcnt(0) (tile c's LDS reads done). Doc scores are stored one iteration
 // late, after the first wait, so a store never holds up a gather.
-template <int EK, int DPAD, int CD, int NBITS, bool FULLD>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >= 128 ? 3 : 4)))
+template <int EK, int DPAD, int CD, int NBITS, bool FULLD, bool SPLIT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >= 128 && !SPLIT ? 3 : 4)))
     plaid_gather_kernel(const Params p) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;            // 8-element chunks per lane (= MFMA k-steps)
@@ -358,15 +358,42 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   constexpr int CBYTES = 32 * RB;
   constexpr int STB = CBYTES + NR * 1024;  // one stage: 32 centroid rows + residual tile
   static_assert(RBL % 4 == 0 && CD != EK_F32, "gather layout");
+  static_assert(!SPLIT || CD == EK, "split form feeds stored centroid chunks to the MFMA");
   constexpr float NEG_INF = -__builtin_huge_valf();
 
-  __shared__ __attribute__((aligned(16))) float s_lut[256 * FPB];
+  // byte -> bucket weights: fp32 values (exact decode), or for the split
+  // form the byte's fields rounded to the MFMA type and packed in pairs
+  // (s_lut as uint2 per byte) and the sum of their squares in fp32 (s_r2)
+  constexpr int LUTW = SPLIT ? 2 * 256 : FPB * 256;
+  __shared__ __attribute__((aligned(16))) float s_lut[LUTW];
   __shared__ __attribute__((aligned(1024))) char s_st[4][STB];
-  for (int i = threadIdx.x; i < 256 * FPB; i += 256) {
-    const int v = i / FPB, k = i % FPB;
-    uint32_t bc = ((uint32_t)v >> (k * NBITS)) & ((1u << NBITS) - 1u);
-    bc = bc < (uint32_t)p.pl.nb ? bc : (uint32_t)(p.pl.nb - 1);
-    s_lut[i] = p.pl.bw[bc];
+  __shared__ __attribute__((aligned(16))) float s_sc[4][SPLIT ? 32 : 1];
+  __shared__ float s_r2[SPLIT ? 256 : 1];
+  if constexpr (SPLIT) {
+    for (int v = threadIdx.x; v < 256; v += 256) {
+      uint32_t h16[4] = {0u, 0u, 0u, 0u};
+      float r2 = 0.f;
+      for (int k = 0; k < FPB; ++k) {
+        uint32_t bc = ((uint32_t)v >> (k * NBITS)) & ((1u << NBITS) - 1u);
+        bc = bc < (uint32_t)p.pl.nb ? bc : (uint32_t)(p.pl.nb - 1);
+        const float w = p.pl.bw[bc];
+        const uint32_t hb = EK == EK_F16 ? f32_to_f16_bits(w) : f32_to_bf16_bits(w);
+        const float wr = EK == EK_F16 ? f16_to_f32((uint16_t)hb) : __uint_as_float(hb << 16);
+        h16[k] = hb;
+        r2 = fmaf(wr, wr, r2);
+      }
+      uint32_t* e = (uint32_t*)&s_lut[v * 2];
+      e[0] = h16[0] | (h16[1] << 16);
+      e[1] = h16[2] | (h16[3] << 16);
+      s_r2[v] = r2;
+    }
+  } else {
+    for (int i = threadIdx.x; i < 256 * FPB; i += 256) {
+      const int v = i / FPB, k = i % FPB;
+      uint32_t bc = ((uint32_t)v >> (k * NBITS)) & ((1u << NBITS) - 1u);
+      bc = bc < (uint32_t)p.pl.nb ? bc : (uint32_t)(p.pl.nb - 1);
+      s_lut[i] = p.pl.bw[bc];
+    }
   }
   __syncthreads();
 
@@ -515,7 +542,77 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       rg.cw[ks] = *(const u32x4*)(stage + l32 * RB + ((cc ^ (l32 % LPR)) * 16));
     }
   };
+  // split form: x = c + r with c the stored centroid chunk and r the bucket
+  // weights rounded to the MFMA type; q.x = q.c + q.r (two MFMA chains into
+  // one accumulator), ||x||^2 = ||c||^2 + 2 c.r + ||r||^2 (dot2 on the
+  // packed pairs, byte sums of r^2 from the table), and the row scale is
+  // applied to the accumulator instead of to every element.
+  auto compute_split = [&](const Tile& d, const Regs& rg) {
+    const uint32_t* rw = rg.rw;
+    float cc = 0.f, cr = 0.f, r2 = 0.f;
+    auto byte_at = [&](int byte_i) -> uint32_t { return (rw[byte_i >> 2] >> ((byte_i & 3) * 8)) & 0xffu; };
+    f32x16 acc;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bool live = FULLD || (h * HALF + ks * 8) < p.q.dim;  // chunks are whole: dim % 8 == 0
+      u32x4 rv;
+      float rs = 0.f;
+      if constexpr (FPB == 4) {
+        const uint32_t b0 = byte_at(2 * ks), b1 = byte_at(2 * ks + 1);
+        const uint2 e0 = *(const uint2*)&s_lut[b0 * 2];
+        const uint2 e1 = *(const uint2*)&s_lut[b1 * 2];
+        rv = u32x4{e0.x, e0.y, e1.x, e1.y};
+        rs = s_r2[b0] + s_r2[b1];
+      } else if constexpr (FPB == 2) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t b = byte_at(4 * ks + k);
+          rv[k] = *(const uint32_t*)&s_lut[b * 2];
+          rs += s_r2[b];
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t b0 = byte_at(8 * ks + 2 * k), b1 = byte_at(8 * ks + 2 * k + 1);
+          rv[k] = (*(const uint32_t*)&s_lut[b0 * 2] & 0xffffu) | (*(const uint32_t*)&s_lut[b1 * 2] << 16);
+          rs += s_r2[b0] + s_r2[b1];
+        }
+      }
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      const u32x4 ca = live ? rg.cw[ks] : z;
+      const u32x4 ra = live ? rv : z;
+      r2 += live ? rs : 0.f;
+      if (f_norm_d) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          cc = dot2<EK>(ca[w], ca[w], cc);
+          cr = dot2<EK>(ca[w], ra[w], cr);
+        }
+      }
+      acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &ca, &bq[ks]);
+      acc = mfma32<EK>(acc, &ra, &bq[ks]);
+    }
+    if (f_norm_d) {
+      float ss = fmaf(2.f, cr, cc) + r2;
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+      ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      // row l32's scale to the accumulator layout (element i of lane l is
+      // row 8 (i / 4) + 4 h + i % 4)
+      if (h == 0) s_sc[wl][l32] = inv_norm(ss);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 sc4 = *(const f32x4*)&s_sc[wl][8 * j + 4 * h];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[4 * j + t] *= sc4[t];
+      }
+    }
+    return acc;
+  };
   auto compute = [&](const Tile& d, const Regs& rg) {
+    f32x16 acc;
+    if constexpr (SPLIT) {
+      acc = compute_split(d, rg);
+    } else {
     const uint32_t* rw = rg.rw;
     float x[KS][8];
     float cs[KS];
@@ -562,7 +659,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
     const float sc = f_norm_d ? inv_norm(ss) : 1.f;
-    f32x16 acc;
+    acc = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 af;
@@ -575,6 +672,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
           af[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, bf16x2));
       }
       acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &af, &bq[ks]);
+    }
     }
     if (d.nv == 32) {
 #pragma unroll
@@ -642,10 +740,20 @@ template <int EK, int DPAD, int CD, int NBITS>
 int launch_stream_nsub(int nsub, const Params& p, int64_t nblocks, hipStream_t s) {
   if (nsub != 1) return LIK_ERR_UNSUPPORTED;
   if (p.gather) {
-    if (p.q.dim == DPAD)
-      hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+    const bool full = p.q.dim == DPAD;
+    if constexpr (CD == EK) {
+      if (p.gather == 2) {
+        if (full)
+          hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, true, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+        else
+          hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, false, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+        return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+      }
+    }
+    if (full)
+      hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, true, false>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, false>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, false, false>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
     return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   }
   if (p.q.dim == DPAD)

@@ -1,14 +1,17 @@
 """GPU parity of the few-query PLAID path (lik_plaid_stream.hip).
 
 lik_plaid_maxsim scores up to 4 queries of <= 32 tokens with one wavefront
-per (query, doc range) that decodes straight into its MFMA fragments. Its
-arithmetic is the tile kernel's (same decode, norm tree, rounding, MFMA
-order and per-query summation order), so the scores are bitwise equal to the
-tile kernel's (LIK_PLAID_STREAM=0 forces that one) and within bf16 tolerance
-of the oracle (oracle/lik_oracle.maxsim_residual[_varlen], reference.py:
-142-179, plaid.py:832-963). Cases: nbits 2 / 4 / 8, bf16 / fp16 / fp32
-centroids, d = 64 / 96 / 128, empty docs, packed and padded layouts, 1 and 3
-queries.
+per (query, doc range). Its exact variants (per-lane and LDS-gather decode;
+LIK_PLAID_STREAM=2 forces the gather one where the layout allows it) use
+the tile kernel's arithmetic (same decode, norm tree, rounding, MFMA order
+and per-query summation order), so their scores are bitwise equal to the
+tile kernel's (LIK_PLAID_STREAM=0 forces that one). The default for
+centroids of the query's type is the split form (q.c + q.r on the stored
+centroid chunks and bf16 / fp16 bucket weights, norm from ||c||^2 + 2 c.r +
+||r||^2): within bf16 tolerance of both. Everything is checked against the
+oracle (oracle/lik_oracle.maxsim_residual[_varlen], reference.py:142-179,
+plaid.py:832-963). Cases: nbits 2 / 4 / 8, bf16 / fp16 / fp32 centroids,
+d = 64 / 96 / 128, empty docs, packed and padded layouts, 1 and 3 queries.
 """
 
 import sys
@@ -59,13 +62,18 @@ def test_stream_varlen_matches_tile_kernel(monkeypatch, nbits, cdtype, d, nq):
     Q = torch.randn(nq, 32, d, generator=g).to(qdt).cuda()
     args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), nbits)
     stream = maxsim_residual_varlen(Q, *args)
+    monkeypatch.setenv("LIK_PLAID_STREAM", "2")
+    exact = maxsim_residual_varlen(Q, *args)
     monkeypatch.setenv("LIK_PLAID_STREAM", "0")
     tile = maxsim_residual_varlen(Q, *args)
-    assert torch.equal(stream, tile)
-    assert stream[:, 0].abs().max().item() == 0.0 and stream[:, 350].abs().max().item() == 0.0
+    assert torch.equal(exact, tile)
+    assert rel_err(stream.cpu().numpy(), tile.cpu().numpy()) < 1e-2
+    for s in (stream, exact):
+        assert s[:, 0].abs().max().item() == 0.0 and s[:, 350].abs().max().item() == 0.0
     ref = O.maxsim_residual_varlen(Q.float().cpu().numpy(), codes.numpy(), res.numpy(), cu.numpy(),
                                    cent.float().numpy(), bw.numpy(), nbits)
     assert rel_err(stream.cpu().numpy(), ref) < 1e-2
+    assert rel_err(exact.cpu().numpy(), ref) < 1e-2
 
 
 @pytest.mark.parametrize("lq", [32, 20])
@@ -85,9 +93,50 @@ def test_stream_padded_and_short_queries(monkeypatch, lq):
     Q = torch.randn(2, lq, d).to(torch.bfloat16).cuda()
     args = (pc.cuda(), pr.cuda(), lens.to(torch.int32).cuda(), cent.cuda(), bw.cuda(), nbits)
     stream = maxsim_residual(Q, *args)
+    monkeypatch.setenv("LIK_PLAID_STREAM", "2")
+    exact = maxsim_residual(Q, *args)
     monkeypatch.setenv("LIK_PLAID_STREAM", "0")
     tile = maxsim_residual(Q, *args)
-    assert torch.equal(stream, tile)
+    assert torch.equal(exact, tile)
+    assert rel_err(stream.cpu().numpy(), tile.cpu().numpy()) < 1e-2
     ref = O.maxsim_residual(Q.float().cpu().numpy(), pc.numpy(), pr.numpy(), lens.numpy(), cent.float().numpy(),
                             bw.numpy(), nbits)
     assert rel_err(stream.cpu().numpy(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("normalize", [True, False])
+def test_split_form_large_index(normalize):
+    """The split form at the benchmark's layout (d = 128, nbits = 2, bf16
+    centroids over a 4096-row table, docs of 30..300 tokens), one query,
+    against the exact gather variant and the oracle: the split form drops
+    only the bf16 rounding of the normalised token (and rounds the bucket
+    weights to bf16), so it stays within a few 1e-3 of both."""
+    import os
+
+    from late_interaction_kernels.plaid import maxsim_residual_varlen
+
+    _case(f"split large normalize={normalize}")
+    g = torch.Generator().manual_seed(77)
+    Nd, d, nbits, nc = 1000, 128, 2, 4096
+    cent = torch.nn.functional.normalize(torch.randn(nc, d, generator=g), dim=-1).to(torch.bfloat16)
+    bw = torch.linspace(-0.1, 0.1, 4)
+    lens = torch.randint(30, 301, (Nd,), generator=g)
+    cu = torch.zeros(Nd + 1, dtype=torch.int32)
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    T = int(cu[-1])
+    codes = torch.randint(0, nc, (T,), generator=g, dtype=torch.int32)
+    res = torch.randint(0, 256, (T, d * nbits // 8), generator=g, dtype=torch.uint8)
+    Q = torch.nn.functional.normalize(torch.randn(1, 32, d, generator=g), dim=-1).to(torch.bfloat16).cuda()
+    args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), nbits)
+    split = maxsim_residual_varlen(Q, *args, normalize=normalize)
+    os.environ["LIK_PLAID_STREAM"] = "2"
+    try:
+        exact = maxsim_residual_varlen(Q, *args, normalize=normalize)
+    finally:
+        del os.environ["LIK_PLAID_STREAM"]
+    e = rel_err(split.cpu().numpy(), exact.cpu().numpy())
+    print(f"split vs exact rel err {e:.2e}")
+    assert e < 5e-3
+    ref = O.maxsim_residual_varlen(Q.float().cpu().numpy(), codes.numpy(), res.numpy(), cu.numpy(),
+                                   cent.float().numpy(), bw.numpy(), nbits, normalize=normalize)
+    assert rel_err(split.cpu().numpy(), ref) < 5e-3

@@ -20,6 +20,7 @@
 // Reference: plaid.py:684-963 (fused residual MaxSim), reference.py:124-179.
 #include "lik_kernel.h"
 
+
 namespace lik {
 
 // Occupancy target: the latency chain is covered by the other waves of the
@@ -367,7 +368,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   constexpr int LUTW = SPLIT ? 2 * 256 : FPB * 256;
   __shared__ __attribute__((aligned(16))) float s_lut[LUTW];
   __shared__ __attribute__((aligned(1024))) char s_st[4][STB];
-  __shared__ __attribute__((aligned(16))) float s_sc[4][SPLIT ? 32 : 1];
+  __shared__ __attribute__((aligned(16))) float s_sc[4][SPLIT ? 64 : 1];
   __shared__ float s_r2[SPLIT ? 256 : 1];
   if constexpr (SPLIT) {
     for (int v = threadIdx.x; v < 256; v += 256) {
@@ -547,6 +548,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   // one accumulator), ||x||^2 = ||c||^2 + 2 c.r + ||r||^2 (dot2 on the
   // packed pairs, byte sums of r^2 from the table), and the row scale is
   // applied to the accumulator instead of to every element.
+  // (the normalise flag stays a runtime branch: compiling both loop bodies
+  // into one straight block raised register pressure past 128 VGPRs)
   auto compute_split = [&](const Tile& d, const Regs& rg) {
     const uint32_t* rw = rg.rw;
     float cc = 0.f, cr = 0.f, r2 = 0.f;
@@ -592,19 +595,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &ca, &bq[ks]);
       acc = mfma32<EK>(acc, &ra, &bq[ks]);
     }
+    // row l32's scale and mask bias (-inf past the tile's end) to the
+    // accumulator layout: element i of lane l is row 8 (i / 4) + 4 h + i % 4
+    float sc = 1.f;
     if (f_norm_d) {
       float ss = fmaf(2.f, cr, cc) + r2;
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
       ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-      // row l32's scale to the accumulator layout (element i of lane l is
-      // row 8 (i / 4) + 4 h + i % 4)
-      if (h == 0) s_sc[wl][l32] = inv_norm(ss);
+      sc = __builtin_amdgcn_rsqf(fmaxf(ss, 1e-24f));  // 1 / max(||x||, 1e-12)
+    }
+    if (h == 0) {
+      s_sc[wl][l32] = sc;
+      s_sc[wl][32 + l32] = l32 < d.nv ? 0.f : NEG_INF;
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 sc4 = *(const f32x4*)&s_sc[wl][8 * j + 4 * h];
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 sc4 = *(const f32x4*)&s_sc[wl][8 * j + 4 * h];
+      const f32x4 b4 = *(const f32x4*)&s_sc[wl][32 + 8 * j + 4 * h];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[4 * j + t] *= sc4[t];
-      }
+      for (int t = 0; t < 4; ++t) acc[4 * j + t] = fmaf(acc[4 * j + t], sc4[t], b4[t]);
     }
     return acc;
   };
@@ -674,7 +683,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &af, &bq[ks]);
     }
     }
-    if (d.nv == 32) {
+    if (SPLIT || d.nv == 32) {  // split form: rows past the end are already -inf
 #pragma unroll
       for (int e = 0; e < 16; ++e) m = fmaxf(m, acc[e]);
     } else {

@@ -484,6 +484,23 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
   if (Q->n == 0 || D->n == 0) return LIK_OK;
   hipStream_t s = (hipStream_t)stream;
 
+  // rows wider than any column block (bf16 / fp16 > 512, fp32 > 256): the
+  // one-wave-per-pair kernel, no workspace
+  if (pick_dpad(Q->dtype, Q->dim) < 0) {
+    if (argmax || Q->dtype == LIK_FP8_E4M3 || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
+    Params p{};
+    p.q = to_dev(*Q);
+    p.d = to_dev(*D);
+    p.normalize = norm_bits(flags);
+    p.out_scale = out_scale;
+    p.out = out;
+    p.osq = out_stride_q;
+    p.osd = out_stride_d;
+    p.kd_K = kd ? D->n / Q->n : 0;
+    p.ndocs_pg = kd ? p.kd_K : D->n;
+    return timed_launch(s, [&] { return launch_maxsim_wide(Q->dtype, p, s); });
+  }
+
   // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: the
   // plan spreads it over at least 4 waves, or the docs are normalised once
   // ahead of the tile kernel

@@ -115,6 +115,8 @@ int launch_dense_fp8(const Plan& pl, const Params& p, int64_t nb, hipStream_t s)
 int launch_plaid_bf16(int cd, const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 // Few-query PLAID scoring, one wavefront per (query group, doc range): lik_plaid_stream.hip.
 int launch_plaid_stream(int ek, int cd, int dpad, int nsub, const Params& p, hipStream_t s);
+// rows wider than the tile kernel takes (lik_wide.hip): one wave per (query, doc)
+int launch_maxsim_wide(int dtype, const Params& p, hipStream_t s);
 // training forward (argmax output), lik_inst_train_*.hip
 int launch_dense_train_bf16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 int launch_dense_train_f16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);

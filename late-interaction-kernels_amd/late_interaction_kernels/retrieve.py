@@ -33,7 +33,8 @@ class MaxSimScorer(torch.nn.Module):
 
     Args:
         normalize: L2-normalise Q and D per token inside the kernel.
-        backward: gradient strategy name (validated; this build is forward-only).
+        backward: gradient strategy name; ``"unified"`` and ``"lowmem"`` both map to
+            the deterministic argmax-scatter backward (validated for compatibility).
         mask_pad_token: pad-token id for :meth:`forward_with_ids`.
     """
 

@@ -513,6 +513,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   };
 
   float m = NEG_INF;
+  // first 4-column chunk of this query's flush order (loop-invariant)
+  const int rot0 = (p.LU & 3) == 0 ? (int)(g % (p.LU >> 2)) : 0;
   int64_t pend_j = -1;
   float pend_v = 0.f;
 
@@ -701,7 +703,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       float s = 0.f;
       if ((p.LU & 3) == 0) {
         const int nv4 = p.LU >> 2;
-        int c = (int)(g % nv4);
+        int c = rot0;
         for (int j = 0; j < nv4; ++j) {
           s += col(4 * c);
           s += col(4 * c + 1);

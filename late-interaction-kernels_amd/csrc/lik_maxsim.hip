@@ -725,8 +725,6 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
     p.osq = out_stride_q;
     p.osd = out_stride_d;
     p.LU = (int)Q->len;
-    const int nsub = 1;  // one query per wavefront
-    p.ngroups = (Q->n + nsub - 1) / nsub;
     // LDS-gather variants need 16-byte aligned residual rows and a residual
     // tile no larger than the padded rows'. Centroids of the query's type take
     // the split form (q.c + q.r, norm from its parts: within bf16 / fp16
@@ -741,6 +739,10 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
       const bool same_type = docs->centroid_dtype == Q->dtype;
       p.gather = !lds_ok || (se && se[0] == '1') ? 0 : (same_type && !(se && se[0] == '2') ? 2 : 1);
     }
+    // the split form scores two queries per wavefront (one gather and
+    // decode serve both); the other variants one
+    const int nsub = (p.gather == 2 && Q->n >= 2) ? 2 : 1;
+    p.ngroups = (Q->n + nsub - 1) / nsub;
     // ~16k wavefronts over the corpus, at most 512 docs each
     int64_t R = (docs->n + 16383) / 16384;
     p.R = (int)(R < 1 ? 1 : (R > 512 ? 512 : R));

@@ -341,8 +341,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
 // wave issued nothing since), and the gather of tile c+1 waits for
 // lgkmcnt(0) (tile c's LDS reads done). Doc scores are stored one iteration
 // late, after the first wait, so a store never holds up a gather.
-template <int EK, int DPAD, int CD, int NBITS, bool FULLD, bool SPLIT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >= 128 && !SPLIT ? 3 : 4)))
+template <int EK, int DPAD, int CD, int NBITS, bool FULLD, bool SPLIT, int QN>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >= 128 ? (QN > 1 ? 2 : (SPLIT ? 4 : 3)) : (QN > 1 ? 3 : 4))))
     plaid_gather_kernel(const Params p) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;            // 8-element chunks per lane (= MFMA k-steps)
@@ -360,6 +360,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   constexpr int STB = CBYTES + NR * 1024;  // one stage: 32 centroid rows + residual tile
   static_assert(RBL % 4 == 0 && CD != EK_F32, "gather layout");
   static_assert(!SPLIT || CD == EK, "split form feeds stored centroid chunks to the MFMA");
+  static_assert(QN == 1 || (SPLIT && QN == 2), "two queries per wavefront in the split form only");
   constexpr float NEG_INF = -__builtin_huge_valf();
 
   // byte -> bucket weights: fp32 values (exact decode), or for the split
@@ -404,31 +405,34 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   const int64_t g = wv / p.NR, r = wv - g * p.NR;
   if (g >= p.ngroups) return;  // wave-uniform, after the only barrier
 
-  // ---- query: token l32 of query g in column l32 ----
-  u32x4 bq[KS];
-  float qsc;
+  // ---- queries g * QN + sub: token l32 of each in column l32 ----
+  u32x4 bq[QN][KS];
+  float qsc[QN];
   const bool f_norm_q = (p.normalize & 1) != 0;
   const bool f_norm_d = (p.normalize & 2) != 0;
-  {
-    const bool valid = g < p.q.n && l32 < seq_len(p.q, g);
-    const char* rowp = valid ? seq_row0(p.q, g) + (int64_t)l32 * p.q.sl_b : nullptr;
+#pragma unroll
+  for (int sub = 0; sub < QN; ++sub) {
+    const int64_t q = g * QN + sub;
+    const bool valid = q < p.q.n && l32 < seq_len(p.q, q);
+    const char* rowp = valid ? seq_row0(p.q, q) + (int64_t)l32 * p.q.sl_b : nullptr;
     float ss = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int e = h * HALF + ks * 8;
-      bq[ks] = (valid && e < p.q.dim) ? *(const u32x4*)(rowp + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
-      if (f_norm_q) ss += chunk_sumsq<EK>(bq[ks]);
+      bq[sub][ks] = (valid && e < p.q.dim) ? *(const u32x4*)(rowp + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
+      if (f_norm_q) ss += chunk_sumsq<EK>(bq[sub][ks]);
     }
     ss += __shfl_xor(ss, 32);
-    qsc = valid ? (f_norm_q ? inv_norm(ss) : 1.f) : 0.f;
+    qsc[sub] = valid ? (f_norm_q ? inv_norm(ss) : 1.f) : 0.f;
   }
 
   const int64_t j0 = r * p.R;
   const int64_t j1 = j0 + p.R < p.pl.n ? j0 + p.R : p.pl.n;
   auto dlen = [&](int64_t j) -> int64_t { return doc_len<SRC_PLAID>(p, j); };
   auto dtok = [&](int64_t j) -> int64_t { return p.pl.cu ? (int64_t)p.pl.cu[j] : j * p.pl.codes_sn; };
-  auto store = [&](int64_t j, float v) {
-    if (g < p.q.n) ((__attribute__((address_space(1))) float*)p.out)[g * p.osq + j * p.osd] = v;
+  auto store = [&](int64_t j, int sub, float v) {
+    const int64_t q = g * QN + sub;
+    if (q < p.q.n) ((__attribute__((address_space(1))) float*)p.out)[q * p.osq + j * p.osd] = v;
   };
   struct Tile {
     int64_t j, tok;
@@ -446,7 +450,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
     while (j < j1) {
       const int64_t len = dlen(j);
       if (len > 0) return uni(Tile{j, dtok(j), 0, (int)(len < 32 ? len : 32)});
-      if (lane == 0) store(j, 0.f);
+      if (lane < QN) store(j, lane, 0.f);
       ++j;
     }
     return Tile{-1, 0, 0, 0};
@@ -512,11 +516,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
     for (int i = 0; i < NR; ++i) dma(lds_addr(CBYTES + i * 1024), (uint32_t)(i * 1024 + lane * 16), dres);
   };
 
-  float m = NEG_INF;
-  // first 4-column chunk of this query's flush order (loop-invariant)
-  const int rot0 = (p.LU & 3) == 0 ? (int)(g % (p.LU >> 2)) : 0;
+  float m[QN], pend_v[QN];
+  int rot0[QN];  // first 4-column chunk of each query's flush order (loop-invariant)
+#pragma unroll
+  for (int sub = 0; sub < QN; ++sub) {
+    m[sub] = NEG_INF;
+    pend_v[sub] = 0.f;
+    rot0[sub] = (p.LU & 3) == 0 ? (int)((g * QN + sub) % (p.LU >> 2)) : 0;
+  }
   int64_t pend_j = -1;
-  float pend_v = 0.f;
 
   // tile data of this wave's stage into registers
   struct Regs {
@@ -552,11 +560,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   // applied to the accumulator instead of to every element.
   // (the normalise flag stays a runtime branch: compiling both loop bodies
   // into one straight block raised register pressure past 128 VGPRs)
-  auto compute_split = [&](const Tile& d, const Regs& rg) {
+  auto compute_split = [&](const Tile& d, const Regs& rg, f32x16* acc) {
     const uint32_t* rw = rg.rw;
     float cc = 0.f, cr = 0.f, r2 = 0.f;
     auto byte_at = [&](int byte_i) -> uint32_t { return (rw[byte_i >> 2] >> ((byte_i & 3) * 8)) & 0xffu; };
-    f32x16 acc;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const bool live = FULLD || (h * HALF + ks * 8) < p.q.dim;  // chunks are whole: dim % 8 == 0
@@ -594,8 +601,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
           cr = dot2<EK>(ca[w], ra[w], cr);
         }
       }
-      acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &ca, &bq[ks]);
-      acc = mfma32<EK>(acc, &ra, &bq[ks]);
+#pragma unroll
+      for (int sub = 0; sub < QN; ++sub) {
+        acc[sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[sub], &ca, &bq[sub][ks]);
+        acc[sub] = mfma32<EK>(acc[sub], &ra, &bq[sub][ks]);
+      }
     }
     // row l32's scale and mask bias (-inf past the tile's end) to the
     // accumulator layout: element i of lane l is row 8 (i / 4) + 4 h + i % 4
@@ -615,14 +625,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       const f32x4 sc4 = *(const f32x4*)&s_sc[wl][8 * j + 4 * h];
       const f32x4 b4 = *(const f32x4*)&s_sc[wl][32 + 8 * j + 4 * h];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[4 * j + t] = fmaf(acc[4 * j + t], sc4[t], b4[t]);
+      for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[sub][4 * j + t] = fmaf(acc[sub][4 * j + t], sc4[t], b4[t]);
     }
-    return acc;
   };
   auto compute = [&](const Tile& d, const Regs& rg) {
-    f32x16 acc;
+    f32x16 acc[QN];
     if constexpr (SPLIT) {
-      acc = compute_split(d, rg);
+      compute_split(d, rg, acc);
     } else {
     const uint32_t* rw = rg.rw;
     float x[KS][8];
@@ -670,7 +681,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
     const float sc = f_norm_d ? inv_norm(ss) : 1.f;
-    acc = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 af;
@@ -682,28 +692,33 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
         else
           af[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, bf16x2));
       }
-      acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &af, &bq[ks]);
+      acc[0] = mfma32<EK>(ks == 0 ? f32x16{} : acc[0], &af, &bq[0][ks]);
     }
     }
-    if (SPLIT || d.nv == 32) {  // split form: rows past the end are already -inf
 #pragma unroll
-      for (int e = 0; e < 16; ++e) m = fmaxf(m, acc[e]);
-    } else {
+    for (int sub = 0; sub < QN; ++sub) {
+      if (SPLIT || d.nv == 32) {  // split form: rows past the end are already -inf
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (8 * (e >> 2) + 4 * h + (e & 3) < d.nv) m = fmaxf(m, acc[e]);
+        for (int e = 0; e < 16; ++e) m[sub] = fmaxf(m[sub], acc[sub][e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (8 * (e >> 2) + 4 * h + (e & 3) < d.nv) m[sub] = fmaxf(m[sub], acc[sub][e]);
+      }
     }
     if ((int64_t)(d.t + 1) * 32 >= dlen(d.j)) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+#pragma unroll
+     for (int sub = 0; sub < QN; ++sub) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
       const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      const float v = __builtin_isfinite(mm) ? mm * qsc : 0.f;
+      const float v = __builtin_isfinite(mm) ? mm * qsc[sub] : 0.f;
       auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
       // the tile kernel's flush order (query g at place g of its group of 4:
       // the sum starts at 4-column chunk g % (Lq / 4) and wraps)
       float s = 0.f;
       if ((p.LU & 3) == 0) {
         const int nv4 = p.LU >> 2;
-        int c = rot0;
+        int c = rot0[sub];
         for (int j = 0; j < nv4; ++j) {
           s += col(4 * c);
           s += col(4 * c + 1);
@@ -714,9 +729,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       } else {
         for (int c = 0; c < p.LU; ++c) s += col(c);
       }
+      pend_v[sub] = s * p.out_scale;
+      m[sub] = NEG_INF;
+     }
       pend_j = d.j;
-      pend_v = s * p.out_scale;
-      m = NEG_INF;
     }
   };
 
@@ -731,7 +747,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
     // tile tc's gather and code1 have landed
     asm volatile("s_waitcnt vmcnt(0)" : "+v"(code1) : : "memory");
     if (pend_j >= 0) {
-      if (lane == 0) store(pend_j, pend_v);
+      if (lane == 0)
+#pragma unroll
+        for (int sub = 0; sub < QN; ++sub) store(pend_j, sub, pend_v[sub]);
       pend_j = -1;
     }
     Regs rg;
@@ -742,30 +760,32 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
     tc = t1;
     t1 = t2;
   }
-  if (pend_j >= 0 && lane == 0) store(pend_j, pend_v);
+  if (pend_j >= 0 && lane == 0)
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub) store(pend_j, sub, pend_v[sub]);
   // no gather may still be writing this wave's LDS when it exits
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <int EK, int DPAD, int CD, int NBITS>
 int launch_stream_nsub(int nsub, const Params& p, int64_t nblocks, hipStream_t s) {
-  if (nsub != 1) return LIK_ERR_UNSUPPORTED;
+  if (nsub != 1 && !(nsub == 2 && p.gather == 2)) return LIK_ERR_UNSUPPORTED;
   if (p.gather) {
     const bool full = p.q.dim == DPAD;
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(256), 0, s, p);
+      return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+    };
     if constexpr (CD == EK) {
-      if (p.gather == 2) {
-        if (full)
-          hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, true, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
-        else
-          hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, false, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
-        return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
-      }
+      if (p.gather == 2 && nsub == 2)
+        return full ? go(plaid_gather_kernel<EK, DPAD, CD, NBITS, true, true, 2>)
+                    : go(plaid_gather_kernel<EK, DPAD, CD, NBITS, false, true, 2>);
+      if (p.gather == 2)
+        return full ? go(plaid_gather_kernel<EK, DPAD, CD, NBITS, true, true, 1>)
+                    : go(plaid_gather_kernel<EK, DPAD, CD, NBITS, false, true, 1>);
     }
-    if (full)
-      hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, true, false>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL((plaid_gather_kernel<EK, DPAD, CD, NBITS, false, false>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
-    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+    return full ? go(plaid_gather_kernel<EK, DPAD, CD, NBITS, true, false, 1>)
+                : go(plaid_gather_kernel<EK, DPAD, CD, NBITS, false, false, 1>);
   }
   if (p.q.dim == DPAD)
     hipLaunchKernelGGL((plaid_stream_kernel<EK, DPAD, CD, NBITS, 1, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);

@@ -285,9 +285,22 @@ int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group,
 // Docs per workgroup: aim for >= ~2048 workgroups so 256 CUs see several
 // waves of work, but keep at least a few docs per workgroup to amortise the
 // query-block load.
-int pick_R(int64_t ngroups, int64_t ndocs) {
+// Docs per workgroup. dpad > 0: a dense MaxSim launch of that row width
+// (PLAID tiles pass 0: their workgroups are latency-bound, more of them help).
+int pick_R(int64_t ngroups, int64_t ndocs, int dpad) {
   const int64_t target = 2048;
   int64_t R = (ndocs * ngroups) / target;
+  if (ngroups == 1 && dpad > 0) {
+    // One query block (a single short query): the launch streams the docs
+    // once and every workgroup pays its prologue and pipeline fill. Fewer,
+    // longer workgroups win until the grid no longer fills the chip; these
+    // workgroup counts measured best on one MI355X for 1k..20k docs of 200 to
+    // 300 tokens (d 512: 250, one workgroup per CU; d 128: about 625).
+    const int64_t wgs = dpad >= 512 ? 250 : dpad >= 256 ? 750 : dpad >= 128 ? 625 : 1250;
+    const int64_t r1 = (ndocs + wgs - 1) / wgs;
+    if (r1 > R) R = r1;
+  }
+  if (const char* e = getenv("LIK_R")) R = atoi(e);  // docs per workgroup (tuning aid)
   if (R < 1) R = 1;
   if (R > ndocs) R = ndocs > 0 ? ndocs : 1;
   if (R > 512) R = 512;  // per-doc metadata of a workgroup lives in LDS (kRMax)
@@ -586,7 +599,7 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
     p.osq = out_stride_q;
     p.osd = out_stride_d;
   }
-  p.R = pick_R(p.ngroups, p.ndocs_pg);
+  p.R = pick_R(p.ngroups, p.ndocs_pg, pl.dpad);
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   p.xcd_map = p.NR >= 8 ? 1 : 0;
   const int64_t nb = p.xcd_map ? p.ngroups * ((p.NR + 7) / 8) * 8 : p.ngroups * p.NR;
@@ -787,7 +800,7 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   p.out = out;
   p.osq = out_stride_q;
   p.osd = out_stride_d;
-  p.R = pick_R(p.ngroups, p.ndocs_pg);
+  p.R = pick_R(p.ngroups, p.ndocs_pg, 0);
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   p.xcd_map = p.NR >= 8 ? 1 : 0;
   const int64_t nb = p.xcd_map ? p.ngroups * ((p.NR + 7) / 8) * 8 : p.ngroups * p.NR;

@@ -39,11 +39,18 @@ def unify_dtype(Q: torch.Tensor, D: torch.Tensor) -> tuple[torch.Tensor, torch.T
 
 
 def _mask_i8(m: torch.Tensor | None, shape: tuple[int, int]) -> torch.Tensor | None:
+    """Keep flags as int8 for the kernels, which read ``mask[i * sn + t * sl] != 0``
+    with the tensor's own strides: a bool / 8-bit mask is reinterpreted in place
+    (no copy, broadcast strides kept); other dtypes become ``m != 0``."""
     if m is None:
         return None
     if tuple(m.shape) != tuple(shape):
         m = m.expand(shape)
-    return m.to(torch.int8).contiguous()
+    if m.dtype == torch.int8:
+        return m
+    if m.dtype in (torch.bool, torch.uint8):
+        return m.view(torch.int8)
+    return (m != 0).view(torch.int8)
 
 
 def _i32(t: torch.Tensor | None) -> torch.Tensor | None:

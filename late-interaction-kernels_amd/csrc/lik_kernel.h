@@ -157,6 +157,19 @@ __global__ void __launch_bounds__(W * 64)
   }
   auto dglob = [&](int64_t jl) -> int64_t { return p.pair_d ? pair_doc : kd_base + jl; };
   auto unit_of = [&](int t) -> int64_t { return p.pair_q ? g : g * p.QPG + t; };
+  // Holes-only launch of the two-launch mask split (doc_filter 2): a
+  // workgroup whose docs all keep prefix masks has nothing to score; it
+  // leaves here, before loading its query block (block-uniform decision).
+  if constexpr (SRC == SRC_DENSE) {
+    if (p.doc_filter == 2) {
+      int any = 0;
+      for (int64_t k = jl0 + tid; k < jl1; k += NT) {
+        const int64_t dg = dglob(k);
+        any |= (dg >= 0 && p.holes[dg] != 0) ? 1 : 0;
+      }
+      if (!__syncthreads_or(any)) return;
+    }
+  }
 
   // Output row pointers of the group's units (shifted to doc jl0), so the doc
   // flush needs only the column stride.

@@ -44,6 +44,37 @@ def test_fp8_per_tensor(Nq, Lq, Nd, Ld):
     assert rel_err(got, deq) < 2e-3
 
 
+@pytest.mark.parametrize("d,Lq", [(128, 24), (128, 32), (64, 30)])
+def test_fp8_wide_column_groups(monkeypatch, d, Lq):
+    """Calls that fill a 768-column group run the fp8 4 x 6 configuration (two
+    workgroups per CU); prefix masks, masks with holes (the second, masked
+    launch) and empty docs, checked against the dequantised oracle and, bit
+    for bit, against the 4 x 4 configuration (LIK_CFG forces it; the per-query
+    column sums are in the same order)."""
+    from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_tensor
+
+    _case(f"fp8 4x6 d={d} Lq={Lq}")
+    g = torch.Generator().manual_seed(d + Lq)
+    Nq, Nd, Ld = 70, 40, 100
+    Q = torch.nn.functional.normalize(torch.randn(Nq, Lq, d, generator=g), dim=-1)
+    D = torch.nn.functional.normalize(torch.randn(Nd, Ld, d, generator=g), dim=-1)
+    dm = torch.arange(Ld)[None] < torch.randint(0, Ld + 1, (Nd,), generator=g)[:, None]
+    dm[3, 10:20] = False  # holes: this doc goes through the masked launch
+    dm[5] = False
+    Qf, sq = quantize_fp8_per_tensor(Q.cuda())
+    Df, sd = quantize_fp8_per_tensor(D.cuda())
+    got = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd, d_mask=dm.cuda())
+    deq = O.maxsim(_np(Qf) * sq.item(), _np(Df) * sd.item(), None, dm.numpy())
+    assert rel_err(_np(got), deq) < 2e-3
+    assert _np(got)[:, 5].max() == 0.0
+    monkeypatch.setenv("LIK_CFG", "4,6")
+    forced = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd, d_mask=dm.cuda())
+    assert torch.equal(forced, got)
+    monkeypatch.setenv("LIK_CFG", "4,4")
+    narrow = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd, d_mask=dm.cuda())
+    assert rel_err(_np(narrow), _np(got)) < 1e-5
+
+
 def test_fp8_per_token_and_masks():
     from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_token
 

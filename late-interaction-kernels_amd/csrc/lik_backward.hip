@@ -213,6 +213,64 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
       u_begin = bp.d_ptr[j];
       u_end = bp.d_ptr[j + 1];
     }
+    if (!bp.d_ptr && !bp.q_cu && bp.lq < 64) {
+      // Short padded queries on the (i, j) grid: the (i, s) pairs of units
+      // [u_begin, u_end) flattened, 64 per pass (one query per pass would
+      // leave lanes idle), the next pass's argmax / G / scale loads issued
+      // before this pass's hits are added. Same pair order as the per-query
+      // loop below, so the same sums. Lane (i, s) advances by 64 per pass.
+      const int64_t f0 = u_begin * bp.lq, f1 = u_end * bp.lq;
+      int64_t li = u_begin + lane / bp.lq, ls = lane % bp.lq;  // pair f0 + lane
+      auto load_pass = [&](int64_t fb, int& a, float& sc, int64_t& qoff) {
+        const int64_t f = fb + lane;
+        const int64_t i = li, s = ls;
+        ls += 64;
+        while (ls >= bp.lq) {
+          ls -= bp.lq;
+          ++li;
+        }
+        a = -1;
+        sc = 0.f;
+        qoff = 0;
+        if (f < f1) {
+          const float gij = bp.grad[i * bp.ld_g + jl];
+          int av = gij != 0.f ? bp.amax[(i * bp.ndoc_pg + jl) * bp.lq + s] : -1;
+          if (av >= 0 && bp.qmask && bp.qmask[i * bp.qm_sn + s * bp.qm_sl] == 0) av = -1;
+          float scv = gij;
+          if (bp.qinv && av >= 0) scv *= bp.qinv[i * bp.lq + s];
+          a = av;
+          sc = scv;
+          qoff = i * bp.q_sn + s * bp.q_sl;
+        }
+      };
+      int a_c, a_n;
+      float sc_c, sc_n;
+      int64_t qo_c, qo_n;
+      load_pass(f0, a_c, sc_c, qo_c);
+      for (int64_t fb = f0; fb < f1; fb += 64) {
+        load_pass(fb + 64, a_n, sc_n, qo_n);
+        uint64_t bal = __ballot(a_c >= wlo && a_c < wlo + n);
+        while (bal) {
+          const int l = __builtin_ctzll(bal);
+          bal &= bal - 1;
+          const int r = off + __builtin_amdgcn_readlane(a_c, l) - (int)wlo;
+          touched |= 1u << r;
+          const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_c), l));
+          const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)qo_c, l);
+          const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)qo_c >> 32), l);
+          const char* qrow = bp.q + (int64_t)(((uint64_t)hi << 32) | lo);
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) {
+            const int e = lane * DPL + k;
+            if (e < bp.dim) s_acc[r][e] = fmaf(c, load_elem<EK>(qrow, e), s_acc[r][e]);
+          }
+        }
+        a_c = a_n;
+        sc_c = sc_n;
+        qo_c = qo_n;
+      }
+      return;
+    }
     for (int64_t u = u_begin; u < u_end; ++u) {
       int64_t i, arow;
       float gij;

@@ -378,10 +378,11 @@ struct WsLayout {
 
 // Doc tokens are normalised once, ahead of the tile kernel, when several
 // workgroups would each normalise every doc tile (cross-product scoring with
-// more than one query group, padded bf16 / fp16 docs, no training forward):
-// the kernel then only normalises its query block.
+// more than one query group, padded bf16 / fp16 docs; scoring or the training
+// forward alike, the rows are bitwise the kernel's own): the kernel then only
+// normalises its query block.
 bool prenorm_docs(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool argmax, const Plan& pl) {
-  return (norm_bits(flags) & 2) && !argmax && !(flags & LIK_KD_LAYOUT) && !D->cu_seqlens && pl.ngroups > 1 &&
+  return (norm_bits(flags) & 2) && !(flags & LIK_KD_LAYOUT) && !D->cu_seqlens && pl.ngroups > 1 &&
          (Q->dtype == LIK_BF16 || Q->dtype == LIK_F16) && D->len > 0;
 }
 

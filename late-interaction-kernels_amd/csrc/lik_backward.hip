@@ -102,6 +102,41 @@ __global__ void __launch_bounds__(256) row_invnorm_kernel(const char* x, int64_t
   if (ok && c0 == 0) inv[r] = inv_norm(ss);
 }
 
+// The same inverse norms for the winning doc rows only (sparse winners, as in
+// the KD layout, where most doc rows win no max): entry w of the argmax array
+// [Nq * docs, Lq] names row a of doc j; the rows no entry names are never read
+// by the gradient kernels. Same lanes, chunk order and reduction as
+// row_invnorm_kernel, so the same values; a row named twice is written twice
+// with the same value.
+template <int EK, int LPR>
+__global__ void __launch_bounds__(256) winner_invnorm_kernel(const char* x, int64_t sn, int64_t sl, int64_t L,
+                                                             const int32_t* amax, int64_t nw, int64_t lq,
+                                                             int64_t ndoc_pg, int kd, int dim, float* inv) {
+  constexpr int EPC = EK == EK_F32 ? 4 : 8;
+  const int64_t w = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
+  const int c0 = threadIdx.x % LPR;
+  int a = -1;
+  int64_t j = 0;
+  if (w < nw) {
+    a = amax[w];
+    const int64_t unit = w / lq;  // i * ndoc_pg + jl
+    const int64_t i = unit / ndoc_pg, jl = unit - i * ndoc_pg;
+    j = kd ? i * ndoc_pg + jl : jl;
+  }
+  const bool ok = a >= 0 && a < L;
+  float ss = 0.f;
+  if (ok) {
+    const char* row = x + j * sn + (int64_t)a * sl;
+    for (int c = c0; c * EPC < dim; c += LPR) {
+      const u32x4 v = *(const u32x4*)(row + (int64_t)c * 16);
+      ss += chunk_sumsq<EK>(v);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
+  if (ok && c0 == 0) inv[j * L + a] = inv_norm(ss);
+}
+
 // Store a gradient value in the input dtype.
 template <int EK>
 __device__ __forceinline__ void store_elem(char* row, int e, float v) {
@@ -420,6 +455,16 @@ int launch_invnorm(const char* x, int64_t sn, int64_t sl, int64_t n, int64_t L, 
   return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
 }
 
+template <int EK>
+int launch_winner_invnorm(const BwdParams& bp, float* inv, hipStream_t s) {
+  constexpr int LPR = 16;
+  const int64_t nw = bp.nq * bp.ndoc_pg * bp.lq;
+  if (nw == 0) return LIK_OK;
+  hipLaunchKernelGGL((winner_invnorm_kernel<EK, LPR>), dim3((unsigned)((nw * LPR + 255) / 256)), dim3(256), 0, s,
+                     bp.d, bp.d_sn, bp.d_sl, bp.ld, bp.amax, nw, bp.lq, bp.ndoc_pg, bp.kd, bp.dim, inv);
+  return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+}
+
 int elem_size(int dt) { return dt == LIK_F32 ? 4 : 2; }
 
 // Sort keys of the pair lists: key = owner (query or doc) index, or n (sorted
@@ -571,7 +616,18 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   }
   if (bwd_norm_d(flags)) {
     bp.dinv = wsf;
-    if ((rc = invnorm(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, wsf)) != LIK_OK) return rc;
+    // fewer winner entries than doc rows (KD layout): norms of the winners only
+    if (bp.amax && bp.nq * bp.ndoc_pg * bp.lq < D->n * D->len &&
+        (bp.nq * bp.ndoc_pg * bp.lq) * 16 < ((int64_t)1 << 31) * 256) {
+      switch (Q->dtype) {
+        case LIK_BF16: rc = launch_winner_invnorm<EK_BF16>(bp, wsf, s); break;
+        case LIK_F16: rc = launch_winner_invnorm<EK_F16>(bp, wsf, s); break;
+        default: rc = launch_winner_invnorm<EK_F32>(bp, wsf, s); break;
+      }
+      if (rc != LIK_OK) return rc;
+    } else if ((rc = invnorm(bp.d, bp.d_sn, bp.d_sl, D->n, D->len, wsf)) != LIK_OK) {
+      return rc;
+    }
   }
   switch (Q->dtype) {
     case LIK_BF16: return launch_bwd_dpl<EK_BF16>(bp, s);

@@ -44,7 +44,7 @@ def test_fp8_per_tensor(Nq, Lq, Nd, Ld):
     assert rel_err(got, deq) < 2e-3
 
 
-@pytest.mark.parametrize("d,Lq", [(128, 24), (128, 32), (64, 30)])
+@pytest.mark.parametrize("d,Lq", [(128, 24), (128, 32), (64, 30), (128, 1000)])
 def test_fp8_wide_column_groups(monkeypatch, d, Lq):
     """Calls that fill a 768-column group run the fp8 4 x 6 configuration (two
     workgroups per CU); prefix masks, masks with holes (the second, masked

@@ -243,8 +243,9 @@ int lik_plaid_approx_score(const float* qcs, int64_t n_centroids, int64_t lq, in
  * (prev_scores[r*prev_ld + i], prev_idx[r*prev_ld + i]) for i < prev_k, and
  * (scores[r*ld + c], idx_base + c) for c < n. Writes the k best, ordered by
  * score (descending if largest, else ascending) and then by lower index,
- * to out_scores/out_idx[r*out_ld + i]. k <= prev_k + n, k <= 1024,
- * n <= 4096, indices < 2^32. prev may alias out.
+ * to out_scores/out_idx[r*out_ld + i]. k <= prev_k + n, k <= 8192,
+ * indices < 2^32. For k <= 1024: prev_k <= 1024 and n <= 4096; for larger k:
+ * prev_k <= 8192 and n <= 8192. prev may alias out.
  * Replaces the torch.topk + cat + gather merge of topk.py:41-86 /
  * retrieve.py:278-305 with a deterministic tie order (lower index first).
  */
@@ -256,9 +257,9 @@ int lik_topk_merge(const float* scores, int64_t rows, int64_t n, int64_t ld, int
 /*
  * Top-k of rows of any width: the same selection and tie rule as
  * lik_topk_merge, but n is unbounded (idx_base + n < 2^32). Rows wider than
- * 4096 scores are reduced as a tree of workgroups (4096-score slices, then
- * merges of k-key lists) in a workspace of
- * lik_topk_select_workspace_size(rows, n, k) bytes (0 when n <= 4096).
+ * one slice (4096 scores for k <= 1024, 8192 above) are reduced as a tree of
+ * workgroups (slices, then merges of k-key lists) in a workspace of
+ * lik_topk_select_workspace_size(rows, n, k) bytes (0 for a single slice).
  * Replaces topk.py:41-86 / retrieve.py:278-305 for an unchunked call
  * (chunk=None): one selection over all Nd scores per query instead of a
  * sequence of per-chunk merges.

@@ -8,12 +8,12 @@
 // "better score, then lower index", so the k best candidates are exactly the
 // k largest keys and any grouping of the candidates selects the same set.
 //
-// One workgroup selects the kk largest of up to TK_MAX_KEYS LDS-resident keys
+// One workgroup selects the kk largest of up to MAX_KEYS LDS-resident keys
 // by an 8-pass MSB-first radix select (256-bin histograms), compacts the
 // winners and bitonic-sorts them. A row wider than one workgroup's share is
-// reduced as a tree: level 0 gives each TK_MAX_N-score slice of a row its own
+// reduced as a tree: level 0 gives each MAX_N-score slice of a row its own
 // workgroup, which writes its k best keys (0-padded) to a workspace; each
-// further level merges up to TK_MAX_KEYS / k such lists per workgroup, and the
+// further level merges up to MAX_KEYS / k such lists per workgroup, and the
 // level with one group left writes scores and indices. The running list
 // (prev_*) joins slice 0 at level 0.
 // This replaces topk.py:41-86 / retrieve.py:278-305 (torch.topk + cat +
@@ -23,9 +23,22 @@
 namespace lik {
 
 constexpr int TK_THREADS = 256;
-constexpr int TK_MAX_N = 4096;  // scores per level-0 group
-constexpr int TK_MAX_K = 1024;
-constexpr int TK_MAX_KEYS = TK_MAX_N + TK_MAX_K;
+// Two LDS capacity classes. Small (k <= 1024): 4096 scores per level-0 group
+// plus a running list, winners sorted in their own array (48 KB). Large
+// (k <= 8192): 16384 keys (128 KB, one workgroup per CU), 8192 scores per
+// level-0 group, winners compacted in place into the key array.
+template <int CLS> struct TkCap;
+template <> struct TkCap<0> {
+  static constexpr int MAX_N = 4096, MAX_K = 1024, MAX_KEYS = MAX_N + MAX_K;
+  static constexpr bool INPLACE = false;
+};
+template <> struct TkCap<1> {
+  static constexpr int MAX_N = 8192, MAX_K = 8192, MAX_KEYS = MAX_N + MAX_K;
+  static constexpr bool INPLACE = true;
+};
+constexpr int TK_MAX_N = TkCap<0>::MAX_N;
+constexpr int TK_MAX_K = TkCap<1>::MAX_K;  // largest k of any class
+inline int topk_class(int64_t k) { return k <= TkCap<0>::MAX_K ? 0 : 1; }
 
 __device__ __forceinline__ uint32_t float_order(float f) {
   uint32_t b = __float_as_uint(f);
@@ -63,13 +76,16 @@ struct TopkArgs {
   int64_t old;
 };
 
-template <bool FROM_KEYS>
+template <int CLS, bool FROM_KEYS>
 __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(TopkArgs a) {
-  __shared__ uint64_t s_keys[TK_MAX_KEYS];
-  __shared__ uint64_t s_sel[TK_MAX_K];
+  using C = TkCap<CLS>;
+  __shared__ uint64_t s_keys[C::MAX_KEYS];
+  __shared__ uint64_t s_sel_own[C::INPLACE ? 1 : C::MAX_K];
+  uint64_t* const s_sel = C::INPLACE ? s_keys : s_sel_own;
   __shared__ uint32_t s_hist[256];
   __shared__ uint64_t s_prefix, s_pmask;
   __shared__ int s_kk, s_done, s_cnt, s_real;
+  __shared__ int s_wcnt[TK_THREADS / 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t row = blockIdx.x / a.groups;
@@ -171,11 +187,35 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(TopkArgs a) {
     // winners: (key & pmask) >= prefix; exactly kk_sel of them (keys are
     // unique and the kk_sel-th largest is a real key, above every 0 pad)
     const uint64_t prefix = s_prefix, pmask = s_pmask;
-    for (int i = tid; i < total; i += TK_THREADS) {
-      const uint64_t key = s_keys[i];
-      if ((key & pmask) >= prefix) {
-        const int pos = atomicAdd(&s_cnt, 1);
-        if (pos < TK_MAX_K) s_sel[pos] = key;
+    if constexpr (C::INPLACE) {
+      // In place, one 256-key chunk at a time: every key of the chunk is read
+      // before any write, and a winner's slot is below the number of keys
+      // read so far, so no unread key is overwritten.
+      int base = 0;
+      for (int i0 = 0; i0 < total; i0 += TK_THREADS) {
+        const int i = i0 + tid;
+        const uint64_t key = i < total ? s_keys[i] : 0;
+        const bool win = i < total && (key & pmask) >= prefix;
+        const uint64_t bal = __ballot(win);
+        if (lane == 0) s_wcnt[wv] = (int)__popcll(bal);
+        __syncthreads();
+        int off = base, all = 0;
+#pragma unroll
+        for (int w = 0; w < TK_THREADS / 64; ++w) {
+          off += w < wv ? s_wcnt[w] : 0;
+          all += s_wcnt[w];
+        }
+        if (win) s_keys[off + (int)__popcll(bal & ((1ull << lane) - 1ull))] = key;
+        base += all;
+        __syncthreads();
+      }
+    } else {
+      for (int i = tid; i < total; i += TK_THREADS) {
+        const uint64_t key = s_keys[i];
+        if ((key & pmask) >= prefix) {
+          const int pos = atomicAdd(&s_cnt, 1);
+          if (pos < C::MAX_K) s_sel[pos] = key;
+        }
       }
     }
   }
@@ -219,13 +259,20 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(TopkArgs a) {
 struct TopkPlan {
   int64_t g0, merge, ws_bytes;
 };
-inline TopkPlan topk_plan(int64_t rows, int64_t n, int64_t k) {
+template <int CLS>
+inline TopkPlan topk_plan_cls(int64_t rows, int64_t n, int64_t k) {
+  using C = TkCap<CLS>;
   TopkPlan t;
-  t.g0 = n <= TK_MAX_N ? 1 : (n + TK_MAX_N - 1) / TK_MAX_N;
-  t.merge = k > 0 ? TK_MAX_KEYS / k : 1;
+  t.g0 = n <= C::MAX_N ? 1 : (n + C::MAX_N - 1) / C::MAX_N;
+  t.merge = k > 0 ? C::MAX_KEYS / k : 1;
   t.ws_bytes = t.g0 > 1 ? 2 * rows * t.g0 * k * (int64_t)sizeof(uint64_t) : 0;
   return t;
 }
+inline TopkPlan topk_plan(int64_t rows, int64_t n, int64_t k) {
+  return topk_class(k) == 0 ? topk_plan_cls<0>(rows, n, k) : topk_plan_cls<1>(rows, n, k);
+}
+inline int64_t topk_max_n(int64_t k) { return topk_class(k) == 0 ? TkCap<0>::MAX_N : TkCap<1>::MAX_N; }
+inline int64_t topk_max_k(int64_t k) { return topk_class(k) == 0 ? TkCap<0>::MAX_K : TkCap<1>::MAX_K; }
 // PLAID approximate score, plaid.py:28-79 semantics: one wavefront per doc,
 // lane s < Lq keeps the running max of qcs[code, s] over the doc's tokens.
 __global__ void __launch_bounds__(256)
@@ -266,7 +313,8 @@ static int topk_validate(const float* scores, int64_t rows, int64_t n, int64_t i
                          const int64_t* prev_idx, int64_t prev_k, int64_t k, float* out_scores, int64_t* out_idx) {
   if (rows < 0 || n < 0 || prev_k < 0 || k < 0) return LIK_ERR_INVALID;
   if (rows == 0 || k == 0) return LIK_OK;
-  if (k > TK_MAX_K || prev_k > TK_MAX_K) return LIK_ERR_UNSUPPORTED;
+  // k picks the capacity class; the running list must fit the same class
+  if (k > TK_MAX_K || prev_k > topk_max_k(k)) return LIK_ERR_UNSUPPORTED;
   if (k > prev_k + n) return LIK_ERR_INVALID;
   if (n > 0 && !scores) return LIK_ERR_INVALID;
   if (prev_k > 0 && (!prev_scores || !prev_idx)) return LIK_ERR_INVALID;
@@ -292,13 +340,16 @@ static int topk_run(const float* scores, int64_t rows, int64_t n, int64_t ld, in
   a.k = k;
   a.largest = largest;
   a.groups = (int)t.g0;
-  a.per_group = TK_MAX_N;
+  a.per_group = topk_max_n(k);
   a.out_s = out_scores;
   a.out_i = out_idx;
   a.old = out_ld;
   uint64_t* bufs[2] = {(uint64_t*)ws, ws ? (uint64_t*)ws + rows * t.g0 * k : nullptr};
   a.keys_out = t.g0 > 1 ? bufs[0] : nullptr;
-  hipLaunchKernelGGL(topk_select_kernel<false>, dim3((unsigned)(rows * t.g0)), dim3(TK_THREADS), 0, st, a);
+  const bool big = topk_class(k) != 0;
+  void (*const level0)(TopkArgs) = big ? topk_select_kernel<1, false> : topk_select_kernel<0, false>;
+  void (*const merge)(TopkArgs) = big ? topk_select_kernel<1, true> : topk_select_kernel<0, true>;
+  hipLaunchKernelGGL(level0, dim3((unsigned)(rows * t.g0)), dim3(TK_THREADS), 0, st, a);
   int64_t lists = t.g0;
   int cur = 0;
   while (lists > 1) {
@@ -308,7 +359,7 @@ static int topk_run(const float* scores, int64_t rows, int64_t n, int64_t ld, in
     a.groups = (int)groups;
     a.per_group = t.merge * k;
     a.keys_out = groups > 1 ? bufs[cur ^ 1] : nullptr;
-    hipLaunchKernelGGL(topk_select_kernel<true>, dim3((unsigned)(rows * groups)), dim3(TK_THREADS), 0, st, a);
+    hipLaunchKernelGGL(merge, dim3((unsigned)(rows * groups)), dim3(TK_THREADS), 0, st, a);
     lists = groups;
     cur ^= 1;
   }
@@ -321,7 +372,7 @@ int lik_topk_merge(const float* scores, int64_t rows, int64_t n, int64_t ld, int
                    lik_stream_t stream) {
   const int v = topk_validate(scores, rows, n, idx_base, prev_scores, prev_idx, prev_k, k, out_scores, out_idx);
   if (v != 1) return v;
-  if (n > TK_MAX_N) return LIK_ERR_UNSUPPORTED;
+  if (n > topk_max_n(k)) return LIK_ERR_UNSUPPORTED;
   return topk_run(scores, rows, n, ld, idx_base, prev_scores, prev_idx, prev_k, prev_ld, k, largest, out_scores,
                   out_idx, out_ld, nullptr, (hipStream_t)stream);
 }

@@ -16,7 +16,7 @@ import torch
 from . import _lib
 from ._core import dense_maxsim, unify_dtype
 
-TOPK_MAX_K = 1024  # largest k the fused merge handles
+TOPK_MAX_K = 8192  # largest k the fused select handles
 
 
 def _merge_sorted_fallback(s, i, k, largest):

@@ -203,7 +203,10 @@ def test_plaid_empty_corpus():
 @pytest.mark.parametrize("largest", [True, False])
 @pytest.mark.parametrize("n,k,chunk", [(100, 10, None), (5000, 100, 4096), (9000, 1000, 2048), (37, 37, 5),
                                        (300, 7, 1), (300000, 100, None), (70000, 1000, None), (20001, 1, None),
-                                       (50000, 64, 20000), (4097, 4097 - 4096, 4096)])
+                                       (50000, 64, 20000), (4097, 4097 - 4096, 4096),
+                                       # large-capacity class (1024 < k <= 8192) and the k > 8192 sort
+                                       (20000, 3000, 4096), (30000, 1025, 10000), (100000, 8192, None),
+                                       (12000, 5000, 6000), (9000, 9000, None)])
 def test_topk_merge_bit_exact(largest, n, k, chunk):
     from late_interaction_kernels.topk import topk_update
 

@@ -82,6 +82,18 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     assert L.lik_topk_select_workspace_size(1, 1 << 20, 100) == 2 * 256 * 100 * 8
     rc = L.lik_topk_select(1, 1, 1 << 20, 1 << 20, 0, None, None, 0, 0, 100, 1, 1, 1, 100, None, 0, None)
     assert rc == _lib.LIK_ERR_WORKSPACE
+    # large-capacity class (1024 < k <= 8192): 8192-score slices
+    assert L.lik_topk_select_workspace_size(2, 8192, 2000) == 0
+    assert L.lik_topk_select_workspace_size(2, 100000, 2000) == 2 * 2 * 13 * 2000 * 8
+    assert L.lik_topk_select_workspace_size(2, 100000, 1024) == 2 * 2 * 25 * 1024 * 8
+    # k beyond the largest class, or a running list wider than k's class, is
+    # rejected before any launch (dummy pointers are never dereferenced)
+    rc = L.lik_topk_select(1, 1, 10000, 10000, 0, None, None, 0, 0, 8193, 1, 1, 1, 8193, None, 0, None)
+    assert rc == _lib.LIK_ERR_UNSUPPORTED
+    rc = L.lik_topk_select(1, 1, 100, 100, 0, 1, 1, 2000, 2000, 1000, 1, 1, 1, 1000, None, 0, None)
+    assert rc == _lib.LIK_ERR_UNSUPPORTED
+    rc = L.lik_topk_merge(1, 1, 8193, 8193, 0, None, None, 0, 0, 2000, 1, 1, 1, 2000, None)
+    assert rc == _lib.LIK_ERR_UNSUPPORTED
 
 
 def test_value_errors_match_the_reference_contract():

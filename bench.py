@@ -8,6 +8,12 @@ D[4096, 300, 128], values N(0,1) L2-normalised per token, document valid
 length ~ U[50, 300] as a prefix d_mask. One step = one ``maxsim(Q, D,
 d_mask=...)`` call over the whole batch (inputs resident in HBM).
 
+The default run also measures the rest of BASELINE.json's metric and puts it
+under ``parts`` in the same JSON line: ``fp8`` (C4 ColPali, K steps),
+``plaid`` (C5 retrieve top-100 over 1M compressed docs, 1,024 queries,
+``--plaid-steps`` steps) and ``plaid_q1`` (the same corpus at one query, the
+HBM-bound case), each with its own roofline. ``--no-parts`` skips them.
+
 Other workloads (``--workload``): ``kd`` (D_kd[512, 64, 300, 128], HBM-bound),
 ``varlen`` (65,536 packed docs, log-uniform [16, 2048] tokens, 256 queries),
 ``fp8`` (ColPali Q[256, 24, 128] x D[8192, 1030, 128] e4m3), ``plaid``
@@ -50,10 +56,11 @@ KERNEL_MS = {}  # filled by _time_steps: summed duration and count of the MaxSim
 
 def _time_steps(fn, steps: int, warmup: int) -> float:
     """ms per step: W untimed steps, then K steps between events on the current
-    stream (the stream every op launches on). Inside the timed region the
-    library also brackets each MaxSim tile-kernel launch with HIP events on
-    that stream (lik_timing_begin/end); their summed duration is what
-    ``roofline.achieved`` divides by."""
+    stream (the stream every op launches on). Inside the timed region each
+    scoring call also records a pair of HIP events on that stream around its
+    MaxSim tile-kernel launch (``_lib.launch_options(timer=...)`` hands them
+    to the C ABI per call through ``lik_launch_opts_t``); their summed
+    duration is what ``roofline.achieved`` divides by."""
     import torch
 
     from late_interaction_kernels import _lib
@@ -63,13 +70,14 @@ def _time_steps(fn, steps: int, warmup: int) -> float:
     _sync()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    _lib.timing_begin()
-    start.record()
-    for _ in range(steps):
-        fn()
-    end.record()
+    timer = _lib.LaunchTimer()
+    with _lib.launch_options(timer=timer):
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
     _sync()
-    kms, n = _lib.timing_end()
+    kms, n = timer.total_ms()
     KERNEL_MS.update(total=kms, launches=n, steps=steps)
     return start.elapsed_time(end) / steps
 
@@ -107,6 +115,17 @@ def _normed(shape, gen, dtype):
     x = torch.randn(*shape, generator=gen, device="cuda", dtype=torch.float32)
     x = torch.nn.functional.normalize(x, dim=-1)
     return x.to(dtype)
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (what ``lscpu`` prints as "Model name")."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def _cpu_threads() -> int:
@@ -168,7 +187,8 @@ def wl_inbatch(args, normalize=False):
         dt = time.perf_counter() - t0
         cpu_flops = 2.0 * d * (nqs * Lq) * float(dlen.sum().item())
         res["cpu_baseline"] = {"value": round(cpu_flops / dt / 1e12, 5), "unit": "TFLOP/s",
-                               "cores": _cpu_threads(), "kind": "port",
+                               "cores": _cpu_threads(), "kind": "port", "cpu_model": _cpu_model(),
+                               "host_cpus": os.cpu_count(),
                                "sample": f"{nqs} of {Nq} queries x all {Nd} docs (oracle/lik_oracle.maxsim, "
                                          f"numpy fp32), {dt:.1f} s"}
     return res
@@ -571,6 +591,9 @@ def main() -> None:
     ap.add_argument("--cpu-sample-queries", type=int, default=256)
     ap.add_argument("--plaid-docs", type=int, default=1_000_000)
     ap.add_argument("--plaid-queries", type=int, default=1024)
+    ap.add_argument("--plaid-steps", type=int, default=5, help="timed steps of the C5 part (about 1 s each)")
+    ap.add_argument("--no-parts", dest="parts", action="store_false",
+                    help="default workload only: skip the fp8 / PLAID parts of the metric")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -586,6 +609,22 @@ def main() -> None:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
     res = WORKLOADS[args.workload](args)
+    parts = None
+    if args.workload == "inbatch" and args.parts:
+        # The rest of BASELINE.json's metric, each on its own config and with
+        # its own roofline: C4 fp8 TFLOP/s, C5 PLAID retrieve queries/s at
+        # top-100, and the PLAID kernel's HBM rate at Nq = 1.
+        parts = {}
+        for name, fn, steps in (("fp8", wl_fp8, args.steps), ("plaid", wl_plaid, args.plaid_steps),
+                                ("plaid_q1", wl_plaid_q1, args.steps)):
+            torch.cuda.empty_cache()
+            sub = argparse.Namespace(**vars(args))
+            sub.steps, sub.warmup = steps, min(args.warmup, 2) if name == "plaid" else args.warmup
+            r = fn(sub)
+            parts[name] = {"metric": r["metric"], "value": r["value"], "unit": r["unit"], "dtype": r["dtype"],
+                           "steps": sub.steps, "warmup": sub.warmup, "ms_per_step": r["ms_per_step"],
+                           "config": r["config"], "roofline": r["roofline"]}
+            print(f"[bench] {name}: {r['value']} {r['unit']}", file=sys.stderr, flush=True)
     out = {
         "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
@@ -594,6 +633,8 @@ def main() -> None:
     }
     if "cpu_baseline" in res:
         out["cpu_baseline"] = res["cpu_baseline"]
+    if parts:
+        out["parts"] = parts
     print(json.dumps(out))
 
 

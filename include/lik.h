@@ -5,7 +5,10 @@
  * launches on the caller's HIP stream, performs no device allocation and no
  * host synchronisation, and returns a status code (LIK_OK == 0, negative on
  * error). Scratch memory, where an entry point needs it, is passed in by the
- * caller; its size comes from the matching *_workspace_size() query.
+ * caller; its size comes from the matching *_workspace_size() query. The
+ * library keeps no mutable state between calls and reads no environment
+ * variables, so every entry point is reentrant; tuning and timing choices
+ * travel with the call (lik_launch_opts_t, the *_ex entry points).
  *
  * The reference library (late-interaction-kernels v0.4.5) has no native ABI:
  * its "FFI" is Triton's Python launcher. Each declaration below names the
@@ -274,15 +277,42 @@ int lik_topk_select(const float* scores, int64_t rows, int64_t n, int64_t ld, in
 const char* lik_version(void);
 
 /*
- * Launch timing (measurement aid, no counterpart in the reference, which
- * times with CUDA events around whole Python calls): between
- * lik_timing_begin() and lik_timing_end(), each scoring call brackets its
- * MaxSim tile-kernel launch with HIP events on the call's stream.
- * lik_timing_end() waits for the recorded launches and returns their summed
- * duration and count. Process-wide and not thread-safe: for benchmarks.
+ * Per-call launch options (no counterpart in the reference, whose Triton
+ * launcher autotunes and times from Python). Passing NULL, or a zeroed
+ * struct, is exactly the plain entry point. The struct is read during the
+ * call only; the library keeps no state between calls, so concurrent calls
+ * with different options are independent.
+ *   col_waves, col_blocks: force the tile kernel's column block (waves per
+ *       workgroup W in {1, 4, 8}, 32-column blocks per wave NSUB in
+ *       {1, 2, 4}; fp8 at d <= 128 also 4 x 6); 0 = automatic. A
+ *       configuration the call cannot use is ignored.
+ *   docs_per_wg: documents per workgroup, 1..512; 0 = automatic.
+ *   plaid_variant (lik_plaid_maxsim_ex): 0 automatic, 1 per-lane stream
+ *       decode, 2 exact LDS-gather decode (bitwise equal to the tile
+ *       kernel), 3 the tile kernel (no stream kernel).
+ *   timing_start, timing_stop: hipEvent_t or NULL. When both are set, they
+ *       are recorded on the call's stream immediately before and after the
+ *       call's main MaxSim launch (the launch that scores the mask-free
+ *       documents), so a caller can time that kernel alone.
  */
-int lik_timing_begin(void);
-int lik_timing_end(double* total_ms, int64_t* launches);
+typedef struct {
+  int32_t col_waves;
+  int32_t col_blocks;
+  int32_t docs_per_wg;
+  int32_t plaid_variant;
+  void* timing_start;
+  void* timing_stop;
+} lik_launch_opts_t;
+
+/* lik_maxsim / lik_maxsim_workspace_size / lik_plaid_maxsim with launch options. */
+int lik_maxsim_ex(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
+                  int64_t out_stride_q, int64_t out_stride_d, void* workspace, size_t workspace_bytes,
+                  const lik_launch_opts_t* opts, lik_stream_t stream);
+size_t lik_maxsim_workspace_size_ex(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
+                                    const lik_launch_opts_t* opts);
+int lik_plaid_maxsim_ex(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t flags, float* out,
+                        int64_t out_stride_q, int64_t out_stride_d, const lik_launch_opts_t* opts,
+                        lik_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -211,7 +211,7 @@ int check_seqs(const lik_seqs_t* s) {
 // (max) length `lq`. `one_query_per_group` is true when each query owns its
 // documents (KD / pairs).
 int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group, Plan& pl, int min_w = 1,
-              bool prefer_two_wg = false) {
+              bool prefer_two_wg = false, const lik_launch_opts_t* opts = nullptr) {
   pl.dpad = pick_dpad(dt, dim);
   if (pl.dpad < 0) return LIK_ERR_UNSUPPORTED;
   const int nsmax = max_nsub(dt, pl.dpad);
@@ -247,15 +247,14 @@ int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group,
     pl.NSUB = 4;
     if (pl.dpad <= 128 && !one_query_per_group && need >= 4 * 6 * 32) pl.NSUB = 6;
   }
-  // LIK_CFG="W,NSUB" forces a column-block configuration (tuning aid).
-  if (const char* e = getenv("LIK_CFG")) {
-    int w = 0, ns = 0;
-    if (sscanf(e, "%d,%d", &w, &ns) == 2 && ns >= 1 && ns <= nsmax &&
-        ((w == 1 && (ns == 1 || ns == 2 || ns == 4)) || (w == 4 && (ns == 1 || ns == 2 || ns == 4)) ||
-         (w == 8 && (ns == 1 || ns == 2 || ns == 4)))) {
-      pl.W = w;
-      pl.NSUB = ns;
-    } else if (sscanf(e, "%d,%d", &w, &ns) == 2 && w == 4 && ns == 6 && dt == LIK_FP8_E4M3 && pl.dpad <= 128) {
+  // a caller-forced column block (lik_launch_opts_t), when this call can use it
+  if (opts && opts->col_waves > 0 && opts->col_blocks > 0) {
+    const int w = opts->col_waves, ns = opts->col_blocks;
+    const bool std_ok = (w == 1 || w == 4 || w == 8) && (ns == 1 || ns == 2 || ns == 4) && ns <= nsmax &&
+                        w >= min_w && !(w == 8 && ns * bfrag_regs(dt, pl.dpad) > 64) &&
+                        !(w == 8 && ns == 4 && dt != LIK_FP8_E4M3);
+    const bool fp8_wide = w == 4 && ns == 6 && dt == LIK_FP8_E4M3 && pl.dpad <= 128 && prefer_two_wg;
+    if (std_ok || fp8_wide) {
       pl.W = w;
       pl.NSUB = ns;
     }
@@ -292,7 +291,7 @@ int make_plan(int dt, int dim, int64_t nq, int64_t lq, bool one_query_per_group,
 // query-block load.
 // Docs per workgroup. dpad > 0: a dense MaxSim launch of that row width
 // (PLAID tiles pass 0: their workgroups are latency-bound, more of them help).
-int pick_R(int64_t ngroups, int64_t ndocs, int dpad) {
+int pick_R(int64_t ngroups, int64_t ndocs, int dpad, const lik_launch_opts_t* opts = nullptr) {
   const int64_t target = 2048;
   int64_t R = (ndocs * ngroups) / target;
   if (ngroups == 1 && dpad > 0) {
@@ -305,7 +304,7 @@ int pick_R(int64_t ngroups, int64_t ndocs, int dpad) {
     const int64_t r1 = (ndocs + wgs - 1) / wgs;
     if (r1 > R) R = r1;
   }
-  if (const char* e = getenv("LIK_R")) R = atoi(e);  // docs per workgroup (tuning aid)
+  if (opts && opts->docs_per_wg > 0) R = opts->docs_per_wg;  // caller-forced (lik_launch_opts_t)
   if (R < 1) R = 1;
   if (R > ndocs) R = ndocs > 0 ? ndocs : 1;
   if (R > 512) R = 512;  // per-doc metadata of a workgroup lives in LDS (kRMax)
@@ -343,31 +342,14 @@ int norm_bits(uint32_t flags) {
   return ((flags & (LIK_NORMALIZE | LIK_NORMALIZE_Q)) ? 1 : 0) | ((flags & (LIK_NORMALIZE | LIK_NORMALIZE_D)) ? 2 : 0);
 }
 
-// Launch timing, a measurement aid that is off unless lik_timing_begin() was
-// called: the tile-kernel launch of each scoring call (the one that scores
-// the mask-free docs, i.e. all of them unless a mask has holes) is bracketed
-// by a pair of HIP events on the call's stream. Events are created once and
-// reused; not thread-safe, meant for a benchmark driver.
-struct LaunchTimer {
-  bool on = false;
-  std::vector<hipEvent_t> ev;  // pairs: start, stop
-  size_t used = 0;             // pairs recorded since lik_timing_begin
-};
-LaunchTimer g_timer;
-
+// Brackets the call's main tile-kernel launch with the caller's HIP events
+// (lik_launch_opts_t::timing_start / timing_stop), when both are given.
 template <typename F>
-int timed_launch(hipStream_t s, F&& launch) {
-  if (!g_timer.on) return launch();
-  const size_t k = g_timer.used;
-  while (g_timer.ev.size() < 2 * (k + 1)) {
-    hipEvent_t e;
-    if (hipEventCreate(&e) != hipSuccess) return LIK_ERR_LAUNCH;
-    g_timer.ev.push_back(e);
-  }
-  if (hipEventRecord(g_timer.ev[2 * k], s) != hipSuccess) return LIK_ERR_LAUNCH;
+int timed_launch(hipStream_t s, const lik_launch_opts_t* opts, F&& launch) {
+  if (!opts || !opts->timing_start || !opts->timing_stop) return launch();
+  if (hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
   const int rc = launch();
-  if (hipEventRecord(g_timer.ev[2 * k + 1], s) != hipSuccess) return LIK_ERR_LAUNCH;
-  g_timer.used = k + 1;
+  if (hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;
   return rc;
 }
 
@@ -389,15 +371,16 @@ bool prenorm_docs(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool
 // The plan of a scoring call: the two-workgroup 4 x 4 block is preferred when
 // the tile loop does no doc-side work (no doc normalise left in the kernel,
 // no argmax, no token scales).
-int plan_call(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool argmax, Plan& pl, bool& prenorm) {
+int plan_call(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool argmax, Plan& pl, bool& prenorm,
+              const lik_launch_opts_t* opts) {
   const bool kd = (flags & LIK_KD_LAYOUT) != 0;
   const int min_w = ((norm_bits(flags) & 2) || argmax) ? 4 : 1;
   const bool plain = !argmax && !Q->token_scale && !D->token_scale;
-  int rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, plain);
+  int rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, plain, opts);
   if (rc != LIK_OK) return rc;
   prenorm = prenorm_docs(Q, D, flags, argmax, pl);
   if ((norm_bits(flags) & 2) && !prenorm && plain)  // docs normalised in the kernel: no 4 x 4 preference
-    rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, false);
+    rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, false, opts);
   return rc;
 }
 
@@ -436,50 +419,41 @@ extern "C" {
 
 const char* lik_version(void) { return "lik-hip 0.1.0 gfx950"; }
 
-int lik_timing_begin(void) {
-  g_timer.on = true;
-  g_timer.used = 0;
-  return LIK_OK;
-}
-
-int lik_timing_end(double* total_ms, int64_t* launches) {
-  double tot = 0.0;
-  for (size_t k = 0; k < g_timer.used; ++k) {
-    if (hipEventSynchronize(g_timer.ev[2 * k + 1]) != hipSuccess) return LIK_ERR_LAUNCH;
-    float ms = 0.f;
-    if (hipEventElapsedTime(&ms, g_timer.ev[2 * k], g_timer.ev[2 * k + 1]) != hipSuccess) return LIK_ERR_LAUNCH;
-    tot += ms;
-  }
-  if (total_ms) *total_ms = tot;
-  if (launches) *launches = (int64_t)g_timer.used;
-  g_timer.on = false;
-  g_timer.used = 0;
-  return LIK_OK;
-}
-
-size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
+size_t lik_maxsim_workspace_size_ex(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
+                                    const lik_launch_opts_t* opts) {
   if (check_seqs(Q) != LIK_OK || check_seqs(D) != LIK_OK) return 0;
   // the same size serves the scoring call and the training forward
   size_t total = 0;
   for (bool argmax : {false, true}) {
     Plan pl;
     bool prenorm = false;
-    if (plan_call(Q, D, flags, argmax, pl, prenorm) != LIK_OK) return 0;
+    if (plan_call(Q, D, flags, argmax, pl, prenorm, opts) != LIK_OK) return 0;
     const size_t t = ws_layout(Q, D, flags, pl, prenorm).total;
     total = t > total ? t : total;
   }
   return total;
 }
 
+size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
+  return lik_maxsim_workspace_size_ex(Q, D, flags, nullptr);
+}
+
 static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
                        int64_t out_stride_q, int64_t out_stride_d, int32_t* argmax, void* workspace,
-                       size_t workspace_bytes, lik_stream_t stream);
+                       size_t workspace_bytes, const lik_launch_opts_t* opts, lik_stream_t stream);
 
 int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
                int64_t out_stride_q, int64_t out_stride_d, void* workspace, size_t workspace_bytes,
                lik_stream_t stream) {
   return maxsim_impl(Q, D, flags, out_scale, out, out_stride_q, out_stride_d, nullptr, workspace, workspace_bytes,
-                     stream);
+                     nullptr, stream);
+}
+
+int lik_maxsim_ex(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
+                  int64_t out_stride_q, int64_t out_stride_d, void* workspace, size_t workspace_bytes,
+                  const lik_launch_opts_t* opts, lik_stream_t stream) {
+  return maxsim_impl(Q, D, flags, out_scale, out, out_stride_q, out_stride_d, nullptr, workspace, workspace_bytes,
+                     opts, stream);
 }
 
 int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float* out, int64_t out_stride_q,
@@ -487,12 +461,13 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
                       lik_stream_t stream) {
   if (!argmax && Q && D && Q->n > 0 && D->n > 0) return LIK_ERR_INVALID;
   if (Q && (Q->dtype == LIK_FP8_E4M3 || Q->token_scale || (D && D->token_scale))) return LIK_ERR_UNSUPPORTED;
-  return maxsim_impl(Q, D, flags, 1.0f, out, out_stride_q, out_stride_d, argmax, workspace, workspace_bytes, stream);
+  return maxsim_impl(Q, D, flags, 1.0f, out, out_stride_q, out_stride_d, argmax, workspace, workspace_bytes, nullptr,
+                     stream);
 }
 
 static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
                        int64_t out_stride_q, int64_t out_stride_d, int32_t* argmax, void* workspace,
-                       size_t workspace_bytes, lik_stream_t stream) {
+                       size_t workspace_bytes, const lik_launch_opts_t* opts, lik_stream_t stream) {
   int rc;
   if ((rc = check_seqs(Q)) != LIK_OK) return rc;
   if ((rc = check_seqs(D)) != LIK_OK) return rc;
@@ -517,7 +492,7 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
     p.osd = out_stride_d;
     p.kd_K = kd ? D->n / Q->n : 0;
     p.ndocs_pg = kd ? p.kd_K : D->n;
-    return timed_launch(s, [&] { return launch_maxsim_wide(Q->dtype, p, s); });
+    return timed_launch(s, opts, [&] { return launch_maxsim_wide(Q->dtype, p, s); });
   }
 
   // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: the
@@ -525,7 +500,7 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
   // ahead of the tile kernel
   Plan pl;
   bool prenorm = false;
-  if ((rc = plan_call(Q, D, flags, argmax != nullptr, pl, prenorm)) != LIK_OK) return rc;
+  if ((rc = plan_call(Q, D, flags, argmax != nullptr, pl, prenorm, opts)) != LIK_OK) return rc;
   const WsLayout wl = ws_layout(Q, D, flags, pl, prenorm);
   if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return LIK_ERR_WORKSPACE;
 
@@ -544,7 +519,7 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
     const unsigned nblk = (unsigned)((rows * lpr + 255) / 256);
     const char* dx = (const char*)D->data;
     const int64_t sn = D->stride_n * eb, sl = D->stride_l * eb;
-    if ((rc = timed_launch(s, [&] {
+    if ((rc = [&] {
            auto go = [&](auto kern) {
              hipLaunchKernelGGL(kern, dim3(nblk), dim3(256), 0, s, dx, sn, sl, D->n, D->len, D->dim, dn);
              return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
@@ -559,7 +534,7 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
            if (lpr == 16) return go(norm_rows_kernel<EK_F16, 16>);
            if (lpr == 32) return go(norm_rows_kernel<EK_F16, 32>);
            return go(norm_rows_kernel<EK_F16, 64>);
-         })) != LIK_OK)
+         }()) != LIK_OK)
       return rc;
     p.d.data = dn;
     p.d.sn_b = D->len * (int64_t)D->dim * eb;
@@ -605,7 +580,7 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
     p.osq = out_stride_q;
     p.osd = out_stride_d;
   }
-  p.R = pick_R(p.ngroups, p.ndocs_pg, pl.dpad);
+  p.R = pick_R(p.ngroups, p.ndocs_pg, pl.dpad, opts);
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   p.xcd_map = p.NR >= 8 ? 1 : 0;
   const int64_t nb = p.xcd_map ? p.ngroups * ((p.NR + 7) / 8) * 8 : p.ngroups * p.NR;
@@ -617,12 +592,12 @@ static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
     Params p1 = p;
     p1.d.mask = nullptr;
     p1.doc_filter = 1;
-    if ((rc = timed_launch(s, [&] { return launch_dense(Q->dtype, pl, p1, nb, s); })) != LIK_OK) return rc;
+    if ((rc = timed_launch(s, opts, [&] { return launch_dense(Q->dtype, pl, p1, nb, s); })) != LIK_OK) return rc;
     p.doc_filter = 2;
   }
   if (wl.need_extent) {
     if ((rc = launch_dense(Q->dtype, pl, p, nb, s)) != LIK_OK) return rc;
-  } else if ((rc = timed_launch(s, [&] { return launch_dense(Q->dtype, pl, p, nb, s); })) != LIK_OK) {
+  } else if ((rc = timed_launch(s, opts, [&] { return launch_dense(Q->dtype, pl, p, nb, s); })) != LIK_OK) {
     return rc;
   }
   if (wl.need_part) {
@@ -677,7 +652,7 @@ static int pairs_impl(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* p
   p.out = out;
   p.osq = 1;
   p.osd = 0;
-  return timed_launch(s, [&] { return launch_dense(Q->dtype, pl, p, num_pairs, s); });
+  return launch_dense(Q->dtype, pl, p, num_pairs, s);
 }
 
 int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, const int32_t* pair_d,
@@ -693,6 +668,12 @@ int lik_maxsim_pairs_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, const int3
 
 int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t flags, float* out,
                      int64_t out_stride_q, int64_t out_stride_d, lik_stream_t stream) {
+  return lik_plaid_maxsim_ex(Q, docs, flags, out, out_stride_q, out_stride_d, nullptr, stream);
+}
+
+int lik_plaid_maxsim_ex(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t flags, float* out,
+                        int64_t out_stride_q, int64_t out_stride_d, const lik_launch_opts_t* opts,
+                        lik_stream_t stream) {
   int rc;
   if ((rc = check_seqs(Q)) != LIK_OK) return rc;
   if (!docs || docs->n < 0) return LIK_ERR_INVALID;
@@ -719,9 +700,9 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   // range) decodes straight into its MFMA fragments (the tile kernel is
   // latency-bound here).
   const int sdp = pick_dpad(Q->dtype, Q->dim);
-  const char* se = getenv("LIK_PLAID_STREAM");
+  const int variant = opts ? opts->plaid_variant : 0;
   if (Q->n <= 4 && Q->len >= 1 && Q->len <= 32 && (sdp == 64 || sdp == 128) && docs->res_stride_tok % 4 == 0 &&
-      docs->centroid_dtype != LIK_F32 && !(se && se[0] == '0')) {
+      docs->centroid_dtype != LIK_F32 && variant != 3) {
     Params p{};
     p.q = to_dev(*Q);
     p.pl.codes = docs->codes;
@@ -748,7 +729,7 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
     // tile no larger than the padded rows'. Centroids of the query's type take
     // the split form (q.c + q.r, norm from its parts: within bf16 / fp16
     // rounding of the decode route, not bitwise equal to it); others the
-    // exact decode. LIK_PLAID_STREAM=1 / =2 force the per-lane / the exact
+    // exact decode. plaid_variant 1 / 2 forces the per-lane / the exact
     // gather variant (tuning and parity aids).
     {
       const int64_t rsb = (int64_t)sdp * docs->nbits / 8, nr = (32 * rsb + 1023) / 1024;
@@ -756,7 +737,7 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
                           32 * docs->res_stride_tok <= nr * 1024 &&
                           docs->n_centroids * docs->cent_stride * ceb <= (int64_t)kInvRow;
       const bool same_type = docs->centroid_dtype == Q->dtype;
-      p.gather = !lds_ok || (se && se[0] == '1') ? 0 : (same_type && !(se && se[0] == '2') ? 2 : 1);
+      p.gather = !lds_ok || variant == 1 ? 0 : (same_type && variant != 2 ? 2 : 1);
     }
     // the split form scores two queries per wavefront (one gather and
     // decode serve both); the other variants one
@@ -769,13 +750,13 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
     const int ek = Q->dtype == LIK_F16 ? EK_F16 : EK_BF16;
     const int cdk = docs->centroid_dtype == LIK_F32 ? EK_F32 : (docs->centroid_dtype == LIK_F16 ? EK_F16 : EK_BF16);
     hipStream_t s = (hipStream_t)stream;
-    return timed_launch(s, [&] { return launch_plaid_stream(ek, cdk, sdp, nsub, p, s); });
+    return timed_launch(s, opts, [&] { return launch_plaid_stream(ek, cdk, sdp, nsub, p, s); });
   }
 
   Plan pl;
   // PLAID tiles carry the decode VALU work: at least 4 waves share each tile
   // even when the query block would fit one wave's columns.
-  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, false, pl, 4)) != LIK_OK) return rc;
+  if ((rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, false, pl, 4, false, opts)) != LIK_OK) return rc;
   if (pl.dpad > 256) return LIK_ERR_UNSUPPORTED;
   if (pl.nc != 1) return LIK_ERR_UNSUPPORTED;  // Lq > 512: chunk on the caller side
   Params p{};
@@ -806,11 +787,11 @@ int lik_plaid_maxsim(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, uint32_t
   p.out = out;
   p.osq = out_stride_q;
   p.osd = out_stride_d;
-  p.R = pick_R(p.ngroups, p.ndocs_pg, 0);
+  p.R = pick_R(p.ngroups, p.ndocs_pg, 0, opts);
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   p.xcd_map = p.NR >= 8 ? 1 : 0;
   const int64_t nb = p.xcd_map ? p.ngroups * ((p.NR + 7) / 8) * 8 : p.ngroups * p.NR;
-  return timed_launch((hipStream_t)stream,
+  return timed_launch((hipStream_t)stream, opts,
                       [&] { return launch_plaid(Q->dtype, docs->centroid_dtype, pl, p, nb, (hipStream_t)stream); });
 }
 

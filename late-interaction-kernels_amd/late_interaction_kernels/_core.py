@@ -264,12 +264,13 @@ def packed_backward(grad, Qp, Dp, cu_q, cu_d, argmax, max_q: int, max_d: int, *,
 
 def _launch(qs, ds, flags: int, out_scale: float, out: torch.Tensor, device: torch.device) -> None:
     lib = _lib.load()
-    nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
+    opts = _lib.call_opts()
+    nbytes = lib.lik_maxsim_workspace_size_ex(ctypes.byref(qs), ctypes.byref(ds), flags, opts)
     ws = _lib.workspace(nbytes, device)
     with torch.cuda.device(device):
-        rc = lib.lik_maxsim(
+        rc = lib.lik_maxsim_ex(
             ctypes.byref(qs), ctypes.byref(ds), flags, float(out_scale), out.data_ptr(), out.stride(0),
-            out.stride(1), _lib.ptr(ws), nbytes, _lib.stream_of(out),
+            out.stride(1), _lib.ptr(ws), nbytes, opts, _lib.stream_of(out),
         )
     _lib.check(rc, "lik_maxsim")
 

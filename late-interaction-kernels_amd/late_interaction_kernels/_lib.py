@@ -8,6 +8,8 @@ tensors are not on a ROCm GPU, the ops raise — there is no CPU fallback.
 
 from __future__ import annotations
 
+import contextlib
+import contextvars
 import ctypes
 import os
 from pathlib import Path
@@ -59,8 +61,9 @@ EXPORTED_SYMBOLS = (
     "lik_topk_select",
     "lik_topk_select_workspace_size",
     "lik_version",
-    "lik_timing_begin",
-    "lik_timing_end",
+    "lik_maxsim_ex",
+    "lik_maxsim_workspace_size_ex",
+    "lik_plaid_maxsim_ex",
 )
 
 _p = ctypes.c_void_p
@@ -110,6 +113,19 @@ class LikPlaidDocs(ctypes.Structure):
         ("bucket_weights", _p),
         ("n_buckets", _i32),
         ("nbits", _i32),
+    ]
+
+
+class LikLaunchOpts(ctypes.Structure):
+    """Mirror of ``lik_launch_opts_t``."""
+
+    _fields_ = [
+        ("col_waves", _i32),
+        ("col_blocks", _i32),
+        ("docs_per_wg", _i32),
+        ("plaid_variant", _i32),
+        ("timing_start", _p),
+        ("timing_stop", _p),
     ]
 
 
@@ -173,10 +189,14 @@ def load() -> ctypes.CDLL:
     lib.lik_topk_select_workspace_size.restype = ctypes.c_size_t
     lib.lik_version.argtypes = []
     lib.lik_version.restype = ctypes.c_char_p
-    lib.lik_timing_begin.argtypes = []
-    lib.lik_timing_begin.restype = ctypes.c_int
-    lib.lik_timing_end.argtypes = [P(ctypes.c_double), P(ctypes.c_int64)]
-    lib.lik_timing_end.restype = ctypes.c_int
+    lib.lik_maxsim_ex.argtypes = [P(LikSeqs), P(LikSeqs), ctypes.c_uint32, ctypes.c_float, _p, _i64, _i64, _p,
+                                  ctypes.c_size_t, P(LikLaunchOpts), _p]
+    lib.lik_maxsim_ex.restype = ctypes.c_int
+    lib.lik_maxsim_workspace_size_ex.argtypes = [P(LikSeqs), P(LikSeqs), ctypes.c_uint32, P(LikLaunchOpts)]
+    lib.lik_maxsim_workspace_size_ex.restype = ctypes.c_size_t
+    lib.lik_plaid_maxsim_ex.argtypes = [P(LikSeqs), P(LikPlaidDocs), ctypes.c_uint32, _p, _i64, _i64,
+                                        P(LikLaunchOpts), _p]
+    lib.lik_plaid_maxsim_ex.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -250,17 +270,62 @@ def version() -> str:
     return load().lik_version().decode()
 
 
-def timing_begin() -> None:
-    """Start bracketing each scoring call's MaxSim tile-kernel launch with HIP events."""
-    check(load().lik_timing_begin(), "lik_timing_begin")
+# Launch options of the scoring calls made in the current context (thread /
+# asyncio task): a forced column block, docs per workgroup, the PLAID kernel
+# variant, and a launch timer. The C library itself keeps no state between
+# calls; these are handed to it per call as a lik_launch_opts_t.
+_OPTS: contextvars.ContextVar[dict | None] = contextvars.ContextVar("lik_launch_opts", default=None)
 
 
-def timing_end() -> tuple[float, int]:
-    """Wait for the launches recorded since :func:`timing_begin`; return (summed ms, count)."""
-    ms = ctypes.c_double()
-    n = ctypes.c_int64()
-    check(load().lik_timing_end(ctypes.byref(ms), ctypes.byref(n)), "lik_timing_end")
-    return float(ms.value), int(n.value)
+class LaunchTimer:
+    """Collects a pair of HIP events around the main MaxSim launch of every
+    scoring call made while it is active (see :func:`launch_options`)."""
+
+    def __init__(self) -> None:
+        self.pairs: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+
+    def new_pair(self) -> tuple[int, int]:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        # materialise the HIP events (torch creates them lazily on first record)
+        a.record()
+        b.record()
+        self.pairs.append((a, b))
+        return a.cuda_event, b.cuda_event
+
+    def total_ms(self) -> tuple[float, int]:
+        """Wait for the recorded launches; return (summed ms, launch count)."""
+        tot = 0.0
+        for a, b in self.pairs:
+            b.synchronize()
+            tot += a.elapsed_time(b)
+        return tot, len(self.pairs)
+
+
+@contextlib.contextmanager
+def launch_options(*, cfg: tuple[int, int] | None = None, docs_per_wg: int = 0, plaid_variant: int = 0,
+                   timer: LaunchTimer | None = None):
+    """Tuning / measurement options for the scoring calls inside the block."""
+    tok = _OPTS.set({"cfg": cfg, "docs_per_wg": docs_per_wg, "plaid_variant": plaid_variant, "timer": timer})
+    try:
+        yield
+    finally:
+        _OPTS.reset(tok)
+
+
+def call_opts():
+    """ctypes pointer to this call's ``lik_launch_opts_t``, or None (defaults)."""
+    o = _OPTS.get()
+    if o is None:
+        return None
+    s = LikLaunchOpts()
+    if o["cfg"]:
+        s.col_waves, s.col_blocks = o["cfg"]
+    s.docs_per_wg = o["docs_per_wg"]
+    s.plaid_variant = o["plaid_variant"]
+    if o["timer"] is not None:
+        s.timing_start, s.timing_stop = o["timer"].new_pair()
+    return ctypes.pointer(s)
 
 
 def _elem_align(dtype: torch.dtype) -> int:

@@ -93,9 +93,9 @@ def _plaid_launch(Q, docs: _lib.LikPlaidDocs, normalize: bool, out: torch.Tensor
         qs = _lib.seqs(Qc, n=Nq, length=Qc.shape[1], stride_n=Qc.stride(0), stride_l=Qc.stride(1))
         dst = out if n == 0 else tmp
         with torch.cuda.device(Q.device):
-            rc = lib.lik_plaid_maxsim(
+            rc = lib.lik_plaid_maxsim_ex(
                 ctypes.byref(qs), ctypes.byref(docs), flags, dst.data_ptr(), dst.stride(0), dst.stride(1),
-                _lib.stream_of(dst),
+                _lib.call_opts(), _lib.stream_of(dst),
             )
         _lib.check(rc, "lik_plaid_maxsim")
         if n > 0:
@@ -411,11 +411,12 @@ def _decoded_chunk_scores(Qp, docs, cu, j0: int, j1: int, t0: int, t1: int, norm
     ds = _lib.seqs(buf, n=j1 - j0, length=0, stride_l=buf.stride(0), cu=cu_rel)
     flags = _lib.LIK_NORMALIZE_Q if normalize else 0
     lib = _lib.load()
-    nbytes = lib.lik_maxsim_workspace_size(ctypes.byref(qs), ctypes.byref(ds), flags)
+    opts = _lib.call_opts()
+    nbytes = lib.lik_maxsim_workspace_size_ex(ctypes.byref(qs), ctypes.byref(ds), flags, opts)
     ws = _lib.workspace(nbytes, Qp.device)
     with torch.cuda.device(Qp.device):
-        rc = lib.lik_maxsim(ctypes.byref(qs), ctypes.byref(ds), flags, 1.0, out.data_ptr(), out.stride(0),
-                            out.stride(1), _lib.ptr(ws), nbytes, _lib.stream_of(out))
+        rc = lib.lik_maxsim_ex(ctypes.byref(qs), ctypes.byref(ds), flags, 1.0, out.data_ptr(), out.stride(0),
+                               out.stride(1), _lib.ptr(ws), nbytes, opts, _lib.stream_of(out))
     _lib.check(rc, "lik_maxsim")
     return buf
 

@@ -14,6 +14,7 @@ import torch
 
 import lik_oracle as O
 from conftest import rel_err
+from late_interaction_kernels._lib import launch_options
 
 pytestmark = pytest.mark.gpu
 
@@ -45,11 +46,11 @@ def test_fp8_per_tensor(Nq, Lq, Nd, Ld):
 
 
 @pytest.mark.parametrize("d,Lq", [(128, 24), (128, 32), (64, 30), (128, 1000)])
-def test_fp8_wide_column_groups(monkeypatch, d, Lq):
+def test_fp8_wide_column_groups(d, Lq):
     """Calls that fill a 768-column group run the fp8 4 x 6 configuration (two
     workgroups per CU); prefix masks, masks with holes (the second, masked
     launch) and empty docs, checked against the dequantised oracle and, bit
-    for bit, against the 4 x 4 configuration (LIK_CFG forces it; the per-query
+    for bit, against the 4 x 4 configuration (launch_options forces it; the per-query
     column sums are in the same order)."""
     from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_tensor
 
@@ -67,11 +68,11 @@ def test_fp8_wide_column_groups(monkeypatch, d, Lq):
     deq = O.maxsim(_np(Qf) * sq.item(), _np(Df) * sd.item(), None, dm.numpy())
     assert rel_err(_np(got), deq) < 2e-3
     assert _np(got)[:, 5].max() == 0.0
-    monkeypatch.setenv("LIK_CFG", "4,6")
-    forced = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd, d_mask=dm.cuda())
+    with launch_options(cfg=(4, 6)):
+        forced = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd, d_mask=dm.cuda())
     assert torch.equal(forced, got)
-    monkeypatch.setenv("LIK_CFG", "4,4")
-    narrow = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd, d_mask=dm.cuda())
+    with launch_options(cfg=(4, 4)):
+        narrow = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd, d_mask=dm.cuda())
     assert rel_err(_np(narrow), _np(got)) < 1e-5
 
 

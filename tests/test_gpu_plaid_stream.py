@@ -2,10 +2,10 @@
 
 lik_plaid_maxsim scores up to 4 queries of <= 32 tokens with one wavefront
 per (query, doc range). Its exact variants (per-lane and LDS-gather decode;
-LIK_PLAID_STREAM=2 forces the gather one where the layout allows it) use
+launch_options(plaid_variant=2) forces the gather one where the layout allows it) use
 the tile kernel's arithmetic (same decode, norm tree, rounding, MFMA order
 and per-query summation order), so their scores are bitwise equal to the
-tile kernel's (LIK_PLAID_STREAM=0 forces that one). The default for
+tile kernel's (launch_options(plaid_variant=3) forces that one). The default for
 centroids of the query's type is the split form (q.c + q.r on the stored
 centroid chunks and bf16 / fp16 bucket weights, norm from ||c||^2 + 2 c.r +
 ||r||^2): within bf16 tolerance of both. Everything is checked against the
@@ -22,6 +22,7 @@ import torch
 
 import lik_oracle as O
 from conftest import rel_err
+from late_interaction_kernels._lib import launch_options
 
 pytestmark = pytest.mark.gpu
 
@@ -52,7 +53,7 @@ def _index(Nd, max_ld, d, nbits, seed, cdtype):
 @pytest.mark.parametrize("cdtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("nq", [1, 3])
-def test_stream_varlen_matches_tile_kernel(monkeypatch, nbits, cdtype, d, nq):
+def test_stream_varlen_matches_tile_kernel(nbits, cdtype, d, nq):
     from late_interaction_kernels.plaid import maxsim_residual_varlen
 
     _case(f"stream varlen nbits={nbits} {cdtype} d={d} nq={nq}")
@@ -62,10 +63,10 @@ def test_stream_varlen_matches_tile_kernel(monkeypatch, nbits, cdtype, d, nq):
     Q = torch.randn(nq, 32, d, generator=g).to(qdt).cuda()
     args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), nbits)
     stream = maxsim_residual_varlen(Q, *args)
-    monkeypatch.setenv("LIK_PLAID_STREAM", "2")
-    exact = maxsim_residual_varlen(Q, *args)
-    monkeypatch.setenv("LIK_PLAID_STREAM", "0")
-    tile = maxsim_residual_varlen(Q, *args)
+    with launch_options(plaid_variant=2):
+        exact = maxsim_residual_varlen(Q, *args)
+    with launch_options(plaid_variant=3):
+        tile = maxsim_residual_varlen(Q, *args)
     assert torch.equal(exact, tile)
     assert rel_err(stream.cpu().numpy(), tile.cpu().numpy()) < 1e-2
     for s in (stream, exact):
@@ -77,7 +78,7 @@ def test_stream_varlen_matches_tile_kernel(monkeypatch, nbits, cdtype, d, nq):
 
 
 @pytest.mark.parametrize("lq", [32, 20])
-def test_stream_padded_and_short_queries(monkeypatch, lq):
+def test_stream_padded_and_short_queries(lq):
     from late_interaction_kernels.plaid import maxsim_residual
 
     _case(f"stream padded lq={lq}")
@@ -93,10 +94,10 @@ def test_stream_padded_and_short_queries(monkeypatch, lq):
     Q = torch.randn(2, lq, d).to(torch.bfloat16).cuda()
     args = (pc.cuda(), pr.cuda(), lens.to(torch.int32).cuda(), cent.cuda(), bw.cuda(), nbits)
     stream = maxsim_residual(Q, *args)
-    monkeypatch.setenv("LIK_PLAID_STREAM", "2")
-    exact = maxsim_residual(Q, *args)
-    monkeypatch.setenv("LIK_PLAID_STREAM", "0")
-    tile = maxsim_residual(Q, *args)
+    with launch_options(plaid_variant=2):
+        exact = maxsim_residual(Q, *args)
+    with launch_options(plaid_variant=3):
+        tile = maxsim_residual(Q, *args)
     assert torch.equal(exact, tile)
     assert rel_err(stream.cpu().numpy(), tile.cpu().numpy()) < 1e-2
     ref = O.maxsim_residual(Q.float().cpu().numpy(), pc.numpy(), pr.numpy(), lens.numpy(), cent.float().numpy(),
@@ -111,8 +112,6 @@ def test_split_form_large_index(normalize):
     against the exact gather variant and the oracle: the split form drops
     only the bf16 rounding of the normalised token (and rounds the bucket
     weights to bf16), so it stays within a few 1e-3 of both."""
-    import os
-
     from late_interaction_kernels.plaid import maxsim_residual_varlen
 
     _case(f"split large normalize={normalize}")
@@ -129,11 +128,8 @@ def test_split_form_large_index(normalize):
     Q = torch.nn.functional.normalize(torch.randn(1, 32, d, generator=g), dim=-1).to(torch.bfloat16).cuda()
     args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), nbits)
     split = maxsim_residual_varlen(Q, *args, normalize=normalize)
-    os.environ["LIK_PLAID_STREAM"] = "2"
-    try:
+    with launch_options(plaid_variant=2):
         exact = maxsim_residual_varlen(Q, *args, normalize=normalize)
-    finally:
-        del os.environ["LIK_PLAID_STREAM"]
     e = rel_err(split.cpu().numpy(), exact.cpu().numpy())
     print(f"split vs exact rel err {e:.2e}")
     assert e < 5e-3

@@ -60,9 +60,11 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
 
 
 def build(jobs: int | None = None, verbose: bool = False, out_dir: Path | None = None,
-          extra_flags: list[str] | None = None) -> Path:
+          extra_flags: list[str] | None = None, incremental: bool = False) -> Path:
     """Compile and link; ``extra_flags`` (e.g. -DLIK_PROF) and ``out_dir`` are for
-    instrumented side builds that must not replace the product library."""
+    instrumented side builds that must not replace the product library.
+    ``incremental`` recompiles only sources newer than their object (or
+    older than the newest header); the default rebuilds everything."""
     out_dir = Path(out_dir) if out_dir else OUT_DIR
     out_dir.mkdir(parents=True, exist_ok=True)
     obj_dir = HERE / ("_build" if not extra_flags else "_build_extra")
@@ -71,9 +73,16 @@ def build(jobs: int | None = None, verbose: bool = False, out_dir: Path | None =
     if not sources:
         raise RuntimeError(f"no sources in {CSRC}")
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
+    newest_hdr = max([h.stat().st_mtime for h in CSRC.glob("*.h")] + [h.stat().st_mtime for h in INCLUDE.glob("*.h")])
     objs = []
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_compile, s, obj_dir / (s.stem + ".o"), extra_flags or []) for s in sources]
+        futs = []
+        for s in sources:
+            o = obj_dir / (s.stem + ".o")
+            if incremental and o.exists() and o.stat().st_mtime > max(s.stat().st_mtime, newest_hdr):
+                objs.append(o)
+                continue
+            futs.append(ex.submit(_compile, s, o, extra_flags or []))
         for f in futs:
             obj, msg = f.result()
             objs.append(obj)
@@ -95,8 +104,9 @@ def main() -> None:
     ap.add_argument("-v", "--verbose", action="store_true")
     ap.add_argument("--out-dir", default=None, help="side build directory (instrumented builds)")
     ap.add_argument("--define", action="append", default=[], help="extra -D macro, e.g. LIK_PROF")
+    ap.add_argument("--incremental", action="store_true", help="recompile only out-of-date objects")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose, args.out_dir, [f"-D{d}" for d in args.define]))
+    print(build(args.jobs, args.verbose, args.out_dir, [f"-D{d}" for d in args.define], args.incremental))
 
 
 if __name__ == "__main__":

@@ -442,6 +442,8 @@ int launch_bwd_dpl(const BwdParams& bp, hipStream_t s) {
   if (bp.dim <= 128) return launch_bwd<EK, 2>(bp, s);
   if (bp.dim <= 256) return launch_bwd<EK, 4>(bp, s);
   if (bp.dim <= 512) return launch_bwd<EK, 8>(bp, s);
+  if (bp.dim <= 1024) return launch_bwd<EK, 16>(bp, s);
+  if (bp.dim <= 2048) return launch_bwd<EK, 32>(bp, s);
   return LIK_ERR_UNSUPPORTED;
 }
 
@@ -563,7 +565,7 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   if ((Q->cu_seqlens && bwd_norm_q(flags)) || (D->cu_seqlens && bwd_norm_d(flags))) return LIK_ERR_UNSUPPORTED;
   if (D->cu_seqlens && (flags & LIK_KD_LAYOUT)) return LIK_ERR_INVALID;
   if (Q->n < 0 || D->n < 0 || Q->len < 0 || D->len < 0) return LIK_ERR_INVALID;
-  if (Q->dim > 512) return LIK_ERR_UNSUPPORTED;
+  if (Q->dim > 2048) return LIK_ERR_UNSUPPORTED;
   const bool kd = (flags & LIK_KD_LAYOUT) != 0;
   if (kd && (Q->n == 0 || D->n % Q->n != 0)) return LIK_ERR_INVALID;
   if (Q->n == 0 || D->n == 0) return LIK_OK;
@@ -645,7 +647,7 @@ int lik_maxsim_pairs_backward(const float* grad, const lik_seqs_t* Q, const lik_
   if (Q->dtype != LIK_BF16 && Q->dtype != LIK_F16 && Q->dtype != LIK_F32) return LIK_ERR_UNSUPPORTED;
   if (Q->lengths || D->lengths || Q->token_scale || D->token_scale || D->mask) return LIK_ERR_UNSUPPORTED;
   if (flags & (LIK_NORMALIZE | LIK_NORMALIZE_Q | LIK_NORMALIZE_D | LIK_KD_LAYOUT)) return LIK_ERR_UNSUPPORTED;
-  if (Q->dim > 512) return LIK_ERR_UNSUPPORTED;
+  if (Q->dim > 2048) return LIK_ERR_UNSUPPORTED;
   if (Q->n < 0 || D->n < 0 || Q->len < 0 || D->len < 0) return LIK_ERR_INVALID;
   if (num_pairs > 0x7fffffffLL || Q->n > 0x7ffffffeLL || D->n > 0x7ffffffeLL) return LIK_ERR_UNSUPPORTED;
   if (num_pairs == 0 || Q->n == 0 || D->n == 0) return LIK_OK;

@@ -254,7 +254,7 @@ __global__ void __launch_bounds__(W * 64)
     int64_t q = 0, tok = 0;
     if (p.pair_q) {
       q = p.pair_q[g];
-      tok = s;
+      tok = p.q_tok0 + s;
       valid = valid && q >= 0 && q < p.q.n;
     } else {
       const int64_t u = g * p.QPG + ul;
@@ -736,7 +736,8 @@ __global__ void __launch_bounds__(W * 64)
       }
       // global (not generic) store: a flat store would also count in the LDS
       // wait counter and force full waits on the A-fragment reads
-      ((__attribute__((address_space(1))) float*)orow)[s_slotk[sl] * p.osd] = sum * p.out_scale;
+      auto* o = &((__attribute__((address_space(1))) float*)orow)[s_slotk[sl] * p.osd];
+      *o = p.accumulate ? sum * p.out_scale + *o : sum * p.out_scale;
     }
   };
 
@@ -814,9 +815,9 @@ __global__ void __launch_bounds__(W * 64)
         if (h == 0 && p.amax && ul < p.QPG) {
           const int64_t u = g * p.QPG + ul;
           const int64_t q = u / p.nc;
-          const int64_t tok = (u - q * p.nc) * p.LU + (col - ul * p.LU);
+          const int64_t tok = p.q_tok0 + (u - q * p.nc) * p.LU + (col - ul * p.LU);
           if (u < p.nunits && tok < p.amax_ld)
-            p.amax[(q * p.ndocs_pg + jl0 + k) * p.amax_ld + tok] = __builtin_isfinite(fmaxf(v0, v1)) ? win : -1;
+            p.amax[(q * p.amax_qs + jl0 + k) * p.amax_ld + tok] = __builtin_isfinite(fmaxf(v0, v1)) ? win : -1;
         }
         mi[sub] = -1;
       }

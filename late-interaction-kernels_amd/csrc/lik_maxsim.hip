@@ -24,7 +24,6 @@
 #include <stdio.h>
 #include <stdlib.h>
 
-#include <vector>
 
 #include "lik_params.h"
 
@@ -356,15 +355,23 @@ int timed_launch(hipStream_t s, const lik_launch_opts_t* opts, F&& launch) {
 struct WsLayout {
   size_t extent_off = 0, holes_off = 0, tbits_off = 0, part_off = 0, dnorm_off = 0, total = 0;
   bool need_extent = false, need_part = false, need_dnorm = false;
+  int64_t dnorm_docs = 0;  // docs per pre-normalised slice
 };
+
+// Largest pre-normalised doc copy a call keeps in its workspace: docs are
+// normalised and scored in slices of at most this many bytes, so the
+// workspace of a large corpus stays bounded (a slice of 512 MiB holds 2M
+// bf16 rows of d = 128 and keeps the tile kernel's grid full).
+constexpr size_t kPrenormCap = (size_t)512 << 20;
 
 // Doc tokens are normalised once, ahead of the tile kernel, when several
 // workgroups would each normalise every doc tile (cross-product scoring with
 // more than one query group, padded bf16 / fp16 docs; scoring or the training
 // forward alike, the rows are bitwise the kernel's own): the kernel then only
-// normalises its query block.
-bool prenorm_docs(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool argmax, const Plan& pl) {
-  return (norm_bits(flags) & 2) && !(flags & LIK_KD_LAYOUT) && !D->cu_seqlens && pl.ngroups > 1 &&
+// normalises its query block. `allow` = false keeps the doc normalise in the
+// tile kernel (callers without room for the normalised copy).
+bool prenorm_docs(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, const Plan& pl, bool allow) {
+  return allow && (norm_bits(flags) & 2) && !(flags & LIK_KD_LAYOUT) && !D->cu_seqlens && pl.ngroups > 1 &&
          (Q->dtype == LIK_BF16 || Q->dtype == LIK_F16) && D->len > 0;
 }
 
@@ -372,13 +379,13 @@ bool prenorm_docs(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool
 // the tile loop does no doc-side work (no doc normalise left in the kernel,
 // no argmax, no token scales).
 int plan_call(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool argmax, Plan& pl, bool& prenorm,
-              const lik_launch_opts_t* opts) {
+              const lik_launch_opts_t* opts, bool allow_prenorm = true) {
   const bool kd = (flags & LIK_KD_LAYOUT) != 0;
   const int min_w = ((norm_bits(flags) & 2) || argmax) ? 4 : 1;
   const bool plain = !argmax && !Q->token_scale && !D->token_scale;
   int rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, plain, opts);
   if (rc != LIK_OK) return rc;
-  prenorm = prenorm_docs(Q, D, flags, argmax, pl);
+  prenorm = prenorm_docs(Q, D, flags, pl, allow_prenorm);
   if ((norm_bits(flags) & 2) && !prenorm && plain)  // docs normalised in the kernel: no 4 x 4 preference
     rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, false, opts);
   return rc;
@@ -388,9 +395,13 @@ WsLayout ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, con
   WsLayout w;
   size_t off = 0;
   if (prenorm) {
+    const size_t row_doc = (size_t)D->len * (size_t)D->dim * 2;
+    int64_t per = (int64_t)(kPrenormCap / row_doc);
+    if (per < 1) per = 1;
+    w.dnorm_docs = per < D->n ? per : D->n;
     w.need_dnorm = true;
     w.dnorm_off = off;
-    off = align256(off + (size_t)D->n * (size_t)D->len * (size_t)D->dim * 2);
+    off = align256(off + (size_t)w.dnorm_docs * row_doc);
   }
   if (D->mask) {
     w.need_extent = true;
@@ -410,6 +421,245 @@ WsLayout ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, con
   }
   w.total = off;
   return w;
+}
+
+// Normalised copy of docs [j0, j0 + n) of D, contiguous [n, len, dim], in dst.
+int launch_norm_rows(const lik_seqs_t* D, int dpad, int64_t j0, int64_t n, char* dst, hipStream_t s) {
+  const int eb = elem_bytes(D->dtype);
+  const int64_t rows = n * D->len;
+  const int lpr = dpad * eb / 16;  // the tile kernel's chunks per row
+  const unsigned nblk = (unsigned)((rows * lpr + 255) / 256);
+  const int64_t sn = D->stride_n * eb, sl = D->stride_l * eb;
+  const char* dx = (const char*)D->data + j0 * sn;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(nblk), dim3(256), 0, s, dx, sn, sl, n, D->len, D->dim, dst);
+    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+  };
+  if (D->dtype == LIK_BF16) {
+    if (lpr == 8) return go(norm_rows_kernel<EK_BF16, 8>);
+    if (lpr == 16) return go(norm_rows_kernel<EK_BF16, 16>);
+    if (lpr == 32) return go(norm_rows_kernel<EK_BF16, 32>);
+    return go(norm_rows_kernel<EK_BF16, 64>);
+  }
+  if (lpr == 8) return go(norm_rows_kernel<EK_F16, 8>);
+  if (lpr == 16) return go(norm_rows_kernel<EK_F16, 16>);
+  if (lpr == 32) return go(norm_rows_kernel<EK_F16, 32>);
+  return go(norm_rows_kernel<EK_F16, 64>);
+}
+
+int launch_fill_i32(int32_t* a, int64_t n, int32_t v, hipStream_t s) {
+  if (n <= 0) return LIK_OK;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, n, v);
+  return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+}
+
+int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
+                int64_t out_stride_q, int64_t out_stride_d, int32_t* argmax, void* workspace, size_t workspace_bytes,
+                const lik_launch_opts_t* opts, bool allow_prenorm, lik_stream_t stream) {
+  int rc;
+  if ((rc = check_seqs(Q)) != LIK_OK) return rc;
+  if ((rc = check_seqs(D)) != LIK_OK) return rc;
+  if (Q->dtype != D->dtype || Q->dim != D->dim) return LIK_ERR_INVALID;
+  if (!out && Q->n > 0 && D->n > 0) return LIK_ERR_INVALID;
+  const bool kd = (flags & LIK_KD_LAYOUT) != 0;
+  if (kd && (D->cu_seqlens || (Q->n > 0 && D->n % Q->n != 0))) return LIK_ERR_INVALID;
+  if (Q->n == 0 || D->n == 0) return LIK_OK;
+  hipStream_t s = (hipStream_t)stream;
+
+  // rows wider than any column block (bf16 / fp16 > 512, fp32 > 256): the
+  // one-wave-per-pair kernel, no workspace
+  if (pick_dpad(Q->dtype, Q->dim) < 0) {
+    if (Q->dtype == LIK_FP8_E4M3 || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
+    Params p{};
+    p.q = to_dev(*Q);
+    p.d = to_dev(*D);
+    p.normalize = norm_bits(flags);
+    p.out_scale = out_scale;
+    p.out = out;
+    p.osq = out_stride_q;
+    p.osd = out_stride_d;
+    p.kd_K = kd ? D->n / Q->n : 0;
+    p.ndocs_pg = kd ? p.kd_K : D->n;
+    if (argmax) {
+      if ((rc = launch_fill_i32(argmax, Q->n * p.ndocs_pg * Q->len, -1, s)) != LIK_OK) return rc;
+      p.amax = argmax;
+      p.amax_ld = Q->len;
+      p.amax_qs = p.ndocs_pg;
+    }
+    return timed_launch(s, opts, [&] { return launch_maxsim_wide(Q->dtype, p, s); });
+  }
+
+  // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: the
+  // plan spreads it over at least 4 waves, or the docs are normalised once
+  // ahead of the tile kernel
+  Plan pl;
+  bool prenorm = false;
+  if ((rc = plan_call(Q, D, flags, argmax != nullptr, pl, prenorm, opts, allow_prenorm)) != LIK_OK) return rc;
+  const WsLayout wl = ws_layout(Q, D, flags, pl, prenorm);
+  if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return LIK_ERR_WORKSPACE;
+
+  Params p{};
+  p.q = to_dev(*Q);
+  p.d = to_dev(*D);
+  p.normalize = norm_bits(flags);
+  char* ws = (char*)workspace;
+  p.out_scale = out_scale;
+  p.nunits = pl.nunits;
+  p.nc = pl.nc;
+  p.LU = pl.LU;
+  p.QPG = pl.QPG;
+  p.ngroups = pl.ngroups;
+  p.kd_K = kd ? D->n / Q->n : 0;
+  p.ndocs_pg = kd ? p.kd_K : D->n;
+  if (argmax) {
+    // entries no doc-end reaches (empty docs) stay -1
+    if ((rc = launch_fill_i32(argmax, Q->n * p.ndocs_pg * Q->len, -1, s)) != LIK_OK) return rc;
+    p.amax = argmax;
+    p.amax_ld = Q->len;
+    p.amax_qs = p.ndocs_pg;
+  }
+
+  if (wl.need_extent) {
+    p.extent = (const int32_t*)(ws + wl.extent_off);
+    p.holes = (const uint8_t*)(ws + wl.holes_off);
+    p.tbits = (const uint32_t*)(ws + wl.tbits_off);
+    p.tbits_sn = (D->len + 31) / 32;
+    hipLaunchKernelGGL(doc_extent_kernel, dim3((unsigned)((D->n + 3) / 4)), dim3(256), 0, s, D->mask,
+                       D->mask_stride_n, D->mask_stride_l, D->n, D->len, D->lengths,
+                       (int32_t*)(ws + wl.extent_off), (uint8_t*)(ws + wl.holes_off),
+                       (uint32_t*)(ws + wl.tbits_off), p.tbits_sn);
+    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+  }
+  if (wl.need_part) {
+    p.out = (float*)(ws + wl.part_off);
+    p.osq = p.ndocs_pg;
+    p.osd = 1;
+  } else {
+    p.out = out;
+    p.osq = out_stride_q;
+    p.osd = out_stride_d;
+  }
+
+  // Tile-kernel launches over docs [j0, j0 + n): the workgroup grid, and with
+  // masks the two-launch split: docs whose kept tokens form a prefix are
+  // scored by the mask-free kernel with the extent as length; a second launch
+  // of the masked kernel scores only the docs with holes (its other
+  // workgroups exit right after reading the doc table).
+  auto score_docs = [&](Params ps, int64_t j0, int64_t n) -> int {
+    ps.ndocs_pg = n;
+    ps.out += j0 * ps.osd;
+    if (ps.extent) {
+      ps.extent += j0;
+      ps.holes += j0;
+      ps.tbits += j0 * ps.tbits_sn;
+    }
+    if (ps.d.mask) ps.d.mask += j0 * ps.d.msn;
+    if (ps.d.lengths) ps.d.lengths += j0;
+    if (ps.amax) ps.amax += j0 * ps.amax_ld;
+    ps.R = pick_R(ps.ngroups, n, pl.dpad, opts);
+    ps.NR = (n + ps.R - 1) / ps.R;
+    ps.xcd_map = ps.NR >= 8 ? 1 : 0;
+    const int64_t nb = ps.xcd_map ? ps.ngroups * ((ps.NR + 7) / 8) * 8 : ps.ngroups * ps.NR;
+    if (ps.extent) {
+      Params p1 = ps;
+      p1.d.mask = nullptr;
+      p1.doc_filter = 1;
+      int r = launch_dense(Q->dtype, pl, p1, nb, s);
+      if (r != LIK_OK) return r;
+      ps.doc_filter = 2;
+    }
+    return launch_dense(Q->dtype, pl, ps, nb, s);
+  };
+
+  const bool timed = opts && opts->timing_start && opts->timing_stop;
+  if (!wl.need_dnorm) {
+    if (timed && hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
+    if ((rc = score_docs(p, 0, p.ndocs_pg)) != LIK_OK) return rc;
+    if (timed && hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;
+  } else {
+    // padded cross-product docs, normalised and scored slice by slice through
+    // one bounded copy; the tile kernel then normalises only its query block
+    char* dn = ws + wl.dnorm_off;
+    const int eb = elem_bytes(D->dtype);
+    for (int64_t j0 = 0; j0 < D->n; j0 += wl.dnorm_docs) {
+      const int64_t n = D->n - j0 < wl.dnorm_docs ? D->n - j0 : wl.dnorm_docs;
+      if ((rc = launch_norm_rows(D, pl.dpad, j0, n, dn, s)) != LIK_OK) return rc;
+      Params ps = p;
+      ps.d.data = dn;  // the copy holds the slice's docs from its first one
+      ps.d.sn_b = D->len * (int64_t)D->dim * eb;
+      ps.d.sl_b = (int64_t)D->dim * eb;
+      ps.normalize &= 1;
+      if (timed && j0 == 0 && hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
+      if ((rc = score_docs(ps, j0, n)) != LIK_OK) return rc;
+    }
+    if (timed && hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;
+  }
+  if (wl.need_part) {
+    const int64_t tot = Q->n * p.ndocs_pg;
+    hipLaunchKernelGGL(unit_sum_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
+                       (const float*)(ws + wl.part_off), Q->n, pl.nc, p.ndocs_pg, out, out_stride_q,
+                       out_stride_d);
+    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+  }
+  return LIK_OK;
+}
+
+// Pair-list scoring. Queries longer than one column block are scored in
+// chunks of query tokens, one launch per chunk, each adding its partial sums
+// to out in chunk order; rows wider than the tile kernel take the
+// one-wave-per-pair kernel.
+int pairs_impl(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, const int32_t* pair_d,
+               int64_t num_pairs, uint32_t flags, float* out, int32_t* argmax, lik_stream_t stream) {
+  int rc;
+  if ((rc = check_seqs(Q)) != LIK_OK) return rc;
+  if ((rc = check_seqs(D)) != LIK_OK) return rc;
+  if (Q->dtype != D->dtype || Q->dim != D->dim) return LIK_ERR_INVALID;
+  if (num_pairs < 0 || (num_pairs > 0 && (!pair_q || !pair_d || !out))) return LIK_ERR_INVALID;
+  if (D->mask || (flags & LIK_KD_LAYOUT)) return LIK_ERR_INVALID;
+  if (num_pairs == 0) return LIK_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (argmax && (Q->dtype == LIK_FP8_E4M3 || Q->token_scale || D->token_scale)) return LIK_ERR_UNSUPPORTED;
+  Params p{};
+  if (argmax) {
+    // pairs with no winner stay -1
+    if ((rc = launch_fill_i32(argmax, num_pairs * Q->len, -1, s)) != LIK_OK) return rc;
+    p.amax = argmax;
+    p.amax_ld = Q->len;
+    p.amax_qs = 1;
+  }
+  p.q = to_dev(*Q);
+  p.d = to_dev(*D);
+  p.normalize = norm_bits(flags);
+  p.out_scale = 1.f;
+  p.pair_q = pair_q;
+  p.pair_d = pair_d;
+  p.out = out;
+  if (pick_dpad(Q->dtype, Q->dim) < 0) {
+    if (Q->dtype == LIK_FP8_E4M3 || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
+    p.ndocs_pg = 1;
+    p.nunits = num_pairs;
+    p.osq = 1;
+    return launch_maxsim_wide(Q->dtype, p, s);
+  }
+  Plan pl;
+  if ((rc = make_plan(Q->dtype, Q->dim, 1, Q->len, true, pl, argmax ? 4 : 1)) != LIK_OK) return rc;
+  p.nunits = num_pairs;
+  p.nc = 1;
+  p.LU = pl.LU;
+  p.QPG = 1;
+  p.ngroups = num_pairs;
+  p.ndocs_pg = 1;
+  p.R = 1;
+  p.NR = 1;
+  p.xcd_map = 0;
+  p.osq = 1;
+  p.osd = 0;
+  for (int c = 0; c < pl.nc; ++c) {
+    p.q_tok0 = (int64_t)c * pl.LU;
+    p.accumulate = c > 0;
+    if ((rc = launch_dense(Q->dtype, pl, p, num_pairs, s)) != LIK_OK) return rc;
+  }
+  return LIK_OK;
 }
 
 }  // namespace
@@ -438,22 +688,18 @@ size_t lik_maxsim_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint3
   return lik_maxsim_workspace_size_ex(Q, D, flags, nullptr);
 }
 
-static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
-                       int64_t out_stride_q, int64_t out_stride_d, int32_t* argmax, void* workspace,
-                       size_t workspace_bytes, const lik_launch_opts_t* opts, lik_stream_t stream);
-
 int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
                int64_t out_stride_q, int64_t out_stride_d, void* workspace, size_t workspace_bytes,
                lik_stream_t stream) {
   return maxsim_impl(Q, D, flags, out_scale, out, out_stride_q, out_stride_d, nullptr, workspace, workspace_bytes,
-                     nullptr, stream);
+                     nullptr, true, stream);
 }
 
 int lik_maxsim_ex(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
                   int64_t out_stride_q, int64_t out_stride_d, void* workspace, size_t workspace_bytes,
                   const lik_launch_opts_t* opts, lik_stream_t stream) {
   return maxsim_impl(Q, D, flags, out_scale, out, out_stride_q, out_stride_d, nullptr, workspace, workspace_bytes,
-                     opts, stream);
+                     opts, true, stream);
 }
 
 int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float* out, int64_t out_stride_q,
@@ -462,197 +708,7 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
   if (!argmax && Q && D && Q->n > 0 && D->n > 0) return LIK_ERR_INVALID;
   if (Q && (Q->dtype == LIK_FP8_E4M3 || Q->token_scale || (D && D->token_scale))) return LIK_ERR_UNSUPPORTED;
   return maxsim_impl(Q, D, flags, 1.0f, out, out_stride_q, out_stride_d, argmax, workspace, workspace_bytes, nullptr,
-                     stream);
-}
-
-static int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
-                       int64_t out_stride_q, int64_t out_stride_d, int32_t* argmax, void* workspace,
-                       size_t workspace_bytes, const lik_launch_opts_t* opts, lik_stream_t stream) {
-  int rc;
-  if ((rc = check_seqs(Q)) != LIK_OK) return rc;
-  if ((rc = check_seqs(D)) != LIK_OK) return rc;
-  if (Q->dtype != D->dtype || Q->dim != D->dim) return LIK_ERR_INVALID;
-  if (!out && Q->n > 0 && D->n > 0) return LIK_ERR_INVALID;
-  const bool kd = (flags & LIK_KD_LAYOUT) != 0;
-  if (kd && (D->cu_seqlens || (Q->n > 0 && D->n % Q->n != 0))) return LIK_ERR_INVALID;
-  if (Q->n == 0 || D->n == 0) return LIK_OK;
-  hipStream_t s = (hipStream_t)stream;
-
-  // rows wider than any column block (bf16 / fp16 > 512, fp32 > 256): the
-  // one-wave-per-pair kernel, no workspace
-  if (pick_dpad(Q->dtype, Q->dim) < 0) {
-    if (argmax || Q->dtype == LIK_FP8_E4M3 || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
-    Params p{};
-    p.q = to_dev(*Q);
-    p.d = to_dev(*D);
-    p.normalize = norm_bits(flags);
-    p.out_scale = out_scale;
-    p.out = out;
-    p.osq = out_stride_q;
-    p.osd = out_stride_d;
-    p.kd_K = kd ? D->n / Q->n : 0;
-    p.ndocs_pg = kd ? p.kd_K : D->n;
-    return timed_launch(s, opts, [&] { return launch_maxsim_wide(Q->dtype, p, s); });
-  }
-
-  // doc-side normalise (or the argmax epilogue) adds per-tile VALU work: the
-  // plan spreads it over at least 4 waves, or the docs are normalised once
-  // ahead of the tile kernel
-  Plan pl;
-  bool prenorm = false;
-  if ((rc = plan_call(Q, D, flags, argmax != nullptr, pl, prenorm, opts)) != LIK_OK) return rc;
-  const WsLayout wl = ws_layout(Q, D, flags, pl, prenorm);
-  if (wl.total > 0 && (!workspace || workspace_bytes < wl.total)) return LIK_ERR_WORKSPACE;
-
-  Params p{};
-  p.q = to_dev(*Q);
-  p.d = to_dev(*D);
-  p.normalize = norm_bits(flags);
-  char* ws = (char*)workspace;
-  if (wl.need_dnorm) {
-    // normalised copy of the docs, contiguous [n, len, dim]; the tile kernel
-    // then normalises only its query block
-    char* dn = ws + wl.dnorm_off;
-    const int eb = elem_bytes(D->dtype);
-    const int64_t rows = D->n * D->len;
-    const int lpr = pl.dpad * eb / 16;  // the tile kernel's chunks per row
-    const unsigned nblk = (unsigned)((rows * lpr + 255) / 256);
-    const char* dx = (const char*)D->data;
-    const int64_t sn = D->stride_n * eb, sl = D->stride_l * eb;
-    if ((rc = [&] {
-           auto go = [&](auto kern) {
-             hipLaunchKernelGGL(kern, dim3(nblk), dim3(256), 0, s, dx, sn, sl, D->n, D->len, D->dim, dn);
-             return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
-           };
-           if (D->dtype == LIK_BF16) {
-             if (lpr == 8) return go(norm_rows_kernel<EK_BF16, 8>);
-             if (lpr == 16) return go(norm_rows_kernel<EK_BF16, 16>);
-             if (lpr == 32) return go(norm_rows_kernel<EK_BF16, 32>);
-             return go(norm_rows_kernel<EK_BF16, 64>);
-           }
-           if (lpr == 8) return go(norm_rows_kernel<EK_F16, 8>);
-           if (lpr == 16) return go(norm_rows_kernel<EK_F16, 16>);
-           if (lpr == 32) return go(norm_rows_kernel<EK_F16, 32>);
-           return go(norm_rows_kernel<EK_F16, 64>);
-         }()) != LIK_OK)
-      return rc;
-    p.d.data = dn;
-    p.d.sn_b = D->len * (int64_t)D->dim * eb;
-    p.d.sl_b = (int64_t)D->dim * eb;
-    p.normalize &= 1;
-  }
-  p.out_scale = out_scale;
-  p.nunits = pl.nunits;
-  p.nc = pl.nc;
-  p.LU = pl.LU;
-  p.QPG = pl.QPG;
-  p.ngroups = pl.ngroups;
-  p.kd_K = kd ? D->n / Q->n : 0;
-  p.ndocs_pg = kd ? p.kd_K : D->n;
-  if (argmax) {
-    // entries no doc-end reaches (empty docs) stay -1
-    const int64_t na = Q->n * p.ndocs_pg * Q->len;
-    if (na > 0) {
-      hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, s, argmax, na, -1);
-      if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
-    }
-    p.amax = argmax;
-    p.amax_ld = Q->len;
-  }
-
-  if (wl.need_extent) {
-    p.extent = (const int32_t*)(ws + wl.extent_off);
-    p.holes = (const uint8_t*)(ws + wl.holes_off);
-    p.tbits = (const uint32_t*)(ws + wl.tbits_off);
-    p.tbits_sn = (D->len + 31) / 32;
-    hipLaunchKernelGGL(doc_extent_kernel, dim3((unsigned)((D->n + 3) / 4)), dim3(256), 0, s, D->mask,
-                       D->mask_stride_n, D->mask_stride_l, D->n, D->len, D->lengths,
-                       (int32_t*)(ws + wl.extent_off), (uint8_t*)(ws + wl.holes_off),
-                       (uint32_t*)(ws + wl.tbits_off), p.tbits_sn);
-    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
-  }
-  if (wl.need_part) {
-    p.out = (float*)(ws + wl.part_off);
-    p.osq = p.ndocs_pg;
-    p.osd = 1;
-  } else {
-    p.out = out;
-    p.osq = out_stride_q;
-    p.osd = out_stride_d;
-  }
-  p.R = pick_R(p.ngroups, p.ndocs_pg, pl.dpad, opts);
-  p.NR = (p.ndocs_pg + p.R - 1) / p.R;
-  p.xcd_map = p.NR >= 8 ? 1 : 0;
-  const int64_t nb = p.xcd_map ? p.ngroups * ((p.NR + 7) / 8) * 8 : p.ngroups * p.NR;
-  if (wl.need_extent) {
-    // Masks: docs whose kept tokens form a prefix (no holes) are scored by the
-    // mask-free kernel with the extent as length; a second launch of the
-    // masked kernel scores only the docs with holes (its other workgroups exit
-    // right after reading the doc table).
-    Params p1 = p;
-    p1.d.mask = nullptr;
-    p1.doc_filter = 1;
-    if ((rc = timed_launch(s, opts, [&] { return launch_dense(Q->dtype, pl, p1, nb, s); })) != LIK_OK) return rc;
-    p.doc_filter = 2;
-  }
-  if (wl.need_extent) {
-    if ((rc = launch_dense(Q->dtype, pl, p, nb, s)) != LIK_OK) return rc;
-  } else if ((rc = timed_launch(s, opts, [&] { return launch_dense(Q->dtype, pl, p, nb, s); })) != LIK_OK) {
-    return rc;
-  }
-  if (wl.need_part) {
-    const int64_t tot = Q->n * p.ndocs_pg;
-    hipLaunchKernelGGL(unit_sum_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
-                       (const float*)(ws + wl.part_off), Q->n, pl.nc, p.ndocs_pg, out, out_stride_q,
-                       out_stride_d);
-    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
-  }
-  return LIK_OK;
-}
-
-static int pairs_impl(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, const int32_t* pair_d,
-                      int64_t num_pairs, uint32_t flags, float* out, int32_t* argmax, lik_stream_t stream) {
-  int rc;
-  if ((rc = check_seqs(Q)) != LIK_OK) return rc;
-  if ((rc = check_seqs(D)) != LIK_OK) return rc;
-  if (Q->dtype != D->dtype || Q->dim != D->dim) return LIK_ERR_INVALID;
-  if (num_pairs < 0 || (num_pairs > 0 && (!pair_q || !pair_d || !out))) return LIK_ERR_INVALID;
-  if (D->mask || (flags & LIK_KD_LAYOUT)) return LIK_ERR_INVALID;
-  if (num_pairs == 0) return LIK_OK;
-  Plan pl;
-  if ((rc = make_plan(Q->dtype, Q->dim, 1, Q->len, true, pl, argmax ? 4 : 1)) != LIK_OK) return rc;
-  if (pl.nc != 1) return LIK_ERR_UNSUPPORTED;
-  hipStream_t s = (hipStream_t)stream;
-  Params p{};
-  if (argmax) {
-    if (Q->dtype == LIK_FP8_E4M3 || Q->token_scale || D->token_scale) return LIK_ERR_UNSUPPORTED;
-    const int64_t na = num_pairs * Q->len;  // pairs with no winner stay -1
-    if (na > 0) {
-      hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, s, argmax, na, -1);
-      if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
-    }
-    p.amax = argmax;
-    p.amax_ld = Q->len;
-  }
-  p.q = to_dev(*Q);
-  p.d = to_dev(*D);
-  p.normalize = norm_bits(flags);
-  p.out_scale = 1.f;
-  p.pair_q = pair_q;
-  p.pair_d = pair_d;
-  p.nunits = num_pairs;
-  p.nc = 1;
-  p.LU = pl.LU;
-  p.QPG = 1;
-  p.ngroups = num_pairs;
-  p.ndocs_pg = 1;
-  p.R = 1;
-  p.NR = 1;
-  p.xcd_map = 0;
-  p.out = out;
-  p.osq = 1;
-  p.osd = 0;
-  return launch_dense(Q->dtype, pl, p, num_pairs, s);
+                     true, stream);
 }
 
 int lik_maxsim_pairs(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, const int32_t* pair_d,

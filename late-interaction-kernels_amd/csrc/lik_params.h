@@ -58,6 +58,9 @@ struct Params {
   int64_t osq, osd;
   int32_t* amax;    // training forward: winner doc-token index per (query, doc, query token), or null
   int64_t amax_ld;  // query tokens per (query, doc) row of amax (the padded Lq)
+  int64_t amax_qs;  // (query, doc) rows of amax per query (the call's docs per query)
+  int64_t q_tok0;   // pair mode: first query token of this launch's query chunk
+  int accumulate;   // add the scores to out instead of storing them (query-chunk launches)
 };
 
 // PLAID gather kernel: byte offset given to a row past the tile end; the

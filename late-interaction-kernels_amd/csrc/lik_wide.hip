@@ -24,9 +24,25 @@ __global__ void __launch_bounds__(256) maxsim_wide_kernel(const Params p) {
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
   const int wl = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t w = (int64_t)blockIdx.x * 4 + wl;
-  const int64_t q = w / p.ndocs_pg, jl = w - q * p.ndocs_pg;
-  if (q >= p.q.n) return;  // wave-uniform; no barrier in this kernel
-  const int64_t j = p.kd_K ? q * p.kd_K + jl : jl;
+  // cross product / KD: wave w is (query q, doc jl); pair list: wave w is pair w
+  int64_t q, jl, j;
+  if (p.pair_q) {
+    if (w >= p.nunits) return;  // wave-uniform; no barrier in this kernel
+    q = p.pair_q[w];
+    j = p.pair_d[w];
+    jl = 0;
+    if (q < 0 || q >= p.q.n || j < 0 || j >= p.d.n) {  // out-of-range pair: score 0, argmax stays -1
+      if (lane == 0) p.out[w * p.osq] = 0.f;
+      return;
+    }
+  } else {
+    q = w / p.ndocs_pg;
+    jl = w - q * p.ndocs_pg;
+    if (q >= p.q.n) return;
+    j = p.kd_K ? q * p.kd_K + jl : jl;
+  }
+  // argmax row of this (query, doc): (q * docs + jl), or the pair index
+  int32_t* const arow = p.amax ? p.amax + (p.pair_q ? w : q * p.amax_qs + jl) * p.amax_ld : nullptr;
   const int64_t lq = seq_len(p.q, q), ld = seq_len(p.d, j);
   const char* q0 = seq_row0(p.q, q);
   const char* d0 = seq_row0(p.d, j);
@@ -84,6 +100,7 @@ __global__ void __launch_bounds__(256) maxsim_wide_kernel(const Params p) {
     if (qv && p.q.mask) qv = p.q.mask[q * p.q.msn + qt * p.q.msl] != 0;
     const char* qrow = q0 + qt * p.q.sl_b;
     float m = NEG_INF, ssq = 0.f;
+    int mi = -1;  // doc row of m (rows visited in increasing order: first index of the max)
     for (int64_t t0 = 0; t0 < ld; t0 += 32) {
       const int64_t r = t0 + l32;
       bool rv = r < ld;
@@ -124,13 +141,30 @@ __global__ void __launch_bounds__(256) maxsim_wide_kernel(const Params p) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const float sc = sc4[t];
-          m = fmaxf(m, sc == NEG_INF ? NEG_INF : acc[4 * jj + t] * sc);
+          const float v = sc == NEG_INF ? NEG_INF : acc[4 * jj + t] * sc;
+          if (arow) {
+            if (v > m) {
+              m = v;
+              mi = (int)(t0 + 8 * jj + 4 * h + t);
+            }
+          } else {
+            m = fmaxf(m, v);
+          }
         }
       }
     }
     // column l32: max over both halves' rows, query scale, validity, sum
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
     float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    if (arow) {
+      // winner over lanes l, l^32: larger value, equal values the lower row;
+      // -1 where the max is not finite (the row contributes 0)
+      const auto si = __builtin_amdgcn_permlane32_swap((uint32_t)mi, (uint32_t)mi, false, false);
+      const float v0 = __uint_as_float(sw[0]), v1 = __uint_as_float(sw[1]);
+      const int i0 = (int)si[0], i1 = (int)si[1];
+      const bool take1 = v1 > v0 || (v1 == v0 && (unsigned)i1 < (unsigned)i0);
+      if (h == 0 && qt < lq && qt < p.amax_ld) arow[qt] = __builtin_isfinite(mm) ? (take1 ? i1 : i0) : -1;
+    }
     if (norm_q) {
       const auto sq = __builtin_amdgcn_permlane32_swap(__float_as_uint(ssq), __float_as_uint(ssq), false, false);
       mm *= inv_norm(__uint_as_float(sq[0]) + __uint_as_float(sq[1]));
@@ -140,11 +174,14 @@ __global__ void __launch_bounds__(256) maxsim_wide_kernel(const Params p) {
     for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
     total += v;
   }
-  if (lane == 0) p.out[q * p.osq + jl * p.osd] = total * p.out_scale;
+  if (lane == 0) {
+    if (p.pair_q) p.out[w * p.osq] = total * p.out_scale;
+    else p.out[q * p.osq + jl * p.osd] = total * p.out_scale;
+  }
 }
 
 int launch_maxsim_wide(int dtype, const Params& p, hipStream_t s) {
-  const int64_t waves = p.q.n * p.ndocs_pg;
+  const int64_t waves = p.pair_q ? p.nunits : p.q.n * p.ndocs_pg;
   const int64_t nb = (waves + 3) / 4;
   if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
   if (dtype == LIK_BF16)

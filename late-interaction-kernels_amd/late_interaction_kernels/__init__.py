@@ -13,8 +13,10 @@ on the current HIP stream. Inputs must be ROCm GPU tensors. ``maxsim``,
 ``maxsim_pairs``, the PLAID scorers (in Q) and ``fused_head.maxsim_from_hidden``
 are differentiable: an argmax-saving forward plus a deterministic HIP backward.
 
-Submodules mirror the reference: ``score_pairs``, ``padded``, ``plaid``,
-``fp8``, ``varlen``, ``topk``, ``retrieve``, ``fused_head``, ``plaid_index``.
+Submodules mirror the reference: ``forward``, ``score_pairs``, ``padded``,
+``plaid``, ``fp8``, ``varlen``, ``topk``, ``retrieve``, ``fused_head``,
+``plaid_index``, and ``reference`` (eager PyTorch ground truth for callers'
+own comparisons; no op here uses it).
 """
 
 from importlib.metadata import PackageNotFoundError
@@ -29,6 +31,7 @@ from late_interaction_kernels.autograd import maxsim, maxsim_pairs  # noqa: E402
 from late_interaction_kernels.padded import maxsim_padded  # noqa: E402
 from late_interaction_kernels.retrieve import MaxSimScorer, retrieve  # noqa: E402
 from late_interaction_kernels.varlen import maxsim_varlen  # noqa: E402
+from late_interaction_kernels import reference  # noqa: E402,F401  (eager PyTorch ground truth)
 
 __all__ = [
     "__version__",
@@ -38,4 +41,5 @@ __all__ = [
     "maxsim",
     "maxsim_pairs",
     "maxsim_varlen",
+    "reference",
 ]

@@ -46,9 +46,10 @@ def score_pairs_packed(
     """``scores[k] = MaxSim(Q_packed[cu_q[pq[k]]:cu_q[pq[k]+1]], D_packed[cu_d[pd[k]]:...])``.
 
     Autograd-aware. Returns ``[num_pairs]`` fp32. Pairs whose query or document is empty
-    (or whose index is out of range) score 0. Query length is bounded by
-    the kernel's query block (512 tokens for d <= 128).
-    """
+    (or whose index is out of range) score 0. Any query length (queries longer
+    than the kernel's 512-token query block are scored in token chunks whose
+    partial sums are added in order) and any embedding dim (rows wider than
+    512 take the one-wave-per-pair kernel)."""
     if Q_packed.dim() != 2 or D_packed.dim() != 2:
         raise ValueError(
             "Q_packed / D_packed must be 2-D [sum(L), d]; "

@@ -273,6 +273,24 @@ int lik_topk_select(const float* scores, int64_t rows, int64_t n, int64_t ld, in
                     int64_t prev_ld, int64_t k, int largest, float* out_scores, int64_t* out_idx,
                     int64_t out_ld, void* workspace, size_t workspace_bytes, lik_stream_t stream);
 
+/*
+ * Allocation-free scoring. No counterpart in the reference: this entry point
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It scores
+ * exactly like lik_maxsim (same flags, layouts and outputs; doc-side
+ * normalisation stays inside the tile kernel instead of a pre-normalised
+ * copy) but takes no workspace: the mask summaries and query-chunk partial
+ * sums live in a fixed per-device scratch array of LIK_NOALLOC_SCRATCH_BYTES
+ * that the library owns until the process ends. It calls no allocator.
+ * A call whose scratch need exceeds that size returns LIK_ERR_WORKSPACE
+ * (use lik_maxsim with a workspace instead). Every call on a device shares
+ * that device's array, so calls that overlap on one device (different
+ * streams, or threads) race; calls on one stream are ordered and safe.
+ */
+#define LIK_NOALLOC_SCRATCH_BYTES (64u << 20)
+int lik_maxsim_noalloc(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
+                       int64_t out_stride_q, int64_t out_stride_d, lik_stream_t stream);
+
 /* Library version string and the gfx target it was built for. */
 const char* lik_version(void);
 

@@ -24,6 +24,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 
 #include "lik_params.h"
 
@@ -662,6 +664,45 @@ int pairs_impl(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, 
   return LIK_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Library-owned scratch for lik_maxsim_noalloc: one fixed array per device,
+// held until the process ends. Host code never uses the symbol itself (its
+// host-side name is not a device address): the array's device address is
+// looked up once per device with hipGetSymbolAddress and only that pointer is
+// handed to kernels.
+constexpr size_t kScratchBytes = LIK_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of this device's scratch array (set up on the first call
+// that runs on the device, with that device current), or null on failure.
+void* device_scratch(hipStream_t s) {
+  int dev = 0;
+  if (s) {
+    hipDevice_t sd;
+    if (hipStreamGetDevice(s, &sd) != hipSuccess) return nullptr;
+    dev = (int)sd;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::call_once(g_scratch_once[dev], [dev] {
+    int cur = 0;
+    g_scratch_err[dev] = hipGetDevice(&cur);
+    if (g_scratch_err[dev] != hipSuccess) return;
+    if (cur != dev && (g_scratch_err[dev] = hipSetDevice(dev)) != hipSuccess) return;
+    void* ptr = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? ptr : nullptr;
+    if (cur != dev) (void)hipSetDevice(cur);
+  });
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 
@@ -700,6 +741,28 @@ int lik_maxsim_ex(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, floa
                   const lik_launch_opts_t* opts, lik_stream_t stream) {
   return maxsim_impl(Q, D, flags, out_scale, out, out_stride_q, out_stride_d, nullptr, workspace, workspace_bytes,
                      opts, true, stream);
+}
+
+int lik_maxsim_noalloc(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,
+                       int64_t out_stride_q, int64_t out_stride_d, lik_stream_t stream) {
+  size_t need = 0;
+  {
+    // the scratch layout this call needs (doc normalise stays in the kernel)
+    int rc;
+    if ((rc = check_seqs(Q)) != LIK_OK) return rc;
+    if ((rc = check_seqs(D)) != LIK_OK) return rc;
+    if (Q->n > 0 && D->n > 0 && pick_dpad(Q->dtype, Q->dim) >= 0) {
+      Plan pl;
+      bool prenorm = false;
+      if ((rc = plan_call(Q, D, flags, false, pl, prenorm, nullptr, false)) != LIK_OK) return rc;
+      need = ws_layout(Q, D, flags, pl, prenorm).total;
+    }
+  }
+  if (need > kScratchBytes) return LIK_ERR_WORKSPACE;
+  void* ws = nullptr;
+  if (need > 0 && !(ws = device_scratch((hipStream_t)stream))) return LIK_ERR_LAUNCH;
+  return maxsim_impl(Q, D, flags, out_scale, out, out_stride_q, out_stride_d, nullptr, ws, kScratchBytes, nullptr,
+                     false, stream);
 }
 
 int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float* out, int64_t out_stride_q,

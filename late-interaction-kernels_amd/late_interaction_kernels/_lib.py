@@ -64,6 +64,7 @@ EXPORTED_SYMBOLS = (
     "lik_maxsim_ex",
     "lik_maxsim_workspace_size_ex",
     "lik_plaid_maxsim_ex",
+    "lik_maxsim_noalloc",
 )
 
 _p = ctypes.c_void_p
@@ -197,6 +198,8 @@ def load() -> ctypes.CDLL:
     lib.lik_plaid_maxsim_ex.argtypes = [P(LikSeqs), P(LikPlaidDocs), ctypes.c_uint32, _p, _i64, _i64,
                                         P(LikLaunchOpts), _p]
     lib.lik_plaid_maxsim_ex.restype = ctypes.c_int
+    lib.lik_maxsim_noalloc.argtypes = [P(LikSeqs), P(LikSeqs), ctypes.c_uint32, ctypes.c_float, _p, _i64, _i64, _p]
+    lib.lik_maxsim_noalloc.restype = ctypes.c_int
     _lib = lib
     return lib
 

@@ -361,6 +361,44 @@ def wl_plaid_q1(args):
             "roofline": roof}
 
 
+def wl_plaid_q1_prepared(args):
+    """PLAID at Nq=1 over a prepared corpus (plaid.ResidualIndex): every
+    token's inverse norm computed once at index load (outside the timed
+    region, like loading the index), then per retrieve one query-centroid
+    score table (65,536 x 32 fp16) and one scan of codes + residual bytes +
+    norms, then the top-k. ``value`` = compressed index bytes (int32 code +
+    32 B residual per token) per second of the scan kernel; the roofline
+    counts the bytes the scan must read, 40 B per token with the norms."""
+    import torch
+
+    from late_interaction_kernels.plaid import ResidualIndex
+
+    Nd, d, nbits = args.plaid_docs, 128, 2
+    g, cu, tot, cent, codes, res, bw = _plaid_index(Nd, 4)
+    Q = _normed((1, 32, d), g, torch.bfloat16)
+    t0 = time.perf_counter()
+    idx = ResidualIndex(codes, res, cu, cent, bw, nbits)
+    _sync()
+    prep_s = time.perf_counter() - t0
+
+    def step():
+        return idx.retrieve(Q, 100)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    cbytes = float(tot) * (4 + d * nbits // 8)
+    sbytes = float(tot) * (4 + d * nbits // 8 + 4)
+    roof = _roofline("hbm", sbytes, "hbm", "plaid_q1_prepared")
+    kms = roof["kernel_ms"]
+    return {"metric": "PLAID compressed-index GB/s at Nq=1 (prepared corpus, scan kernel)",
+            "value": round(cbytes / (kms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(ms, 4),
+            "dtype": "bf16",
+            "config": {"workload": f"PLAID {Nd} docs U[30,300], 1x32 query, nbits=2, top-100, prepared corpus "
+                                   "(token norms precomputed)", "doc_tokens": tot, "compressed_bytes": cbytes,
+                       "scan_bytes_with_norms": sbytes, "prepare_s": round(prep_s, 3),
+                       "queries_per_s": round(1000.0 / ms, 1)},
+            "roofline": roof}
+
+
 def wl_plaid_decode(args):
     """Decode-only pass of the 1M-doc corpus in 16M-token slices: codes +
     residual bits -> normalised bf16 rows. ``value`` = (compressed bytes read
@@ -569,6 +607,7 @@ def wl_hbm_copy(args):
 WORKLOADS = {
     "hbm_copy": wl_hbm_copy,
     "plaid_q1": wl_plaid_q1,
+    "plaid_q1_prepared": wl_plaid_q1_prepared,
     "ref_shapes": wl_ref_shapes,
     "train_shapes": wl_train_shapes,
     "plaid_decode": wl_plaid_decode,
@@ -616,7 +655,8 @@ def main() -> None:
         # top-100, and the PLAID kernel's HBM rate at Nq = 1.
         parts = {}
         for name, fn, steps in (("fp8", wl_fp8, args.steps), ("plaid", wl_plaid, args.plaid_steps),
-                                ("plaid_q1", wl_plaid_q1, args.steps)):
+                                ("plaid_q1", wl_plaid_q1, args.steps),
+                                ("plaid_q1_prepared", wl_plaid_q1_prepared, args.steps)):
             torch.cuda.empty_cache()
             sub = argparse.Namespace(**vars(args))
             sub.steps, sub.warmup = steps, min(args.warmup, 2) if name == "plaid" else args.warmup

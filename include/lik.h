@@ -52,7 +52,10 @@ typedef enum {
  * lengths (optional, padded only): valid length of each sequence (prefix).
  * mask (optional, padded only): int8 keep-flags, mask[i*mask_stride_n + t*mask_stride_l].
  * token_scale (optional, fp8 only): fp32 per-token dequant scale,
- *           token_scale[i*scale_stride_n + t*scale_stride_l].
+ *           token_scale[i*scale_stride_n + t*scale_stride_l]. With both
+ *           strides 0 it is one per-tensor scale in device memory, folded
+ *           into the score scale in the kernel's epilogue (no host read, so
+ *           the call can be captured in a HIP graph).
  */
 typedef struct {
   const void* data;
@@ -72,6 +75,34 @@ typedef struct {
   int64_t scale_stride_l;
 } lik_seqs_t;
 
+/*
+ * Per-call launch options (no counterpart in the reference, whose Triton
+ * launcher autotunes and times from Python). Passing NULL, or a zeroed
+ * struct, is exactly the plain entry point. The struct is read during the
+ * call only; the library keeps no state between calls, so concurrent calls
+ * with different options are independent.
+ *   col_waves, col_blocks: force the tile kernel's column block (waves per
+ *       workgroup W in {1, 4, 8}, 32-column blocks per wave NSUB in
+ *       {1, 2, 4}; fp8 at d <= 128 also 4 x 6); 0 = automatic. A
+ *       configuration the call cannot use is ignored.
+ *   docs_per_wg: documents per workgroup, 1..512; 0 = automatic.
+ *   plaid_variant (lik_plaid_maxsim_ex): 0 automatic, 1 per-lane stream
+ *       decode, 2 exact LDS-gather decode (bitwise equal to the tile
+ *       kernel), 3 the tile kernel (no stream kernel).
+ *   timing_start, timing_stop: hipEvent_t or NULL. When both are set, they
+ *       are recorded on the call's stream immediately before and after the
+ *       call's main MaxSim launch (the launch that scores the mask-free
+ *       documents), so a caller can time that kernel alone.
+ */
+typedef struct {
+  int32_t col_waves;
+  int32_t col_blocks;
+  int32_t docs_per_wg;
+  int32_t plaid_variant;
+  void* timing_start;
+  void* timing_stop;
+} lik_launch_opts_t;
+
 /* flags for lik_maxsim */
 #define LIK_NORMALIZE 1u /* per-token L2 normalise Q and D (F.normalize, eps 1e-12) */
 #define LIK_KD_LAYOUT 2u /* D holds n = Nq*K docs; query i scores docs [i*K, (i+1)*K) */
@@ -88,8 +119,8 @@ typedef struct {
  * _maxsim_fwd_kernel (forward.py:45-186) — both the in-batch and the
  * kd_layout variants — varlen.py:_varlen_forward (varlen.py:271-364) and
  * fp8.py:maxsim_inference_fp8's launch of _maxsim_fp8_fwd_kernel
- * (fp8.py:234-422; Q and D fp8, per-tensor scales passed as out_scale,
- * per-token scales as token_scale).
+ * (fp8.py:234-422; Q and D fp8, per-tensor scales as token_scale with
+ * strides 0 or as out_scale, per-token scales as token_scale).
  */
 int lik_maxsim(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale,
                float* out, int64_t out_stride_q, int64_t out_stride_d, void* workspace,
@@ -221,6 +252,35 @@ int lik_plaid_decode(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t to
                      int32_t out_dtype, void* out, int64_t out_stride, lik_stream_t stream);
 
 /*
+ * Per-token inverse norms of decoded PLAID tokens: inv[tok] =
+ * 1 / max(||x_tok||, 1e-12) with x = centroids[code] + bucket weights (fp32,
+ * the decode arithmetic of lik_plaid_decode) for tok in [tok_begin,
+ * tok_end); inv is indexed by absolute token. Computed once per corpus, it
+ * lets lik_plaid_maxsim_qc score normalised tokens without their centroid
+ * rows. No counterpart in the reference (its kernels re-decode every token
+ * per query, plaid.py:780-801).
+ */
+int lik_plaid_token_norms(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end, float* inv,
+                          lik_stream_t stream);
+
+/*
+ * Few-query PLAID scoring from centroid scores (up to 64 queries of <= 32
+ * tokens, bf16 / f16 query and centroids of the same type, d <= 128): the
+ * same scores as lik_plaid_maxsim (plaid.py:832-963; within bf16 rounding:
+ * q.c comes from an fp16 table of query-centroid scores, q.r from the MFMA
+ * on bucket weights rounded to the query type, both divided by the token's
+ * precomputed norm). token_inv (from lik_plaid_token_norms) is required when
+ * flags normalise the docs (LIK_NORMALIZE / LIK_NORMALIZE_D) and ignored
+ * otherwise. The workspace holds the [Q->n, n_centroids, 32] fp16 table
+ * (lik_plaid_maxsim_qc_workspace_size bytes). opts: docs_per_wg and the
+ * timing events (around the scan kernel) are honoured.
+ */
+size_t lik_plaid_maxsim_qc_workspace_size(const lik_seqs_t* Q, const lik_plaid_docs_t* docs);
+int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, const float* token_inv, uint32_t flags,
+                        float* out, int64_t out_stride_q, int64_t out_stride_d, void* workspace,
+                        size_t workspace_bytes, const lik_launch_opts_t* opts, lik_stream_t stream);
+
+/*
  * Reverse the bit order inside each of nbytes bytes (in may equal out; both
  * 4-byte aligned). Converts ColBERTv2 / fast-plaid residual bytes (each code's
  * bits least-significant first, packed most-significant-bit first by
@@ -294,33 +354,6 @@ int lik_maxsim_noalloc(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags,
 /* Library version string and the gfx target it was built for. */
 const char* lik_version(void);
 
-/*
- * Per-call launch options (no counterpart in the reference, whose Triton
- * launcher autotunes and times from Python). Passing NULL, or a zeroed
- * struct, is exactly the plain entry point. The struct is read during the
- * call only; the library keeps no state between calls, so concurrent calls
- * with different options are independent.
- *   col_waves, col_blocks: force the tile kernel's column block (waves per
- *       workgroup W in {1, 4, 8}, 32-column blocks per wave NSUB in
- *       {1, 2, 4}; fp8 at d <= 128 also 4 x 6); 0 = automatic. A
- *       configuration the call cannot use is ignored.
- *   docs_per_wg: documents per workgroup, 1..512; 0 = automatic.
- *   plaid_variant (lik_plaid_maxsim_ex): 0 automatic, 1 per-lane stream
- *       decode, 2 exact LDS-gather decode (bitwise equal to the tile
- *       kernel), 3 the tile kernel (no stream kernel).
- *   timing_start, timing_stop: hipEvent_t or NULL. When both are set, they
- *       are recorded on the call's stream immediately before and after the
- *       call's main MaxSim launch (the launch that scores the mask-free
- *       documents), so a caller can time that kernel alone.
- */
-typedef struct {
-  int32_t col_waves;
-  int32_t col_blocks;
-  int32_t docs_per_wg;
-  int32_t plaid_variant;
-  void* timing_start;
-  void* timing_stop;
-} lik_launch_opts_t;
 
 /* lik_maxsim / lik_maxsim_workspace_size / lik_plaid_maxsim with launch options. */
 int lik_maxsim_ex(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float out_scale, float* out,

@@ -707,6 +707,9 @@ __global__ void __launch_bounds__(W * 64)
   };
 
   int nend = 0;  // documents finished so far
+  // score scale: out_scale times the per-tensor scales read from device
+  // memory (fp8 per-tensor dequant scales, no host read)
+  const float osc = p.out_scale * (p.scale_q ? *p.scale_q : 1.f) * (p.scale_d ? *p.scale_d : 1.f);
 
   // Sum the per-column maxima of finished docs [s0, s0+n) per unit and write
   // scores: one thread per (doc, unit), columns added in a fixed (rotated)
@@ -737,7 +740,7 @@ __global__ void __launch_bounds__(W * 64)
       // global (not generic) store: a flat store would also count in the LDS
       // wait counter and force full waits on the A-fragment reads
       auto* o = &((__attribute__((address_space(1))) float*)orow)[s_slotk[sl] * p.osd];
-      *o = p.accumulate ? sum * p.out_scale + *o : sum * p.out_scale;
+      *o = p.accumulate ? sum * osc + *o : sum * osc;
     }
   };
 
@@ -1080,7 +1083,7 @@ int launch_dpad(const Plan& pl, const Params& p, int64_t nb, hipStream_t s) {
 
 // Features a call needs (FEAT bits).
 inline int needed_feat(const Params& p) {
-  return (p.d.mask ? F_MASK : 0) | (p.d.ts ? F_TS : 0) |
+  return (p.d.mask ? F_MASK : 0) | ((p.d.ts || p.q.ts) ? F_TS : 0) |
          ((p.normalize & 2) ? F_NORM : (p.normalize & 1) ? F_NORMQ : 0) | (p.d.cu ? F_CU : 0);
 }
 

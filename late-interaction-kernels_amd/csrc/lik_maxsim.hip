@@ -171,6 +171,12 @@ int max_nsub(int dt, int dpad) {
   return n > 4 ? 4 : n;
 }
 
+// A token scale with both strides 0 is one per-tensor scale: it is folded
+// into the score scale at the epilogue (read from device memory there)
+// instead of scaling rows.
+bool tensor_scale(const lik_seqs_t& s) { return s.token_scale && s.scale_stride_n == 0 && s.scale_stride_l == 0; }
+bool row_scale(const lik_seqs_t* s) { return s->token_scale && !tensor_scale(*s); }
+
 SeqDev to_dev(const lik_seqs_t& s) {
   SeqDev d;
   const int eb = elem_bytes(s.dtype);
@@ -182,7 +188,7 @@ SeqDev to_dev(const lik_seqs_t& s) {
   d.mask = s.mask;
   d.msn = s.mask_stride_n;
   d.msl = s.mask_stride_l;
-  d.ts = s.token_scale;
+  d.ts = tensor_scale(s) ? nullptr : s.token_scale;
   d.tsn = s.scale_stride_n;
   d.tsl = s.scale_stride_l;
   d.n = s.n;
@@ -384,7 +390,7 @@ int plan_call(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, bool arg
               const lik_launch_opts_t* opts, bool allow_prenorm = true) {
   const bool kd = (flags & LIK_KD_LAYOUT) != 0;
   const int min_w = ((norm_bits(flags) & 2) || argmax) ? 4 : 1;
-  const bool plain = !argmax && !Q->token_scale && !D->token_scale;
+  const bool plain = !argmax && !row_scale(Q) && !row_scale(D);
   int rc = make_plan(Q->dtype, Q->dim, Q->n, Q->len, kd, pl, min_w, plain, opts);
   if (rc != LIK_OK) return rc;
   prenorm = prenorm_docs(Q, D, flags, pl, allow_prenorm);
@@ -503,6 +509,8 @@ int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float 
   Params p{};
   p.q = to_dev(*Q);
   p.d = to_dev(*D);
+  p.scale_q = tensor_scale(*Q) ? Q->token_scale : nullptr;
+  p.scale_d = tensor_scale(*D) ? D->token_scale : nullptr;
   p.normalize = norm_bits(flags);
   char* ws = (char*)workspace;
   p.out_scale = out_scale;
@@ -631,6 +639,8 @@ int pairs_impl(const lik_seqs_t* Q, const lik_seqs_t* D, const int32_t* pair_q, 
   }
   p.q = to_dev(*Q);
   p.d = to_dev(*D);
+  p.scale_q = tensor_scale(*Q) ? Q->token_scale : nullptr;
+  p.scale_d = tensor_scale(*D) ? D->token_scale : nullptr;
   p.normalize = norm_bits(flags);
   p.out_scale = 1.f;
   p.pair_q = pair_q;

@@ -61,6 +61,8 @@ struct Params {
   int64_t amax_qs;  // (query, doc) rows of amax per query (the call's docs per query)
   int64_t q_tok0;   // pair mode: first query token of this launch's query chunk
   int accumulate;   // add the scores to out instead of storing them (query-chunk launches)
+  const float* scale_q;  // per-tensor scales in device memory folded into the score scale, or null
+  const float* scale_d;
 };
 
 // PLAID gather kernel: byte offset given to a row past the tile end; the

@@ -92,17 +92,21 @@ def dense_maxsim(
     dm = _mask_i8(d_mask, (Nd, Ld))
     ql = _i32(q_lengths)
     dl = _i32(d_lengths)
-    qsc = None if q_scale is None else q_scale.to(torch.float32).expand(Nq, Lq).contiguous()
-    dsc = None if d_scale is None else d_scale.to(torch.float32).expand(Nd, Ld).contiguous()
+    # a 0-d scale is one per-tensor scale (strides 0: the kernel folds it
+    # into the score scale); [N, L] scales are per token
+    qsc = None if q_scale is None else (q_scale.to(torch.float32).reshape(1, 1) if q_scale.dim() == 0
+                                        else q_scale.to(torch.float32).expand(Nq, Lq).contiguous())
+    dsc = None if d_scale is None else (d_scale.to(torch.float32).reshape(1, 1) if d_scale.dim() == 0
+                                        else d_scale.to(torch.float32).expand(Nd, Ld).contiguous())
     qs = _lib.seqs(
         Q, n=Nq, length=Lq, stride_n=Q.stride(0), stride_l=Q.stride(1), lengths=ql, mask=qm,
         mask_strides=(qm.stride(0), qm.stride(1)) if qm is not None else (0, 0),
-        token_scale=qsc, scale_strides=(qsc.stride(0), qsc.stride(1)) if qsc is not None else (0, 0),
+        token_scale=qsc, scale_strides=(qsc.stride(0), qsc.stride(1)) if qsc is not None and qsc.numel() > 1 else (0, 0),
     )
     ds = _lib.seqs(
         D, n=Nd, length=Ld, stride_n=D.stride(0), stride_l=D.stride(1), lengths=dl, mask=dm,
         mask_strides=(dm.stride(0), dm.stride(1)) if dm is not None else (0, 0),
-        token_scale=dsc, scale_strides=(dsc.stride(0), dsc.stride(1)) if dsc is not None else (0, 0),
+        token_scale=dsc, scale_strides=(dsc.stride(0), dsc.stride(1)) if dsc is not None and dsc.numel() > 1 else (0, 0),
     )
     if norm is None:
         norm = 3 if normalize else 0

@@ -65,6 +65,9 @@ EXPORTED_SYMBOLS = (
     "lik_maxsim_workspace_size_ex",
     "lik_plaid_maxsim_ex",
     "lik_maxsim_noalloc",
+    "lik_plaid_token_norms",
+    "lik_plaid_maxsim_qc",
+    "lik_plaid_maxsim_qc_workspace_size",
 )
 
 _p = ctypes.c_void_p
@@ -200,6 +203,13 @@ def load() -> ctypes.CDLL:
     lib.lik_plaid_maxsim_ex.restype = ctypes.c_int
     lib.lik_maxsim_noalloc.argtypes = [P(LikSeqs), P(LikSeqs), ctypes.c_uint32, ctypes.c_float, _p, _i64, _i64, _p]
     lib.lik_maxsim_noalloc.restype = ctypes.c_int
+    lib.lik_plaid_token_norms.argtypes = [P(LikPlaidDocs), _i64, _i64, _p, _p]
+    lib.lik_plaid_token_norms.restype = ctypes.c_int
+    lib.lik_plaid_maxsim_qc_workspace_size.argtypes = [P(LikSeqs), P(LikPlaidDocs)]
+    lib.lik_plaid_maxsim_qc_workspace_size.restype = ctypes.c_size_t
+    lib.lik_plaid_maxsim_qc.argtypes = [P(LikSeqs), P(LikPlaidDocs), _p, ctypes.c_uint32, _p, _i64, _i64, _p,
+                                        ctypes.c_size_t, P(LikLaunchOpts), _p]
+    lib.lik_plaid_maxsim_qc.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -307,13 +317,21 @@ class LaunchTimer:
 
 @contextlib.contextmanager
 def launch_options(*, cfg: tuple[int, int] | None = None, docs_per_wg: int = 0, plaid_variant: int = 0,
-                   timer: LaunchTimer | None = None):
-    """Tuning / measurement options for the scoring calls inside the block."""
-    tok = _OPTS.set({"cfg": cfg, "docs_per_wg": docs_per_wg, "plaid_variant": plaid_variant, "timer": timer})
+                   plaid_route: str = "auto", timer: LaunchTimer | None = None):
+    """Tuning / measurement options for the scoring calls inside the block.
+    ``plaid_route``: "fused" or "decode" forces the PLAID route of large
+    query batches (default: by query-token count)."""
+    tok = _OPTS.set({"cfg": cfg, "docs_per_wg": docs_per_wg, "plaid_variant": plaid_variant,
+                     "plaid_route": plaid_route, "timer": timer})
     try:
         yield
     finally:
         _OPTS.reset(tok)
+
+
+def plaid_route() -> str:
+    o = _OPTS.get()
+    return "auto" if o is None else o["plaid_route"]
 
 
 def call_opts():

@@ -64,8 +64,9 @@ def maxsim_inference_fp8(
 
     Returns ``[Nq, Nd]`` fp32, squeezed for 2-D inputs. ``float8_e4m3fn`` runs
     on the fp8 MFMA path; ``float8_e5m2`` inputs are dequantised to bf16 and
-    scored by the bf16 kernel. Per-tensor scales cost one device->host read
-    (as in the reference).
+    scored by the bf16 kernel. Per-tensor scales are read by the kernel from
+    device memory (no host sync, graph-capturable; the reference reads them
+    on the host).
     """
     q_was_2d = Q.dim() == 2
     d_was_2d = D.dim() == 2
@@ -87,30 +88,20 @@ def maxsim_inference_fp8(
 
     q_tok = scale_Q.dim() >= 2
     d_tok = scale_D.dim() >= 2
-    if q_tok and d_tok:
-        out_scale = 1.0
-    elif q_tok:
-        out_scale = float(scale_D.reshape(()).item())
-    elif d_tok:
-        out_scale = float(scale_Q.reshape(()).item())
-    else:
-        out_scale = float((scale_Q.reshape(()) * scale_D.reshape(())).item())
 
     if Q.dtype == _E4M3 and D.dtype == _E4M3:
+        # Per-tensor scales stay on the device: the kernel reads them in its
+        # epilogue (score * s_q * s_d), so the call needs no host sync and can
+        # be captured in a graph.
         scores = dense_maxsim(
             Q, D, q_mask, d_mask,
-            q_scale=scale_Q.to(Q.device) if q_tok else None,
-            d_scale=scale_D.to(D.device) if d_tok else None,
-            out_scale=out_scale,
+            q_scale=(scale_Q if q_tok else scale_Q.reshape(())).to(device=Q.device, dtype=torch.float32),
+            d_scale=(scale_D if d_tok else scale_D.reshape(())).to(device=D.device, dtype=torch.float32),
         )
     elif Q.dtype in (_E4M3, _E5M2) and D.dtype in (_E4M3, _E5M2):
-        Qd = Q.to(torch.float32)
-        Dd = D.to(torch.float32)
-        if q_tok:
-            Qd = Qd * scale_Q.unsqueeze(-1)
-        if d_tok:
-            Dd = Dd * scale_D.unsqueeze(-1)
-        scores = dense_maxsim(Qd.to(torch.bfloat16), Dd.to(torch.bfloat16), q_mask, d_mask, out_scale=out_scale)
+        Qd = Q.to(torch.float32) * (scale_Q.unsqueeze(-1) if q_tok else scale_Q.reshape(()))
+        Dd = D.to(torch.float32) * (scale_D.unsqueeze(-1) if d_tok else scale_D.reshape(()))
+        scores = dense_maxsim(Qd.to(torch.bfloat16), Dd.to(torch.bfloat16), q_mask, d_mask)
     else:
         raise TypeError(f"maxsim_inference_fp8 needs fp8 Q and D; got {Q.dtype} and {D.dtype}")
 

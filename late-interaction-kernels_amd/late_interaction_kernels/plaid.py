@@ -21,7 +21,6 @@ bucket, so corrupt indices cannot fault.
 from __future__ import annotations
 
 import ctypes
-import os
 
 import torch
 
@@ -276,8 +275,9 @@ def _token_chunks(cu_host: torch.Tensor, j0: int, j1: int):
 
 
 def _use_decode_route(Nq: int, Lq: int) -> bool:
-    """``LIK_PLAID_ROUTE=fused|decode`` forces a route; otherwise by query-token count."""
-    forced = os.environ.get("LIK_PLAID_ROUTE", "auto")
+    """``_lib.launch_options(plaid_route="fused" | "decode")`` forces a route;
+    otherwise by query-token count."""
+    forced = _lib.plaid_route()
     if forced == "fused":
         return False
     if forced == "decode":
@@ -490,7 +490,115 @@ def retrieve_residual_varlen(
     return run_s, run_i
 
 
+class ResidualIndex:
+    """A PLAID-compressed corpus prepared once for repeated few-query scoring.
+
+    Same inputs as :func:`maxsim_residual_varlen` (``codes_flat``,
+    ``residuals_flat``, ``cu_seqlens_d``, ``centroids``, ``bucket_weights``,
+    ``nbits``). Construction computes every token's inverse L2 norm once
+    (``lik_plaid_token_norms``: 4 bytes per token, one decode pass). Scoring
+    up to 64 queries of at most 32 tokens then runs ``lik_plaid_maxsim_qc``:
+    per query a table of query-centroid scores (``[n_centroids, 32]`` fp16),
+    and a scan that reads each token's code, residual bytes and norm from HBM
+    and one 64-byte table row instead of a 256-byte centroid row. Scores
+    match :func:`maxsim_residual_varlen` within bf16 rounding (the centroid
+    term is rounded to fp16). Larger batches, queries needing gradients, and
+    layouts the scan cannot take use :func:`maxsim_residual_varlen`.
+
+    The tensors are borrowed: modifying them after construction invalidates
+    the precomputed norms.
+    """
+
+    def __init__(self, codes_flat, residuals_flat, cu_seqlens_d, centroids, bucket_weights, nbits: int):
+        _check_nbits(nbits)
+        if codes_flat.dim() != 1 or residuals_flat.dim() != 2 or cu_seqlens_d.dim() != 1:
+            raise ValueError("codes_flat [T], residuals_flat [T, packed_dim] and cu_seqlens_d [Nd + 1] expected")
+        _lib.require_gpu(codes_flat, residuals_flat, cu_seqlens_d, centroids, bucket_weights)
+        d = centroids.shape[-1]
+        self.residuals, self.centroids, self.bucket_weights = _prep_index(residuals_flat, centroids, bucket_weights,
+                                                                          nbits, d)
+        self.codes = codes_flat.contiguous().to(torch.int32)
+        self.cu = cu_seqlens_d.contiguous().to(torch.int32)
+        self.nbits = nbits
+        self.d = d
+        self.n_docs = self.cu.numel() - 1
+        T = self.codes.numel()
+        self.token_inv = torch.empty(T, device=self.codes.device, dtype=torch.float32)
+        if T:
+            docs = self._docs()
+            lib = _lib.load()
+            with torch.cuda.device(self.codes.device):
+                rc = lib.lik_plaid_token_norms(ctypes.byref(docs), 0, T, self.token_inv.data_ptr(),
+                                               _lib.stream_of(self.token_inv))
+            _lib.check(rc, "lik_plaid_token_norms")
+
+    def _docs(self) -> _lib.LikPlaidDocs:
+        return _plaid_docs(self.codes, self.residuals, self.centroids, self.bucket_weights, self.nbits, self.d,
+                           cu=self.cu, n=self.n_docs, max_len=0)
+
+    def _scan_ok(self, Qp: torch.Tensor) -> bool:
+        Nq, Lq, d = Qp.shape
+        return (Nq <= 64 and 0 < Lq <= 32 and d <= 128 and self.centroids.dtype == Qp.dtype
+                and self.residuals.shape[-1] % 16 == 0 and self.residuals.data_ptr() % 16 == 0)
+
+    def score(self, Q: torch.Tensor, *, normalize: bool = True) -> torch.Tensor:
+        """``[Nq, Nd]`` fp32 scores (``[Nd]`` for 2-D Q), as :func:`maxsim_residual_varlen`."""
+        q_squeeze = Q.dim() == 2
+        if q_squeeze:
+            Q = Q.unsqueeze(0)
+        if Q.shape[-1] != self.d:
+            raise ValueError(f"Q has d={Q.shape[-1]}, the index d={self.d}")
+        _lib.require_gpu(Q)
+        Qp = _prep_q(Q)
+        if (torch.is_grad_enabled() and Q.requires_grad) or not self._scan_ok(Qp):
+            out = maxsim_residual_varlen(Q, self.codes, self.residuals, self.cu, self.centroids, self.bucket_weights,
+                                         self.nbits, normalize=normalize)
+            return out.squeeze(0) if q_squeeze else out
+        Nq, Lq, _ = Qp.shape
+        out = torch.empty(Nq, max(self.n_docs, 0), device=Q.device, dtype=torch.float32)
+        if Nq and self.n_docs > 0:
+            if self.codes.numel() == 0:
+                return out.zero_()
+            docs = self._docs()
+            qs = _lib.seqs(Qp, n=Nq, length=Lq, stride_n=Qp.stride(0), stride_l=Qp.stride(1))
+            lib = _lib.load()
+            nbytes = lib.lik_plaid_maxsim_qc_workspace_size(ctypes.byref(qs), ctypes.byref(docs))
+            ws = _lib.workspace(nbytes, Q.device)
+            flags = _lib.LIK_NORMALIZE if normalize else 0
+            with torch.cuda.device(Q.device):
+                rc = lib.lik_plaid_maxsim_qc(ctypes.byref(qs), ctypes.byref(docs), self.token_inv.data_ptr(), flags,
+                                             out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(ws), nbytes,
+                                             _lib.call_opts(), _lib.stream_of(out))
+            _lib.check(rc, "lik_plaid_maxsim_qc")
+        return out.squeeze(0) if q_squeeze else out
+
+    def retrieve(self, Q: torch.Tensor, top_k: int, *, chunk: int | None = None, normalize: bool = True,
+                 largest: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+        """Top-``top_k`` documents per query, as :func:`retrieve_residual_varlen`
+        (ties to the lower doc index). The few-query scan scores every document
+        in one launch (``chunk`` does not change the result, only how the
+        fallback route bounds its score buffers)."""
+        if top_k <= 0:
+            raise ValueError(f"top_k must be positive, got {top_k}")
+        q_squeeze = Q.dim() == 2
+        Q3 = Q.unsqueeze(0) if q_squeeze else Q
+        if not self._scan_ok(_prep_q(Q3)) or (torch.is_grad_enabled() and Q.requires_grad):
+            return retrieve_residual_varlen(Q, self.codes, self.residuals, self.cu, self.centroids,
+                                            self.bucket_weights, self.nbits, top_k, chunk=chunk, normalize=normalize,
+                                            largest=largest)
+        k = min(top_k, max(self.n_docs, 0))
+        Nq = Q3.shape[0]
+        if k == 0:
+            e = torch.empty(Nq, 0, device=Q.device)
+            return (e[0], e.long()[0]) if q_squeeze else (e, e.long())
+        with torch.no_grad():
+            s = self.score(Q3, normalize=normalize)
+            run_s, run_i = topk_update(s, 0, None, None, k, largest)
+        return (run_s[0], run_i[0]) if q_squeeze else (run_s, run_i)
+
+
 __all__ = [
+    "ResidualIndex",
     "decode_residual_tokens",
     "plaid_approx_score",
     "maxsim_residual",

@@ -94,6 +94,57 @@ def test_fp8_per_token_and_masks():
     assert rel_err(got, O.maxsim(Q.numpy(), D.numpy(), qm.numpy(), dm.numpy())) < 3e-2
 
 
+@pytest.mark.parametrize("q_tok,d_tok", [(True, False), (False, True)])
+def test_fp8_mixed_scales(q_tok, d_tok):
+    """One side per-token, the other per-tensor (a 0-d device scale read by
+    the kernel): against the oracle on the dequantised values."""
+    from late_interaction_kernels.fp8 import (maxsim_inference_fp8, quantize_fp8_per_tensor,
+                                              quantize_fp8_per_token)
+
+    _case(f"fp8 mixed q_tok={q_tok} d_tok={d_tok}")
+    g = torch.Generator().manual_seed(12)
+    Q = torch.randn(5, 24, 128, generator=g)
+    D = torch.randn(9, 70, 128, generator=g)
+    Qf, sq = (quantize_fp8_per_token if q_tok else quantize_fp8_per_tensor)(Q.cuda())
+    Df, sd = (quantize_fp8_per_token if d_tok else quantize_fp8_per_tensor)(D.cuda())
+    got = _np(maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd))
+    Qd = _np(Qf) * (sq.cpu().numpy()[..., None] if q_tok else sq.item())
+    Dd = _np(Df) * (sd.cpu().numpy()[..., None] if d_tok else sd.item())
+    assert rel_err(got, O.maxsim(Qd, Dd)) < 2e-3
+
+
+def test_fp8_graph_capture_replay():
+    """Per-tensor scales are read on the device, so an fp8 call can be
+    captured: every replay equals the eager result, also after the scale
+    tensors change in place (the graph reads them at replay time)."""
+    from late_interaction_kernels.fp8 import maxsim_inference_fp8, quantize_fp8_per_tensor
+
+    _case("fp8 graph")
+    g = torch.Generator().manual_seed(13)
+    Qf, sq = quantize_fp8_per_tensor(torch.randn(8, 32, 128, generator=g).cuda())
+    Df, sd = quantize_fp8_per_tensor(torch.randn(64, 100, 128, generator=g).cuda())
+    eager = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd)  # warm the allocator
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        _ = maxsim_inference_fp8(Qf[:2], Df[:5], scale_Q=sq, scale_D=sd)  # eager work between replays
+        torch.cuda.synchronize()
+    sd.mul_(2.0)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, maxsim_inference_fp8(Qf, Df, scale_Q=sq, scale_D=sd))
+    assert rel_err(_np(out), 2 * _np(eager)) < 1e-6
+
+
 def test_fp8_per_token_after_other_kernels():
     """Regression: the per-row-scale epilogue must not read stale LDS on its
     first iteration. Interleave other MaxSim launches (which leave negative

@@ -1,0 +1,132 @@
+"""GPU parity of the prepared-corpus PLAID scan (plaid.ResidualIndex,
+lik_plaid_token_norms + lik_plaid_maxsim_qc).
+
+* Token inverse norms equal 1 / max(||centroid + bucket weights||, 1e-12) of
+  the oracle's float64 decode (oracle/lik_oracle.decode_residual_tokens,
+  reference.py:142-179) to fp32 rounding (1e-6 relative).
+* Scores match the oracle's decode + normalise + MaxSim within the bf16 bar
+  (1e-2) and the exact LDS-gather decode route within 5e-3 (the query-centroid
+  term is rounded to fp16, the bucket weights to the query type), with and
+  without normalisation, for nbits 2 / 4 / 8, d = 64 / 128, bf16 and fp16,
+  1 to 5 queries (two queries per wavefront, a partial last group) and
+  empty docs (score 0).
+* retrieve: indices equal a stable sort of the scan's own score row (ties
+  to the lower index), scores equal the row at those indices.
+* Calls the scan cannot take (Lq > 32, residual rows not a multiple of
+  16 bytes) go to maxsim_residual_varlen and give its result exactly.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import lik_oracle as O
+from conftest import rel_err
+from late_interaction_kernels._lib import launch_options
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(tag):
+    print(f"[case] {tag}", flush=True)
+    sys.stdout.flush()
+
+
+def _index(Nd, max_ld, d, nbits, seed, cdtype, ncent=300):
+    g = torch.Generator().manual_seed(seed)
+    cent = torch.nn.functional.normalize(torch.randn(ncent, d, generator=g), dim=-1).to(cdtype)
+    bw = torch.linspace(-0.1, 0.1, 2**nbits)
+    lens = torch.randint(1, max_ld + 1, (Nd,), generator=g)
+    lens[0] = 0
+    lens[Nd // 2] = 0
+    lens[3] = max_ld
+    T = int(lens.sum())
+    codes = torch.randint(0, ncent, (T,), generator=g, dtype=torch.int32)
+    bcodes = np.random.default_rng(seed).integers(0, 2**nbits, (T, d))
+    res = torch.from_numpy(O.pack_residuals(bcodes, nbits))
+    cu = torch.zeros(Nd + 1, dtype=torch.int32)
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    return cent, bw, codes, res, cu
+
+
+@pytest.mark.parametrize("nbits,d", [(2, 128), (4, 128), (8, 128), (2, 64), (4, 64)])
+@pytest.mark.parametrize("cdtype", [torch.bfloat16, torch.float16])
+def test_token_norms_and_scores(nbits, d, cdtype):
+    from late_interaction_kernels.plaid import ResidualIndex, maxsim_residual_varlen
+
+    _case(f"qc nbits={nbits} d={d} {cdtype}")
+    cent, bw, codes, res, cu = _index(400, 90, d, nbits, nbits * 7 + d, cdtype)
+    args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), nbits)
+    idx = ResidualIndex(*args)
+    emb = O.decode_residual_tokens(codes.numpy(), res.numpy(), cent.double().numpy(), bw.numpy(), nbits)
+    inv_ref = 1.0 / np.maximum(np.linalg.norm(emb, axis=-1), 1e-12)
+    assert rel_err(idx.token_inv.cpu().numpy(), inv_ref) < 1e-6
+    g = torch.Generator().manual_seed(d + nbits)
+    for nq, lq in ((1, 32), (2, 32), (5, 20)):
+        Q = torch.randn(nq, lq, d, generator=g).to(cdtype).cuda()
+        for normalize in (True, False):
+            got = idx.score(Q, normalize=normalize)
+            with launch_options(plaid_variant=2):
+                exact = maxsim_residual_varlen(Q, *args, normalize=normalize)
+            assert rel_err(got.cpu().numpy(), exact.cpu().numpy()) < 5e-3, (nq, normalize)
+            ref = O.maxsim_residual_varlen(Q.double().cpu().numpy(), codes.numpy(), res.numpy(), cu.numpy(),
+                                           cent.double().numpy(), bw.numpy(), nbits, normalize=normalize)
+            assert rel_err(got.cpu().numpy(), ref) < 1e-2, (nq, normalize)
+            assert got[:, 0].abs().max().item() == 0.0 and got[:, 200].abs().max().item() == 0.0
+
+
+def test_retrieve_and_large_table():
+    """A 65,536-centroid table (the benchmark's size: 4 MB of fp16 scores per
+    query), 3,000 docs of 30..300 tokens, one and two queries: top-100
+    against a stable sort of the scan's own scores."""
+    from late_interaction_kernels.plaid import ResidualIndex, retrieve_residual_varlen
+
+    _case("qc retrieve 65536 centroids")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    Nd, d, nbits, nc = 3000, 128, 2, 65536
+    lens = torch.randint(30, 301, (Nd,), generator=g, device="cuda")
+    cu = torch.zeros(Nd + 1, dtype=torch.int32, device="cuda")
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    T = int(cu[-1])
+    cent = torch.nn.functional.normalize(torch.randn(nc, d, generator=g, device="cuda"), dim=-1).to(torch.bfloat16)
+    codes = torch.randint(0, nc, (T,), generator=g, device="cuda", dtype=torch.int32)
+    res = torch.randint(0, 256, (T, 32), generator=g, device="cuda", dtype=torch.uint8)
+    bw = torch.linspace(-0.1, 0.1, 4, device="cuda")
+    idx = ResidualIndex(codes, res, cu, cent, bw, nbits)
+    for nq in (1, 2):
+        Q = torch.nn.functional.normalize(torch.randn(nq, 32, d, generator=g, device="cuda"), dim=-1).to(torch.bfloat16)
+        s, i = idx.retrieve(Q, 100)
+        full = idx.score(Q)
+        order = torch.sort(full, dim=1, descending=True, stable=True).indices[:, :100]
+        assert torch.equal(i, order)
+        assert torch.equal(s, torch.gather(full, 1, i))
+        rs, ri = retrieve_residual_varlen(Q, codes, res, cu, cent, bw, nbits, 100, chunk=None)
+        assert rel_err(s.cpu().numpy(), rs.cpu().numpy()) < 5e-3
+        # both routes select nearly the same documents (near-ties may swap at the margin)
+        for r in range(nq):
+            assert len(set(i[r].tolist()) & set(ri[r].tolist())) >= 95
+        dj = torch.tensor([0, 1, 1500, Nd - 1])
+        spans = [(int(cu[j]), int(cu[j + 1])) for j in dj.tolist()]
+        tok = torch.cat([torch.arange(a, b) for a, b in spans]).cuda()
+        cs = np.concatenate([[0], np.cumsum([b - a for a, b in spans])])
+        ref = O.maxsim_residual_varlen(Q.double().cpu().numpy(), codes[tok].cpu().numpy(), res[tok].cpu().numpy(), cs,
+                                       cent.double().cpu().numpy(), bw.cpu().numpy(), nbits)
+        assert rel_err(full[:, dj.cuda()].cpu().numpy(), ref) < 1e-2
+
+
+def test_fallbacks_equal_varlen_route():
+    from late_interaction_kernels.plaid import ResidualIndex, maxsim_residual_varlen
+
+    _case("qc fallbacks")
+    cent, bw, codes, res, cu = _index(50, 40, 96, 2, 3, torch.bfloat16)  # 24-byte residual rows
+    args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), 2)
+    idx = ResidualIndex(*args)
+    Q = torch.randn(2, 32, 96).to(torch.bfloat16).cuda()
+    assert torch.equal(idx.score(Q), maxsim_residual_varlen(Q, *args))
+    cent, bw, codes, res, cu = _index(50, 40, 128, 2, 4, torch.bfloat16)
+    args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), 2)
+    idx = ResidualIndex(*args)
+    Q = torch.randn(2, 40, 128).to(torch.bfloat16).cuda()  # Lq > 32
+    assert torch.equal(idx.score(Q), maxsim_residual_varlen(Q, *args))

@@ -574,6 +574,70 @@ def wl_train_shapes(args):
             "roofline": None}
 
 
+# The reference's fused-head training shapes and its published H100 times of
+# its fused kernel, forward + backward (docs/benchmarks.md:239-247,
+# benchmarks/kernels/bench_fused_head_train.py:53-66).
+REF_HEAD = [
+    ("lateon-B4-Ld300", 4, 16, 32, 300, 768, 128, 0.98),
+    ("lateon-B8-Ld1k", 8, 32, 32, 1024, 768, 128, 0.99),
+    ("lateon-code-Nd128-Ld1k", 4, 128, 32, 1024, 768, 128, 1.04),
+    ("lateon-code-Nd256-Ld1k", 2, 256, 32, 1024, 768, 128, 1.09),
+    ("lateon-code-Nd512-Ld2k", 1, 512, 32, 2048, 768, 128, 1.71),
+    ("lateon-code-Nd1024-Ld2k", 1, 1024, 32, 2048, 768, 128, 3.15),
+    ("lateon-code-edge-Nd256-Ld4k", 2, 256, 32, 4096, 384, 96, 1.33),
+]
+
+
+def wl_fused_head(args):
+    """maxsim_from_hidden forward + backward (scores.sum().backward(), all of
+    Q, H_d, W, b requiring grad, normalize=True, bf16) per reference shape,
+    next to the reference's published H100 time of its fused kernel.
+    ``value`` = geometric mean speedup."""
+    import torch
+
+    from late_interaction_kernels.fused_head import maxsim_from_hidden
+
+    rows = []
+    for name, Nq, Nd, Lq, Ld, dm_, do, ref_ms in REF_HEAD:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        H = torch.randn(Nd, Ld, dm_, generator=g, device="cuda", dtype=torch.bfloat16).requires_grad_()
+        W = (torch.randn(do, dm_, generator=g, device="cuda", dtype=torch.bfloat16) * dm_**-0.5).requires_grad_()
+        b = (torch.randn(do, generator=g, device="cuda", dtype=torch.bfloat16) * 0.01).requires_grad_()
+        Q = _normed((Nq, Lq, do), g, torch.bfloat16).requires_grad_()
+
+        def step():
+            for t in (Q, H, W, b):
+                t.grad = None
+            maxsim_from_hidden(Q, H, W, b, normalize=True).sum().backward()
+
+        for _ in range(3):
+            step()
+        _sync()
+        torch.cuda.reset_peak_memory_stats()
+        a = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        n = 20
+        a.record()
+        for _ in range(n):
+            step()
+        e.record()
+        _sync()
+        ms = a.elapsed_time(e) / n
+        rows.append({"shape": name, "ms": round(ms, 4), "ref_h100_fused_ms": ref_ms,
+                     "speedup": round(ref_ms / ms, 2),
+                     "peak_mb": round(torch.cuda.max_memory_allocated() / 2**20, 1)})
+        del H, W, b, Q
+        torch.cuda.empty_cache()
+    gm = math.exp(sum(math.log(r["speedup"]) for r in rows) / len(rows))
+    return {"metric": "maxsim_from_hidden fwd+bwd speedup over the reference's published H100 fused-head times "
+                      "(geomean)",
+            "value": round(gm, 2), "unit": "x", "ms_per_step": round(sum(r["ms"] for r in rows), 4),
+            "dtype": "bf16",
+            "config": {"workload": "reference fused-head training shapes (docs/benchmarks.md:239-247)",
+                       "shapes": rows},
+            "roofline": None}
+
+
 def wl_hbm_copy(args):
     """Calibration: a plain 2 GiB device copy (torch's copy kernel). Its GB/s is the
     achievable HBM rate on this box, and its rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -610,6 +674,7 @@ WORKLOADS = {
     "plaid_q1_prepared": wl_plaid_q1_prepared,
     "ref_shapes": wl_ref_shapes,
     "train_shapes": wl_train_shapes,
+    "fused_head": wl_fused_head,
     "plaid_decode": wl_plaid_decode,
     "inbatch": wl_inbatch,
     "inbatch_norm": lambda a: wl_inbatch(a, normalize=True),

@@ -2,20 +2,66 @@
 (reference fused_head.py:262-332).
 
 Computes ``maxsim(Q, normalize(F.linear(H_d, W, b)))`` with the doc-token
-normalisation done inside the MaxSim kernel (``LIK_NORMALIZE_D``; Q is taken
-as already projected and normalised, as in the reference). The projection is a
-plain GEMM, left to hipBLASLt through ``F.linear``; the reference fuses it into
-its Triton kernel to avoid materialising ``D``, which at MI355X's 288 GB costs
-``Nd * Ld * d_out`` elements of scratch. Gradients flow into ``Q``, ``H_d``,
-``W`` and ``b`` (MaxSim backward in HIP, the projection's in hipBLASLt).
+normalisation inside the MaxSim kernel (``LIK_NORMALIZE_D``; Q is taken as
+already projected and normalised, as in the reference).
+
+Forward: the projection is one GEMM (hipBLASLt through ``F.linear``, at its
+GEMM rate; ``D`` costs ``Nd * Ld * d_out`` elements of HBM, a few hundred MB
+at the reference's largest shape against 288 GB), then the MaxSim tile
+kernel. Backward (when anything requires grad): the HIP MaxSim backward gives
+grad_Q and grad_D; grad_D is nonzero only on the doc rows that win a max
+(at most ``Nq * Nd * Lq`` of ``Nd * Ld``), so the projection's gradients are
+taken on those rows alone: grad_W = g^T H_win, grad_b = sum g, and grad_H =
+g W scattered into a zeroed tensor. The reference's fused kernel gets the
+same sparsity by gathering ``H_d`` at winning positions
+(fused_head.py:1-17); here the winners are found from the saved argmax.
 """
 
 from __future__ import annotations
 
 import torch
 
-from .autograd import _score, _validate_devices
-from ._core import unify_dtype
+from .autograd import _needs_grad, _score, _validate_devices
+from ._core import dense_maxsim_train, maxsim_backward, unify_dtype
+
+
+class _FromHiddenFn(torch.autograd.Function):
+    """Projection + MaxSim with the projection's gradients on winning rows only."""
+
+    @staticmethod
+    def forward(ctx, Q, H_d, W, b, d_mask, normalize):
+        D = torch.nn.functional.linear(H_d.detach(), W.detach(), None if b is None else b.detach())
+        Qc, Dc = unify_dtype(Q.detach(), D)
+        norm = 2 if normalize else 0
+        scores, argmax, Qp, Dp, qm = dense_maxsim_train(Qc, Dc, None, d_mask, norm=norm, kd=False)
+        ctx.save_for_backward(Qp, Dp, argmax, H_d, W)
+        ctx.norm = norm
+        ctx.q_dtype = Q.dtype
+        ctx.has_b = b is not None
+        ctx.b_dtype = None if b is None else b.dtype
+        return scores
+
+    @staticmethod
+    def backward(ctx, G):
+        Qp, Dp, argmax, H_d, W = ctx.saved_tensors
+        gq, gd = maxsim_backward(G, Qp, Dp, argmax, None, norm=ctx.norm, kd=False)
+        Nq, Lq, d_out = Qp.shape[0], Qp.shape[1], W.shape[0]
+        Nd, Ld, d_model = H_d.shape
+        grad_q = gq[..., :d_out].to(ctx.q_dtype) if ctx.needs_input_grad[0] else None
+        # doc rows that won a max (the only rows with a nonzero grad_D)
+        am = argmax.view(Nq, Nd, Lq)
+        rows = (torch.arange(Nd, device=am.device).view(1, Nd, 1) * Ld + am.long())[am >= 0]
+        rows = torch.unique(rows)
+        g_rows = gd.reshape(Nd * Ld, -1)[rows, :d_out].float()
+        grad_h = grad_w = grad_b = None
+        if ctx.needs_input_grad[1]:
+            grad_h = torch.zeros_like(H_d)
+            grad_h.view(Nd * Ld, d_model)[rows] = (g_rows @ W.float()).to(H_d.dtype)
+        if ctx.needs_input_grad[2]:
+            grad_w = (g_rows.t() @ H_d.reshape(Nd * Ld, d_model)[rows].float()).to(W.dtype)
+        if ctx.has_b and ctx.needs_input_grad[3]:
+            grad_b = g_rows.sum(0).to(ctx.b_dtype)
+        return grad_q, grad_h, grad_w, grad_b, None, None
 
 
 def maxsim_from_hidden(
@@ -44,9 +90,14 @@ def maxsim_from_hidden(
     if b is not None and (b.dim() != 1 or b.shape[0] != Q.shape[-1]):
         raise ValueError(f"b must be [d_out={Q.shape[-1]}]; got {tuple(b.shape) if b is not None else None}")
     _validate_devices(Q, H_d, None, d_mask)
-    D = torch.nn.functional.linear(H_d, W, b)
-    Q, D = unify_dtype(Q, D)
-    scores = _score(Q, D, None, d_mask, normalize=2 if normalize else 0)
+    if _needs_grad(*(t for t in (Q, H_d, W, b) if t is not None)):
+        if torch.float64 in (Q.dtype, H_d.dtype, W.dtype):
+            raise TypeError("maxsim_from_hidden gradients support fp16 / bf16 / fp32 inputs")
+        scores = _FromHiddenFn.apply(Q, H_d, W, b, d_mask, bool(normalize))
+    else:
+        D = torch.nn.functional.linear(H_d, W, b)
+        Qc, Dc = unify_dtype(Q, D)
+        scores = _score(Qc, Dc, None, d_mask, normalize=2 if normalize else 0)
     return scores.squeeze(0) if q_was_2d else scores
 
 

@@ -89,9 +89,9 @@ __global__ void __launch_bounds__(W * 64)
   // Direct global -> LDS tile loads (buffer_load ... lds) in the two-workgroup
   // kernel with 256-byte rows: no staging registers, no LDS writes of staged
   // data. A DMA instruction writes 64 x 16 bytes contiguously, so those tiles
-  // are unpadded with a XOR swizzle (16-byte chunk c of row r at slot
-  // c ^ (r & 15)), which keeps the A-fragment reads conflict-free; they cycle
-  // through 4 buffers (tile i multiplied, tiles i+1 .. i+3 landing).
+  // are unpadded and chunk-major (16-byte chunk c of row r at c * 512 + r * 16),
+  // which keeps the A-fragment reads conflict-free; they cycle through 4
+  // buffers (tile i multiplied, tiles i+1 .. i+3 landing).
   constexpr bool kDMA = two_wg_per_cu<EK, W, NSUB, SRC, FEAT>() && DPAD * T::CB == 256;
   // otherwise tile j lives in LDS buffer j % 3: tile i is being multiplied
   // (from registers), tile i+1's A fragments are being read, tile i+2 is
@@ -301,9 +301,9 @@ __global__ void __launch_bounds__(W * 64)
   // ---------------- tile cursor and descriptors ----------------
   // One cursor walks the workgroup's tiles in order (tile t of the m-th
   // non-empty doc). Each iteration it emits the descriptor of the newest tile
-  // (the one being fetched) and advances, branch-free: a doc boundary selects
-  // the next table entry, and past the last doc the sentinel entry (length
-  // 0) makes every further tile empty. Older tiles' descriptors move down a
+  // (the one being fetched) and advances: a doc boundary selects the next
+  // table entry, and past the last doc the sentinel entry (length 0) makes
+  // every further tile empty. Older tiles' descriptors move down a
   // short register queue (fetch -> commit -> MFMA -> epilogue).
   struct Cur {
     int m, t, len, k;
@@ -330,20 +330,16 @@ __global__ void __launch_bounds__(W * 64)
             ((int64_t)__builtin_amdgcn_readfirstlane(e[3]) << 32);
   };
   auto cur_adv = [&](Cur& c) {
-    const bool last = (c.t + 1) * 32 >= c.len;
-    Cur n;
-    cur_entry(n, c.m + 1 < nnz ? c.m + 1 : nnz);
-    c.t = last ? 0 : c.t + 1;
-    c.m = last ? n.m : c.m;
-    c.k = last ? n.k : c.k;
-    c.len = last ? n.len : c.len;
-    c.holes = last ? n.holes : c.holes;
-    c.off = last ? n.off : c.off;
+    // the table is read only at a doc's last tile (a uniform branch)
+    if ((c.t + 1) * 32 >= c.len)
+      cur_entry(c, c.m + 1 < nnz ? c.m + 1 : nnz);
+    else
+      c.t += 1;
   };
   auto produce = [&](const Cur& c) -> Desc {
     Desc d;
-    const int rem = c.len - c.t * 32;
-    d.nv = rem >= 32 ? 32 : (rem > 0 ? rem : 0);
+    const int rem = c.len - c.t * 32;  // >= 0: the cursor stops at a doc's end
+    d.nv = rem < 32 ? rem : 32;  // (min, not a clamp: a clamp would leave the scalar unit)
     d.k = c.k;
     d.t = c.t;
     d.docend = c.len > 0 && rem <= 32;
@@ -376,10 +372,10 @@ __global__ void __launch_bounds__(W * 64)
   int lcc[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    // DMA: chunk i of this lane is LDS slot (wave * NCH + i) * 64 + lane,
-    // i.e. row slot / 16 and global chunk (slot % 16) ^ (row & 15)
+    // DMA: chunk i of this lane is LDS slot (wave * NCH + i) * 64 + lane of
+    // the chunk-major tile, i.e. row slot % 32 and chunk slot / 32
     const int c = kDMA ? (wv * NCH + i) * 64 + lane : tid + i * NT;
-    const int row = c / SCPR, cc = kDMA ? ((c % SCPR) ^ (row & 15)) : c % SCPR;
+    const int row = kDMA ? c % 32 : c / SCPR, cc = kDMA ? c / 32 : c % SCPR;
     const bool inr = FULLCH || c < 32 * SCPR;
     lcc[i] = cc;
     if constexpr (SRC == SRC_DENSE) {
@@ -390,6 +386,11 @@ __global__ void __launch_bounds__(W * 64)
       loff[i] = (uint32_t)row;
     }
   }
+
+  // DMA lane offsets from the tile's row 0 (padding chunks out of range)
+  uint32_t dmaoff[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) dmaoff[i] = lrow[i] < 32 ? loff[i] : kOOB;
 
   // PLAID phase A: centroid codes of tile d
   auto fetch_codes = [&](auto SS, const Desc& d) {
@@ -409,21 +410,24 @@ __global__ void __launch_bounds__(W * 64)
   // later LDS read and would wait for all DMA before each A-fragment read;
   // here the ordering is explicit (the step-end wait and barrier). M0 (the
   // LDS destination) is saved and restored around the load.
+  // The buffer descriptor starts at the tile's first row and ends with its
+  // last valid row, so rows past the doc end fall out of range (and read 0)
+  // with no per-lane test: the lane offsets are loop constants (dmaoff).
   auto fetch_dma = [&](const Cur& c, const Desc& d, int buf) {
     if constexpr (kDMA) {
-      const uint32_t span = (uint32_t)(c.len > 1 ? c.len - 1 : 0) * (uint32_t)p.d.sl_b + (uint32_t)(p.d.dim * T::IN_B);
-      const uint64_t base = (uint64_t)(p.d.data + c.off);
+      const uint32_t sl = (uint32_t)p.d.sl_b;
+      const uint32_t span = d.nv > 0 ? (uint32_t)(d.nv - 1) * sl + (uint32_t)(p.d.dim * T::IN_B) : 0u;
+      const uint64_t base = (uint64_t)(p.d.data + c.off) + (uint64_t)((uint32_t)c.t * 32u * sl);
       // raw buffer descriptor: base, stride 0, num_records = span, untyped 32-bit format
       const u32x4 desc = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
                           (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu),
                           (uint32_t)__builtin_amdgcn_readfirstlane(span), 0x00020000u};
-      const uint32_t toff = (uint32_t)c.t * 32u * (uint32_t)p.d.sl_b;
       const int wu = __builtin_amdgcn_readfirstlane(wv);
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
         const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
             (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(s_tile[buf][0] + (wu * NCH + i) * 1024));
-        const uint32_t voff = lrow[i] < d.nv ? loff[i] + toff : kOOB;
+        const uint32_t voff = dmaoff[i];
         uint32_t saved;
         asm volatile(
             "s_mov_b32 %0, m0\n\t"
@@ -658,19 +662,16 @@ __global__ void __launch_bounds__(W * 64)
       // MFMAs (three rotating registers). The fences keep LDS reads and
       // MFMAs in this order and let other instructions move across them.
       constexpr int kFence = 0x2 | 0x4 | 0x10 | 0x20 | 0x40 | 0x200 | 0x400;
-      // A fragment k-step ks of this lane: logical chunk h * KS + ks of row
-      // l32 (DMA layout: at slot chunk ^ (l32 & 15) of a 256-byte row)
-      auto afrag = [&](int ks) -> const u32x4* {
-        if constexpr (kDMA)
-          return (const u32x4*)(s_tile[buf][0] + l32 * 256 + (((h * KS + ks) ^ (l32 & 15)) * 16));
-        else
-          return (const u32x4*)(A + ks * T::FRAG_B);
-      };
+      // A fragment k-step ks of this lane: bytes [(h * KS + ks) * FRAG_B, +FRAG_B)
+      // of row l32. DMA tiles are chunk-major (16-byte chunk j of row r at
+      // j * 512 + r * 16): a fragment's rows are contiguous, so the reads are
+      // conflict-free and every (k-step, chunk) offset is an immediate.
+      const char* AD = s_tile[buf][0] + h * (KS * FV * 512) + l32 * 16;
       u32x4 a3[3][FV];
       auto lda = [&](int slot, int ks) {
-        const u32x4* src = afrag(ks);
 #pragma unroll
-        for (int v = 0; v < FV; ++v) a3[slot][v] = src[v];
+        for (int v = 0; v < FV; ++v)
+          a3[slot][v] = kDMA ? *(const u32x4*)(AD + (ks * FV + v) * 512) : ((const u32x4*)(A + ks * T::FRAG_B))[v];
       };
       lda(0, 0);
       if constexpr (KS > 1) lda(1, 1);
@@ -957,6 +958,10 @@ __global__ void __launch_bounds__(W * 64)
     } else {
       epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
       mma_tile(IP{}, IP{}, bx);
+      // the max stays with the MFMAs that overwrite its accumulators (sunk
+      // below the branches that follow, it would keep two sets live)
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) asm volatile("" : "+v"(m[sub]));
     }
     if constexpr (kPrefetchA) load_a(IQ{}, buf_a);
     if constexpr (!kDMA) commit(IP{}, q2, buf_c, (i + 2) & 3);

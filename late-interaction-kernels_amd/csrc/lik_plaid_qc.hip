@@ -305,7 +305,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   // 8a + 4h + b, i.e. + h for even b and - h for odd b
   const int res_lane = RES0 + l32 * (int)p.pl.res_st + h * RBL;
   const int qv_even = (4 * h + h) * 64 + l32 * 2, qv_odd = (4 * h - h) * 64 + l32 * 2;
-  auto read_stage = [&](Regs& rg, int stage) {
+  auto read_stage = [&](Regs& rg, int stage, auto NORMD) {
     const char* st = &s_st[wl][stage][0];
     const char* rp = st + res_lane;
     if constexpr (RVL % 4 == 0) {
@@ -323,7 +323,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
     }
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
-      rg.inv[jj] = tinv ? *(const f32x4*)(st + INV0 + (8 * jj + 4 * h) * 4) : (f32x4){1.f, 1.f, 1.f, 1.f};
+      rg.inv[jj] = decltype(NORMD)::value ? *(const f32x4*)(st + INV0 + (8 * jj + 4 * h) * 4) : (f32x4){1.f, 1.f, 1.f, 1.f};
 #pragma unroll
     for (int sub = 0; sub < QN; ++sub)
 #pragma unroll
@@ -436,22 +436,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   code_dma(tq2, 2);
   gather(tq1, 1, 1);
   code_dma(tq3, 3);
-  int c = 0;
-  while (tq0.j >= 0) {
-    const Tile tq4 = next_tile(tq3);
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(G + 1) : "memory");
-    const int stage = c & 1;
-    Regs rg;
-    read_stage(rg, stage);
-    gather(tq2, (c + 2) & 3, stage);
-    code_dma(tq4, c & 3);
-    compute(tq0, rg);
-    tq0 = tq1;
-    tq1 = tq2;
-    tq2 = tq3;
-    tq3 = tq4;
-    ++c;
-  }
+  // (two copies of the loop: with and without token inverse norms)
+  auto scan = [&](auto NORMD) {
+    int c = 0;
+    while (tq0.j >= 0) {
+      const Tile tq4 = next_tile(tq3);
+      asm volatile("s_waitcnt vmcnt(%0)" : : "n"(G + 1) : "memory");
+      const int stage = c & 1;
+      Regs rg;
+      read_stage(rg, stage, NORMD);
+      gather(tq2, (c + 2) & 3, stage);
+      code_dma(tq4, c & 3);
+      compute(tq0, rg);
+      tq0 = tq1;
+      tq1 = tq2;
+      tq2 = tq3;
+      tq3 = tq4;
+      ++c;
+    }
+  };
+  if (tinv)
+    scan(std::true_type{});
+  else
+    scan(std::false_type{});
   // no gather may still be writing this wave's LDS when it exits
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   // this wave's doc scores (written by lane 0: visible to the whole wave)

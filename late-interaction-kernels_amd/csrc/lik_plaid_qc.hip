@@ -84,7 +84,7 @@ __global__ void __launch_bounds__(256) centroid_scores_kernel(const Params p, ui
 }
 
 template <int EK, int DPAD, int NBITS, int QN, bool FULLD>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1 ? 3 : 4)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1 ? 2 : 4)))
     plaid_qc_kernel(const Params p, const uint16_t* __restrict__ qc, int64_t qc_qs, const float* __restrict__ tinv) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;
@@ -114,11 +114,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   __shared__ __attribute__((aligned(16))) int32_t s_codes[4][4][32];
   // this wave's doc scores, written to memory once after its loop
   __shared__ float s_out[4][QN][kQcRMax];
-  // this wave's doc table (first token, length), read from LDS in the loop:
-  // a vector load there would make the compiler wait for every load in
-  // flight, the gathers included
-  __shared__ int64_t s_dtok[4][kQcRMax];
-  __shared__ int32_t s_dlen[4][kQcRMax];
+  // this wave's doc boundaries (cu_seqlens[j0 .. j1]), read from LDS in the
+  // loop at doc ends only: a vector load there would make the compiler wait
+  // for every load in flight, the gathers included
+  __shared__ int32_t s_cu[4][kQcRMax + 1];
   for (int v = threadIdx.x; v < 256; v += 256) {
     uint32_t h16[4] = {0u, 0u, 0u, 0u};
     for (int k = 0; k < FPB; ++k) {
@@ -165,46 +164,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
     for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(bq[sub][ks]));
   }
 
+  // ---- this wave's docs [j0, j1): tokens [T0, T1) of the packed corpus ----
   const int64_t j0 = r * p.R;
   const int64_t j1 = j0 + p.R < p.pl.n ? j0 + p.R : p.pl.n;
-  for (int64_t j = j0 + lane; j < j1; j += 64) {
-    s_dlen[wl][j - j0] = (int32_t)doc_len<SRC_PLAID>(p, j);
-    s_dtok[wl][j - j0] = p.pl.cu ? (int64_t)p.pl.cu[j] : j * p.pl.codes_sn;
-  }
+  const int nd = (int)(j1 - j0);
+  for (int k = lane; k <= nd; k += 64) s_cu[wl][k] = p.pl.cu[j0 + k];
   __builtin_amdgcn_wave_barrier();
-  auto dlen = [&](int64_t j) -> int64_t { return s_dlen[wl][j - j0]; };
-  auto dtok = [&](int64_t j) -> int64_t { return s_dtok[wl][j - j0]; };
-  struct Tile {
-    int64_t j, tok;
-    int t, nv;
-  };
-  auto uni64 = [](int64_t x) -> int64_t {
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
-    return (int64_t)(((uint64_t)hi << 32) | lo);
-  };
-  auto uni = [&](const Tile& t) -> Tile {
-    return Tile{uni64(t.j), uni64(t.tok), __builtin_amdgcn_readfirstlane(t.t), __builtin_amdgcn_readfirstlane(t.nv)};
-  };
-  auto open_doc = [&](int64_t j) -> Tile {
-    while (j < j1) {
-      const int64_t len = dlen(j);
-      if (len > 0) return uni(Tile{j, dtok(j), 0, (int)(len < 32 ? len : 32)});
-      if (lane < QN) s_out[wl][lane][j - j0] = 0.f;
-      ++j;
-    }
-    return Tile{-1, 0, 0, 0};
-  };
-  auto next_tile = [&](const Tile& c) -> Tile {
-    if (c.j < 0) return c;
-    const int64_t len = dlen(c.j);
-    const int64_t start = (int64_t)(c.t + 1) * 32;
-    if (start < len) {
-      const int64_t rem = len - start;
-      return uni(Tile{c.j, c.tok + 32, c.t + 1, (int)(rem < 32 ? rem : 32)});
-    }
-    return open_doc(c.j + 1);
-  };
+  const int T0 = __builtin_amdgcn_readfirstlane(s_cu[wl][0]);
+  const int T1 = __builtin_amdgcn_readfirstlane(s_cu[wl][nd]);
+  const int ntile = (T1 - T0 + 31) >> 5;
+
+  // raw buffer descriptor words (stride 0, untyped 32-bit format)
   auto rsrc_words = [](const void* base, uint32_t nbytes) -> u32x4 {
     const uint64_t b = (uint64_t)base;
     return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b),
@@ -219,10 +189,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
     const int64_t q = g * QN + sub;
     dqc[sub] = rsrc_words(qc + (q < p.q.n ? q : 0) * qc_qs, q < p.q.n ? (uint32_t)(p.pl.ncent * 64) : 0u);
   }
-  auto lds_addr = [&](int stage, int off) -> uint32_t {
-    return (uint32_t)__builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_st[wl][stage][0]) + (uint32_t)off);
-  };
+  // LDS addresses of the two stages and four code slots (loop constants)
+  uint32_t st_lds[2], cs_lds[4];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    st_lds[k] = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_st[wl][k][0]));
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    cs_lds[k] = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t*)(&s_codes[wl][k][0]));
   auto dma = [&](uint32_t lds, uint32_t voff, const u32x4& desc) {
     uint32_t saved;
     asm volatile(
@@ -249,42 +225,44 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   // R and R + 4 that one fragment read touches (lanes of the two halves)
   // then sit in different banks. Instruction i fills positions 16 i + lane / 4.
   auto rowpos = [](int row) { return row ^ ((row >> 2) & 1); };
-  // codes of tile d into code slot `slot` (lanes 0..7, 16 bytes each; one
-  // load instruction whether or not the tile exists)
-  auto code_dma = [&](const Tile& d, int slot) {
-    const bool ok = d.j >= 0;
-    const u32x4 dc = rsrc_words(ok ? (const void*)(p.pl.codes + d.tok) : (const void*)p.pl.codes,
-                                ok ? (uint32_t)d.nv * 4u : 0u);
-    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t*)(&s_codes[wl][slot][0]));
-    if (lane < 8) dma_nt(lds, (uint32_t)(lane * 16), dc);
+  // Tiles are 32 consecutive tokens of [T0, T1), tile i at T0 + 32 i, in
+  // whichever docs they fall; a tile past the range loads nothing (record
+  // count 0). Codes of tile i into code slot `slot` (lanes 0..7, 16 bytes each).
+  // (token indices in 64 bits: T1 + 128 may pass 2^31)
+  auto code_dma = [&](int i, int slot) {
+    const int64_t T = (int64_t)T0 + 32 * i;
+    const uint32_t nrec = T < T1 ? (uint32_t)(T1 - T < 32 ? T1 - T : 32) * 4u : 0u;
+    const u32x4 dc = rsrc_words(p.pl.codes + (T < T1 ? T : T0), nrec);
+    if (lane < 8) dma_nt(cs_lds[slot], (uint32_t)(lane * 16), dc);
   };
-  // gather tile d (code of row l32 in code slot `slot`) into stage `stage`,
+  // gather tile i (code of row l32 in code slot `slot`) into stage `stage`,
   // once the stage's previous contents have been read (lgkmcnt(0)); exactly
   // G load instructions whether or not the tile exists
-  auto gather = [&](const Tile& d, int slot, int stage) {
-    const bool ok = d.j >= 0;
+  auto gather = [&](int i, int slot, int stage) {
+    const int64_t T = (int64_t)T0 + 32 * i;
+    const int nv = T < T1 ? (int)(T1 - T < 32 ? T1 - T : 32) : 0;  // rows of the tile that exist
     int64_t cd = s_codes[wl][slot][l32];
     cd = (cd < 0 || cd >= p.pl.ncent) ? 0 : cd;
-    const uint32_t rowoff = ok && l32 < d.nv ? (uint32_t)cd * 64u : kInvRow;
+    const uint32_t rowoff = l32 < nv ? (uint32_t)cd * 64u : kInvRow;
     uint32_t voff[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = rowpos(i * 16 + lane / 4);  // P is its own inverse
-      voff[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(row * 4, (int)rowoff) + (uint32_t)((lane & 3) * 16);
+    for (int k = 0; k < 2; ++k) {
+      const int row = rowpos(k * 16 + lane / 4);  // P is its own inverse
+      voff[k] = (uint32_t)__builtin_amdgcn_ds_bpermute(row * 4, (int)rowoff) + (uint32_t)((lane & 3) * 16);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
     for (int sub = 0; sub < QN; ++sub)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) dma(lds_addr(stage, sub * QCT + i * 1024), voff[i], dqc[sub]);
-    const u32x4 dres = rsrc_words(ok ? (const void*)(p.pl.res + d.tok * p.pl.res_st) : (const void*)p.pl.res,
-                                  ok ? (uint32_t)d.nv * (uint32_t)p.pl.res_st : 0u);
+      for (int k = 0; k < 2; ++k) dma(st_lds[stage] + (uint32_t)(sub * QCT + k * 1024), voff[k], dqc[sub]);
+    const bool ok = nv > 0;
+    const int64_t Tb = ok ? T : T0;
+    const u32x4 dres = rsrc_words(p.pl.res + Tb * p.pl.res_st, (uint32_t)nv * (uint32_t)p.pl.res_st);
 #pragma unroll
-    for (int i = 0; i < NRI; ++i) dma_nt(lds_addr(stage, RES0 + i * 1024), (uint32_t)(i * 1024 + lane * 16), dres);
-    const u32x4 dinv = rsrc_words(ok && tinv ? (const void*)(tinv + d.tok) : (const void*)p.pl.res,
-                                  ok && tinv ? (uint32_t)d.nv * 4u : 0u);
-    if (lane < 8) dma_nt(lds_addr(stage, INV0), (uint32_t)(lane * 16), dinv);
+    for (int k = 0; k < NRI; ++k) dma_nt(st_lds[stage] + (uint32_t)(RES0 + k * 1024), (uint32_t)(k * 1024 + lane * 16), dres);
+    const u32x4 dinv = rsrc_words(tinv ? (const void*)(tinv + Tb) : (const void*)p.pl.res,
+                                  tinv ? (uint32_t)nv * 4u : 0u);
+    if (lane < 8) dma_nt(st_lds[stage] + (uint32_t)INV0, (uint32_t)(lane * 16), dinv);
   };
 
   float m[QN];
@@ -342,7 +320,43 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
       asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,0,1]" : "=v"(r) : "v"(a), "v"(b), "v"(wb));
     return r;
   };
-  auto compute = [&](const Tile& d, const Regs& rg) {
+  // The doc whose tokens continue into the current tile (jc, ending at token
+  // ec); its end is known without a table read until it is reached.
+  int jc = 0;
+  int64_t ec = __builtin_amdgcn_readfirstlane(s_cu[wl][1]);
+  // park doc jc's maxima (sum over the query's columns in the tile kernel's
+  // order) and move to the next doc
+  auto doc_end = [&]() {
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
+      const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const float v = __builtin_isfinite(mm) ? mm : 0.f;
+      auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
+      // the tile kernel's flush order (query g at place g of its group of 4:
+      // the sum starts at 4-column chunk g % (Lq / 4) and wraps)
+      float sum = 0.f;
+      if ((p.LU & 3) == 0) {
+        const int nv4 = p.LU >> 2;
+        int c = rot0[sub];
+        for (int jj = 0; jj < nv4; ++jj) {
+          sum += col(4 * c);
+          sum += col(4 * c + 1);
+          sum += col(4 * c + 2);
+          sum += col(4 * c + 3);
+          c = (c + 1 == nv4) ? 0 : c + 1;
+        }
+      } else {
+        for (int c = 0; c < p.LU; ++c) sum += col(c);
+      }
+      if (lane == 0) s_out[wl][sub][jc] = sum * p.out_scale;
+      m[sub] = NEG_INF;
+    }
+    ++jc;
+    ec = jc < nd ? (int64_t)__builtin_amdgcn_readfirstlane(s_cu[wl][jc + 1]) : ((int64_t)1 << 40);
+  };
+  auto compute = [&](int i, const Regs& rg) {
+    const int64_t T = (int64_t)T0 + 32 * i;
     f32x16 acc[QN];
     const uint32_t* rw = rg.rw;
     auto byte_at = [&](int byte_i) -> uint32_t { return (rw[byte_i >> 2] >> ((byte_i & 3) * 8)) & 0xffu; };
@@ -370,53 +384,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
 #pragma unroll
       for (int sub = 0; sub < QN; ++sub) acc[sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[sub], &ra, &bq[sub][ks]);
     }
+    if (ec > T + 32) {
+      // the whole tile belongs to doc jc (the common case)
 #pragma unroll
-    for (int sub = 0; sub < QN; ++sub) {
-      if (d.nv == 32) {
+      for (int sub = 0; sub < QN; ++sub)
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-          const float v0 = fma_mix(acc[sub][i], qsc[sub], rg.qv[sub][i >> 1], std::false_type{}) * rg.inv[i >> 2][i & 3];
-          const float v1 = fma_mix(acc[sub][i + 1], qsc[sub], rg.qv[sub][i >> 1], std::true_type{}) *
-                           rg.inv[(i + 1) >> 2][(i + 1) & 3];
+        for (int e = 0; e < 16; e += 2) {
+          const float v0 = fma_mix(acc[sub][e], qsc[sub], rg.qv[sub][e >> 1], std::false_type{}) * rg.inv[e >> 2][e & 3];
+          const float v1 = fma_mix(acc[sub][e + 1], qsc[sub], rg.qv[sub][e >> 1], std::true_type{}) *
+                           rg.inv[(e + 1) >> 2][(e + 1) & 3];
           m[sub] = fmaxf(m[sub], fmaxf(v0, v1));
         }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-          const int row = 8 * (i >> 2) + 4 * h + (i & 3);
-          const float v0 = fma_mix(acc[sub][i], qsc[sub], rg.qv[sub][i >> 1], std::false_type{}) * rg.inv[i >> 2][i & 3];
-          const float v1 = fma_mix(acc[sub][i + 1], qsc[sub], rg.qv[sub][i >> 1], std::true_type{}) *
-                           rg.inv[(i + 1) >> 2][(i + 1) & 3];
-          m[sub] = fmaxf(m[sub], fmaxf(row < d.nv ? v0 : NEG_INF, row + 1 < d.nv ? v1 : NEG_INF));
-        }
-      }
+      return;
     }
-    if ((int64_t)(d.t + 1) * 32 >= dlen(d.j)) {
+    // doc ends inside the tile: rows [a, b) of each doc in turn (values
+    // recomputed per segment: holding them would cost 16 registers a query)
+    int a = 0;
+    while (true) {
+      const int b = ec - T < 32 ? (int)(ec - T) : 32;
+      const int la = a - 4 * h, lb = b - 4 * h;  // row r = 8 (e / 4) + 4 h + e % 4
 #pragma unroll
-      for (int sub = 0; sub < QN; ++sub) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
-        const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        const float v = __builtin_isfinite(mm) ? mm : 0.f;
-        auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
-        // the tile kernel's flush order (query g at place g of its group of 4:
-        // the sum starts at 4-column chunk g % (Lq / 4) and wraps)
-        float s = 0.f;
-        if ((p.LU & 3) == 0) {
-          const int nv4 = p.LU >> 2;
-          int c = rot0[sub];
-          for (int jj = 0; jj < nv4; ++jj) {
-            s += col(4 * c);
-            s += col(4 * c + 1);
-            s += col(4 * c + 2);
-            s += col(4 * c + 3);
-            c = (c + 1 == nv4) ? 0 : c + 1;
-          }
-        } else {
-          for (int c = 0; c < p.LU; ++c) s += col(c);
+      for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float v0 = fma_mix(acc[sub][e], qsc[sub], rg.qv[sub][e >> 1], std::false_type{}) * rg.inv[e >> 2][e & 3];
+          const float v1 = fma_mix(acc[sub][e + 1], qsc[sub], rg.qv[sub][e >> 1], std::true_type{}) *
+                           rg.inv[(e + 1) >> 2][(e + 1) & 3];
+          const int r0 = 8 * (e >> 2) + (e & 3);
+          m[sub] = fmaxf(m[sub], fmaxf((r0 >= la && r0 < lb) ? v0 : NEG_INF, (r0 + 1 >= la && r0 + 1 < lb) ? v1 : NEG_INF));
         }
-        if (lane == 0) s_out[wl][sub][d.j - j0] = s * p.out_scale;
-        m[sub] = NEG_INF;
-      }
+      if (ec > T + 32 || jc >= nd) break;  // doc jc continues in the next tile
+      doc_end();
+      a = b;
     }
   };
 
@@ -425,45 +424,36 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   // gather and the codes of tile c + 3 may be in flight (G + 1 loads).
   // Iteration c reads its stage, gathers tile c + 2 into it, loads the codes
   // of tile c + 4, then scores tile c.
-  Tile tq0 = open_doc(j0);
-  Tile tq1 = next_tile(tq0);
-  Tile tq2 = next_tile(tq1);
-  Tile tq3 = next_tile(tq2);
-  code_dma(tq0, 0);
-  code_dma(tq1, 1);
+  code_dma(0, 0);
+  code_dma(1, 1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  gather(tq0, 0, 0);
-  code_dma(tq2, 2);
-  gather(tq1, 1, 1);
-  code_dma(tq3, 3);
+  gather(0, 0, 0);
+  code_dma(2, 2);
+  gather(1, 1, 1);
+  code_dma(3, 3);
   // (two copies of the loop: with and without token inverse norms)
   auto scan = [&](auto NORMD) {
-    int c = 0;
-    while (tq0.j >= 0) {
-      const Tile tq4 = next_tile(tq3);
+    for (int c = 0; c < ntile; ++c) {
       asm volatile("s_waitcnt vmcnt(%0)" : : "n"(G + 1) : "memory");
       const int stage = c & 1;
       Regs rg;
       read_stage(rg, stage, NORMD);
-      gather(tq2, (c + 2) & 3, stage);
-      code_dma(tq4, c & 3);
-      compute(tq0, rg);
-      tq0 = tq1;
-      tq1 = tq2;
-      tq2 = tq3;
-      tq3 = tq4;
-      ++c;
+      gather(c + 2, (c + 2) & 3, stage);
+      code_dma(c + 4, c & 3);
+      compute(c, rg);
     }
   };
   if (tinv)
     scan(std::true_type{});
   else
     scan(std::false_type{});
+  // docs left (empty docs at the range's end, or an empty range)
+  while (jc < nd) doc_end();
   // no gather may still be writing this wave's LDS when it exits
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   // this wave's doc scores (written by lane 0: visible to the whole wave)
   __builtin_amdgcn_wave_barrier();
-  for (int k = lane; k < (int)(j1 - j0); k += 64)
+  for (int k = lane; k < nd; k += 64)
 #pragma unroll
     for (int sub = 0; sub < QN; ++sub) {
       const int64_t q = g * QN + sub;
@@ -534,6 +524,7 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   if (docs->dim != Q->dim || Q->dim <= 0 || Q->dim % 8 != 0 || Q->dim > 128) return LIK_ERR_UNSUPPORTED;
   if (docs->n_buckets < 1 || docs->n_buckets > 256 || !docs->bucket_weights) return LIK_ERR_INVALID;
   if (!docs->cu_seqlens && !docs->lengths) return LIK_ERR_INVALID;
+  if (!docs->cu_seqlens) return LIK_ERR_UNSUPPORTED;  // the scan walks the packed token stream
   if ((flags & LIK_KD_LAYOUT) || Q->mask || Q->token_scale || Q->cu_seqlens) return LIK_ERR_INVALID;
   if (Q->len > 32 || Q->n > kQcMaxQueries) return LIK_ERR_UNSUPPORTED;
   const bool norm_d = (flags & (LIK_NORMALIZE | LIK_NORMALIZE_D)) != 0;

@@ -170,9 +170,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   const int nd = (int)(j1 - j0);
   for (int k = lane; k <= nd; k += 64) s_cu[wl][k] = p.pl.cu[j0 + k];
   __builtin_amdgcn_wave_barrier();
+  // tokens are counted from T0 (the range spans < 2^31 tokens)
   const int T0 = __builtin_amdgcn_readfirstlane(s_cu[wl][0]);
-  const int T1 = __builtin_amdgcn_readfirstlane(s_cu[wl][nd]);
-  const int ntile = (T1 - T0 + 31) >> 5;
+  const int span = __builtin_amdgcn_readfirstlane(s_cu[wl][nd]) - T0;
+  const int ntile = (span + 31) >> 5;
 
   // raw buffer descriptor words (stride 0, untyped 32-bit format)
   auto rsrc_words = [](const void* base, uint32_t nbytes) -> u32x4 {
@@ -189,16 +190,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
     const int64_t q = g * QN + sub;
     dqc[sub] = rsrc_words(qc + (q < p.q.n ? q : 0) * qc_qs, q < p.q.n ? (uint32_t)(p.pl.ncent * 64) : 0u);
   }
-  // LDS addresses of the two stages and four code slots (loop constants)
-  uint32_t st_lds[2], cs_lds[4];
+  // LDS addresses of the two stages and of code slot 0 (loop constants)
+  uint32_t st_lds[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k)
     st_lds[k] = (uint32_t)__builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_st[wl][k][0]));
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    cs_lds[k] = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t*)(&s_codes[wl][k][0]));
+  const uint32_t cs_lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t*)(&s_codes[wl][0][0]));
   auto dma = [&](uint32_t lds, uint32_t voff, const u32x4& desc) {
     uint32_t saved;
     asm volatile(
@@ -225,25 +224,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   // R and R + 4 that one fragment read touches (lanes of the two halves)
   // then sit in different banks. Instruction i fills positions 16 i + lane / 4.
   auto rowpos = [](int row) { return row ^ ((row >> 2) & 1); };
-  // Tiles are 32 consecutive tokens of [T0, T1), tile i at T0 + 32 i, in
+  // Tiles are 32 consecutive tokens of the range, tile i at T0 + 32 i, in
   // whichever docs they fall; a tile past the range loads nothing (record
-  // count 0). Codes of tile i into code slot `slot` (lanes 0..7, 16 bytes each).
-  // (token indices in 64 bits: T1 + 128 may pass 2^31)
-  auto code_dma = [&](int i, int slot) {
-    const int64_t T = (int64_t)T0 + 32 * i;
-    const uint32_t nrec = T < T1 ? (uint32_t)(T1 - T < 32 ? T1 - T : 32) * 4u : 0u;
-    const u32x4 dc = rsrc_words(p.pl.codes + (T < T1 ? T : T0), nrec);
-    if (lane < 8) dma_nt(cs_lds[slot], (uint32_t)(lane * 16), dc);
+  // count 0). The streams' base addresses advance by one tile per iteration
+  // (64-bit scalar adds; no multiplies in the loop).
+  auto rows_of = [&](int i) {  // rows of tile i that exist
+    const int rem = span - 32 * i;
+    return rem < 0 ? 0 : (rem < 32 ? rem : 32);
+  };
+  const char* code_p = (const char*)(p.pl.codes + T0);  // tile 0
+  const char* res_p = (const char*)p.pl.res + (int64_t)T0 * p.pl.res_st;
+  const char* inv_p = (const char*)(tinv ? tinv + T0 : nullptr);
+  const int64_t res_tile = 32 * p.pl.res_st;
+  // codes of tile i (at code_p) into code slot `slot` (lanes 0..7, 16 bytes each)
+  auto code_dma = [&](int i, int slot, const char* cp) {
+    const u32x4 dc = rsrc_words(cp, (uint32_t)rows_of(i) * 4u);
+    if (lane < 8) dma_nt(cs_lds0 + (uint32_t)(slot * 128), (uint32_t)(lane * 16), dc);
   };
   // gather tile i (code of row l32 in code slot `slot`) into stage `stage`,
   // once the stage's previous contents have been read (lgkmcnt(0)); exactly
   // G load instructions whether or not the tile exists
-  auto gather = [&](int i, int slot, int stage) {
-    const int64_t T = (int64_t)T0 + 32 * i;
-    const int nv = T < T1 ? (int)(T1 - T < 32 ? T1 - T : 32) : 0;  // rows of the tile that exist
-    int64_t cd = s_codes[wl][slot][l32];
-    cd = (cd < 0 || cd >= p.pl.ncent) ? 0 : cd;
-    const uint32_t rowoff = l32 < nv ? (uint32_t)cd * 64u : kInvRow;
+  auto gather = [&](int i, int slot, int stage, const char* rp, const char* ip) {
+    const int nv = rows_of(i);
+    const uint32_t cd = (uint32_t)s_codes[wl][slot][l32];
+    const uint32_t rowoff = l32 < nv ? (cd < (uint32_t)p.pl.ncent ? cd : 0u) * 64u : kInvRow;
     uint32_t voff[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -255,13 +259,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
     for (int sub = 0; sub < QN; ++sub)
 #pragma unroll
       for (int k = 0; k < 2; ++k) dma(st_lds[stage] + (uint32_t)(sub * QCT + k * 1024), voff[k], dqc[sub]);
-    const bool ok = nv > 0;
-    const int64_t Tb = ok ? T : T0;
-    const u32x4 dres = rsrc_words(p.pl.res + Tb * p.pl.res_st, (uint32_t)nv * (uint32_t)p.pl.res_st);
+    const u32x4 dres = rsrc_words(rp, (uint32_t)nv * (uint32_t)p.pl.res_st);
 #pragma unroll
     for (int k = 0; k < NRI; ++k) dma_nt(st_lds[stage] + (uint32_t)(RES0 + k * 1024), (uint32_t)(k * 1024 + lane * 16), dres);
-    const u32x4 dinv = rsrc_words(tinv ? (const void*)(tinv + Tb) : (const void*)p.pl.res,
-                                  tinv ? (uint32_t)nv * 4u : 0u);
+    const u32x4 dinv = rsrc_words(ip ? (const void*)ip : (const void*)p.pl.res, ip ? (uint32_t)nv * 4u : 0u);
     if (lane < 8) dma_nt(st_lds[stage] + (uint32_t)INV0, (uint32_t)(lane * 16), dinv);
   };
 
@@ -323,7 +324,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   // The doc whose tokens continue into the current tile (jc, ending at token
   // ec); its end is known without a table read until it is reached.
   int jc = 0;
-  int64_t ec = __builtin_amdgcn_readfirstlane(s_cu[wl][1]);
+  int ec = __builtin_amdgcn_readfirstlane(s_cu[wl][1]) - T0;  // relative to T0
   // park doc jc's maxima (sum over the query's columns in the tile kernel's
   // order) and move to the next doc
   auto doc_end = [&]() {
@@ -353,10 +354,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
       m[sub] = NEG_INF;
     }
     ++jc;
-    ec = jc < nd ? (int64_t)__builtin_amdgcn_readfirstlane(s_cu[wl][jc + 1]) : ((int64_t)1 << 40);
+    ec = jc < nd ? __builtin_amdgcn_readfirstlane(s_cu[wl][jc + 1]) - T0 : 0x7fffffff;
   };
   auto compute = [&](int i, const Regs& rg) {
-    const int64_t T = (int64_t)T0 + 32 * i;
+    const int T = 32 * i;  // relative to T0
     f32x16 acc[QN];
     const uint32_t* rw = rg.rw;
     auto byte_at = [&](int byte_i) -> uint32_t { return (rw[byte_i >> 2] >> ((byte_i & 3) * 8)) & 0xffu; };
@@ -384,7 +385,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
 #pragma unroll
       for (int sub = 0; sub < QN; ++sub) acc[sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[sub], &ra, &bq[sub][ks]);
     }
-    if (ec > T + 32) {
+    if (ec - T > 32) {
       // the whole tile belongs to doc jc (the common case)
 #pragma unroll
       for (int sub = 0; sub < QN; ++sub)
@@ -401,7 +402,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
     // recomputed per segment: holding them would cost 16 registers a query)
     int a = 0;
     while (true) {
-      const int b = ec - T < 32 ? (int)(ec - T) : 32;
+      const int b = ec - T < 32 ? ec - T : 32;
       const int la = a - 4 * h, lb = b - 4 * h;  // row r = 8 (e / 4) + 4 h + e % 4
 #pragma unroll
       for (int sub = 0; sub < QN; ++sub)
@@ -413,7 +414,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
           const int r0 = 8 * (e >> 2) + (e & 3);
           m[sub] = fmaxf(m[sub], fmaxf((r0 >= la && r0 < lb) ? v0 : NEG_INF, (r0 + 1 >= la && r0 + 1 < lb) ? v1 : NEG_INF));
         }
-      if (ec > T + 32 || jc >= nd) break;  // doc jc continues in the next tile
+      if (ec - T > 32 || jc >= nd) break;  // doc jc continues in the next tile
       doc_end();
       a = b;
     }
@@ -424,23 +425,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   // gather and the codes of tile c + 3 may be in flight (G + 1 loads).
   // Iteration c reads its stage, gathers tile c + 2 into it, loads the codes
   // of tile c + 4, then scores tile c.
-  code_dma(0, 0);
-  code_dma(1, 1);
+  code_dma(0, 0, code_p);
+  code_dma(1, 1, code_p + 128);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  gather(0, 0, 0);
-  code_dma(2, 2);
-  gather(1, 1, 1);
-  code_dma(3, 3);
+  gather(0, 0, 0, res_p, inv_p);
+  code_dma(2, 2, code_p + 256);
+  gather(1, 1, 1, res_p + res_tile, inv_p ? inv_p + 128 : nullptr);
+  code_dma(3, 3, code_p + 384);
   // (two copies of the loop: with and without token inverse norms)
   auto scan = [&](auto NORMD) {
+    const char* cp = code_p + 512;                 // tile c + 4
+    const char* rp = res_p + 2 * res_tile;         // tile c + 2
+    const char* ip = NORMD ? inv_p + 256 : nullptr;
     for (int c = 0; c < ntile; ++c) {
       asm volatile("s_waitcnt vmcnt(%0)" : : "n"(G + 1) : "memory");
       const int stage = c & 1;
       Regs rg;
       read_stage(rg, stage, NORMD);
-      gather(c + 2, (c + 2) & 3, stage);
-      code_dma(c + 4, c & 3);
+      gather(c + 2, (c + 2) & 3, stage, rp, ip);
+      code_dma(c + 4, c & 3, cp);
       compute(c, rg);
+      cp += 128;
+      rp += res_tile;
+      if (NORMD) ip += 128;
     }
   };
   if (tinv)

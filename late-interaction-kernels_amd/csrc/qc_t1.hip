@@ -1,0 +1,595 @@
+// PLAID residual MaxSim for a few queries over a prepared corpus (gfx950):
+// scores from centroid scores instead of centroid rows.
+//
+// A decoded token is x = c + r: c its centroid row, r the bucket weights
+// picked by its residual fields. With the token's inverse norm known ahead
+// (lik_plaid_token_norms, once per corpus), the normalised score of query
+// token s is
+//     q_s . x / ||x|| = (q_s . c + q_s . r) / ||x||.
+// q_s . c depends on the centroid alone, so for each query it is one
+// [n_centroids, 32] table (centroid_scores_kernel: 32 centroids x 32 query
+// tokens per MFMA tile, times the query token's inverse norm, stored as
+// fp16, 64 bytes per centroid), computed per call in a few microseconds.
+// The scan then needs, per token, its code, residual bytes and inverse norm
+// (40 B at d = 128, nbits = 2) from HBM and one 64-byte table row from L2,
+// instead of a 256-byte centroid row: 4x fewer gathered bytes, and no
+// per-element decode or norm arithmetic in the loop. q_s . r stays on the
+// MFMA (residual fields -> bucket weights rounded to the MFMA type, one
+// 32x32 tile product per 32 tokens, as in the split-form gather kernel).
+//
+// Per wavefront: one (query group, doc range), docs tiled 32 tokens at a
+// time. Everything a tile needs arrives in LDS by buffer_load ... lds (M0
+// saved and restored): the table rows of its tokens (gathered by code, row R
+// at position R ^ ((R / 4) % 2) so the two rows one fragment read touches
+// sit in different banks), its residual bytes and inverse norms (streaming,
+// non-temporal, so they do not push the table out of L2), and, two tiles
+// earlier, its codes. Two stages per wave: while tile c is scored from one,
+// tile c + 1 lands in the other, and tile c + 2's gather is issued as soon
+// as tile c has been read into registers. All of these are loads, which
+// return in issue order, so one fixed vmcnt per iteration waits for exactly
+// the tile about to be scored. Nothing else in the loop touches vector
+// memory: the doc table is staged in LDS and doc scores are collected in LDS
+// and written after the loop (a compiler-visible vector memory access in the
+// loop would bring a full vmcnt(0) with it). The tile is scored as
+//     v[t][s] = (acc[t][s] * qsc[s] + qc[code_t][s]) * inv_t
+// (acc = the q . r MFMA, the fp16 table value added by v_fma_mix), rows past
+// the tile's end -inf, a running max per column, and at a doc's end the
+// column maxima are summed in the tile kernel's order.
+//
+// Reference semantics: plaid.py:684-963 / reference.py:142-179 (decode,
+// normalise, MaxSim); out-of-range codes decode as centroid 0, out-of-range
+// bucket codes as the last bucket.
+#include "lik_kernel.h"
+
+namespace lik {
+
+constexpr int kQcRMax = 128;  // docs per wavefront of the scan (host caps R)
+
+// qc[q * qc_qs + c * 32 + s] = fp16(qsc_s * (q_s . c)), for every centroid c
+// and the 32 token slots of query q (0 past its length). One wavefront per
+// (query, 32 centroids).
+template <int EK, int DPAD>
+__global__ void __launch_bounds__(256) centroid_scores_kernel(const Params p, uint16_t* __restrict__ qc,
+                                                              int64_t qc_qs, int64_t ntile) {
+  using T = KT<EK, DPAD>;
+  constexpr int KS = T::KSTEPS;
+  constexpr int HALF = DPAD / 2;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t q = w / ntile, tile = w - q * ntile;
+  if (q >= p.q.n) return;
+  const bool valid = l32 < seq_len(p.q, q);
+  const char* qrow = valid ? seq_row0(p.q, q) + (int64_t)l32 * p.q.sl_b : nullptr;
+  const int64_t c = tile * 32 + l32;
+  const bool cvalid = c < p.pl.ncent;
+  const char* crow = p.pl.cent + (cvalid ? c : 0) * p.pl.cent_sb;
+  float ss = 0.f;
+  f32x16 acc = {};
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int e = h * HALF + ks * 8;
+    const u32x4 b = (valid && e < p.q.dim) ? *(const u32x4*)(qrow + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
+    const u32x4 a = (cvalid && e < p.q.dim) ? *(const u32x4*)(crow + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
+    if (p.normalize & 1) ss += chunk_sumsq<EK>(b);
+    acc = mfma32<EK>(acc, &a, &b);
+  }
+  ss += __shfl_xor(ss, 32);
+  const float qsc = valid ? ((p.normalize & 1) ? inv_norm(ss) : 1.f) : 0.f;
+  uint16_t* o = qc + q * qc_qs;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = tile * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+    if (row < p.pl.ncent) o[row * 32 + l32] = (uint16_t)f32_to_f16_bits(acc[i] * qsc);
+  }
+}
+
+template <int EK, int DPAD, int NBITS, int QN, bool FULLD>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1 ? 2 : 4)))
+    plaid_qc_kernel(const Params p, const uint16_t* __restrict__ qc, int64_t qc_qs, const float* __restrict__ tinv) {
+  using T = KT<EK, DPAD>;
+  constexpr int KS = T::KSTEPS;
+  constexpr int HALF = DPAD / 2;
+  constexpr int RSB = DPAD * NBITS / 8;            // residual bytes per (padded) row
+  constexpr int NRI = (32 * RSB + 1023) / 1024;    // residual gather instructions per tile
+  constexpr int RBL = HALF * NBITS / 8;            // residual bytes per lane
+  constexpr int RVL = RBL / 4;
+  constexpr int FPB = 8 / NBITS;
+  constexpr int QCT = 32 * 64;                     // table rows of one query per tile
+  constexpr int RES0 = QN * QCT;                   // stage offsets
+  constexpr int INV0 = RES0 + NRI * 1024;
+  constexpr int STB = INV0 + 128;
+  // vector memory instructions issued per iteration: the gather (table rows,
+  // residual bytes, norms: G) and one code load, all loads into LDS, which
+  // return in issue order, so a fixed count identifies the tile in flight
+  constexpr int G = 2 * QN + NRI + 1;
+  static_assert(RBL % 4 == 0, "residual lane bytes");
+  static_assert(G + 1 <= 63, "vmcnt range");
+  constexpr float NEG_INF = -__builtin_huge_valf();
+
+  // byte -> its fields' bucket weights rounded to the MFMA type, packed in pairs
+  __shared__ __attribute__((aligned(16))) float s_lut[2 * 256];
+  // two stages per wave: tile c is read from one while tile c+1 lands in the other
+  __shared__ __attribute__((aligned(1024))) char s_st[4][2][STB];
+  // codes of tiles c+2 .. c+4 (slot t % 4), loaded two iterations ahead of their gather
+  __shared__ __attribute__((aligned(16))) int32_t s_codes[4][4][32];
+  // this wave's doc scores, written to memory once after its loop
+  __shared__ float s_out[4][QN][kQcRMax];
+  // this wave's doc boundaries (cu_seqlens[j0 .. j1]), read from LDS in the
+  // loop at doc ends only: a vector load there would make the compiler wait
+  // for every load in flight, the gathers included
+  __shared__ int32_t s_cu[4][kQcRMax + 1];
+  for (int v = threadIdx.x; v < 256; v += 256) {
+    uint32_t h16[4] = {0u, 0u, 0u, 0u};
+    for (int k = 0; k < FPB; ++k) {
+      uint32_t bc = ((uint32_t)v >> (k * NBITS)) & ((1u << NBITS) - 1u);
+      bc = bc < (uint32_t)p.pl.nb ? bc : (uint32_t)(p.pl.nb - 1);
+      const float wgt = p.pl.bw[bc];
+      h16[k] = EK == EK_F16 ? f32_to_f16_bits(wgt) : f32_to_bf16_bits(wgt);
+    }
+    uint32_t* e = (uint32_t*)&s_lut[v * 2];
+    e[0] = h16[0] | (h16[1] << 16);
+    e[1] = h16[2] | (h16[3] << 16);
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wl = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t wv = (int64_t)blockIdx.x * 4 + wl;
+  const int64_t g = wv / p.NR, r = wv - g * p.NR;
+  if (g >= p.ngroups) return;  // wave-uniform, after the only barrier
+
+  // ---- queries g * QN + sub: token l32 of each in column l32 ----
+  u32x4 bq[QN][KS];
+  float qsc[QN];
+  const bool f_norm_q = (p.normalize & 1) != 0;
+#pragma unroll
+  for (int sub = 0; sub < QN; ++sub) {
+    const int64_t q = g * QN + sub;
+    const bool valid = q < p.q.n && l32 < seq_len(p.q, q);
+    const char* rowp = valid ? seq_row0(p.q, q) + (int64_t)l32 * p.q.sl_b : nullptr;
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int e = h * HALF + ks * 8;
+      bq[sub][ks] = (valid && (FULLD || e < p.q.dim)) ? *(const u32x4*)(rowp + (int64_t)e * 2)
+                                                      : (u32x4){0u, 0u, 0u, 0u};
+      if (f_norm_q) ss += chunk_sumsq<EK>(bq[sub][ks]);
+    }
+    ss += __shfl_xor(ss, 32);
+    qsc[sub] = valid ? (f_norm_q ? inv_norm(ss) : 1.f) : 0.f;
+    // complete the fragment loads here: a load still pending in the
+    // compiler's view at the loop would put a full vmcnt(0) wait (all the
+    // gathers in flight) in front of every tile's MFMAs
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(bq[sub][ks]));
+  }
+
+  // ---- this wave's docs [j0, j1): tokens [T0, T1) of the packed corpus ----
+  const int64_t j0 = r * p.R;
+  const int64_t j1 = j0 + p.R < p.pl.n ? j0 + p.R : p.pl.n;
+  const int nd = (int)(j1 - j0);
+  for (int k = lane; k <= nd; k += 64) s_cu[wl][k] = p.pl.cu[j0 + k];
+  __builtin_amdgcn_wave_barrier();
+  // tokens are counted from T0 (the range spans < 2^31 tokens)
+  const int T0 = __builtin_amdgcn_readfirstlane(s_cu[wl][0]);
+  const int span = __builtin_amdgcn_readfirstlane(s_cu[wl][nd]) - T0;
+  const int ntile = (span + 31) >> 5;
+
+  // raw buffer descriptor words (stride 0, untyped 32-bit format)
+  auto rsrc_words = [](const void* base, uint32_t nbytes) -> u32x4 {
+    const uint64_t b = (uint64_t)base;
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu),
+                 (uint32_t)__builtin_amdgcn_readfirstlane(nbytes), 0x00020000u};
+  };
+  // the queries' tables (a query past the batch reads zeros: record count 0);
+  // rows past the tile's end get offset kInvRow, beyond every table
+  u32x4 dqc[QN];
+#pragma unroll
+  for (int sub = 0; sub < QN; ++sub) {
+    const int64_t q = g * QN + sub;
+    dqc[sub] = rsrc_words(qc + (q < p.q.n ? q : 0) * qc_qs, q < p.q.n ? (uint32_t)(p.pl.ncent * 64) : 0u);
+  }
+  // LDS addresses of the two stages and of code slot 0 (loop constants)
+  uint32_t st_lds[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    st_lds[k] = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_st[wl][k][0]));
+  const uint32_t cs_lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t*)(&s_codes[wl][0][0]));
+  auto dma = [&](uint32_t lds, uint32_t voff, const u32x4& desc) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(desc)
+        : "memory");
+  };
+  auto dma_nt = [&](uint32_t lds, uint32_t voff, const u32x4& desc) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(desc)
+        : "memory");
+  };
+  // Table rows land at row positions P(R) = R ^ ((R >> 2) & 1): the rows
+  // R and R + 4 that one fragment read touches (lanes of the two halves)
+  // then sit in different banks. Instruction i fills positions 16 i + lane / 4.
+  auto rowpos = [](int row) { return row ^ ((row >> 2) & 1); };
+  // Tiles are 32 consecutive tokens of the range, tile i at T0 + 32 i, in
+  // whichever docs they fall; a tile past the range loads nothing (record
+  // count 0). The streams' base addresses advance by one tile per iteration
+  // (64-bit scalar adds; no multiplies in the loop).
+  auto rows_of = [&](int i) {  // rows of tile i that exist
+    const int rem = span - 32 * i;
+    return rem < 0 ? 0 : (rem < 32 ? rem : 32);
+  };
+  const char* code_p = (const char*)(p.pl.codes + T0);  // tile 0
+  const char* res_p = (const char*)p.pl.res + (int64_t)T0 * p.pl.res_st;
+  const char* inv_p = (const char*)(tinv ? tinv + T0 : nullptr);
+  const int64_t res_tile = 32 * p.pl.res_st;
+  // codes of tile i (at code_p) into code slot `slot` (lanes 0..7, 16 bytes each)
+  auto code_dma = [&](int i, int slot, const char* cp) {
+    const u32x4 dc = rsrc_words(cp, (uint32_t)rows_of(i) * 4u);
+    if (lane < 8) dma_nt(cs_lds0 + (uint32_t)(slot * 128), (uint32_t)(lane * 16), dc);
+  };
+  // gather tile i (code of row l32 in code slot `slot`) into stage `stage`,
+  // once the stage's previous contents have been read (lgkmcnt(0)); exactly
+  // G load instructions whether or not the tile exists
+  auto gather = [&](int i, int slot, int stage, const char* rp, const char* ip) {
+    const int nv = rows_of(i);
+    const uint32_t cd = (uint32_t)s_codes[wl][slot][l32];
+    const uint32_t rowoff = l32 < nv ? (cd < (uint32_t)p.pl.ncent ? cd : 0u) * 64u : kInvRow;
+    uint32_t voff[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int row = rowpos(k * 16 + lane / 4);  // P is its own inverse
+      voff[k] = (uint32_t)__builtin_amdgcn_ds_bpermute(row * 4, (int)rowoff) + (uint32_t)((lane & 3) * 16);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) dma(st_lds[stage] + (uint32_t)(sub * QCT + k * 1024), voff[k], dqc[sub]);
+    const u32x4 dres = rsrc_words(rp, (uint32_t)nv * (uint32_t)p.pl.res_st);
+#pragma unroll
+    for (int k = 0; k < NRI; ++k) dma_nt(st_lds[stage] + (uint32_t)(RES0 + k * 1024), (uint32_t)(k * 1024 + lane * 16), dres);
+    const u32x4 dinv = rsrc_words(ip ? (const void*)ip : (const void*)p.pl.res, ip ? (uint32_t)nv * 4u : 0u);
+    if (lane < 8) dma_nt(st_lds[stage] + (uint32_t)INV0, (uint32_t)(lane * 16), dinv);
+  };
+
+  float m[QN];
+  int rot0[QN];  // first 4-column chunk of each query's flush order (loop-invariant)
+#pragma unroll
+  for (int sub = 0; sub < QN; ++sub) {
+    m[sub] = NEG_INF;
+    rot0[sub] = (p.LU & 3) == 0 ? (int)((g * QN + sub) % (p.LU >> 2)) : 0;
+  }
+
+  struct Regs {
+    uint32_t rw[RVL];
+    f32x4 inv[4];
+    f16x2 qv[QN][8];  // table values of the lane's 16 rows, two per register
+  };
+  // lane-constant LDS offsets within a stage: residual bytes of row l32's
+  // half h; table row positions P(row) = 8a + 4h + (b ^ h) for row
+  // 8a + 4h + b, i.e. + h for even b and - h for odd b
+  const int res_lane = RES0 + l32 * (int)p.pl.res_st + h * RBL;
+  const int qv_even = (4 * h + h) * 64 + l32 * 2, qv_odd = (4 * h - h) * 64 + l32 * 2;
+  auto read_stage = [&](Regs& rg, int stage, auto NORMD) {
+    const char* st = &s_st[wl][stage][0];
+    const char* rp = st + res_lane;
+    if constexpr (RVL % 4 == 0) {
+#pragma unroll
+      for (int v = 0; v < RVL / 4; ++v) {
+        const u32x4 t = *(const u32x4*)(rp + 16 * v);
+        rg.rw[4 * v] = t[0]; rg.rw[4 * v + 1] = t[1]; rg.rw[4 * v + 2] = t[2]; rg.rw[4 * v + 3] = t[3];
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < RVL / 2; ++v) {
+        const uint2 t = *(const uint2*)(rp + 8 * v);
+        rg.rw[2 * v] = t.x; rg.rw[2 * v + 1] = t.y;
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+      rg.inv[jj] = decltype(NORMD)::value ? *(const f32x4*)(st + INV0 + (8 * jj + 4 * h) * 4) : (f32x4){1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int rel = (8 * (i >> 2) + (i & 3)) * 64 + sub * QCT;  // compile-time
+        rg.qv[sub][i >> 1][i & 1] = *(const _Float16*)(st + ((i & 1) ? qv_odd : qv_even) + rel);
+      }
+  };
+  // a * b + (fp16 half of w) in one instruction (the half converted exactly)
+  auto fma_mix = [](float a, float b, f16x2 w, auto HI) -> float {
+    float r;
+    const uint32_t wb = __builtin_bit_cast(uint32_t, w);
+    if constexpr (decltype(HI)::value)
+      asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(r) : "v"(a), "v"(b), "v"(wb));
+    else
+      asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,0,1]" : "=v"(r) : "v"(a), "v"(b), "v"(wb));
+    return r;
+  };
+  // The doc whose tokens continue into the current tile (jc, ending at token
+  // ec); its end is known without a table read until it is reached.
+  int jc = 0;
+  int ec = __builtin_amdgcn_readfirstlane(s_cu[wl][1]) - T0;  // relative to T0
+  // park doc jc's maxima (sum over the query's columns in the tile kernel's
+  // order) and move to the next doc
+  auto doc_end = [&]() {
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
+      const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const float v = __builtin_isfinite(mm) ? mm : 0.f;
+      auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
+      // the tile kernel's flush order (query g at place g of its group of 4:
+      // the sum starts at 4-column chunk g % (Lq / 4) and wraps)
+      float sum = 0.f;
+      if ((p.LU & 3) == 0) {
+        const int nv4 = p.LU >> 2;
+        int c = rot0[sub];
+        for (int jj = 0; jj < nv4; ++jj) {
+          sum += col(4 * c);
+          sum += col(4 * c + 1);
+          sum += col(4 * c + 2);
+          sum += col(4 * c + 3);
+          c = (c + 1 == nv4) ? 0 : c + 1;
+        }
+      } else {
+        for (int c = 0; c < p.LU; ++c) sum += col(c);
+      }
+      if (lane == 0) s_out[wl][sub][jc] = sum * p.out_scale;
+      m[sub] = NEG_INF;
+    }
+    ++jc;
+    ec = jc < nd ? __builtin_amdgcn_readfirstlane(s_cu[wl][jc + 1]) - T0 : 0x7fffffff;
+  };
+  auto compute = [&](int i, const Regs& rg) {
+    const int T = 32 * i;  // relative to T0
+    f32x16 acc[QN];
+    const uint32_t* rw = rg.rw;
+    auto byte_at = [&](int byte_i) -> uint32_t { return (rw[byte_i >> 2] >> ((byte_i & 3) * 8)) & 0xffu; };
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 rv;
+      if constexpr (FPB == 4) {
+        const uint2 e0 = *(const uint2*)&s_lut[byte_at(2 * ks) * 2];
+        const uint2 e1 = *(const uint2*)&s_lut[byte_at(2 * ks + 1) * 2];
+        rv = u32x4{e0.x, e0.y, e1.x, e1.y};
+      } else if constexpr (FPB == 2) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) rv[k] = *(const uint32_t*)&s_lut[byte_at(4 * ks + k) * 2];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t b0 = byte_at(8 * ks + 2 * k), b1 = byte_at(8 * ks + 2 * k + 1);
+          rv[k] = (*(const uint32_t*)&s_lut[b0 * 2] & 0xffffu) | (*(const uint32_t*)&s_lut[b1 * 2] << 16);
+        }
+      }
+      u32x4 ra = rv;
+      if constexpr (!FULLD) {
+        if ((h * HALF + ks * 8) >= p.q.dim) ra = (u32x4){0u, 0u, 0u, 0u};  // chunks are whole: dim % 8 == 0
+      }
+#pragma unroll
+      for (int sub = 0; sub < QN; ++sub) acc[sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[sub], &ra, &bq[sub][ks]);
+    }
+    if (ec - T > 32) {
+      // the whole tile belongs to doc jc (the common case)
+#pragma unroll
+      for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float v0 = fma_mix(acc[sub][e], qsc[sub], rg.qv[sub][e >> 1], std::false_type{}) * rg.inv[e >> 2][e & 3];
+          const float v1 = fma_mix(acc[sub][e + 1], qsc[sub], rg.qv[sub][e >> 1], std::true_type{}) *
+                           rg.inv[(e + 1) >> 2][(e + 1) & 3];
+          m[sub] = fmaxf(m[sub], fmaxf(v0, v1));
+        }
+      return;
+    }
+    // doc ends inside the tile: rows [a, b) of each doc in turn (values
+    // recomputed per segment: holding them would cost 16 registers a query)
+    int a = 0;
+    while (true) {
+      const int b = ec - T < 32 ? ec - T : 32;
+      const int la = a - 4 * h, lb = b - 4 * h;  // row r = 8 (e / 4) + 4 h + e % 4
+#pragma unroll
+      for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float v0 = fma_mix(acc[sub][e], qsc[sub], rg.qv[sub][e >> 1], std::false_type{}) * rg.inv[e >> 2][e & 3];
+          const float v1 = fma_mix(acc[sub][e + 1], qsc[sub], rg.qv[sub][e >> 1], std::true_type{}) *
+                           rg.inv[(e + 1) >> 2][(e + 1) & 3];
+          const int r0 = 8 * (e >> 2) + (e & 3);
+          m[sub] = fmaxf(m[sub], fmaxf((r0 >= la && r0 < lb) ? v0 : NEG_INF, (r0 + 1 >= la && r0 + 1 < lb) ? v1 : NEG_INF));
+        }
+      if (ec - T > 32 || jc >= nd) break;  // doc jc continues in the next tile
+      doc_end();
+      a = b;
+    }
+  };
+
+  // Pipeline: at the top of iteration c, tile c's gather (stage c % 2) and
+  // the codes of tile c + 2 (slot (c + 2) % 4) have landed; tile c + 1's
+  // gather and the codes of tile c + 3 may be in flight (G + 1 loads).
+  // Iteration c reads its stage, gathers tile c + 2 into it, loads the codes
+  // of tile c + 4, then scores tile c.
+  code_dma(0, 0, code_p);
+  code_dma(1, 1, code_p + 128);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  gather(0, 0, 0, res_p, inv_p);
+  code_dma(2, 2, code_p + 256);
+  gather(1, 1, 1, res_p + res_tile, inv_p ? inv_p + 128 : nullptr);
+  code_dma(3, 3, code_p + 384);
+  // (two copies of the loop: with and without token inverse norms)
+  auto scan = [&](auto NORMD) {
+    const char* cp = code_p + 512;                 // tile c + 4
+    const char* rp = res_p + 2 * res_tile;         // tile c + 2
+    const char* ip = inv_p + 256;
+    for (int c = 0; c < ntile; ++c) {
+      asm volatile("s_waitcnt vmcnt(%0)" : : "n"(G + 1) : "memory");
+      const int stage = c & 1;
+      Regs rg;
+      read_stage(rg, stage, NORMD);
+      gather(c + 2, (c + 2) & 3, stage, rp, ip);
+      code_dma(c + 4, c & 3, cp);
+      compute(c, rg);
+      cp += 128;
+      rp += res_tile;
+      ip += 128;
+    }
+  };
+  // docs left (empty docs at the range's end, or an empty range)
+  while (jc < nd) doc_end();
+  // no gather may still be writing this wave's LDS when it exits
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // this wave's doc scores (written by lane 0: visible to the whole wave)
+  __builtin_amdgcn_wave_barrier();
+  for (int k = lane; k < nd; k += 64)
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub) {
+      const int64_t q = g * QN + sub;
+      if (q < p.q.n) p.out[q * p.osq + (j0 + k) * p.osd] = s_out[wl][sub][k];
+    }
+}
+
+template <int EK, int DPAD, int NBITS>
+int launch_qc_scan(int qn, const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s) {
+  const int64_t waves = p.ngroups * p.NR;
+  const int64_t nb = (waves + 3) / 4;
+  if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(256), 0, s, p, qc, qc_qs, tinv);
+    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+  };
+  const bool full = p.q.dim == DPAD;
+  if (qn == 2)
+    return full ? go(plaid_qc_kernel<EK, DPAD, NBITS, 2, true>) : go(plaid_qc_kernel<EK, DPAD, NBITS, 2, false>);
+  return full ? go(plaid_qc_kernel<EK, DPAD, NBITS, 1, true>) : go(plaid_qc_kernel<EK, DPAD, NBITS, 1, false>);
+}
+
+template <int EK, int DPAD>
+int launch_qc(int qn, const Params& p, uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s,
+              const lik_launch_opts_t* opts) {
+  const int64_t ntile = (p.pl.ncent + 31) / 32;
+  const int64_t waves = p.q.n * ntile;
+  if ((waves + 3) / 4 > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((centroid_scores_kernel<EK, DPAD>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, qc,
+                     qc_qs, ntile);
+  if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+  const bool timed = opts && opts->timing_start && opts->timing_stop;
+  if (timed && hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
+  int rc;
+  switch (p.pl.nbits) {
+    case 2: rc = launch_qc_scan<EK, DPAD, 2>(qn, p, qc, qc_qs, tinv, s); break;
+    case 4: rc = launch_qc_scan<EK, DPAD, 4>(qn, p, qc, qc_qs, tinv, s); break;
+    case 8: rc = launch_qc_scan<EK, DPAD, 8>(qn, p, qc, qc_qs, tinv, s); break;
+    default: rc = LIK_ERR_UNSUPPORTED;
+  }
+  if (rc == LIK_OK && timed && hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;
+  return rc;
+}
+
+}  // namespace lik
+
+using namespace lik;
+
+namespace {
+constexpr int64_t kQcMaxQueries = 64;  // the table is per query: a few-query path
+
+size_t qc_bytes(int64_t nq, int64_t ncent) { return (size_t)nq * (size_t)ncent * 64; }
+}  // namespace
+
+extern "C" size_t lik_plaid_maxsim_qc_workspace_size(const lik_seqs_t* Q, const lik_plaid_docs_t* docs) {
+  if (!Q || !docs || Q->n < 0 || docs->n_centroids < 0) return 0;
+  return (qc_bytes(Q->n, docs->n_centroids) + 255) & ~(size_t)255;
+}
+
+extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, const float* token_inv,
+                                   uint32_t flags, float* out, int64_t out_stride_q, int64_t out_stride_d,
+                                   void* workspace, size_t workspace_bytes, const lik_launch_opts_t* opts,
+                                   lik_stream_t stream) {
+  if (!Q || !docs || Q->n < 0 || Q->len < 0 || docs->n < 0) return LIK_ERR_INVALID;
+  if (Q->dtype != LIK_BF16 && Q->dtype != LIK_F16) return LIK_ERR_UNSUPPORTED;
+  if (docs->centroid_dtype != Q->dtype) return LIK_ERR_UNSUPPORTED;
+  if (docs->nbits != 2 && docs->nbits != 4 && docs->nbits != 8) return LIK_ERR_INVALID;
+  if (docs->dim != Q->dim || Q->dim <= 0 || Q->dim % 8 != 0 || Q->dim > 128) return LIK_ERR_UNSUPPORTED;
+  if (docs->n_buckets < 1 || docs->n_buckets > 256 || !docs->bucket_weights) return LIK_ERR_INVALID;
+  if (!docs->cu_seqlens && !docs->lengths) return LIK_ERR_INVALID;
+  if (!docs->cu_seqlens) return LIK_ERR_UNSUPPORTED;  // the scan walks the packed token stream
+  if ((flags & LIK_KD_LAYOUT) || Q->mask || Q->token_scale || Q->cu_seqlens) return LIK_ERR_INVALID;
+  if (Q->len > 32 || Q->n > kQcMaxQueries) return LIK_ERR_UNSUPPORTED;
+  const bool norm_d = (flags & (LIK_NORMALIZE | LIK_NORMALIZE_D)) != 0;
+  if (norm_d && !token_inv) return LIK_ERR_INVALID;
+  if (Q->n == 0 || docs->n == 0) return LIK_OK;
+  if (!out || !Q->data || !docs->codes || !docs->residuals || !docs->centroids || docs->n_centroids < 1)
+    return LIK_ERR_INVALID;
+  if (((uintptr_t)Q->data) % 16 || (Q->stride_l * 2) % 16 || (Q->stride_n * 2) % 16) return LIK_ERR_UNSUPPORTED;
+  if (((uintptr_t)docs->centroids) % 16 != 0 || (docs->cent_stride * 2) % 16 != 0) return LIK_ERR_UNSUPPORTED;
+  const int dpad = Q->dim <= 64 ? 64 : 128;
+  const int64_t rsb = (int64_t)dpad * docs->nbits / 8, nri = (32 * rsb + 1023) / 1024;
+  if (((uintptr_t)docs->residuals) % 16 != 0 || docs->res_stride_tok % 16 != 0 || 32 * docs->res_stride_tok > nri * 1024)
+    return LIK_ERR_UNSUPPORTED;
+  if (docs->res_stride_tok * 8 < (int64_t)docs->dim * docs->nbits) return LIK_ERR_INVALID;
+  if (token_inv && ((uintptr_t)token_inv) % 4) return LIK_ERR_UNSUPPORTED;
+  // table rows are gathered with 32-bit byte offsets below kInvRow
+  if (docs->n_centroids * 64 >= (int64_t)kInvRow) return LIK_ERR_UNSUPPORTED;
+  const size_t need = qc_bytes(Q->n, docs->n_centroids);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace) % 16) return LIK_ERR_WORKSPACE;
+
+  Params p{};
+  p.q.data = (const char*)Q->data;
+  p.q.sn_b = Q->stride_n * 2;
+  p.q.sl_b = Q->stride_l * 2;
+  p.q.lengths = Q->lengths;
+  p.q.n = Q->n;
+  p.q.L = Q->len;
+  p.q.dim = Q->dim;
+  p.pl.codes = docs->codes;
+  p.pl.res = docs->residuals;
+  p.pl.cu = docs->cu_seqlens;
+  p.pl.lengths = docs->lengths;
+  p.pl.n = docs->n;
+  p.pl.L = docs->max_len;
+  p.pl.codes_sn = docs->codes_stride_n;
+  p.pl.res_st = docs->res_stride_tok;
+  p.pl.cent = (const char*)docs->centroids;
+  p.pl.cent_sb = docs->cent_stride * 2;
+  p.pl.ncent = docs->n_centroids;
+  p.pl.bw = docs->bucket_weights;
+  p.pl.nb = docs->n_buckets;
+  p.pl.nbits = docs->nbits;
+  p.normalize = (flags & (LIK_NORMALIZE | LIK_NORMALIZE_Q)) ? 1 : 0;
+  p.out_scale = 1.f;
+  p.out = out;
+  p.osq = out_stride_q;
+  p.osd = out_stride_d;
+  p.LU = (int)Q->len;
+  const int qn = Q->n >= 2 ? 2 : 1;
+  p.ngroups = (Q->n + qn - 1) / qn;
+  // ~16k wavefronts over the corpus, at most 512 docs each
+  int64_t R = (docs->n + 16383) / 16384;
+  if (opts && opts->docs_per_wg > 0) R = opts->docs_per_wg;
+  p.R = (int)(R < 1 ? 1 : (R > kQcRMax ? kQcRMax : R));
+  p.NR = (docs->n + p.R - 1) / p.R;
+  uint16_t* qc = (uint16_t*)workspace;
+  const int64_t qc_qs = docs->n_centroids * 32;
+  const float* tinv = norm_d ? token_inv : nullptr;
+  hipStream_t s = (hipStream_t)stream;
+  if (Q->dtype == LIK_BF16)
+    return dpad == 64 ? launch_qc<EK_BF16, 64>(qn, p, qc, qc_qs, tinv, s, opts)
+                      : launch_qc<EK_BF16, 128>(qn, p, qc, qc_qs, tinv, s, opts);
+  return dpad == 64 ? launch_qc<EK_F16, 64>(qn, p, qc, qc_qs, tinv, s, opts)
+                    : launch_qc<EK_F16, 128>(qn, p, qc, qc_qs, tinv, s, opts);
+}

@@ -14,6 +14,8 @@ lik_plaid_token_norms + lik_plaid_maxsim_qc).
   to the lower index), scores equal the row at those indices.
 * Calls the scan cannot take (Lq > 32, residual rows not a multiple of
   16 bytes) go to maxsim_residual_varlen and give its result exactly.
+* Docs split inside the scan's 32-token tiles (short and empty docs, 1 to
+  128 docs per wavefront): the same bits for every split.
 """
 
 import sys
@@ -130,3 +132,45 @@ def test_fallbacks_equal_varlen_route():
     idx = ResidualIndex(*args)
     Q = torch.randn(2, 40, 128).to(torch.bfloat16).cuda()  # Lq > 32
     assert torch.equal(idx.score(Q), maxsim_residual_varlen(Q, *args))
+
+
+@pytest.mark.parametrize("nq", [1, 3])
+def test_docs_split_inside_tiles(nq):
+    """The scan walks each wavefront's docs as one token stream in 32-token
+    tiles, so a tile can hold the end of one doc, whole short docs and the
+    start of the next. Many short docs (0..40 tokens, runs of empty docs, a
+    leading and a trailing empty doc) scored with 1, 3, 37 and 128 docs per
+    wavefront: a doc's score is a max per column (exact in any order) summed
+    in a fixed order, so every split gives the same bits; and the scores match
+    the exact decode route within the split form's 5e-3."""
+    from late_interaction_kernels.plaid import ResidualIndex, maxsim_residual_varlen
+
+    _case(f"qc short docs nq={nq}")
+    g = torch.Generator().manual_seed(11 + nq)
+    Nd, d, nbits, ncent = 700, 128, 2, 500
+    lens = torch.randint(0, 41, (Nd,), generator=g)
+    lens[:3] = 0
+    lens[100:140] = 0
+    lens[-2:] = 0
+    lens[200:260] = torch.randint(1, 4, (60,), generator=g)
+    cu = torch.zeros(Nd + 1, dtype=torch.int32)
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    T = int(cu[-1])
+    cent = torch.nn.functional.normalize(torch.randn(ncent, d, generator=g), dim=-1).to(torch.bfloat16)
+    codes = torch.randint(0, ncent, (T,), generator=g, dtype=torch.int32)
+    res = torch.randint(0, 256, (T, 32), generator=g, dtype=torch.uint8)
+    bw = torch.linspace(-0.1, 0.1, 4)
+    args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), nbits)
+    idx = ResidualIndex(*args)
+    Q = torch.randn(nq, 32, d, generator=g).to(torch.bfloat16).cuda()
+    for normalize in (True, False):
+        base = idx.score(Q, normalize=normalize)
+        for r in (3, 37, 128):
+            with launch_options(docs_per_wg=r):
+                got = idx.score(Q, normalize=normalize)
+            assert torch.equal(got, base), (r, normalize)
+        with launch_options(plaid_variant=2):
+            exact = maxsim_residual_varlen(Q, *args, normalize=normalize)
+        assert rel_err(base.cpu().numpy(), exact.cpu().numpy()) < 5e-3, normalize
+        empty = (lens == 0).nonzero().flatten().cuda()
+        assert base[:, empty].abs().max().item() == 0.0

@@ -271,9 +271,10 @@ int lik_plaid_token_norms(const lik_plaid_docs_t* docs, int64_t tok_begin, int64
  * on bucket weights rounded to the query type, both divided by the token's
  * precomputed norm). token_inv (from lik_plaid_token_norms) is required when
  * flags normalise the docs (LIK_NORMALIZE / LIK_NORMALIZE_D) and ignored
- * otherwise. The workspace holds the [Q->n, n_centroids, 32] fp16 table
- * (lik_plaid_maxsim_qc_workspace_size bytes). opts: docs_per_wg and the
- * timing events (around the scan kernel) are honoured.
+ * otherwise. Docs must be packed (docs->cu_seqlens; a lengths-only layout
+ * returns LIK_ERR_UNSUPPORTED). The workspace holds the [Q->n, n_centroids,
+ * 32] fp16 table (lik_plaid_maxsim_qc_workspace_size bytes). opts:
+ * docs_per_wg and the timing events (around the scan kernel) are honoured.
  */
 size_t lik_plaid_maxsim_qc_workspace_size(const lik_seqs_t* Q, const lik_plaid_docs_t* docs);
 int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, const float* token_inv, uint32_t flags,

@@ -17,8 +17,12 @@
 // MFMA (residual fields -> bucket weights rounded to the MFMA type, one
 // 32x32 tile product per 32 tokens, as in the split-form gather kernel).
 //
-// Per wavefront: one (query group, doc range), docs tiled 32 tokens at a
-// time. Everything a tile needs arrives in LDS by buffer_load ... lds (M0
+// Per wavefront: one (query group, doc range). The range's tokens are one
+// contiguous slice of the packed corpus (cu_seqlens layout), walked in flat
+// 32-token tiles that ignore doc boundaries, so stream addresses simply
+// advance by a tile per iteration; the doc whose tokens continue into the
+// tile is tracked by its end token, and a tile holding a doc end is reduced
+// segment by segment. Everything a tile needs arrives in LDS by buffer_load ... lds (M0
 // saved and restored): the table rows of its tokens (gathered by code, row R
 // at position R ^ ((R / 4) % 2) so the two rows one fragment read touches
 // sit in different banks), its residual bytes and inverse norms (streaming,
@@ -28,13 +32,13 @@
 // as tile c has been read into registers. All of these are loads, which
 // return in issue order, so one fixed vmcnt per iteration waits for exactly
 // the tile about to be scored. Nothing else in the loop touches vector
-// memory: the doc table is staged in LDS and doc scores are collected in LDS
-// and written after the loop (a compiler-visible vector memory access in the
-// loop would bring a full vmcnt(0) with it). The tile is scored as
+// memory: the doc boundaries are staged in LDS and doc scores are collected
+// in LDS and written after the loop (a compiler-visible vector memory access
+// in the loop would bring a full vmcnt(0) with it). The tile is scored as
 //     v[t][s] = (acc[t][s] * qsc[s] + qc[code_t][s]) * inv_t
-// (acc = the q . r MFMA, the fp16 table value added by v_fma_mix), rows past
-// the tile's end -inf, a running max per column, and at a doc's end the
-// column maxima are summed in the tile kernel's order.
+// (acc = the q . r MFMA, the fp16 table value added by v_fma_mix), a running
+// max per column over each doc's rows, and at a doc's end the column maxima
+// are summed in the tile kernel's order.
 //
 // Reference semantics: plaid.py:684-963 / reference.py:142-179 (decode,
 // normalise, MaxSim); out-of-range codes decode as centroid 0, out-of-range

@@ -6,6 +6,7 @@
 
 namespace lik {
 int launch_dense_bf16_generic(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
+int launch_dense_bf16_wide(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 
 int launch_dense_bf16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s) {
   if (pl.dpad == 128) {
@@ -22,6 +23,7 @@ int launch_dense_bf16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s
       default: break;
     }
   }
+  if (pl.dpad == 64 || pl.dpad == 512) return launch_dense_bf16_wide(pl, p, nb, s);
   return launch_dense_bf16_generic(pl, p, nb, s);
 }
 }  // namespace lik

@@ -139,3 +139,25 @@ def test_wide_rows_kd_and_varlen():
             if dl[k] and ql[i]:
                 ref[i, k] = O.maxsim(_np(Qp[cq[i] : cq[i + 1]]), _np(Dp[cd[k] : cd[k + 1]]))
     assert rel_err(_np(got), ref) < 1e-2
+
+
+@pytest.mark.parametrize("d", [48, 64, 300, 512])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_bf16_narrow_and_wide_rows(d, normalize):
+    """bf16 at d <= 64 and 256 < d <= 512 runs kernels with only the call's
+    features compiled in (none; query-only or full normalise): one query
+    (a corpus scan) and six, prefix doc masks (the extent path) and an
+    empty doc, against the oracle."""
+    from late_interaction_kernels import maxsim
+
+    _case(f"bf16 d={d} normalize={normalize}")
+    g = torch.Generator().manual_seed(d + int(normalize))
+    D = torch.randn(40, 70, d, generator=g).to(torch.bfloat16)
+    dm = torch.arange(70)[None] < torch.randint(1, 71, (40,), generator=g)[:, None]
+    dm[7] = False
+    for nq in (1, 6):
+        Q = torch.randn(nq, 32, d, generator=g).to(torch.bfloat16)
+        got = maxsim(Q.cuda(), D.cuda(), d_mask=dm.cuda(), normalize=normalize)
+        ref = O.maxsim(_np(Q), _np(D), None, dm.numpy(), normalize=normalize)
+        assert rel_err(_np(got).reshape(ref.shape), ref) < 1e-2, nq
+        assert _np(got).reshape(ref.shape)[:, 7].max() == 0.0

@@ -586,7 +586,7 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   p.LU = (int)Q->len;
   const int qn = Q->n >= 2 ? 2 : 1;
   p.ngroups = (Q->n + qn - 1) / qn;
-  // ~16k wavefronts over the corpus, at most 512 docs each
+  // ~16k wavefronts over the corpus, at most kQcRMax docs each
   int64_t R = (docs->n + 16383) / 16384;
   if (opts && opts->docs_per_wg > 0) R = opts->docs_per_wg;
   p.R = (int)(R < 1 ? 1 : (R > kQcRMax ? kQcRMax : R));

@@ -327,6 +327,7 @@ int launch_dense(int dt, const Plan& pl, const Params& p, int64_t nb, hipStream_
       default: return LIK_ERR_UNSUPPORTED;
     }
   }
+  if (q1_eligible(dt, pl, p)) return launch_q1(dt, pl, p, s);
   switch (dt) {
     case LIK_BF16: return launch_dense_bf16(pl, p, nb, s);
     case LIK_F16: return launch_dense_f16(pl, p, nb, s);

@@ -118,6 +118,10 @@ int launch_dense_f16(const Plan& pl, const Params& p, int64_t nb, hipStream_t s)
 int launch_dense_f32(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 int launch_dense_fp8(const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
 int launch_plaid_bf16(int cd, const Plan& pl, const Params& p, int64_t nb, hipStream_t s);
+// One-column-block plans (lik_q1.hip): the streaming kernel when the call
+// qualifies (q1_eligible), else the tile kernel.
+bool q1_eligible(int dt, const Plan& pl, const Params& p);
+int launch_q1(int dt, const Plan& pl, const Params& p, hipStream_t s);
 // Few-query PLAID scoring, one wavefront per (query group, doc range): lik_plaid_stream.hip.
 int launch_plaid_stream(int ek, int cd, int dpad, int nsub, const Params& p, hipStream_t s);
 // rows wider than the tile kernel takes (lik_wide.hip): one wave per (query, doc)

@@ -1,0 +1,305 @@
+// MaxSim for launches with one 32-column block per group (W = 1, NSUB = 1
+// plans: the KD layout, where every query scores its own K docs, and calls
+// with one short query): a streaming kernel, one independent wavefront per
+// (group, doc range), four per workgroup, no barriers.
+//
+// With a single column block a doc tile is used by one wavefront only, and
+// the work is HBM-bound: what matters is that the loads are coalesced and
+// that enough of them are in flight. Each wavefront keeps two 8 KB tiles in
+// flight in an LDS ring of its own, loaded by buffer_load ... lds (M0 saved
+// and restored): instruction i of a tile covers rows 4i .. 4i+3, lane L the
+// 16-byte chunk j = (L % 16 - 4 (L / 16) - i) mod 16 of row 4i + L / 16, so
+// an instruction reads 1 KB of consecutive rows (8 cache lines; a lane per
+// half row would touch 32) and lands it at LDS offset 1024 i + 16 L. The
+// rotation by 4 (row % 4) + row / 4 makes the A-fragment reads (lane (r, h)
+// reads chunk 8 h + ks of row r) conflict-free. A tile's fragments go to
+// registers first, then the next DMA reuses its slot, so two tiles stay in
+// flight during the MFMAs. Everything in the loop that touches vector
+// memory is a DMA load (8 per tile), so one fixed vmcnt per tile waits for
+// exactly the tile being scored; doc scores are kept in LDS and written
+// after the loop. Rows past a doc's end are outside the buffer range (read
+// as 0) and masked to -inf before the running max; dims past d read as 0.
+//
+// Scores are bitwise those of the tile kernel: the same MFMA sequence per
+// tile (k-steps in order from a zero accumulator), the max over rows is
+// exact, and a doc's column maxima are summed in the tile kernel's flush
+// order (4-column chunks from chunk t % (LU / 4) on for unit t of the group,
+// or columns in order when LU % 4 != 0).
+//
+// Reference semantics: autograd.py:356-461 / reference.py:26-98 (MaxSim with
+// prefix masks and the KD layout), varlen.py:452-493 (packed docs).
+#include "lik_kernel.h"
+
+namespace lik {
+
+constexpr int kQ1RMax = 128;  // docs per wavefront (the host routes larger R to the tile kernel)
+constexpr int kQ1Scores = 256;  // doc scores per wavefront held until the loop ends (docs x units)
+
+// two workgroups per CU (their LDS rings take 2 x 64 KB): two waves per SIMD
+template <int EK, int DPAD, bool FULLD, bool NORMQ>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) maxsim_q1_kernel(const Params p) {
+  using T = KT<EK, DPAD>;
+  constexpr int KS = T::KSTEPS;
+  static_assert(T::FRAG_V == 1 && !T::SPLIT && T::IN_B == 2 && DPAD == 128, "16-bit rows of 256 bytes");
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  __shared__ int32_t s_len[4][kQ1RMax];   // doc length (0: empty or not in this launch)
+  __shared__ int64_t s_off[4][kQ1RMax];   // byte offset of the doc's token 0
+  // doc scores, written to memory after the loop: a store in the loop would
+  // make the compiler's load counting wait for tiles still in flight
+  __shared__ float s_score[4][kQ1Scores];
+  // per-wave ring of two 8 KB tiles (chunks rotated as described above)
+  __shared__ __attribute__((aligned(1024))) char s_ring[4][2][8192];
+
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wl = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t item = (int64_t)blockIdx.x * 4 + wl;
+  const int64_t g = item / p.NR, r = item - g * p.NR;
+  if (g >= p.ngroups) return;  // wave-uniform; the kernel has no barrier
+
+  const int64_t jl0 = r * (int64_t)p.R;
+  const int64_t jl1 = (jl0 + p.R < p.ndocs_pg) ? jl0 + p.R : p.ndocs_pg;
+  const int nloc = (int)(jl1 - jl0);
+  const int64_t kd_base = p.kd_K ? (g / p.nc) * p.kd_K : 0;  // KD: one query per group
+
+  // ---- this group's query tokens as the B fragments of column l32 ----
+  u32x4 bq[KS];
+  float qsc = 1.f;
+  {
+    const int col = l32;
+    const int ul = col / p.LU;
+    const int s = col - ul * p.LU;
+    const int64_t u = g * p.QPG + ul;
+    bool valid = ul < p.QPG && u < p.nunits;
+    const int64_t q = u / p.nc;
+    const int64_t tok = (u - q * p.nc) * (int64_t)p.LU + s;
+    const char* rowp = nullptr;
+    if (valid) {
+      valid = tok < seq_len(p.q, q);
+      if (valid && p.q.mask) valid = p.q.mask[q * p.q.msn + tok * p.q.msl] != 0;
+      rowp = seq_row0(p.q, q) + tok * p.q.sl_b;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int e = h * (DPAD / 2) + ks * T::FE;
+      bq[ks] = (valid && (FULLD || e < p.q.dim)) ? *(const u32x4*)(rowp + (int64_t)e * T::IN_B)
+                                                 : (u32x4){0u, 0u, 0u, 0u};
+      if constexpr (NORMQ) ss += chunk_sumsq<EK>(bq[ks]);
+    }
+    if constexpr (NORMQ) {
+      ss += __shfl_xor(ss, 32);
+      qsc = valid ? inv_norm(ss) : 0.f;
+    }
+    // complete these loads here: pending in the compiler's view at the loop,
+    // they would put a full vmcnt(0) in front of the first tile
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(bq[ks]));
+  }
+
+  // ---- doc table of this wavefront's range (empty docs score 0 here) ----
+  for (int k = lane; k < nloc; k += 64) {
+    const int64_t dg = kd_base + jl0 + k;
+    const int64_t L = doc_len<SRC_DENSE>(p, dg);
+    const bool skip = p.doc_filter == 1 && p.holes != nullptr && p.holes[dg] != 0;
+    s_len[wl][k] = skip ? 0 : (int32_t)L;
+    s_off[wl][k] = p.d.cu ? (int64_t)p.d.cu[dg] * p.d.sl_b : dg * p.d.sn_b;
+    if (L == 0 && !skip) {
+      for (int t = 0; t < p.QPG; ++t) {
+        const int64_t u = g * p.QPG + t;
+        if (u < p.nunits) p.out[u * p.osq + (jl0 + k) * p.osd] = 0.f;
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  const float osc = p.out_scale;
+
+  // DMA lane offsets of instruction i (row 4i + L/16, rotated chunk; dims
+  // past d out of range) and A-fragment LDS offsets of k-step ks
+  const uint32_t sl = (uint32_t)p.d.sl_b;
+  uint32_t doff[8], aoff[KS];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int a = lane >> 4, j = ((lane & 15) - 4 * a - i) & 15;
+    doff[i] = (FULLD || j * 8 < p.d.dim) ? (uint32_t)(4 * i + a) * sl + (uint32_t)(j * 16) : kOOB;
+  }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int i = l32 >> 2, a = l32 & 3, j = 8 * h + ks;
+    aoff[ks] = (uint32_t)(i * 1024 + a * 256 + ((j + 4 * a + i) & 15) * 16);
+  }
+  const uint32_t ring_lds = (uint32_t)__builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_ring[wl][0][0]));
+
+  // ---- tile cursor: tile t of local doc k (k == nloc: past the range) ----
+  struct Cur {
+    int k, t, len;
+    int64_t off;
+  };
+  auto cur_doc = [&](Cur& c, int k) {
+    while (k < nloc && s_len[wl][k] == 0) ++k;
+    c.k = k;
+    c.t = 0;
+    c.len = k < nloc ? __builtin_amdgcn_readfirstlane(s_len[wl][k]) : 0;
+    const int64_t o = k < nloc ? s_off[wl][k] : 0;
+    c.off = (int64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)o) |
+            ((int64_t)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)o >> 32)) << 32);
+  };
+  struct Desc {
+    int nv, k;
+    bool docend;
+  };
+  // DMA of the cursor's tile into ring slot S (exactly 8 load instructions,
+  // whether or not the tile exists), then advance the cursor
+  auto fetch = [&](auto SS, Cur& c) -> Desc {
+    constexpr int S = decltype(SS)::value;
+    Desc d;
+    const int rem = c.len - 32 * c.t;
+    d.nv = rem < 32 ? rem : 32;
+    d.k = c.k;
+    d.docend = c.len > 0 && rem <= 32;
+    // the buffer covers rows [32 t, len) of the doc: later rows read 0
+    const uint64_t base = (uint64_t)(p.d.data + c.off) + (uint64_t)((uint32_t)c.t * 32u * sl);
+    const uint32_t span = d.nv > 0 ? (uint32_t)(d.nv - 1) * sl + (uint32_t)(p.d.dim * T::IN_B) : 0u;
+    const u32x4 desc = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
+                        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu),
+                        (uint32_t)__builtin_amdgcn_readfirstlane(span), 0x00020000u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %1\n\t"
+          "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "s"(ring_lds + (uint32_t)(S * 8192 + i * 1024)), "v"(doff[i]), "s"(desc)
+          : "memory");
+    }
+    if (d.docend)
+      cur_doc(c, c.k + 1);
+    else
+      c.t += 1;
+    return d;
+  };
+
+  float m = NEG_INF;
+  // a doc ends: column maxima (max over lanes l, l ^ 32) summed per unit in
+  // the tile kernel's flush order, written by lane 0
+  auto doc_end = [&](int k) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    const float v = __builtin_isfinite(mm) ? (NORMQ ? mm * qsc : mm) : 0.f;
+    auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
+    for (int t = 0; t < p.QPG; ++t) {
+      const int64_t u = g * p.QPG + t;
+      if (u >= p.nunits) break;
+      float sum = 0.f;
+      if ((p.LU & 3) == 0) {
+        const int nv4 = p.LU >> 2;
+        int c = t % nv4;
+        for (int j = 0; j < nv4; ++j) {
+          const int c0 = t * p.LU + 4 * c;
+          sum += col(c0);
+          sum += col(c0 + 1);
+          sum += col(c0 + 2);
+          sum += col(c0 + 3);
+          c = (c + 1 == nv4) ? 0 : c + 1;
+        }
+      } else {
+        for (int j = 0; j < p.LU; ++j) sum += col(t * p.LU + j);
+      }
+      if (lane == 0) s_score[wl][k * p.QPG + t] = sum * osc;
+    }
+    m = NEG_INF;
+  };
+  // tile in slot S: wait for it, read its A fragments, hand the slot to
+  // the next fetch (tile + 2), then score
+  auto step = [&](auto SS, const Desc& d, Cur& c) -> Desc {
+    constexpr int S = decltype(SS)::value;
+    // the tile after this one (8 loads) may still be in flight
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    u32x4 af[KS];
+    const char* slot = (const char*)&s_ring[wl][S][0];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) af[ks] = *(const u32x4*)(slot + aoff[ks]);
+    // the fragments are in registers before the DMA overwrites the slot
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const Desc dn = fetch(SS, c);
+    f32x16 acc;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &af[ks], &bq[ks]);
+    // element e is row 8 (e / 4) + 4 h + e % 4
+    if (d.nv < 32) {
+      const int lim = d.nv - 4 * h;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (8 * (e >> 2) + (e & 3) >= lim) acc[e] = NEG_INF;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) m = fmaxf(m, acc[e]);
+    if (d.docend) doc_end(d.k);
+    return dn;
+  };
+
+  Cur cur;
+  cur_doc(cur, 0);
+  if (cur.k >= nloc) return;  // (empty docs were written above)
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  // tiles i (slot i % 2) and i + 1 in flight; a tile past the range (nv 0,
+  // no doc end) loads nothing and ends the loop
+  // (the prologue's stores and query loads complete before the fixed counts start)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  Desc d0 = fetch(I0{}, cur);
+  Desc d1 = fetch(I1{}, cur);
+  for (;;) {
+    const Desc d2 = step(I0{}, d0, cur);
+    if (d1.nv <= 0) break;
+    d0 = step(I1{}, d1, cur);
+    if (d2.nv <= 0) break;
+    d1 = d0;
+    d0 = d2;
+  }
+  // no DMA may still be writing this wave's LDS (tiles past the range load nothing)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+  for (int i = lane; i < nloc * p.QPG; i += 64) {
+    const int k = i / p.QPG, t = i - k * p.QPG;
+    const int64_t u = g * p.QPG + t;
+    if (u < p.nunits && s_len[wl][k] > 0) p.out[u * p.osq + (jl0 + k) * p.osd] = s_score[wl][i];
+  }
+}
+
+template <int EK, int DPAD>
+int launch_q1_t(const Params& p, bool normq, hipStream_t s) {
+  const int64_t waves = p.ngroups * p.NR;
+  const int64_t nb = (waves + 3) / 4;
+  if (nb <= 0) return LIK_OK;
+  if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  const bool full = p.d.dim == DPAD && p.q.dim == DPAD;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(256), 0, s, p);
+    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+  };
+  if (full)
+    return normq ? go(maxsim_q1_kernel<EK, DPAD, true, true>) : go(maxsim_q1_kernel<EK, DPAD, true, false>);
+  return normq ? go(maxsim_q1_kernel<EK, DPAD, false, true>) : go(maxsim_q1_kernel<EK, DPAD, false, false>);
+}
+
+// Routed here: 16-bit dense scoring with a one-block plan and nothing in the
+// tile loop beyond the plain max (no doc mask holes, token scales, doc
+// normalisation or argmax), at most kQ1RMax docs per wavefront.
+bool q1_eligible(int dt, const Plan& pl, const Params& p) {
+  return (dt == LIK_BF16 || dt == LIK_F16) && pl.W == 1 && pl.NSUB == 1 && pl.dpad == 128 &&
+         ((uintptr_t)p.d.data) % 16 == 0 && p.d.sl_b % 16 == 0 && (p.d.cu || p.d.sn_b % 16 == 0) &&
+         !p.amax && !p.pair_q && !p.pair_d && !p.d.mask && !p.d.ts && !p.q.ts && !(p.normalize & 2) &&
+         !p.scale_q && !p.scale_d && p.doc_filter != 2 && !p.accumulate && p.R <= kQ1RMax &&
+         (int64_t)p.R * pl.QPG <= kQ1Scores;
+}
+
+int launch_q1(int dt, const Plan& pl, const Params& p, hipStream_t s) {
+  const bool normq = (p.normalize & 1) != 0;
+  return dt == LIK_BF16 ? launch_q1_t<EK_BF16, 128>(p, normq, s) : launch_q1_t<EK_F16, 128>(p, normq, s);
+}
+
+}  // namespace lik

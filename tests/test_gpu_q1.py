@@ -1,0 +1,150 @@
+"""One-column-block launches (the KD layout, one short query, packed docs for
+one query) run the streaming kernel of lik_q1.hip: doc tiles loaded by
+coalesced, non-temporal buffer_load ... lds into a per-wavefront LDS ring,
+no workgroup barriers.
+
+* The same bits as the tile kernel (forced with cfg=(1, 2), a two-block
+  plan the streaming kernel does not take): same MFMA sequence per tile,
+  exact maxima, the tile kernel's column-sum order (also for two queries
+  sharing the block, Lq = 16).
+* Against the float64 oracle (lik_oracle.maxsim / maxsim_kd / maxsim_varlen,
+  reference.py:26-98) on the same 16-bit values within 1e-4.
+* Doc lengths around the tile edges (0, 1, 31, 32, 33, 63, 64, 65, Ld),
+  masks with holes (their docs go to the masked tile kernel in the same
+  call), query-only normalisation, d = 96 (dims past d), and d = 100 (rows
+  not a multiple of 16 bytes: the tile kernel) against the oracle.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import lik_oracle as O
+from conftest import rel_err
+from late_interaction_kernels._lib import launch_options
+
+pytestmark = pytest.mark.gpu
+
+EDGE = [0, 1, 31, 32, 33, 63, 64, 65]
+
+
+def _case(tag):
+    print(f"[case] {tag}", flush=True)
+    sys.stdout.flush()
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _normed(shape, g, dtype):
+    return torch.nn.functional.normalize(torch.randn(*shape, generator=g), dim=-1).to(dtype)
+
+
+def _tile(fn):
+    with launch_options(cfg=(1, 2)):
+        return fn()
+
+
+def _lens(shape, ld, g):
+    lens = torch.randint(0, ld + 1, shape, generator=g)
+    flat = lens.view(-1)
+    flat[: len(EDGE)] = torch.tensor(EDGE)
+    flat[len(EDGE)] = ld
+    return lens
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("normalize", [False, 1])
+def test_kd_prefix_masks(dtype, normalize):
+    from late_interaction_kernels import maxsim
+
+    _case(f"q1 kd {dtype} normalize={normalize}")
+    g = torch.Generator().manual_seed(3)
+    Nq, K, Ld, d = 6, 40, 130, 128
+    Q = torch.randn(Nq, 32, d, generator=g).to(dtype)
+    D = _normed((Nq, K, Ld, d), g, dtype)
+    dm = torch.arange(Ld)[None, None] < _lens((Nq, K), Ld, g)[..., None]
+    Qc, Dc, dmc = Q.cuda(), D.cuda(), dm.cuda()
+    got = maxsim(Qc, Dc, None, dmc, normalize=normalize)
+    assert torch.equal(got, _tile(lambda: maxsim(Qc, Dc, None, dmc, normalize=normalize)))
+    Qn = _np(Q)
+    if normalize:
+        Qn = Qn / np.maximum(np.linalg.norm(Qn.astype(np.float64), axis=-1, keepdims=True), 1e-12)
+    ref = O.maxsim_kd(Qn, _np(D), None, dm.numpy())
+    assert rel_err(_np(got), ref) < 1e-4
+    assert got[dmc.sum(-1) == 0].abs().max().item() == 0.0
+
+
+def test_kd_mask_holes_and_query_mask():
+    from late_interaction_kernels import maxsim
+
+    _case("q1 kd holes")
+    g = torch.Generator().manual_seed(5)
+    Nq, K, Ld, d = 4, 30, 100, 128
+    Q = _normed((Nq, 32, d), g, torch.bfloat16)
+    D = _normed((Nq, K, Ld, d), g, torch.bfloat16)
+    dm = torch.arange(Ld)[None, None] < _lens((Nq, K), Ld, g)[..., None]
+    dm[:, ::3] &= torch.rand(Nq, (K + 2) // 3, Ld, generator=g) > 0.3  # holes in every third doc
+    qm = torch.arange(32)[None] < torch.tensor([32, 20, 1, 7])[:, None]
+    args = (Q.cuda(), D.cuda(), qm.cuda(), dm.cuda())
+    got = maxsim(*args)
+    assert torch.equal(got, _tile(lambda: maxsim(*args)))
+    ref = O.maxsim_kd(_np(Q), _np(D), qm.numpy(), dm.numpy())
+    assert rel_err(_np(got), ref) < 1e-4
+
+
+@pytest.mark.parametrize("nq,lq", [(1, 32), (2, 16), (1, 5)])
+def test_short_queries_cross_product(nq, lq):
+    from late_interaction_kernels import maxsim
+
+    _case(f"q1 cross nq={nq} lq={lq}")
+    g = torch.Generator().manual_seed(7 + lq)
+    Nd, Ld, d = 300, 90, 128
+    Q = _normed((nq, lq, d), g, torch.bfloat16)
+    D = _normed((Nd, Ld, d), g, torch.bfloat16)
+    dm = torch.arange(Ld)[None] < _lens((Nd,), Ld, g)[:, None]
+    args = (Q.cuda(), D.cuda(), None, dm.cuda())
+    got = maxsim(*args)
+    assert torch.equal(got, _tile(lambda: maxsim(*args)))
+    ref = O.maxsim(_np(Q), _np(D), None, dm.numpy())
+    assert rel_err(_np(got), ref) < 1e-4
+
+
+def test_varlen_one_query():
+    from late_interaction_kernels import maxsim_varlen
+
+    _case("q1 varlen")
+    g = torch.Generator().manual_seed(11)
+    d = 128
+    ld = _lens((200,), 150, g)
+    cu_d = torch.zeros(len(ld) + 1, dtype=torch.int32)
+    cu_d[1:] = ld.cumsum(0)
+    cu_q = torch.tensor([0, 32], dtype=torch.int32)
+    Qp = _normed((32, d), g, torch.bfloat16)
+    Dp = _normed((int(cu_d[-1]), d), g, torch.bfloat16)
+    args = (Qp.cuda(), Dp.cuda(), cu_q.cuda(), cu_d.cuda())
+    got = maxsim_varlen(*args)
+    assert torch.equal(got, _tile(lambda: maxsim_varlen(*args)))
+    ref = O.maxsim_varlen(_np(Qp), _np(Dp), cu_q.numpy(), cu_d.numpy())
+    assert rel_err(_np(got), ref) < 1e-4
+    assert got[:, ld.cuda() == 0].abs().max().item() == 0.0
+
+
+@pytest.mark.parametrize("d", [96, 100])
+def test_narrow_rows(d):
+    from late_interaction_kernels import maxsim
+
+    _case(f"q1 kd d={d}")
+    g = torch.Generator().manual_seed(d)
+    Nq, K, Ld = 3, 20, 70
+    Q = _normed((Nq, 32, d), g, torch.bfloat16)
+    D = _normed((Nq, K, Ld, d), g, torch.bfloat16)
+    dm = torch.arange(Ld)[None, None] < _lens((Nq, K), Ld, g)[..., None]
+    args = (Q.cuda(), D.cuda(), None, dm.cuda())
+    got = maxsim(*args)
+    assert torch.equal(got, _tile(lambda: maxsim(*args)))
+    ref = O.maxsim_kd(_np(Q), _np(D), None, dm.numpy())
+    assert rel_err(_np(got), ref) < 1e-4

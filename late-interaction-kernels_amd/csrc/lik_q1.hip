@@ -286,6 +286,15 @@ int launch_q1_t(const Params& p, bool normq, hipStream_t s) {
   return normq ? go(maxsim_q1_kernel<EK, DPAD, false, true>) : go(maxsim_q1_kernel<EK, DPAD, false, false>);
 }
 
+// Docs per wavefront: about 2048 wavefronts (two per SIMD, the kernel's
+// occupancy) over the launch, at most kQ1RMax; the tile kernel's choice
+// aims at workgroups of several waves and leaves too few wavefronts here.
+int q1_docs_per_wave(const Params& p) {
+  int64_t R = (p.ndocs_pg * p.ngroups + 2047) / 2048;
+  R = R < 1 ? 1 : R;
+  return (int)(R > kQ1RMax ? kQ1RMax : R);
+}
+
 // Routed here: 16-bit dense scoring with a one-block plan and nothing in the
 // tile loop beyond the plain max (no doc mask holes, token scales, doc
 // normalisation or argmax), at most kQ1RMax docs per wavefront.
@@ -293,11 +302,15 @@ bool q1_eligible(int dt, const Plan& pl, const Params& p) {
   return (dt == LIK_BF16 || dt == LIK_F16) && pl.W == 1 && pl.NSUB == 1 && pl.dpad == 128 &&
          ((uintptr_t)p.d.data) % 16 == 0 && p.d.sl_b % 16 == 0 && (p.d.cu || p.d.sn_b % 16 == 0) &&
          !p.amax && !p.pair_q && !p.pair_d && !p.d.mask && !p.d.ts && !p.q.ts && !(p.normalize & 2) &&
-         !p.scale_q && !p.scale_d && p.doc_filter != 2 && !p.accumulate && p.R <= kQ1RMax &&
-         (int64_t)p.R * pl.QPG <= kQ1Scores;
+         !p.scale_q && !p.scale_d && p.doc_filter != 2 && !p.accumulate &&
+         (int64_t)q1_docs_per_wave(p) * pl.QPG <= kQ1Scores;
 }
 
-int launch_q1(int dt, const Plan& pl, const Params& p, hipStream_t s) {
+int launch_q1(int dt, const Plan& pl, const Params& p0, hipStream_t s) {
+  (void)pl;
+  Params p = p0;
+  p.R = q1_docs_per_wave(p0);
+  p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   const bool normq = (p.normalize & 1) != 0;
   return dt == LIK_BF16 ? launch_q1_t<EK_BF16, 128>(p, normq, s) : launch_q1_t<EK_F16, 128>(p, normq, s);
 }

@@ -6,13 +6,15 @@
 // With a single column block a doc tile is used by one wavefront only, and
 // the work is HBM-bound: what matters is that the loads are coalesced and
 // that enough of them are in flight. Each wavefront keeps two 8 KB tiles in
-// flight in an LDS ring of its own, loaded by buffer_load ... lds (M0 saved
-// and restored): instruction i of a tile covers rows 4i .. 4i+3, lane L the
-// 16-byte chunk j = (L % 16 - 4 (L / 16) - i) mod 16 of row 4i + L / 16, so
-// an instruction reads 1 KB of consecutive rows (8 cache lines; a lane per
-// half row would touch 32) and lands it at LDS offset 1024 i + 16 L. The
-// rotation by 4 (row % 4) + row / 4 makes the A-fragment reads (lane (r, h)
-// reads chunk 8 h + ks of row r) conflict-free. A tile's fragments go to
+// flight in an LDS ring of its own, loaded by non-temporal buffer_load ...
+// lds (M0 saved and restored): with 256-byte rows (d 128), instruction i of
+// a tile covers rows 4i .. 4i+3, lane L the 16-byte chunk
+// j = (L % 16 - 4 (L / 16) - i) mod 16 of row 4i + L / 16, so an instruction
+// reads 1 KB of consecutive rows (8 cache lines; a lane per half row would
+// touch 32) and lands it at LDS offset 1024 i + 16 L. The rotation by
+// 4 (row % 4) + row / 4 makes the A-fragment reads (lane (r, h) reads chunk
+// 8 h + ks of row r) conflict-free. 128-byte rows (d 64) take 8 rows per
+// instruction and the rotation (row % 8) / 2 + 4 (row / 8) mod 8. A tile's fragments go to
 // registers first, then the next DMA reuses its slot, so two tiles stay in
 // flight during the MFMAs. Everything in the loop that touches vector
 // memory is a DMA load (8 per tile), so one fixed vmcnt per tile waits for
@@ -40,7 +42,10 @@ template <int EK, int DPAD, bool FULLD, bool NORMQ>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) maxsim_q1_kernel(const Params p) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;
-  static_assert(T::FRAG_V == 1 && !T::SPLIT && T::IN_B == 2 && DPAD == 128, "16-bit rows of 256 bytes");
+  static_assert(T::FRAG_V == 1 && !T::SPLIT && T::IN_B == 2 && (DPAD == 128 || DPAD == 64), "16-bit rows");
+  // one DMA instruction moves 1 KB: RPI rows of CPR 16-byte chunks; a tile
+  // of 32 rows takes NI instructions
+  constexpr int CPR = DPAD * 2 / 16, RPI = 16 * 4 / CPR, NI = 32 / RPI, TB = NI * 1024;
   constexpr float NEG_INF = -__builtin_huge_valf();
   __shared__ int32_t s_len[4][kQ1RMax];   // doc length (0: empty or not in this launch)
   __shared__ int64_t s_off[4][kQ1RMax];   // byte offset of the doc's token 0
@@ -48,7 +53,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
   // make the compiler's load counting wait for tiles still in flight
   __shared__ float s_score[4][kQ1Scores];
   // per-wave ring of two 8 KB tiles (chunks rotated as described above)
-  __shared__ __attribute__((aligned(1024))) char s_ring[4][2][8192];
+  __shared__ __attribute__((aligned(1024))) char s_ring[4][2][TB];
 
   const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
   const int wl = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -113,19 +118,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
   __builtin_amdgcn_wave_barrier();
   const float osc = p.out_scale;
 
-  // DMA lane offsets of instruction i (row 4i + L/16, rotated chunk; dims
-  // past d out of range) and A-fragment LDS offsets of k-step ks
+  // DMA lane offsets of instruction i (row RPI i + L / CPR, chunk rotated
+  // by rot(a, i); dims past d out of range) and A-fragment LDS offsets of
+  // k-step ks. The rotation gives the 16 lanes of a fragment-read pass 16
+  // different bank groups: (4a + i) mod 16 for 256-byte rows (a = row % 4,
+  // i = row / 4), (a / 2 + 4i) mod 8 for 128-byte rows (a = row % 8).
+  auto rot = [](int a, int i) { return CPR == 16 ? (4 * a + i) & 15 : ((a >> 1) + 4 * i) & 7; };
   const uint32_t sl = (uint32_t)p.d.sl_b;
-  uint32_t doff[8], aoff[KS];
+  uint32_t doff[NI], aoff[KS];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int a = lane >> 4, j = ((lane & 15) - 4 * a - i) & 15;
-    doff[i] = (FULLD || j * 8 < p.d.dim) ? (uint32_t)(4 * i + a) * sl + (uint32_t)(j * 16) : kOOB;
+  for (int i = 0; i < NI; ++i) {
+    const int a = lane / CPR, j = ((lane % CPR) - rot(a, i)) & (CPR - 1);
+    doff[i] = (FULLD || j * 8 < p.d.dim) ? (uint32_t)(RPI * i + a) * sl + (uint32_t)(j * 16) : kOOB;
   }
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const int i = l32 >> 2, a = l32 & 3, j = 8 * h + ks;
-    aoff[ks] = (uint32_t)(i * 1024 + a * 256 + ((j + 4 * a + i) & 15) * 16);
+    const int i = l32 / RPI, a = l32 % RPI, j = (CPR / 2) * h + ks;
+    aoff[ks] = (uint32_t)(i * 1024 + a * (CPR * 16) + ((j + rot(a, i)) & (CPR - 1)) * 16);
   }
   const uint32_t ring_lds = (uint32_t)__builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_ring[wl][0][0]));
@@ -148,7 +157,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
     int nv, k;
     bool docend;
   };
-  // DMA of the cursor's tile into ring slot S (exactly 8 load instructions,
+  // DMA of the cursor's tile into ring slot S (exactly NI load instructions,
   // whether or not the tile exists), then advance the cursor
   auto fetch = [&](auto SS, Cur& c) -> Desc {
     constexpr int S = decltype(SS)::value;
@@ -164,7 +173,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
                         (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu),
                         (uint32_t)__builtin_amdgcn_readfirstlane(span), 0x00020000u};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NI; ++i) {
       uint32_t saved;
       asm volatile(
           "s_mov_b32 %0, m0\n\t"
@@ -172,7 +181,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
           "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
           "s_mov_b32 m0, %0"
           : "=&s"(saved)
-          : "s"(ring_lds + (uint32_t)(S * 8192 + i * 1024)), "v"(doff[i]), "s"(desc)
+          : "s"(ring_lds + (uint32_t)(S * TB + i * 1024)), "v"(doff[i]), "s"(desc)
           : "memory");
     }
     if (d.docend)
@@ -217,7 +226,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
   auto step = [&](auto SS, const Desc& d, Cur& c) -> Desc {
     constexpr int S = decltype(SS)::value;
     // the tile after this one (8 loads) may still be in flight
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NI) : "memory");
     u32x4 af[KS];
     const char* slot = (const char*)&s_ring[wl][S][0];
 #pragma unroll
@@ -299,7 +308,7 @@ int q1_docs_per_wave(const Params& p) {
 // tile loop beyond the plain max (no doc mask holes, token scales, doc
 // normalisation or argmax), at most kQ1RMax docs per wavefront.
 bool q1_eligible(int dt, const Plan& pl, const Params& p) {
-  return (dt == LIK_BF16 || dt == LIK_F16) && pl.W == 1 && pl.NSUB == 1 && pl.dpad == 128 &&
+  return (dt == LIK_BF16 || dt == LIK_F16) && pl.W == 1 && pl.NSUB == 1 && (pl.dpad == 128 || pl.dpad == 64) &&
          ((uintptr_t)p.d.data) % 16 == 0 && p.d.sl_b % 16 == 0 && (p.d.cu || p.d.sn_b % 16 == 0) &&
          !p.amax && !p.pair_q && !p.pair_d && !p.d.mask && !p.d.ts && !p.q.ts && !(p.normalize & 2) &&
          !p.scale_q && !p.scale_d && p.doc_filter != 2 && !p.accumulate &&
@@ -307,11 +316,12 @@ bool q1_eligible(int dt, const Plan& pl, const Params& p) {
 }
 
 int launch_q1(int dt, const Plan& pl, const Params& p0, hipStream_t s) {
-  (void)pl;
   Params p = p0;
   p.R = q1_docs_per_wave(p0);
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   const bool normq = (p.normalize & 1) != 0;
+  if (pl.dpad == 64)
+    return dt == LIK_BF16 ? launch_q1_t<EK_BF16, 64>(p, normq, s) : launch_q1_t<EK_F16, 64>(p, normq, s);
   return dt == LIK_BF16 ? launch_q1_t<EK_BF16, 128>(p, normq, s) : launch_q1_t<EK_F16, 128>(p, normq, s);
 }
 

@@ -11,8 +11,9 @@ no workgroup barriers.
   reference.py:26-98) on the same 16-bit values within 1e-4.
 * Doc lengths around the tile edges (0, 1, 31, 32, 33, 63, 64, 65, Ld),
   masks with holes (their docs go to the masked tile kernel in the same
-  call), query-only normalisation, d = 96 (dims past d), and d = 100 (rows
-  not a multiple of 16 bytes: the tile kernel) against the oracle.
+  call), query-only normalisation, d = 128 and 64 (full 256- and 128-byte
+  rows), d = 96, 48 and 40 (dims past d; rows shorter than the padded
+  width) and d = 100 (a row stride that is not a multiple of 16 bytes).
 """
 
 import sys
@@ -96,13 +97,13 @@ def test_kd_mask_holes_and_query_mask():
     assert rel_err(_np(got), ref) < 1e-4
 
 
-@pytest.mark.parametrize("nq,lq", [(1, 32), (2, 16), (1, 5)])
-def test_short_queries_cross_product(nq, lq):
+@pytest.mark.parametrize("nq,lq,d", [(1, 32, 128), (2, 16, 128), (1, 5, 128), (1, 32, 64), (2, 16, 64)])
+def test_short_queries_cross_product(nq, lq, d):
     from late_interaction_kernels import maxsim
 
-    _case(f"q1 cross nq={nq} lq={lq}")
-    g = torch.Generator().manual_seed(7 + lq)
-    Nd, Ld, d = 300, 90, 128
+    _case(f"q1 cross nq={nq} lq={lq} d={d}")
+    g = torch.Generator().manual_seed(7 + lq + d)
+    Nd, Ld = 300, 90
     Q = _normed((nq, lq, d), g, torch.bfloat16)
     D = _normed((Nd, Ld, d), g, torch.bfloat16)
     dm = torch.arange(Ld)[None] < _lens((Nd,), Ld, g)[:, None]
@@ -133,7 +134,7 @@ def test_varlen_one_query():
     assert got[:, ld.cuda() == 0].abs().max().item() == 0.0
 
 
-@pytest.mark.parametrize("d", [96, 100])
+@pytest.mark.parametrize("d", [96, 100, 64, 48, 40])
 def test_narrow_rows(d):
     from late_interaction_kernels import maxsim
 

@@ -9,7 +9,8 @@ length ~ U[50, 300] as a prefix d_mask. One step = one ``maxsim(Q, D,
 d_mask=...)`` call over the whole batch (inputs resident in HBM).
 
 The default run also measures the rest of BASELINE.json's metric and puts it
-under ``parts`` in the same JSON line: ``fp8`` (C4 ColPali, K steps),
+under ``parts`` in the same JSON line: ``kd`` (C2's KD layout, K steps),
+``varlen`` (C3, K steps), ``fp8`` (C4 ColPali, K steps),
 ``plaid`` (C5 retrieve top-100 over 1M compressed docs, 1,024 queries,
 ``--plaid-steps`` steps) and ``plaid_q1`` (the same corpus at one query, the
 HBM-bound case), each with its own roofline. ``--no-parts`` skips them.
@@ -716,10 +717,12 @@ def main() -> None:
     parts = None
     if args.workload == "inbatch" and args.parts:
         # The rest of BASELINE.json's metric, each on its own config and with
-        # its own roofline: C4 fp8 TFLOP/s, C5 PLAID retrieve queries/s at
-        # top-100, and the PLAID kernel's HBM rate at Nq = 1.
+        # its own roofline: C2's KD layout (HBM), C3 varlen TFLOP/s, C4 fp8
+        # TFLOP/s, C5 PLAID retrieve queries/s at top-100, and the PLAID
+        # kernels' HBM rate at Nq = 1.
         parts = {}
-        for name, fn, steps in (("fp8", wl_fp8, args.steps), ("plaid", wl_plaid, args.plaid_steps),
+        for name, fn, steps in (("kd", wl_kd, args.steps), ("varlen", wl_varlen, args.steps),
+                                ("fp8", wl_fp8, args.steps), ("plaid", wl_plaid, args.plaid_steps),
                                 ("plaid_q1", wl_plaid_q1, args.steps),
                                 ("plaid_q1_prepared", wl_plaid_q1_prepared, args.steps)):
             torch.cuda.empty_cache()

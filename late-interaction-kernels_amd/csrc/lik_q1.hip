@@ -42,10 +42,15 @@ template <int EK, int DPAD, bool FULLD, bool NORMQ>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) maxsim_q1_kernel(const Params p) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;
-  static_assert(T::FRAG_V == 1 && !T::SPLIT && T::IN_B == 2 && (DPAD == 128 || DPAD == 64), "16-bit rows");
-  // one DMA instruction moves 1 KB: RPI rows of CPR 16-byte chunks; a tile
-  // of 32 rows takes NI instructions
-  constexpr int CPR = DPAD * 2 / 16, RPI = 16 * 4 / CPR, NI = 32 / RPI, TB = NI * 1024;
+  static_assert(T::FRAG_V == 1 && !T::SPLIT && T::IN_B == 2 && DPAD >= 64 && DPAD <= 512, "16-bit rows");
+  // The ring moves units of 32 rows: a whole tile for rows of <= 256 bytes;
+  // wider rows (d 256, 512) are split into NU units of 256 bytes per row,
+  // unit c holding bytes [128 c, 128 c + 128) of each half row, which are
+  // the A fragments of k-steps 8c .. 8c + 7. One DMA instruction moves 1 KB:
+  // RPI rows of CPR 16-byte chunks; a unit takes NI instructions.
+  constexpr int NU = DPAD >= 256 ? DPAD / 128 : 1;
+  constexpr int KSU = KS / NU;  // k-steps per unit
+  constexpr int CPR = NU > 1 ? 16 : DPAD * 2 / 16, RPI = 16 * 4 / CPR, NI = 32 / RPI, TB = NI * 1024;
   constexpr float NEG_INF = -__builtin_huge_valf();
   __shared__ int32_t s_len[4][kQ1RMax];   // doc length (0: empty or not in this launch)
   __shared__ int64_t s_off[4][kQ1RMax];   // byte offset of the doc's token 0
@@ -119,27 +124,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
   const float osc = p.out_scale;
 
   // DMA lane offsets of instruction i (row RPI i + L / CPR, chunk rotated
-  // by rot(a, i); dims past d out of range) and A-fragment LDS offsets of
-  // k-step ks. The rotation gives the 16 lanes of a fragment-read pass 16
-  // different bank groups: (4a + i) mod 16 for 256-byte rows (a = row % 4,
+  // by rot(a, i)) and A-fragment LDS offsets of k-step ks of a unit. The
+  // rotation gives the 16 lanes of a fragment-read pass 16 different bank
+  // groups: (4a + i) mod 16 for 256-byte unit rows (a = row % 4,
   // i = row / 4), (a / 2 + 4i) mod 8 for 128-byte rows (a = row % 8).
+  // Chunk j of a unit row is byte chunkb(j) + 128 c of the doc row.
   auto rot = [](int a, int i) { return CPR == 16 ? (4 * a + i) & 15 : ((a >> 1) + 4 * i) & 7; };
+  auto chunkb = [](int j) { return NU > 1 && j >= 8 ? DPAD + 16 * (j - 8) : 16 * j; };
   const uint32_t sl = (uint32_t)p.d.sl_b;
-  uint32_t doff[NI], aoff[KS];
+  uint32_t drow[NI], dchunk[NI], aoff[KSU];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int a = lane / CPR, j = ((lane % CPR) - rot(a, i)) & (CPR - 1);
-    doff[i] = (FULLD || j * 8 < p.d.dim) ? (uint32_t)(RPI * i + a) * sl + (uint32_t)(j * 16) : kOOB;
+    drow[i] = (uint32_t)(RPI * i + a) * sl;
+    dchunk[i] = (uint32_t)chunkb(j);
   }
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
+  for (int ks = 0; ks < KSU; ++ks) {
     const int i = l32 / RPI, a = l32 % RPI, j = (CPR / 2) * h + ks;
     aoff[ks] = (uint32_t)(i * 1024 + a * (CPR * 16) + ((j + rot(a, i)) & (CPR - 1)) * 16);
   }
   const uint32_t ring_lds = (uint32_t)__builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_ring[wl][0][0]));
 
-  // ---- tile cursor: tile t of local doc k (k == nloc: past the range) ----
+  // ---- cursor: unit c of tile t of local doc k (k == nloc: past the range) ----
   struct Cur {
     int k, t, len;
     int64_t off;
@@ -155,17 +163,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
   };
   struct Desc {
     int nv, k;
-    bool docend;
+    bool docend;  // last unit of the doc's last tile
   };
-  // DMA of the cursor's tile into ring slot S (exactly NI load instructions,
-  // whether or not the tile exists), then advance the cursor
-  auto fetch = [&](auto SS, Cur& c) -> Desc {
-    constexpr int S = decltype(SS)::value;
+  // DMA of unit CU of the cursor's tile into ring slot S (exactly NI load
+  // instructions, whether or not the tile exists); after the tile's last
+  // unit the cursor advances
+  auto fetch = [&](auto SS, auto CC, Cur& c) -> Desc {
+    constexpr int S = decltype(SS)::value, CU = decltype(CC)::value;
     Desc d;
     const int rem = c.len - 32 * c.t;
     d.nv = rem < 32 ? rem : 32;
     d.k = c.k;
-    d.docend = c.len > 0 && rem <= 32;
+    const bool tile_end = c.len > 0 && rem <= 32;
+    d.docend = tile_end && CU == NU - 1;
     // the buffer covers rows [32 t, len) of the doc: later rows read 0
     const uint64_t base = (uint64_t)(p.d.data + c.off) + (uint64_t)((uint32_t)c.t * 32u * sl);
     const uint32_t span = d.nv > 0 ? (uint32_t)(d.nv - 1) * sl + (uint32_t)(p.d.dim * T::IN_B) : 0u;
@@ -174,6 +184,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
                         (uint32_t)__builtin_amdgcn_readfirstlane(span), 0x00020000u};
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
+      const uint32_t cb = dchunk[i] + (uint32_t)(128 * CU);
+      // dims past d: out of range
+      const uint32_t voff = (FULLD || cb / 2 < (uint32_t)p.d.dim) ? drow[i] + cb : kOOB;
       uint32_t saved;
       asm volatile(
           "s_mov_b32 %0, m0\n\t"
@@ -181,13 +194,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
           "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
           "s_mov_b32 m0, %0"
           : "=&s"(saved)
-          : "s"(ring_lds + (uint32_t)(S * TB + i * 1024)), "v"(doff[i]), "s"(desc)
+          : "s"(ring_lds + (uint32_t)(S * TB + i * 1024)), "v"(voff), "s"(desc)
           : "memory");
     }
-    if (d.docend)
-      cur_doc(c, c.k + 1);
-    else
-      c.t += 1;
+    if (CU == NU - 1) {
+      if (tile_end)
+        cur_doc(c, c.k + 1);
+      else
+        c.t += 1;
+    }
     return d;
   };
 
@@ -221,53 +236,72 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
     }
     m = NEG_INF;
   };
-  // tile in slot S: wait for it, read its A fragments, hand the slot to
-  // the next fetch (tile + 2), then score
-  auto step = [&](auto SS, const Desc& d, Cur& c) -> Desc {
-    constexpr int S = decltype(SS)::value;
-    // the tile after this one (8 loads) may still be in flight
+  // unit CU in slot S: wait for it, read its A fragments, hand the slot to
+  // the next fetch (two units on, unit CN), then its MFMAs; the tile's last
+  // unit ends with the running max (and the doc's end)
+  f32x16 acc;
+  auto step = [&](auto SS, auto CC, auto CN, const Desc& d, Cur& c) -> Desc {
+    constexpr int S = decltype(SS)::value, CU = decltype(CC)::value;
+    // the unit after this one (NI loads) may still be in flight
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(NI) : "memory");
-    u32x4 af[KS];
+    u32x4 af[KSU];
     const char* slot = (const char*)&s_ring[wl][S][0];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) af[ks] = *(const u32x4*)(slot + aoff[ks]);
+    for (int ks = 0; ks < KSU; ++ks) af[ks] = *(const u32x4*)(slot + aoff[ks]);
     // the fragments are in registers before the DMA overwrites the slot
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const Desc dn = fetch(SS, c);
-    f32x16 acc;
+    const Desc dn = fetch(SS, CN, c);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &af[ks], &bq[ks]);
-    // element e is row 8 (e / 4) + 4 h + e % 4
-    if (d.nv < 32) {
-      const int lim = d.nv - 4 * h;
+    for (int ks = 0; ks < KSU; ++ks)
+      acc = mfma32<EK>(CU == 0 && ks == 0 ? f32x16{} : acc, &af[ks], &bq[CU * KSU + ks]);
+    if constexpr (CU == NU - 1) {
+      // element e is row 8 (e / 4) + 4 h + e % 4
+      if (d.nv < 32) {
+        const int lim = d.nv - 4 * h;
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (8 * (e >> 2) + (e & 3) >= lim) acc[e] = NEG_INF;
+        for (int e = 0; e < 16; ++e)
+          if (8 * (e >> 2) + (e & 3) >= lim) acc[e] = NEG_INF;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) m = fmaxf(m, acc[e]);
+      if (d.docend) doc_end(d.k);
     }
-#pragma unroll
-    for (int e = 0; e < 16; ++e) m = fmaxf(m, acc[e]);
-    if (d.docend) doc_end(d.k);
     return dn;
   };
 
   Cur cur;
   cur_doc(cur, 0);
   if (cur.k >= nloc) return;  // (empty docs were written above)
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  // tiles i (slot i % 2) and i + 1 in flight; a tile past the range (nv 0,
-  // no doc end) loads nothing and ends the loop
+  // Units u, u + 1 in flight (slots u % 2); the loop body is unrolled over
+  // U units so slots and unit indices are compile-time. A unit past the
+  // range (nv 0) loads nothing and ends the loop.
+  constexpr int U = NU > 2 ? NU : 2;
   // (the prologue's stores and query loads complete before the fixed counts start)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  Desc d0 = fetch(I0{}, cur);
-  Desc d1 = fetch(I1{}, cur);
-  for (;;) {
-    const Desc d2 = step(I0{}, d0, cur);
-    if (d1.nv <= 0) break;
-    d0 = step(I1{}, d1, cur);
-    if (d2.nv <= 0) break;
-    d1 = d0;
-    d0 = d2;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  Desc q0 = fetch(I0{}, I0{}, cur);
+  Desc q1 = fetch(I1{}, std::integral_constant<int, 1 % NU>{}, cur);
+  bool run = true;
+  auto one = [&](auto SI) {
+    constexpr int s = decltype(SI)::value;
+    if (!run) return;
+    const Desc qn = step(std::integral_constant<int, s % 2>{}, std::integral_constant<int, s % NU>{},
+                         std::integral_constant<int, (s + 2) % NU>{}, q0, cur);
+    if (q1.nv <= 0) {
+      run = false;
+      return;
+    }
+    q0 = q1;
+    q1 = qn;
+  };
+  while (run) {
+    one(std::integral_constant<int, 0>{});
+    one(std::integral_constant<int, 1>{});
+    if constexpr (U > 2) {
+      one(std::integral_constant<int, 2>{});
+      one(std::integral_constant<int, 3>{});
+    }
   }
   // no DMA may still be writing this wave's LDS (tiles past the range load nothing)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -308,7 +342,11 @@ int q1_docs_per_wave(const Params& p) {
 // tile loop beyond the plain max (no doc mask holes, token scales, doc
 // normalisation or argmax), at most kQ1RMax docs per wavefront.
 bool q1_eligible(int dt, const Plan& pl, const Params& p) {
-  return (dt == LIK_BF16 || dt == LIK_F16) && pl.W == 1 && pl.NSUB == 1 && (pl.dpad == 128 || pl.dpad == 64) &&
+  // one 32-column block holds every unit of a group (W = 1 plans), or the
+  // call's only group (a one-query call whose plan is wider)
+  const bool one_block = (pl.W == 1 && pl.NSUB == 1) ||
+                         ((int64_t)pl.QPG * pl.LU <= 32) || (pl.ngroups == 1 && pl.nunits * pl.LU <= 32);
+  return (dt == LIK_BF16 || dt == LIK_F16) && one_block && pl.dpad >= 64 && pl.dpad <= 512 &&
          ((uintptr_t)p.d.data) % 16 == 0 && p.d.sl_b % 16 == 0 && (p.d.cu || p.d.sn_b % 16 == 0) &&
          !p.amax && !p.pair_q && !p.pair_d && !p.d.mask && !p.d.ts && !p.q.ts && !(p.normalize & 2) &&
          !p.scale_q && !p.scale_d && p.doc_filter != 2 && !p.accumulate &&
@@ -317,11 +355,18 @@ bool q1_eligible(int dt, const Plan& pl, const Params& p) {
 
 int launch_q1(int dt, const Plan& pl, const Params& p0, hipStream_t s) {
   Params p = p0;
+  // units of the group in one 32-column block (unit t keeps its place t, so
+  // the column sums keep the tile kernel's order)
+  if ((int64_t)p.QPG * p.LU > 32) p.QPG = 32 / p.LU;
   p.R = q1_docs_per_wave(p0);
   p.NR = (p.ndocs_pg + p.R - 1) / p.R;
   const bool normq = (p.normalize & 1) != 0;
   if (pl.dpad == 64)
     return dt == LIK_BF16 ? launch_q1_t<EK_BF16, 64>(p, normq, s) : launch_q1_t<EK_F16, 64>(p, normq, s);
+  if (pl.dpad == 256)
+    return dt == LIK_BF16 ? launch_q1_t<EK_BF16, 256>(p, normq, s) : launch_q1_t<EK_F16, 256>(p, normq, s);
+  if (pl.dpad == 512)
+    return dt == LIK_BF16 ? launch_q1_t<EK_BF16, 512>(p, normq, s) : launch_q1_t<EK_F16, 512>(p, normq, s);
   return dt == LIK_BF16 ? launch_q1_t<EK_BF16, 128>(p, normq, s) : launch_q1_t<EK_F16, 128>(p, normq, s);
 }
 

@@ -149,3 +149,30 @@ def test_narrow_rows(d):
     assert torch.equal(got, _tile(lambda: maxsim(*args)))
     ref = O.maxsim_kd(_np(Q), _np(D), None, dm.numpy())
     assert rel_err(_np(got), ref) < 1e-4
+
+
+@pytest.mark.parametrize("d", [256, 512, 300, 200])
+def test_wide_rows(d):
+    """Rows of 512 and 1024 bytes move through the ring as 256-byte units.
+    One query (the streaming kernel) gives the bits of the same query scored
+    next to a second one (64 columns: the tile kernel); KD against the
+    oracle."""
+    from late_interaction_kernels import maxsim
+
+    _case(f"q1 wide d={d}")
+    g = torch.Generator().manual_seed(d + 1)
+    Nd, Ld = 150, 80
+    Q = _normed((2, 32, d), g, torch.bfloat16)
+    D = _normed((Nd, Ld, d), g, torch.bfloat16)
+    dm = torch.arange(Ld)[None] < _lens((Nd,), Ld, g)[:, None]
+    Qc, Dc, dmc = Q.cuda(), D.cuda(), dm.cuda()
+    one = maxsim(Qc[:1], Dc, None, dmc)
+    two = maxsim(Qc, Dc, None, dmc)
+    assert torch.equal(one[0], two[0])
+    ref = O.maxsim(_np(Q), _np(D), None, dm.numpy())
+    assert rel_err(_np(two), ref) < 1e-4
+    Dk = _normed((2, 30, Ld, d), g, torch.bfloat16)
+    dmk = torch.arange(Ld)[None, None] < _lens((2, 30), Ld, g)[..., None]
+    got = maxsim(Qc, Dk.cuda(), None, dmk.cuda())
+    ref = O.maxsim_kd(_np(Q), _np(Dk), None, dmk.numpy())
+    assert rel_err(_np(got), ref) < 1e-4

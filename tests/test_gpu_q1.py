@@ -176,3 +176,37 @@ def test_wide_rows(d):
     got = maxsim(Qc, Dk.cuda(), None, dmk.cuda())
     ref = O.maxsim_kd(_np(Q), _np(Dk), None, dmk.numpy())
     assert rel_err(_np(got), ref) < 1e-4
+
+
+def test_one_query_c3_scale():
+    """One query over C3's corpus (65,536 packed docs, log-uniform lengths in
+    [16, 2048]): the same bits as the tile kernel; sampled docs against the
+    oracle."""
+    import math
+
+    from late_interaction_kernels import maxsim_varlen
+
+    _case("q1 one query x 65536 varlen docs")
+    g = torch.Generator(device="cuda").manual_seed(13)
+    Nd, d = 65536, 128
+    u = torch.rand(Nd, generator=g, device="cuda")
+    lens = torch.floor(torch.exp(math.log(16) + u * (math.log(2049) - math.log(16)))).clamp(16, 2048).long()
+    cu_d = torch.zeros(Nd + 1, dtype=torch.int32, device="cuda")
+    cu_d[1:] = lens.cumsum(0).to(torch.int32)
+    tot = int(cu_d[-1].item())
+    Dp = torch.empty(tot, d, device="cuda", dtype=torch.bfloat16)
+    for s in range(0, tot, 1 << 22):
+        e = min(tot, s + (1 << 22))
+        Dp[s:e] = torch.nn.functional.normalize(torch.randn(e - s, d, generator=g, device="cuda"), dim=-1)
+    Qp = torch.nn.functional.normalize(torch.randn(32, d, generator=g, device="cuda"), dim=-1).to(torch.bfloat16)
+    cu_q = torch.tensor([0, 32], dtype=torch.int32, device="cuda")
+    got = maxsim_varlen(Qp, Dp, cu_q, cu_d, max_seqlen_q=32, max_seqlen_d=2048)
+    assert torch.equal(got, _tile(lambda: maxsim_varlen(Qp, Dp, cu_q, cu_d, max_seqlen_q=32, max_seqlen_d=2048)))
+    dj = [0, 1, 777, 30000, int(lens.argmax()), Nd - 1]
+    cu_h = cu_d.cpu()
+    for j in dj:
+        a, b = int(cu_h[j]), int(cu_h[j + 1])
+        ref = O.maxsim(_np(Qp)[None], _np(Dp[a:b])[None])
+        assert rel_err(_np(got[:, j:j + 1]), ref) < 1e-4, j
+    del Dp
+    torch.cuda.empty_cache()

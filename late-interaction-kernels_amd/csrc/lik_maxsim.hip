@@ -513,6 +513,7 @@ int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float 
   p.scale_q = tensor_scale(*Q) ? Q->token_scale : nullptr;
   p.scale_d = tensor_scale(*D) ? D->token_scale : nullptr;
   p.normalize = norm_bits(flags);
+  p.forced_w = (opts && opts->col_waves > 0 && opts->col_blocks > 0) ? opts->col_waves : 0;
   char* ws = (char*)workspace;
   p.out_scale = out_scale;
   p.nunits = pl.nunits;

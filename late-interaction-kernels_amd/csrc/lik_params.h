@@ -63,6 +63,7 @@ struct Params {
   int accumulate;   // add the scores to out instead of storing them (query-chunk launches)
   const float* scale_q;  // per-tensor scales in device memory folded into the score scale, or null
   const float* scale_d;
+  int forced_w;  // caller-forced column block with this many waves (0: the library's plan)
 };
 
 // PLAID gather kernel: byte offset given to a row past the tile end; the

@@ -338,19 +338,22 @@ int q1_docs_per_wave(const Params& p) {
   return (int)(R > kQ1RMax ? kQ1RMax : R);
 }
 
-// Routed here: 16-bit dense scoring with a one-block plan and nothing in the
-// tile loop beyond the plain max (no doc mask holes, token scales, doc
-// normalisation or argmax), at most kQ1RMax docs per wavefront.
+// Routed here: 16-bit dense scoring in which one 32-column block holds the
+// columns of a group as planned (W = 1 plans, the KD layout) or of the
+// call's only group (a one-query call whose plan is wider), with nothing in
+// the tile loop beyond the plain max (no doc mask holes, token scales, doc
+// normalisation, argmax, pair lists or query-chunk accumulation), unless the
+// caller forced a column block of several waves (lik_launch_opts_t). (Two
+// and four blocks per wavefront for queries of up to 128 tokens measured
+// slower than the tile kernel's four waves sharing a tile.)
 bool q1_eligible(int dt, const Plan& pl, const Params& p) {
-  // one 32-column block holds every unit of a group (W = 1 plans), or the
-  // call's only group (a one-query call whose plan is wider)
   const bool one_block = (pl.W == 1 && pl.NSUB == 1) ||
                          ((int64_t)pl.QPG * pl.LU <= 32) || (pl.ngroups == 1 && pl.nunits * pl.LU <= 32);
   return (dt == LIK_BF16 || dt == LIK_F16) && one_block && pl.dpad >= 64 && pl.dpad <= 512 &&
          ((uintptr_t)p.d.data) % 16 == 0 && p.d.sl_b % 16 == 0 && (p.d.cu || p.d.sn_b % 16 == 0) &&
          !p.amax && !p.pair_q && !p.pair_d && !p.d.mask && !p.d.ts && !p.q.ts && !(p.normalize & 2) &&
          !p.scale_q && !p.scale_d && p.doc_filter != 2 && !p.accumulate &&
-         (int64_t)q1_docs_per_wave(p) * pl.QPG <= kQ1Scores;
+         (int64_t)q1_docs_per_wave(p) * pl.QPG <= kQ1Scores && p.forced_w <= 1;
 }
 
 int launch_q1(int dt, const Plan& pl, const Params& p0, hipStream_t s) {

@@ -3,10 +3,10 @@ one query) run the streaming kernel of lik_q1.hip: doc tiles loaded by
 coalesced, non-temporal buffer_load ... lds into a per-wavefront LDS ring,
 no workgroup barriers.
 
-* The same bits as the tile kernel (forced with cfg=(1, 2), a two-block
-  plan the streaming kernel does not take): same MFMA sequence per tile,
-  exact maxima, the tile kernel's column-sum order (also for two queries
-  sharing the block, Lq = 16).
+* The same bits as the tile kernel (forced with cfg=(4, 1): a forced
+  multi-wave block is the tile kernel's): same MFMA sequence per tile, exact
+  maxima, the tile kernel's column-sum order (also for two queries sharing
+  a block, Lq = 16).
 * Against the float64 oracle (lik_oracle.maxsim / maxsim_kd / maxsim_varlen,
   reference.py:26-98) on the same 16-bit values within 1e-4.
 * Doc lengths around the tile edges (0, 1, 31, 32, 33, 63, 64, 65, Ld),
@@ -45,7 +45,9 @@ def _normed(shape, g, dtype):
 
 
 def _tile(fn):
-    with launch_options(cfg=(1, 2)):
+    # a forced four-wave block: the tile kernel (unit t of a group keeps its
+    # place, so its column sums run in the same order)
+    with launch_options(cfg=(4, 1)):
         return fn()
 
 
@@ -97,7 +99,7 @@ def test_kd_mask_holes_and_query_mask():
     assert rel_err(_np(got), ref) < 1e-4
 
 
-@pytest.mark.parametrize("nq,lq,d", [(1, 32, 128), (2, 16, 128), (1, 5, 128), (1, 32, 64), (2, 16, 64)])
+@pytest.mark.parametrize("nq,lq,d", [(1, 32, 128), (2, 16, 128), (1, 5, 128), (1, 32, 64), (2, 16, 64), (1, 32, 512)])
 def test_short_queries_cross_product(nq, lq, d):
     from late_interaction_kernels import maxsim
 

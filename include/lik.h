@@ -84,8 +84,12 @@ typedef struct {
  *   col_waves, col_blocks: force the tile kernel's column block (waves per
  *       workgroup W in {1, 4, 8}, 32-column blocks per wave NSUB in
  *       {1, 2, 4}; fp8 at d <= 128 also 4 x 6); 0 = automatic. A
- *       configuration the call cannot use is ignored.
- *   docs_per_wg: documents per workgroup, 1..512; 0 = automatic.
+ *       configuration the call cannot use is ignored. Calls whose query
+ *       group fits one 32-column block otherwise run a streaming
+ *       one-block kernel; a forced block of 4 or 8 waves keeps them on
+ *       the tile kernel.
+ *   docs_per_wg: documents per workgroup of the tile kernel, 1..512;
+ *       0 = automatic (the streaming kernel picks its own).
  *   plaid_variant (lik_plaid_maxsim_ex): 0 automatic, 1 per-lane stream
  *       decode, 2 exact LDS-gather decode (bitwise equal to the tile
  *       kernel), 3 the tile kernel (no stream kernel).

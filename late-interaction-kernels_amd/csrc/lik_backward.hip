@@ -268,13 +268,15 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
         sc = 0.f;
         qoff = 0;
         if (f < f1) {
+          // independent loads (no load waits on another), so a pass costs one
+          // memory latency; a zero G or a masked query token drops the pair
           const float gij = bp.grad[i * bp.ld_g + jl];
-          int av = gij != 0.f ? bp.amax[(i * bp.ndoc_pg + jl) * bp.lq + s] : -1;
-          if (av >= 0 && bp.qmask && bp.qmask[i * bp.qm_sn + s * bp.qm_sl] == 0) av = -1;
-          float scv = gij;
-          if (bp.qinv && av >= 0) scv *= bp.qinv[i * bp.lq + s];
+          int av = bp.amax[(i * bp.ndoc_pg + jl) * bp.lq + s];
+          const bool keep = !bp.qmask || bp.qmask[i * bp.qm_sn + s * bp.qm_sl] != 0;
+          const float qi = bp.qinv ? bp.qinv[i * bp.lq + s] : 1.f;
+          if (gij == 0.f || !keep) av = -1;
           a = av;
-          sc = scv;
+          sc = bp.qinv ? gij * qi : gij;
           qoff = i * bp.q_sn + s * bp.q_sl;
         }
       };

@@ -145,6 +145,50 @@ __device__ __forceinline__ void store_elem(char* row, int e, float v) {
   else *(float*)(row + 4 * e) = v;
 }
 
+// acc[k] += c * row[e0 + k], k < DPL: the DPL elements of one lane loaded at
+// once (rows start on 16-byte boundaries and e0 = lane * DPL, so the load is
+// aligned to its size), elements at or past dim read as 0.
+template <int EK, int DPL>
+__device__ __forceinline__ void axpy_lane(float* acc, const char* row, int e0, int dim, float c) {
+  constexpr int EB = sizeof_ek<EK>();
+  float x[DPL];
+  if (e0 + DPL <= dim) {
+    const char* p = row + (int64_t)e0 * EB;
+    if constexpr (DPL * EB == 2) {
+      x[0] = load_elem<EK>(row, e0);
+    } else if constexpr (DPL * EB == 4) {
+      const uint32_t w = *(const uint32_t*)p;
+      if constexpr (EK == EK_F32) x[0] = __uint_as_float(w);
+      else if constexpr (EK == EK_BF16) { x[0] = bf16lo_to_f32(w); x[1] = bf16hi_to_f32(w); }
+      else { x[0] = f16_to_f32((uint16_t)(w & 0xffffu)); x[1] = f16_to_f32((uint16_t)(w >> 16)); }
+    } else {
+      constexpr int NW = DPL * EB / 4;  // 32-bit words, loaded 8 / 16 bytes at a time
+      uint32_t w[NW];
+#pragma unroll
+      for (int v = 0; v < NW; v += (NW >= 4 ? 4 : 2)) {
+        if constexpr (NW >= 4) {
+          const u32x4 t = *(const u32x4*)(p + 4 * v);
+          w[v] = t[0]; w[v + 1] = t[1]; w[v + 2] = t[2]; w[v + 3] = t[3];
+        } else {
+          const u32x2 t = *(const u32x2*)(p + 4 * v);
+          w[v] = t[0]; w[v + 1] = t[1];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) {
+        if constexpr (EK == EK_F32) x[k] = __uint_as_float(w[k]);
+        else if constexpr (EK == EK_BF16) x[k] = (k & 1) ? bf16hi_to_f32(w[k >> 1]) : bf16lo_to_f32(w[k >> 1]);
+        else x[k] = f16_to_f32((uint16_t)((k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu)));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) x[k] = e0 + k < dim ? load_elem<EK>(row, e0 + k) : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) acc[k] = fmaf(c, x[k], acc[k]);
+}
+
 template <int EK, int DPL>
 __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
   const int lane = threadIdx.x & 63;
@@ -229,7 +273,7 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
 template <int EK, int DPL>
 __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
   constexpr int RB = 64 / DPL < 32 ? 64 / DPL : 32;
-  __shared__ float s_acc[RB][64 * DPL];
+  __shared__ __attribute__((aligned(16))) float s_acc[RB][64 * DPL];
   const int lane = threadIdx.x;
 #pragma unroll
   for (int r = 0; r < RB; ++r)
@@ -296,11 +340,15 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
           const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)qo_c, l);
           const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)qo_c >> 32), l);
           const char* qrow = bp.q + (int64_t)(((uint64_t)hi << 32) | lo);
+          // this lane's DPL dims of row r: one LDS read, one write (the
+          // elements past dim accumulate zeros and are never stored)
+          float* ar = &s_acc[r][lane * DPL];
+          float av[DPL];
 #pragma unroll
-          for (int k = 0; k < DPL; ++k) {
-            const int e = lane * DPL + k;
-            if (e < bp.dim) s_acc[r][e] = fmaf(c, load_elem<EK>(qrow, e), s_acc[r][e]);
-          }
+          for (int k = 0; k < DPL; ++k) av[k] = ar[k];
+          axpy_lane<EK, DPL>(av, qrow, lane * DPL, bp.dim, c);
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) ar[k] = av[k];
         }
         a_c = a_n;
         sc_c = sc_n;
@@ -341,11 +389,15 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
           touched |= 1u << r;
           const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
           const char* qrow = bp.q_cu ? bp.q + (qbase + s0 + l) * bp.q_sl : bp.q + i * bp.q_sn + (s0 + l) * bp.q_sl;
+          // this lane's DPL dims of row r: one LDS read, one write (the
+          // elements past dim accumulate zeros and are never stored)
+          float* ar = &s_acc[r][lane * DPL];
+          float av[DPL];
 #pragma unroll
-          for (int k = 0; k < DPL; ++k) {
-            const int e = lane * DPL + k;
-            if (e < bp.dim) s_acc[r][e] = fmaf(c, load_elem<EK>(qrow, e), s_acc[r][e]);
-          }
+          for (int k = 0; k < DPL; ++k) av[k] = ar[k];
+          axpy_lane<EK, DPL>(av, qrow, lane * DPL, bp.dim, c);
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) ar[k] = av[k];
         }
       }
     }

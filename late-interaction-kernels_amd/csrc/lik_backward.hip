@@ -145,13 +145,12 @@ __device__ __forceinline__ void store_elem(char* row, int e, float v) {
   else *(float*)(row + 4 * e) = v;
 }
 
-// acc[k] += c * row[e0 + k], k < DPL: the DPL elements of one lane loaded at
-// once (rows start on 16-byte boundaries and e0 = lane * DPL, so the load is
+// x[k] = row[e0 + k], k < DPL: the DPL elements of one lane loaded at once
+// (rows start on 16-byte boundaries and e0 = lane * DPL, so the load is
 // aligned to its size), elements at or past dim read as 0.
 template <int EK, int DPL>
-__device__ __forceinline__ void axpy_lane(float* acc, const char* row, int e0, int dim, float c) {
+__device__ __forceinline__ void load_lane(float* x, const char* row, int e0, int dim) {
   constexpr int EB = sizeof_ek<EK>();
-  float x[DPL];
   if (e0 + DPL <= dim) {
     const char* p = row + (int64_t)e0 * EB;
     if constexpr (DPL * EB == 2) {
@@ -185,6 +184,13 @@ __device__ __forceinline__ void axpy_lane(float* acc, const char* row, int e0, i
 #pragma unroll
     for (int k = 0; k < DPL; ++k) x[k] = e0 + k < dim ? load_elem<EK>(row, e0 + k) : 0.f;
   }
+}
+
+// acc[k] += c * row[e0 + k], k < DPL
+template <int EK, int DPL>
+__device__ __forceinline__ void axpy_lane(float* acc, const char* row, int e0, int dim, float c) {
+  float x[DPL];
+  load_lane<EK, DPL>(x, row, e0, dim);
 #pragma unroll
   for (int k = 0; k < DPL; ++k) acc[k] = fmaf(c, x[k], acc[k]);
 }
@@ -230,17 +236,31 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
     float sv = gv;
     if (bp.dinv && av >= 0) sv *= bp.dinv[(int64_t)jd * bp.ld + av];  // dinv only for padded docs
     uint64_t bal = __ballot(av >= 0 && gv != 0.f);
+    // up to HB winning rows loaded before any is added (one memory latency
+    // per batch instead of one per doc), added in doc order
+    constexpr int HB = DPL <= 2 ? 8 : (DPL == 4 ? 4 : (DPL == 8 ? 2 : 1));
     while (bal) {
-      const int l = __builtin_ctzll(bal);
-      bal &= bal - 1;
-      const int a = __builtin_amdgcn_readlane(av, l);
-      const float sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), l));
-      const int64_t jg = __builtin_amdgcn_readlane(jd, l);
-      const char* row = bp.d_cu ? bp.d + ((int64_t)bp.d_cu[jg] + a) * bp.d_sl : bp.d + jg * bp.d_sn + (int64_t)a * bp.d_sl;
+      float xs[HB][DPL], scs[HB];
+      int nb = 0;
 #pragma unroll
-      for (int k = 0; k < DPL; ++k) {
-        const int e = lane * DPL + k;
-        if (e < bp.dim) acc[k] = fmaf(sc, load_elem<EK>(row, e), acc[k]);
+      for (int b = 0; b < HB; ++b) {
+        if (bal) {
+          const int l = __builtin_ctzll(bal);
+          bal &= bal - 1;
+          const int a = __builtin_amdgcn_readlane(av, l);
+          scs[b] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), l));
+          const int64_t jg = __builtin_amdgcn_readlane(jd, l);
+          const char* row = bp.d_cu ? bp.d + ((int64_t)bp.d_cu[jg] + a) * bp.d_sl
+                                    : bp.d + jg * bp.d_sn + (int64_t)a * bp.d_sl;
+          load_lane<EK, DPL>(xs[b], row, lane * DPL, bp.dim);
+          nb = b + 1;
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < HB; ++b) {
+        if (b >= nb) break;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) acc[k] = fmaf(scs[b], xs[b][k], acc[k]);
       }
     }
   }

@@ -287,19 +287,26 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
   }
 }
 
-// RB doc rows per wavefront, RB * 64 * DPL floats of LDS accumulator (16 KB).
+// Doc rows per grad_d block: every block rescans all the (i, s) pairs of its
+// doc, but the scan is latency-bound, so more, shorter blocks (more waves per
+// CU) win: 16 rows measured best for up to 2 dims per lane (8 KB of
+// accumulator; 8 and 32 rows slower, 64 much slower), 64 / DPL rows beyond.
+template <int DPL>
+constexpr int grad_d_rows() { return DPL <= 2 ? 16 : (64 / DPL < 32 ? 64 / DPL : 32); }
+
+// RB doc rows per wavefront, RB * 64 * DPL floats of LDS accumulator.
 // Padded docs: block b is rows [t0, t0 + RB) of doc b / nrb. Packed docs: block
 // b is storage rows [cu[0] + b*RB, +RB), each doc overlapping it scanned in turn.
 template <int EK, int DPL>
 __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
-  constexpr int RB = 64 / DPL < 32 ? 64 / DPL : 32;
+  constexpr int RB = grad_d_rows<DPL>();
   __shared__ __attribute__((aligned(16))) float s_acc[RB][64 * DPL];
   const int lane = threadIdx.x;
 #pragma unroll
   for (int r = 0; r < RB; ++r)
 #pragma unroll
     for (int k = 0; k < DPL; ++k) s_acc[r][lane * DPL + k] = 0.f;
-  uint32_t touched = 0;  // rows of the block that received a contribution (wave-uniform)
+  uint64_t touched = 0;  // rows of the block that received a contribution (wave-uniform)
 
   // Add the contributions of doc j whose winner a lies in [wlo, wlo + n) to
   // accumulator rows off + (a - wlo).
@@ -355,7 +362,7 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
           const int l = __builtin_ctzll(bal);
           bal &= bal - 1;
           const int r = off + __builtin_amdgcn_readlane(a_c, l) - (int)wlo;
-          touched |= 1u << r;
+          touched |= 1ull << r;
           const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_c), l));
           const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)qo_c, l);
           const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)qo_c >> 32), l);
@@ -406,7 +413,7 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
           const int l = __builtin_ctzll(bal);
           bal &= bal - 1;
           const int r = off + __builtin_amdgcn_readlane(a, l) - (int)wlo;
-          touched |= 1u << r;
+          touched |= 1ull << r;
           const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
           const char* qrow = bp.q_cu ? bp.q + (qbase + s0 + l) * bp.q_sl : bp.q + i * bp.q_sn + (s0 + l) * bp.q_sl;
           // this lane's DPL dims of row r: one LDS read, one write (the
@@ -458,7 +465,7 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
   // finished rows: normalisation Jacobian (padded docs only), then store
   for (int r = 0; r < nrows; ++r) {
     char* out = bp.gd + (out_row0 + r) * bp.dim * (int64_t)sizeof_ek<EK>();
-    if (!((touched >> r) & 1u)) {  // no winner in this row: zero gradient, no D read
+    if (!((touched >> r) & 1ull)) {  // no winner in this row: zero gradient, no D read
 #pragma unroll
       for (int k = 0; k < DPL; ++k) {
         const int e = lane * DPL + k;
@@ -494,7 +501,7 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
 
 template <int EK, int DPL>
 int launch_bwd(const BwdParams& bp, hipStream_t s) {
-  constexpr int RB = 64 / DPL < 32 ? 64 / DPL : 32;
+  constexpr int RB = grad_d_rows<DPL>();
   const int64_t nw = bp.nq * bp.lq;
   if (nw > 0) {
     hipLaunchKernelGGL((grad_q_kernel<EK, DPL>), dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, s, bp);

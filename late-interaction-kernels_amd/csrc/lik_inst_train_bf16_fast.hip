@@ -2,7 +2,7 @@
 // bf16 tokens at d = 128 with the common feature sets compiled to exactly
 // what the call uses: no doc mask, or prefix / holes masks, with or without
 // the query-side normalise (docs arrive normalised by the pre-normalise
-// pass). The argmax plans have at least four waves per workgroup, so only
+// pass), and the in-kernel doc normalise of maxsim_from_hidden. The argmax plans have at least four waves per workgroup, so only
 // those column blocks are instantiated. Other calls go to the all-features
 // instantiation (lik_inst_train_bf16.hip).
 #include "lik_kernel.h"
@@ -27,6 +27,7 @@ int launch_dense_train_bf16(const Plan& pl, const Params& p, int64_t nb, hipStre
       case F_NORMQ: return launch_train_w4<F_NORMQ>(pl, p, nb, s);
       case F_MASK: return launch_train_w4<F_MASK>(pl, p, nb, s);
       case F_MASK | F_NORMQ: return launch_train_w4<F_MASK | F_NORMQ>(pl, p, nb, s);
+      case F_NORM: return launch_train_w4<F_NORM>(pl, p, nb, s);  // docs normalised in the kernel
       default: break;
     }
   }

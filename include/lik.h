@@ -156,8 +156,10 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
  * flags) zeroes the masked query tokens' terms; doc masks / lengths act only
  * through the argmax. A packed side cannot be normalised here. With
  * LIK_NORMALIZE (both sides), LIK_NORMALIZE_Q or LIK_NORMALIZE_D the
- * gradients are taken through x / max(||x||, 1e-12) on those sides and the
- * caller passes lik_maxsim_backward_workspace_size() bytes.
+ * gradients are taken through x / max(||x||, 1e-12) on those sides. The
+ * caller passes lik_maxsim_backward_workspace_size() bytes of workspace
+ * (inverse norms, and the partial grad_q rows when few query tokens split
+ * their docs over several wavefronts; may be 0).
  * Deterministic: fixed summation order, no atomics.
  * Replaces backward/unified.py:maxsim_backward_unified and
  * backward/lowmem.py:maxsim_backward_lowmem (+ the normalise Jacobian of

@@ -13,7 +13,10 @@
 //
 // * grad_q_kernel: one wavefront per query token (i, s); lanes own d/64
 //   embedding dims. The argmax and G entries of 64 docs are loaded at once
-//   (one per lane) and walked in doc order, so the sum order is fixed.
+//   (one per lane) and walked in doc order, so the sum order is fixed. With
+//   few query tokens (small Nq) the docs are split into fixed chunks, one
+//   wavefront per (chunk, token), and grad_q_finish_kernel adds the chunks'
+//   partial rows in chunk order: still a fixed order.
 // * grad_d_kernel: one wavefront per (doc j, block of RB doc tokens) with an
 //   LDS accumulator of RB rows. It scans the (i, s) pairs in order, 64 query
 //   tokens per ballot; each pair whose winner falls in the block adds its
@@ -77,6 +80,13 @@ struct BwdParams {
   const int32_t* d_list;
   int kd;
   int dim;
+  // grad_q split over docs (dense layouts only): split c of a query token
+  // walks units [c * qchunk, (c + 1) * qchunk) and leaves its fp32 partial
+  // row in gq_part[c][token][64 * DPL]; grad_q_finish_kernel adds the splits
+  // in order. qsplit == 1: one wavefront walks all units and stores grad_q.
+  float* gq_part;
+  int64_t qchunk;
+  int qsplit;
 };
 
 // inv[r] = 1 / max(||row r||, 1e-12) for rows r = i*L + t of a [n, L, dim]
@@ -195,18 +205,52 @@ __device__ __forceinline__ void axpy_lane(float* acc, const char* row, int e0, i
   for (int k = 0; k < DPL; ++k) acc[k] = fmaf(c, x[k], acc[k]);
 }
 
+// Query token w = i * lq + s: its storage row (packed queries: through cu_q),
+// or -1 when s is past query i's length.
+__device__ __forceinline__ int64_t grad_q_row(const BwdParams& bp, int64_t i, int64_t s, int64_t w) {
+  if (!bp.q_cu) return w;
+  const int64_t q0 = bp.q_cu[i];
+  return s < (int64_t)bp.q_cu[i + 1] - q0 ? q0 + s : -1;
+}
+
+// Query mask, the normalisation Jacobian on the finished row, store.
+template <int EK, int DPL>
+__device__ __forceinline__ void grad_q_store(const BwdParams& bp, int64_t i, int64_t s, int64_t qr, float* acc,
+                                             int lane) {
+  const bool keep = !bp.qmask || bp.qmask[i * bp.qm_sn + s * bp.qm_sl] != 0;
+  if (bp.qinv) {
+    const float qi = bp.qinv[qr];
+    const char* qrow = bp.q_cu ? bp.q + qr * bp.q_sl : bp.q + i * bp.q_sn + s * bp.q_sl;
+    float xh[DPL], dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      const int e = lane * DPL + k;
+      xh[k] = e < bp.dim ? load_elem<EK>(qrow, e) * qi : 0.f;
+      dot = fmaf(acc[k], xh[k], dot);
+    }
+    dot = wave_sum(dot);
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) acc[k] = (acc[k] - dot * xh[k]) * qi;
+  }
+  char* out = bp.gq + qr * bp.dim * (int64_t)sizeof_ek<EK>();
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) {
+    const int e = lane * DPL + k;
+    if (e < bp.dim) store_elem<EK>(out, e, keep ? acc[k] : 0.f);
+  }
+}
+
 template <int EK, int DPL>
 __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
   const int lane = threadIdx.x & 63;
-  const int64_t w = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
-  if (w >= bp.nq * bp.lq) return;
+  const int64_t nwt = bp.nq * bp.lq;
+  int64_t w = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  if (w >= nwt * bp.qsplit) return;
+  const int64_t c = w / nwt;  // doc split
+  w -= c * nwt;
   const int64_t i = w / bp.lq, s = w % bp.lq;
-  int64_t qr = w;  // storage row of token (i, s)
-  if (bp.q_cu) {
-    const int64_t q0 = bp.q_cu[i];
-    if (s >= (int64_t)bp.q_cu[i + 1] - q0) return;
-    qr = q0 + s;
-  }
+  const int64_t qr = grad_q_row(bp, i, s, w);  // storage row of token (i, s)
+  if (qr < 0) return;
   const int64_t j0 = bp.kd ? i * bp.ndoc_pg : 0;
   // units of query i: docs jl < ndoc_pg, or its pairs q_list[u0 .. u0 + nu)
   int64_t nu = bp.ndoc_pg, u0 = 0;
@@ -214,14 +258,19 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
     u0 = bp.q_ptr[i];
     nu = (int64_t)bp.q_ptr[i + 1] - u0;
   }
+  int64_t ub = 0, ue = nu;
+  if (bp.qsplit > 1) {
+    ub = c * bp.qchunk;
+    ue = ub + bp.qchunk < nu ? ub + bp.qchunk : nu;
+  }
   float acc[DPL];
 #pragma unroll
   for (int k = 0; k < DPL; ++k) acc[k] = 0.f;
-  for (int64_t c0 = 0; c0 < nu; c0 += 64) {
+  for (int64_t c0 = ub; c0 < ue; c0 += 64) {
     const int64_t jl = c0 + lane;
     int av = -1, jd = 0;
     float gv = 0.f;
-    if (jl < nu) {
+    if (jl < ue) {
       if (bp.q_ptr) {
         const int64_t pr = bp.q_list[u0 + jl];
         av = bp.amax[pr * bp.lq + s];
@@ -264,27 +313,34 @@ __global__ void __launch_bounds__(256) grad_q_kernel(const BwdParams bp) {
       }
     }
   }
-  const bool keep = !bp.qmask || bp.qmask[i * bp.qm_sn + s * bp.qm_sl] != 0;
-  if (bp.qinv) {
-    const float qi = bp.qinv[qr];
-    const char* qrow = bp.q_cu ? bp.q + qr * bp.q_sl : bp.q + i * bp.q_sn + s * bp.q_sl;
-    float xh[DPL], dot = 0.f;
+  if (bp.qsplit > 1) {
+    float* part = bp.gq_part + ((c * nwt + w) * 64 + lane) * DPL;
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) {
-      const int e = lane * DPL + k;
-      xh[k] = e < bp.dim ? load_elem<EK>(qrow, e) * qi : 0.f;
-      dot = fmaf(acc[k], xh[k], dot);
-    }
-    dot = wave_sum(dot);
-#pragma unroll
-    for (int k = 0; k < DPL; ++k) acc[k] = (acc[k] - dot * xh[k]) * qi;
+    for (int k = 0; k < DPL; ++k) part[k] = acc[k];
+    return;
   }
-  char* out = bp.gq + qr * bp.dim * (int64_t)sizeof_ek<EK>();
+  grad_q_store<EK, DPL>(bp, i, s, qr, acc, lane);
+}
+
+// Sum of the doc splits' partial rows, in split order, then the store.
+template <int EK, int DPL>
+__global__ void __launch_bounds__(256) grad_q_finish_kernel(const BwdParams bp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwt = bp.nq * bp.lq;
+  const int64_t w = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  if (w >= nwt) return;
+  const int64_t i = w / bp.lq, s = w % bp.lq;
+  const int64_t qr = grad_q_row(bp, i, s, w);
+  if (qr < 0) return;
+  float acc[DPL];
 #pragma unroll
-  for (int k = 0; k < DPL; ++k) {
-    const int e = lane * DPL + k;
-    if (e < bp.dim) store_elem<EK>(out, e, keep ? acc[k] : 0.f);
+  for (int k = 0; k < DPL; ++k) acc[k] = 0.f;
+  for (int c = 0; c < bp.qsplit; ++c) {
+    const float* part = bp.gq_part + ((c * nwt + w) * 64 + lane) * DPL;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) acc[k] += part[k];
   }
+  grad_q_store<EK, DPL>(bp, i, s, qr, acc, lane);
 }
 
 // Doc rows per grad_d block: every block rescans all the (i, s) pairs of its
@@ -504,8 +560,12 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
   constexpr int RB = grad_d_rows<DPL>();
   const int64_t nw = bp.nq * bp.lq;
   if (nw > 0) {
-    hipLaunchKernelGGL((grad_q_kernel<EK, DPL>), dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, s, bp);
+    hipLaunchKernelGGL((grad_q_kernel<EK, DPL>), dim3((unsigned)((nw * bp.qsplit + 3) / 4)), dim3(256), 0, s, bp);
     if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+    if (bp.qsplit > 1) {
+      hipLaunchKernelGGL((grad_q_finish_kernel<EK, DPL>), dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, s, bp);
+      if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+    }
   }
   // packed docs: sum of lengths <= nd * ld, so nd * ld / RB blocks cover them
   const int64_t nb = !bp.gd ? 0 : bp.d_cu ? (bp.nd * bp.ld + RB - 1) / RB : bp.nd * ((bp.ld + RB - 1) / RB);
@@ -626,12 +686,45 @@ size_t lik_maxsim_pairs_backward_workspace_size(const lik_seqs_t* Q, const lik_s
   return pair_ws_layout(num_pairs, Q->n, D->n).total;
 }
 
-size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
-  if (!Q || !D) return 0;
+// Doc splits of grad_q (dense layouts): when the query tokens alone give
+// fewer than 2048 wavefronts (counting 32 tokens per query), each token's docs
+// are split into chunks of >= 16 so that about 2048 wavefronts walk them. The
+// split depends on Nq and the docs per query only, not on Lq, so a query
+// batch padded to another length gets the same bits.
+static void grad_q_split(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, int64_t* split, int64_t* chunk) {
+  *split = 1;
+  *chunk = 0;
+  if (Q->n <= 0 || D->n <= 0 || Q->len <= 0 || Q->dim <= 0 || Q->dim > 2048) return;
+  const int64_t ndoc = (flags & LIK_KD_LAYOUT) ? D->n / Q->n : D->n;
+  const int64_t want = 2048 / (32 * Q->n), most = (ndoc + 15) / 16;
+  const int64_t ns = want < most ? want : most;
+  if (ns <= 1) return;
+  *chunk = (ndoc + ns - 1) / ns;
+  *split = (ndoc + *chunk - 1) / *chunk;
+}
+
+// fp32 partial rows of the grad_q doc splits: [split][Nq * Lq][64 * DPL]
+static size_t grad_q_part_bytes(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
+  int64_t split, chunk;
+  grad_q_split(Q, D, flags, &split, &chunk);
+  if (split <= 1) return 0;
+  int64_t dpl = 1;
+  while (dpl * 64 < Q->dim) dpl *= 2;
+  return (size_t)(split * Q->n * Q->len * 64 * dpl) * sizeof(float);
+}
+
+// float entries of the inverse-norm arrays at the start of the workspace
+static size_t bwd_norm_floats(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
   size_t n = 0;
   if (bwd_norm_q(flags)) n += (size_t)(Q->n * Q->len);
   if (bwd_norm_d(flags)) n += (size_t)(D->n * D->len);
-  return n ? n * sizeof(float) + 256 : 0;
+  return n;
+}
+
+size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
+  if (!Q || !D || Q->n < 0 || D->n < 0 || Q->len < 0 || D->len < 0) return 0;
+  const size_t b = align256(bwd_norm_floats(Q, D, flags) * sizeof(float)) + grad_q_part_bytes(Q, D, flags);
+  return b ? b + 256 : 0;
 }
 
 int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q, const lik_seqs_t* D,
@@ -654,6 +747,7 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
   hipStream_t s = (hipStream_t)stream;
   const int eb = elem_size(Q->dtype);
   BwdParams bp{};
+  bp.qsplit = 1;
   bp.grad = grad;
   bp.ld_g = grad_ld;
   bp.q = (const char*)Q->data;
@@ -712,6 +806,12 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
       return rc;
     }
   }
+  if (grad_q_part_bytes(Q, D, flags)) {
+    int64_t split;
+    grad_q_split(Q, D, flags, &split, &bp.qchunk);
+    bp.qsplit = (int)split;
+    bp.gq_part = (float*)((char*)workspace + align256(bwd_norm_floats(Q, D, flags) * sizeof(float)));
+  }
   switch (Q->dtype) {
     case LIK_BF16: return launch_bwd_dpl<EK_BF16>(bp, s);
     case LIK_F16: return launch_bwd_dpl<EK_F16>(bp, s);
@@ -761,6 +861,7 @@ int lik_maxsim_pairs_backward(const float* grad, const lik_seqs_t* Q, const lik_
     if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
   }
   BwdParams bp{};
+  bp.qsplit = 1;
   bp.grad = grad;
   bp.ld_g = 1;
   bp.q = (const char*)Q->data;

@@ -259,9 +259,11 @@ def packed_backward(grad, Qp, Dp, cu_q, cu_d, argmax, max_q: int, max_d: int, *,
     qs = _lib.seqs(Qp, n=Nq, length=max_q, stride_l=Qp.stride(0), cu=cu_q)
     ds = _lib.seqs(Dp, n=Nd, length=max(int(max_d), 0), stride_l=Dp.stride(0), cu=cu_d)
     lib = _lib.load()
+    nbytes = lib.lik_maxsim_backward_workspace_size(ctypes.byref(qs), ctypes.byref(ds), 0)
+    ws = _lib.workspace(nbytes, Qp.device)
     with torch.cuda.device(Qp.device):
         rc = lib.lik_maxsim_backward(g.data_ptr(), g.stride(0), ctypes.byref(qs), ctypes.byref(ds), argmax.data_ptr(),
-                                     0, gq.data_ptr(), _lib.ptr(gd), None, 0, _lib.stream_of(gq))
+                                     0, gq.data_ptr(), _lib.ptr(gd), _lib.ptr(ws), nbytes, _lib.stream_of(gq))
     _lib.check(rc, "lik_maxsim_backward")
     return gq, gd
 

@@ -92,6 +92,29 @@ def test_argmax_and_grads_match_oracle(dtype, tol, gap, normalize, kd):
     assert np.all(_np(gd)[0] == 0)  # fully masked doc: no winners, zero grad
 
 
+@pytest.mark.parametrize("Nq,kd", [(1, False), (2, False), (3, True)])
+def test_grad_q_doc_splits(Nq, kd):
+    """Few query tokens and many docs: grad_q splits each token's docs into
+    chunks walked by separate wavefronts and adds the chunk sums in order.
+    Against the oracle (fp32 inputs, 1e-5), chunk edges not on a 64-doc
+    boundary, and bitwise equal on a second run."""
+    from late_interaction_kernels._core import dense_maxsim_train, maxsim_backward
+
+    _case(f"bwd grad_q splits Nq={Nq} kd={kd}")
+    Lq, d, Ld = 20, 64, 30
+    Nd = Nq * 333 if kd else 701
+    Q, D, qm, dm = _inputs(Nq, Nd, Lq, Ld, d, torch.float32, 40 + Nq)
+    scores, am, Qp, Dp, qmi = dense_maxsim_train(Q.cuda(), D.cuda(), qm.cuda(), dm.cuda(), norm=3, kd=kd)
+    docs = Nd // Nq if kd else Nd
+    G = torch.randn(Nq, docs)
+    gq, gd = maxsim_backward(G.cuda(), Qp, Dp, am, qmi, norm=3, kd=kd)
+    rq, rd = O.maxsim_grads(G.numpy(), _np(Q), _np(D), am.cpu().numpy(), qm.numpy(), normalize=True, kd=kd)
+    assert rel_err(_np(gq), rq) < 1e-5
+    assert rel_err(_np(gd), rd) < 1e-5
+    gq2, _ = maxsim_backward(G.cuda(), Qp, Dp, am, qmi, norm=3, kd=kd)
+    assert torch.equal(gq, gq2)
+
+
 def _torch_ref(Q, D, qm, dm, normalize):
     """Plain fp32 autograd restatement of the forward (reference.py:26-98)."""
     if normalize:

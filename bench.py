@@ -596,6 +596,7 @@ def wl_fused_head(args):
     ``value`` = geometric mean speedup."""
     import torch
 
+    from late_interaction_kernels.autograd import _score
     from late_interaction_kernels.fused_head import maxsim_from_hidden
 
     rows = []
@@ -624,9 +625,30 @@ def wl_fused_head(args):
         e.record()
         _sync()
         ms = a.elapsed_time(e) / n
-        rows.append({"shape": name, "ms": round(ms, 4), "ref_h100_fused_ms": ref_ms,
-                     "speedup": round(ref_ms / ms, 2),
-                     "peak_mb": round(torch.cuda.max_memory_allocated() / 2**20, 1)})
+        row = {"shape": name, "ms": round(ms, 4), "ref_h100_fused_ms": ref_ms,
+               "speedup": round(ref_ms / ms, 2),
+               "peak_mb": round(torch.cuda.max_memory_allocated() / 2**20, 1)}
+        # inference (no grad): the fused kernel against projecting first
+        # (hipBLASLt GEMM, then the MaxSim kernel on the materialised docs)
+        with torch.no_grad():
+            Qd, Hd, Wd, bd = Q.detach(), H.detach(), W.detach(), b.detach()
+
+            def projected():
+                D = torch.nn.functional.linear(Hd, Wd, bd)
+                return _score(Qd, D, None, None, normalize=2)
+
+            for label, fn in (("infer_fused_ms", lambda: maxsim_from_hidden(Qd, Hd, Wd, bd, normalize=True)),
+                              ("infer_projected_ms", projected)):
+                for _ in range(3):
+                    fn()
+                _sync()
+                a.record()
+                for _ in range(n):
+                    fn()
+                e.record()
+                _sync()
+                row[label] = round(a.elapsed_time(e) / n, 4)
+        rows.append(row)
         del H, W, b, Q
         torch.cuda.empty_cache()
     gm = math.exp(sum(math.log(r["speedup"]) for r in rows) / len(rows))

@@ -146,6 +146,29 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
                       size_t workspace_bytes, lik_stream_t stream);
 
 /*
+ * MaxSim against docs given as hidden states through a linear head, without
+ * forming the projected docs: D[j, t] = H[j, t] @ W^T + b, each row L2
+ * normalised (x / max(||x||, 1e-12)) with LIK_NORMALIZE_D, rounded to the
+ * input dtype, then score[i, j] as lik_maxsim (cross product, out_scale 1).
+ * Q: padded [Q->n, Q->len, d_out], already projected (and normalised by the
+ * caller if wanted), no mask. H: padded [H->n, H->len, d_model] with its mask
+ * and lengths marking the doc tokens that can win. W: [d_out, d_model] with
+ * row stride w_stride elements; bias: fp32 [d_out] or NULL. bf16 / f16 (Q, H
+ * and W in one dtype); d_out <= 128; Q->n * Q->len <= 256; d_model, the H
+ * strides and w_stride multiples of 8; H and W 16-byte aligned (other shapes:
+ * LIK_ERR_UNSUPPORTED, and the caller projects first). argmax (optional)
+ * as lik_maxsim_argmax: [(i * H->n + j) * Q->len + s], -1 for no valid token.
+ * Workspace: lik_maxsim_from_hidden_workspace_size() bytes.
+ * Replaces fused_head.py:_fused_head_forward (fused_head.py:192-259)
+ * launching _fused_head_fwd_kernel (fused_head.py:46-189).
+ */
+int lik_maxsim_from_hidden(const lik_seqs_t* Q, const lik_seqs_t* H, const void* W, int64_t w_stride,
+                           const float* bias, uint32_t flags, float* out, int64_t out_stride_q,
+                           int64_t out_stride_d, int32_t* argmax, void* workspace, size_t workspace_bytes,
+                           lik_stream_t stream);
+size_t lik_maxsim_from_hidden_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* H);
+
+/*
  * Backward: given grad[i * grad_ld + j] = dL/dscore[i, j] (fp32) and the
  * argmax of lik_maxsim_argmax, writes grad_q [Q->n, Q->len, dim] and grad_d
  * [D->n, D->len, dim], contiguous, in the dtype of Q and D (accumulated in

@@ -1,0 +1,438 @@
+// Projection head fused into MaxSim for gfx950: scores of queries Q against
+// docs given as hidden states H [Nd, Ld, d_model] and a linear head (W, b),
+//   D[j, t] = normalize(H[j, t] @ W^T + b),  score[i, j] = sum_s max_t <Q[i, s], D[j, t]>,
+// without forming D in memory. Semantics of the reference's fused head
+// (late_interaction_kernels/fused_head.py:46-189, 262-332): fp32 projection of
+// 16-bit H and W, bias and row L2-normalise in fp32, the normalised row
+// rounded to the input dtype for the MaxSim product, a doc token that is
+// masked (or past the doc's length) never wins, a query token whose doc has
+// no valid token scores 0 and gets argmax -1, ties go to the lowest doc token.
+//
+// head_tile_kernel: one workgroup of 8 wavefronts per (doc j, chunk of 256
+// doc tokens); wavefront w owns tokens [256 c + 32 w, +32).
+//  * Projection as P^T = W . H^T on 32x32x16 MFMAs: W (A operand, 32 output
+//    dims per lane row) is staged in LDS one k-unit (64 model dims) at a time,
+//    double-buffered and shared by the 8 wavefronts; H (B operand, one doc
+//    token per lane row) is read straight from HBM into registers, each lane
+//    64 contiguous bytes of its token per unit, two units ahead of the MFMAs.
+//    Within a unit, lane half h supplies model dims [32 h, 32 h + 32) and k-step
+//    kk the 8 dims at 8 kk of them: the same order for W and H, so the
+//    contraction runs over the same dims whatever the pairing.
+//  * The accumulators start at the bias. Element e of lane (l32, h) holds
+//    output dim 32 n + 8 (e / 4) + 4 h + e % 4 of doc token l32, so a token's
+//    squared norm is the lane's sum plus its partner lane's (l32 + 32).
+//  * The normalised, rounded values are the A operand of the MaxSim MFMAs
+//    as they sit: k-step (n, kk2) is the lane's elements 8 kk2 .. 8 kk2 + 7,
+//    and the query fragments (B operand, staged once per workgroup in LDS)
+//    are built with that same dim order. No transpose through LDS.
+//  * Max over the 32 tokens in registers (plus one exchange between the lane
+//    halves), then over the 8 wavefronts in LDS in token order; the chunk's
+//    (max, argmax) per query token goes to the workspace.
+// head_finish_kernel: per (query i, doc j), the chunks in order, then the sum
+// over the query tokens in order: a fixed order, so the bits do not depend on
+// scheduling.
+#include "lik_common.h"
+
+namespace lik {
+
+namespace {
+
+#ifndef LIK_HEAD_AUX
+#define LIK_HEAD_AUX 2
+#endif
+#ifndef LIK_HEAD_NW
+#define LIK_HEAD_NW 8
+#endif
+constexpr int HEAD_WAVES = LIK_HEAD_NW;     // wavefronts per workgroup
+constexpr int HEAD_THREADS = 64 * HEAD_WAVES;
+constexpr int HEAD_ROWS = 32 * HEAD_WAVES;  // doc tokens per workgroup
+constexpr int HEAD_MAXCOL = 256;            // query tokens (Nq * Lq) per call
+constexpr int HEAD_MAXNB = 4;               // 32-wide output blocks (d_out <= 128)
+
+struct HeadParams {
+  const char* q;  // Q rows: q + i * q_sn + s * q_sl (bytes)
+  int64_t q_sn, q_sl;
+  const char* h;  // H rows: h + j * h_sn + t * h_sl (bytes)
+  int64_t h_sn, h_sl;
+  const char* w;  // W rows: w + o * w_sl (bytes)
+  int64_t w_sl;
+  const float* bias;  // [d_out] or null
+  const int8_t* dmask;  // keep flags, or null
+  int64_t dm_sn, dm_sl;
+  const int32_t* dlen;  // doc lengths, or null
+  float2* part;         // [ncol][nd][nchunk] (max, argmax bits)
+  float* out;
+  int64_t os_q, os_d;
+  int32_t* amax;  // [(i * nd + j) * lq + s], or null
+  int nq, lq, ncol, nd, ld, dmodel, dout, nchunk, nunit, norm;
+};
+
+constexpr uint32_t kHeadOOB = 0xffffffffu;  // buffer offset past num_records: the load returns 0, no fetch
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void* base, uint32_t nbytes) {
+  // dword3 0x00020000: raw (untyped) access, stride 0, byte range check
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
+}
+
+template <int EK>
+__device__ __forceinline__ uint32_t to16(float f) {
+  if constexpr (EK == EK_F16) return f32_to_f16_bits(f);
+  else return f32_to_bf16_bits(f);
+}
+
+template <int EK>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return to16<EK>(a) | (to16<EK>(b) << 16);
+}
+
+template <int EK, int NB>
+__global__ void __launch_bounds__(HEAD_THREADS) head_tile_kernel(const HeadParams p) {
+  constexpr int KS2 = 2 * NB;  // MaxSim k-steps over the (padded) output dims
+  __shared__ u32x4 s_w[2][NB * 4 * 64];
+  extern __shared__ u32x4 s_q[];  // [ncb * KS2 * 64], sized at launch
+  __shared__ float2 s_red[HEAD_WAVES][HEAD_MAXCOL];
+  __shared__ float s_bias[32 * NB];
+  __shared__ u32x4 s_h[HEAD_WAVES * 32 * 9];  // per-wave H unit tile
+
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t j = blockIdx.x / p.nchunk;
+  const int chunk = blockIdx.x - (int)j * p.nchunk;
+  const int ncb = (p.ncol + 31) >> 5;
+
+  // query fragments: k-step ks = (n, kk2) of column block cb, lane (col, h):
+  // dims 32 n + 16 kk2 + 4 h + {0..3} and the same + 8
+  for (int f = tid; f < ncb * KS2 * 64; f += HEAD_THREADS) {
+    const int ln = f & 63, ks = (f >> 6) % KS2, cb = f / (64 * KS2);
+    const int col = cb * 32 + (ln & 31), h = ln >> 5;
+    const int base = 32 * (ks >> 1) + 16 * (ks & 1) + 4 * h;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (col < p.ncol) {
+      const int i = col / p.lq, s = col - i * p.lq;
+      const uint16_t* row = (const uint16_t*)(p.q + i * p.q_sn + s * p.q_sl);
+      uint32_t e16[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int d = base + (k < 4 ? k : k + 4);
+        e16[k] = d < p.dout ? row[d] : 0u;
+      }
+      v = u32x4{e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16), e16[4] | (e16[5] << 16), e16[6] | (e16[7] << 16)};
+    }
+    s_q[f] = v;
+  }
+  if (tid < 32 * NB) s_bias[tid] = (p.bias && tid < p.dout) ? p.bias[tid] : 0.f;
+
+  // this lane's doc token and whether it takes part (in the doc, kept)
+  const int t = chunk * HEAD_ROWS + wave * 32 + l32;
+  const int dl = p.dlen ? min(p.dlen[j], p.ld) : p.ld;
+  bool valid = t < dl;
+  if (valid && p.dmask) valid = p.dmask[j * p.dm_sn + (int64_t)t * p.dm_sl] != 0;
+  const uint64_t vb = __ballot(valid);
+  const bool wave_on = (uint32_t)vb != 0u;  // any kept token in this wave's 32
+  // Every global load of the loop is issued by every lane (an offset out of
+  // range returns 0 without a fetch), so the compiler can count them.
+  // H: this doc's rows [0, ld); a lane whose token is not kept fetches nothing
+  const __amdgpu_buffer_rsrc_t rh =
+      head_rsrc(p.h + j * p.h_sn, (uint32_t)((int64_t)(p.ld - 1) * p.h_sl + 2 * (int64_t)p.dmodel));
+  // W fragment f = (n, kk, lane) of unit u: out dim 32 n + l32, model dims
+  // 64 u + 32 h + 8 kk .. + 8
+  const __amdgpu_buffer_rsrc_t rw =
+      head_rsrc(p.w, (uint32_t)((int64_t)(p.dout - 1) * p.w_sl + 2 * (int64_t)p.dmodel));
+  // fragments per thread: the unit has NB * 256 of them
+  constexpr int WPT = (NB * 256 + HEAD_THREADS - 1) / HEAD_THREADS;
+  auto load_w = [&](u32x4* dst, int u) {
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+      const int f = tid + HEAD_THREADS * k;
+      const int o = 32 * (f >> 8) + (f & 31), hw = (f >> 5) & 1, kw = (f >> 6) & 3;
+      const int e = 64 * u + 32 * hw + 8 * kw;
+      const bool on = f < NB * 256 && o < p.dout && e < p.dmodel;
+      dst[k] = __builtin_amdgcn_raw_buffer_load_b128(rw, on ? (uint32_t)(o * p.w_sl) + 2u * (uint32_t)e : kHeadOOB, 0, 0);
+    }
+  };
+  auto store_w = [&](int buf, const u32x4* v) {
+#pragma unroll
+    for (int k = 0; k < WPT; ++k)
+      if (tid + HEAD_THREADS * k < NB * 256) s_w[buf][tid + HEAD_THREADS * k] = v[k];
+  };
+  // H unit u of this wave's 32 tokens: instruction c reads tokens 8 c .. 8 c + 7,
+  // 8 lanes x 16 bytes each (coalesced 128-byte row segments); a token that is
+  // not kept fetches nothing. The unit goes through the wave's LDS tile
+  // (rows padded to 144 bytes: conflict-free fragment reads) into the B
+  // fragments: lane (l32, h), k-step kk = token l32, model dims 64 u + 32 h + 8 kk.
+  const int crow = lane >> 3, cseg = lane & 7;
+  uint32_t coff[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int r = 8 * c + crow;
+    coff[c] = ((vb >> r) & 1u) ? (uint32_t)((int64_t)(chunk * HEAD_ROWS + wave * 32 + r) * p.h_sl) + 16u * cseg
+                               : kHeadOOB;
+  }
+  auto load_h = [&](u32x4* dst, int u) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool on = coff[c] != kHeadOOB && u < p.nunit && 64 * u + 8 * cseg < p.dmodel;
+      dst[c] = __builtin_amdgcn_raw_buffer_load_b128(rh, on ? coff[c] + 128u * u : kHeadOOB, 0, LIK_HEAD_AUX);
+    }
+  };
+  u32x4* tile = s_h + wave * (32 * 9);  // 32 rows x 9 slots of 16 bytes
+  auto frag_h = [&](const u32x4* g, u32x4* bf) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) tile[(8 * c + crow) * 9 + cseg] = g[c];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) bf[kk] = tile[l32 * 9 + 4 * hh + kk];
+  };
+
+  // accumulators start at the bias
+  f32x16 acc[NB];
+  __syncthreads();  // s_bias
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[n][4 * g + r] = s_bias[32 * n + 8 * g + 4 * hh + r];
+    }
+  }
+  // H and W three units ahead of the MFMAs (register rings of 4; W unit u + 1
+  // goes to LDS at the end of step u)
+  u32x4 hb[4][4];
+  u32x4 wr[4][WPT];
+  load_w(wr[0], 0);
+  store_w(0, wr[0]);
+  load_w(wr[1], 1);
+  load_w(wr[2], 2);
+  load_h(hb[0], 0);
+  load_h(hb[1], 1);
+  load_h(hb[2], 2);
+  __syncthreads();
+
+  auto step = [&](auto slot_c, int u) {
+    constexpr int S = decltype(slot_c)::value;  // u % 4
+    load_w(wr[(S + 3) & 3], u + 3);  // past the last unit: out of range, no fetch
+    load_h(hb[(S + 3) & 3], u + 3);
+    if (wave_on) {
+      u32x4 bf[4];
+      frag_h(hb[S], bf);
+      const u32x4* sw = s_w[u & 1];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+          const u32x4 a = sw[(n * 4 + kk) * 64 + lane];
+          acc[n] = mfma32<EK>(acc[n], &a, &bf[kk]);
+        }
+      }
+    }
+    if (u + 1 < p.nunit) store_w((u + 1) & 1, wr[(S + 1) & 3]);
+    __syncthreads();
+  };
+  for (int u = 0; u < p.nunit; u += 4) {
+    step(std::integral_constant<int, 0>{}, u);
+    if (u + 1 < p.nunit) step(std::integral_constant<int, 1>{}, u + 1);
+    if (u + 2 < p.nunit) step(std::integral_constant<int, 2>{}, u + 2);
+    if (u + 3 < p.nunit) step(std::integral_constant<int, 3>{}, u + 3);
+  }
+
+  // row L2 normalise (x / max(||x||, 1e-12)), round to the input dtype: the
+  // A fragments of the MaxSim MFMAs
+  float ss = 0.f;
+#pragma unroll
+  for (int n = 0; n < NB; ++n)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ss = fmaf(acc[n][e], acc[n][e], ss);
+  ss += __shfl_xor(ss, 32);
+  const float inv = p.norm ? inv_norm(ss) : 1.f;
+  u32x4 df[KS2];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const int e0 = 8 * k2;
+      df[2 * n + k2] = u32x4{pack2<EK>(acc[n][e0] * inv, acc[n][e0 + 1] * inv),
+                             pack2<EK>(acc[n][e0 + 2] * inv, acc[n][e0 + 3] * inv),
+                             pack2<EK>(acc[n][e0 + 4] * inv, acc[n][e0 + 5] * inv),
+                             pack2<EK>(acc[n][e0 + 6] * inv, acc[n][e0 + 7] * inv)};
+    }
+  }
+
+  const uint32_t vrow = (uint32_t)vb;  // bit r: token r of this wave is kept
+  for (int cb = 0; cb < ncb; ++cb) {
+    float m = -INFINITY;
+    int idx = -1;
+    if (wave_on) {
+      f32x16 c = {};
+#pragma unroll
+      for (int ks = 0; ks < KS2; ++ks) {
+        const u32x4 b = s_q[(cb * KS2 + ks) * 64 + lane];
+        c = mfma32<EK>(c, &df[ks], &b);
+      }
+      // element e: doc token 8 (e / 4) + 4 h + e % 4 (increasing in e), query column l32
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = 8 * (e >> 2) + 4 * hh + (e & 3);
+        if (((vrow >> r) & 1u) && c[e] > m) {
+          m = c[e];
+          idx = r;
+        }
+      }
+      const float om = __shfl_xor(m, 32);
+      const int oi = __shfl_xor(idx, 32);
+      if (om > m || (om == m && oi >= 0 && (idx < 0 || oi < idx))) {
+        m = om;
+        idx = oi;
+      }
+    }
+    if (hh == 0) s_red[wave][cb * 32 + l32] = float2{m, __int_as_float(idx < 0 ? -1 : wave * 32 + idx)};
+  }
+  __syncthreads();
+  if (tid < p.ncol) {
+    float m = -INFINITY;
+    int idx = -1;
+    for (int w = 0; w < HEAD_WAVES; ++w) {
+      const float2 v = s_red[w][tid];
+      if (v.x > m) {
+        m = v.x;
+        idx = __float_as_int(v.y);
+      }
+    }
+    p.part[((int64_t)tid * p.nd + j) * p.nchunk + chunk] =
+        float2{m, __int_as_float(idx < 0 ? -1 : chunk * HEAD_ROWS + idx)};
+  }
+}
+
+// One wavefront per (query i, doc j): lane l takes query tokens l, l + 64, ...
+// (chunks in order, then its tokens in order), then a fixed shuffle tree.
+__global__ void __launch_bounds__(256) head_finish_kernel(const HeadParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (u >= (int64_t)p.nq * p.nd) return;
+  const int64_t i = u / p.nd, j = u - i * p.nd;
+  float sum = 0.f;
+  for (int s = lane; s < p.lq; s += 64) {
+    const int64_t col = i * p.lq + s;
+    float m = -INFINITY;
+    int idx = -1;
+    for (int c = 0; c < p.nchunk; ++c) {
+      const float2 v = p.part[(col * p.nd + j) * p.nchunk + c];
+      if (v.x > m) {
+        m = v.x;
+        idx = __float_as_int(v.y);
+      }
+    }
+    const bool any = m > -INFINITY;
+    sum += any ? m : 0.f;
+    if (p.amax) p.amax[(i * p.nd + j) * p.lq + s] = any ? idx : -1;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+  if (lane == 0) p.out[i * p.os_q + j * p.os_d] = sum;
+}
+
+template <int EK>
+int launch_head(const HeadParams& p, hipStream_t s) {
+  const int nb = (p.dout + 31) / 32;
+  const int64_t grid = (int64_t)p.nd * p.nchunk;
+  if (grid > 0) {
+    // query fragments: 32-column blocks x 2 NB k-steps x 64 lanes x 16 bytes
+    const size_t qlds = (size_t)((p.ncol + 31) / 32) * (2 * nb) * 64 * 16;
+    const dim3 g((unsigned)grid), b(HEAD_THREADS);
+    switch (nb) {
+      case 1: hipLaunchKernelGGL((head_tile_kernel<EK, 1>), g, b, qlds, s, p); break;
+      case 2: hipLaunchKernelGGL((head_tile_kernel<EK, 2>), g, b, qlds, s, p); break;
+      case 3: hipLaunchKernelGGL((head_tile_kernel<EK, 3>), g, b, qlds, s, p); break;
+      default: hipLaunchKernelGGL((head_tile_kernel<EK, 4>), g, b, qlds, s, p); break;
+    }
+    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+  }
+  const int64_t nu = (int64_t)p.nq * p.nd;
+  hipLaunchKernelGGL(head_finish_kernel, dim3((unsigned)((nu + 3) / 4)), dim3(256), 0, s, p);
+  return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+}
+
+// shape checks shared by the entry point and its workspace query
+int head_check(const lik_seqs_t* Q, const lik_seqs_t* H, const void* W, int64_t w_stride) {
+  if (!Q || !H) return LIK_ERR_INVALID;
+  if (Q->dtype != H->dtype) return LIK_ERR_INVALID;
+  if (Q->dtype != LIK_BF16 && Q->dtype != LIK_F16) return LIK_ERR_UNSUPPORTED;
+  if (Q->n < 0 || Q->len < 0 || H->n < 0 || H->len < 0 || Q->dim <= 0 || H->dim <= 0) return LIK_ERR_INVALID;
+  if (Q->cu_seqlens || Q->lengths || Q->mask || Q->token_scale) return LIK_ERR_UNSUPPORTED;
+  if (H->cu_seqlens || H->token_scale) return LIK_ERR_UNSUPPORTED;
+  if (Q->dim > 32 * HEAD_MAXNB || Q->n * Q->len > HEAD_MAXCOL) return LIK_ERR_UNSUPPORTED;
+  if (H->dim % 8 || H->stride_n % 8 || H->stride_l % 8 || w_stride % 8 || w_stride < H->dim) return LIK_ERR_UNSUPPORTED;
+  if (H->len > 0x7fffff00LL || H->n > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  // 32-bit buffer offsets: one doc's rows and all of W within 4 GB
+  if (H->len * H->stride_l * 2 >= ((int64_t)1 << 32) - 256 || Q->dim * w_stride * 2 >= ((int64_t)1 << 32) - 256)
+    return LIK_ERR_UNSUPPORTED;
+  if (((uintptr_t)H->data) % 16 || ((uintptr_t)W) % 16) return LIK_ERR_UNSUPPORTED;
+  return LIK_OK;
+}
+
+size_t head_part_bytes(const lik_seqs_t* Q, const lik_seqs_t* H) {
+  const int64_t nchunk = (H->len + HEAD_ROWS - 1) / HEAD_ROWS;
+  return (size_t)(Q->n * Q->len) * (size_t)H->n * (size_t)nchunk * sizeof(float2);
+}
+
+}  // namespace
+
+}  // namespace lik
+
+using namespace lik;
+
+extern "C" {
+
+size_t lik_maxsim_from_hidden_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* H) {
+  if (!Q || !H || Q->n < 0 || Q->len < 0 || H->n < 0 || H->len < 0) return 0;
+  const size_t b = head_part_bytes(Q, H);
+  return b ? b + 256 : 0;
+}
+
+int lik_maxsim_from_hidden(const lik_seqs_t* Q, const lik_seqs_t* H, const void* W, int64_t w_stride,
+                           const float* bias, uint32_t flags, float* out, int64_t out_stride_q,
+                           int64_t out_stride_d, int32_t* argmax, void* workspace, size_t workspace_bytes,
+                           lik_stream_t stream) {
+  int rc = head_check(Q, H, W, w_stride);
+  if (rc != LIK_OK) return rc;
+  if (flags & ~(uint32_t)LIK_NORMALIZE_D) return LIK_ERR_INVALID;
+  if (Q->n == 0 || H->n == 0) return LIK_OK;
+  if (!out || !Q->data || (!H->data && H->len > 0) || !W) return LIK_ERR_INVALID;
+  const size_t need = lik_maxsim_from_hidden_workspace_size(Q, H);
+  if (need && (!workspace || workspace_bytes < need)) return LIK_ERR_WORKSPACE;
+  HeadParams p{};
+  p.q = (const char*)Q->data;
+  p.q_sn = Q->stride_n * 2;
+  p.q_sl = Q->stride_l * 2;
+  p.h = (const char*)H->data;
+  p.h_sn = H->stride_n * 2;
+  p.h_sl = H->stride_l * 2;
+  p.w = (const char*)W;
+  p.w_sl = w_stride * 2;
+  p.bias = bias;
+  p.dmask = H->mask;
+  p.dm_sn = H->mask_stride_n;
+  p.dm_sl = H->mask_stride_l;
+  p.dlen = H->lengths;
+  p.part = (float2*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  p.out = out;
+  p.os_q = out_stride_q;
+  p.os_d = out_stride_d;
+  p.amax = argmax;
+  p.nq = (int)Q->n;
+  p.lq = (int)Q->len;
+  p.ncol = (int)(Q->n * Q->len);
+  p.nd = (int)H->n;
+  p.ld = (int)H->len;
+  p.dmodel = H->dim;
+  p.dout = Q->dim;
+  p.nchunk = (int)((H->len + HEAD_ROWS - 1) / HEAD_ROWS);
+  p.nunit = (H->dim + 63) / 64;
+  p.norm = (flags & LIK_NORMALIZE_D) ? 1 : 0;
+  if (p.lq == 0) {
+    // no query tokens: every score is 0
+    p.nchunk = 0;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  return Q->dtype == LIK_F16 ? launch_head<EK_F16>(p, s) : launch_head<EK_BF16>(p, s);
+}
+
+}  // extern "C"

@@ -374,3 +374,41 @@ def assert_max_seqlen_covers(cu: torch.Tensor, max_seqlen: int, name: str) -> No
         f"{name}={max_seqlen} is smaller than the longest sequence in cu_seqlens; "
         "it is a hard bound and would silently truncate tokens.",
     )
+
+
+def from_hidden_forward(Q, H, W, b, d_mask, *, normalize: bool, want_argmax: bool):
+    """Projection head fused into MaxSim (``lik_maxsim_from_hidden``): scores of
+    ``Q [Nq, Lq, d_out]`` against ``normalize(H @ W^T + b)`` for ``H [Nd, Ld, d_model]``
+    without forming the projected docs. Returns ``(scores, argmax or None)``, or
+    ``None`` when the library reports the shape or dtype unsupported (the
+    caller then projects first)."""
+    _lib.require_gpu(Q, H, W, b, d_mask)
+    if not (Q.dtype == H.dtype == W.dtype and Q.dtype in (torch.bfloat16, torch.float16)):
+        return None
+    Nq, Lq, d_out = Q.shape
+    Nd, Ld, _ = H.shape
+    out = torch.zeros(Nq, Nd, device=Q.device, dtype=torch.float32)
+    argmax = torch.full((Nq * Nd, Lq), -1, device=Q.device, dtype=torch.int32) if want_argmax else None
+    Qc = Q.detach().contiguous()
+    Hc = H.detach()
+    if Hc.stride(-1) != 1 or Hc.data_ptr() % 16 or any(s % 8 for s in Hc.stride()[:-1]):
+        Hc = Hc.contiguous()
+    Wc = W.detach().contiguous()
+    bias = None if b is None else b.detach().to(torch.float32).contiguous()
+    dm = _mask_i8(d_mask, (Nd, Ld))
+    qs = _lib.seqs(Qc, n=Nq, length=Lq, stride_n=Qc.stride(0), stride_l=Qc.stride(1))
+    hs = _lib.seqs(Hc, n=Nd, length=Ld, stride_n=Hc.stride(0), stride_l=Hc.stride(1), mask=dm,
+                   mask_strides=(dm.stride(0), dm.stride(1)) if dm is not None else (0, 0))
+    lib = _lib.load()
+    nbytes = lib.lik_maxsim_from_hidden_workspace_size(ctypes.byref(qs), ctypes.byref(hs))
+    ws = _lib.workspace(nbytes, Q.device)
+    flags = _lib.LIK_NORMALIZE_D if normalize else 0
+    with torch.cuda.device(Q.device):
+        rc = lib.lik_maxsim_from_hidden(ctypes.byref(qs), ctypes.byref(hs), Wc.data_ptr(), Wc.stride(0),
+                                        _lib.ptr(bias), flags, out.data_ptr(), out.stride(0), out.stride(1),
+                                        _lib.ptr(argmax), _lib.ptr(ws), nbytes, _lib.stream_of(out))
+    if rc == _lib.LIK_ERR_UNSUPPORTED:
+        return None
+    _lib.check(rc, "lik_maxsim_from_hidden")
+    return out, argmax
+

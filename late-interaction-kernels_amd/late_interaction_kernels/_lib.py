@@ -47,6 +47,8 @@ EXPORTED_SYMBOLS = (
     "lik_maxsim",
     "lik_maxsim_workspace_size",
     "lik_maxsim_argmax",
+    "lik_maxsim_from_hidden",
+    "lik_maxsim_from_hidden_workspace_size",
     "lik_maxsim_backward",
     "lik_maxsim_backward_workspace_size",
     "lik_maxsim_pairs",
@@ -161,6 +163,11 @@ def load() -> ctypes.CDLL:
     lib.lik_maxsim_argmax.argtypes = [P(LikSeqs), P(LikSeqs), ctypes.c_uint32, _p, _i64, _i64, _p, _p,
                                       ctypes.c_size_t, _p]
     lib.lik_maxsim_argmax.restype = ctypes.c_int
+    lib.lik_maxsim_from_hidden.argtypes = [P(LikSeqs), P(LikSeqs), _p, _i64, _p, ctypes.c_uint32, _p, _i64, _i64,
+                                           _p, _p, ctypes.c_size_t, _p]
+    lib.lik_maxsim_from_hidden.restype = ctypes.c_int
+    lib.lik_maxsim_from_hidden_workspace_size.argtypes = [P(LikSeqs), P(LikSeqs)]
+    lib.lik_maxsim_from_hidden_workspace_size.restype = ctypes.c_size_t
     lib.lik_maxsim_backward.argtypes = [_p, _i64, P(LikSeqs), P(LikSeqs), _p, ctypes.c_uint32, _p, _p, _p,
                                         ctypes.c_size_t, _p]
     lib.lik_maxsim_backward.restype = ctypes.c_int

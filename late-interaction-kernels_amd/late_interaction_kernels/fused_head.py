@@ -1,20 +1,25 @@
 """``maxsim_from_hidden``: MaxSim with the doc-side projection head in front
 (reference fused_head.py:262-332).
 
-Computes ``maxsim(Q, normalize(F.linear(H_d, W, b)))`` with the doc-token
-normalisation inside the MaxSim kernel (``LIK_NORMALIZE_D``; Q is taken as
-already projected and normalised, as in the reference).
+Computes ``maxsim(Q, normalize(F.linear(H_d, W, b)))``; Q is taken as already
+projected and normalised, as in the reference.
 
-Forward: the projection is one GEMM (hipBLASLt through ``F.linear``, at its
-GEMM rate; ``D`` costs ``Nd * Ld * d_out`` elements of HBM, a few hundred MB
-at the reference's largest shape against 288 GB), then the MaxSim tile
-kernel. Backward (when anything requires grad): the HIP MaxSim backward gives
-grad_Q and grad_D; grad_D is nonzero only on the doc rows that win a max
-(at most ``Nq * Nd * Lq`` of ``Nd * Ld``), so the projection's gradients are
-taken on those rows alone: grad_W = g^T H_win, grad_b = sum g, and grad_H =
-g W scattered into a zeroed tensor. The reference's fused kernel gets the
-same sparsity by gathering ``H_d`` at winning positions
-(fused_head.py:1-17); here the winners are found from the saved argmax.
+Inference (nothing requires grad): one HIP kernel (``lik_maxsim_from_hidden``)
+projects each 32-token tile of H on the MFMA units, adds the bias, normalises
+and rounds the rows in registers and scores them against the queries: the
+projected docs never reach memory (reference fused_head.py:46-189). Shapes
+the kernel does not take (fp32 inputs, d_out > 128, more than 256 query
+tokens) project with one GEMM (``F.linear``) and score the materialised docs.
+
+Training: the projection is one GEMM, then the argmax-saving MaxSim kernel
+with the doc-only normalise. Only doc tokens that won some query token's max
+have a gradient, so the projection's gradients are taken on those rows alone:
+grad_W = g^T H_win, grad_b = sum g and grad_H = g W scattered into a zeroed
+tensor (the reference's backward, fused_head.py:347-460, gathers H at the
+winners the same way). Projecting first is the faster training route here:
+with the fused forward, the backward has to gather and project the winning
+rows again, and those extra small launches cost more than the fused forward
+saves on the reference's training shapes.
 """
 
 from __future__ import annotations
@@ -22,7 +27,7 @@ from __future__ import annotations
 import torch
 
 from .autograd import _needs_grad, _score, _validate_devices
-from ._core import dense_maxsim_train, maxsim_backward, unify_dtype
+from ._core import dense_maxsim_train, from_hidden_forward, maxsim_backward, unify_dtype
 
 
 class _FromHiddenFn(torch.autograd.Function):
@@ -95,9 +100,13 @@ def maxsim_from_hidden(
             raise TypeError("maxsim_from_hidden gradients support fp16 / bf16 / fp32 inputs")
         scores = _FromHiddenFn.apply(Q, H_d, W, b, d_mask, bool(normalize))
     else:
-        D = torch.nn.functional.linear(H_d, W, b)
-        Qc, Dc = unify_dtype(Q, D)
-        scores = _score(Qc, Dc, None, d_mask, normalize=2 if normalize else 0)
+        fused = from_hidden_forward(Q, H_d, W, b, d_mask, normalize=bool(normalize), want_argmax=False)
+        if fused is not None:
+            scores = fused[0]
+        else:
+            D = torch.nn.functional.linear(H_d, W, b)
+            Qc, Dc = unify_dtype(Q, D)
+            scores = _score(Qc, Dc, None, d_mask, normalize=2 if normalize else 0)
     return scores.squeeze(0) if q_was_2d else scores
 
 

@@ -168,12 +168,16 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_tile_kernel(const HeadParam
     coff[c] = ((vb >> r) & 1u) ? (uint32_t)((int64_t)(chunk * HEAD_ROWS + wave * 32 + r) * p.h_sl) + 16u * cseg
                                : kHeadOOB;
   }
+  // (a unit past the row's end, u >= nunit included, is out of range by the
+  // byte test alone: offsets are selected, never branched around)
+  const uint32_t row_bytes = 2u * (uint32_t)p.dmodel;
   auto load_h = [&](u32x4* dst, int u) {
+    const uint32_t ub = 128u * (uint32_t)u;
+    const bool inrow = ub + 16u * cseg < row_bytes;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bool on = coff[c] != kHeadOOB && u < p.nunit && 64 * u + 8 * cseg < p.dmodel;
-      dst[c] = __builtin_amdgcn_raw_buffer_load_b128(rh, on ? coff[c] + 128u * u : kHeadOOB, 0, LIK_HEAD_AUX);
-    }
+    for (int c = 0; c < 4; ++c)
+      dst[c] = __builtin_amdgcn_raw_buffer_load_b128(rh, (inrow && coff[c] != kHeadOOB) ? coff[c] + ub : kHeadOOB, 0,
+                                                     LIK_HEAD_AUX);
   };
   u32x4* tile = s_h + wave * (32 * 9);  // 32 rows x 9 slots of 16 bytes
   auto frag_h = [&](const u32x4* g, u32x4* bf) {
@@ -211,27 +215,28 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_tile_kernel(const HeadParam
     constexpr int S = decltype(slot_c)::value;  // u % 4
     load_w(wr[(S + 3) & 3], u + 3);  // past the last unit: out of range, no fetch
     load_h(hb[(S + 3) & 3], u + 3);
-    if (wave_on) {
-      u32x4 bf[4];
-      frag_h(hb[S], bf);
-      const u32x4* sw = s_w[u & 1];
+    u32x4 bf[4];
+    frag_h(hb[S], bf);
+    const u32x4* sw = s_w[u & 1];
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-        for (int n = 0; n < NB; ++n) {
-          const u32x4 a = sw[(n * 4 + kk) * 64 + lane];
-          acc[n] = mfma32<EK>(acc[n], &a, &bf[kk]);
-        }
+      for (int n = 0; n < NB; ++n) {
+        const u32x4 a = sw[(n * 4 + kk) * 64 + lane];
+        acc[n] = mfma32<EK>(acc[n], &a, &bf[kk]);
       }
     }
-    if (u + 1 < p.nunit) store_w((u + 1) & 1, wr[(S + 1) & 3]);
+    store_w((u + 1) & 1, wr[(S + 1) & 3]);
     __syncthreads();
   };
+  // A straight-line body (no branches for the compiler's load counting to
+  // merge): the unit count is rounded up to a multiple of 4, the extra steps
+  // load nothing (out of range: zeros) and add 0.
   for (int u = 0; u < p.nunit; u += 4) {
     step(std::integral_constant<int, 0>{}, u);
-    if (u + 1 < p.nunit) step(std::integral_constant<int, 1>{}, u + 1);
-    if (u + 2 < p.nunit) step(std::integral_constant<int, 2>{}, u + 2);
-    if (u + 3 < p.nunit) step(std::integral_constant<int, 3>{}, u + 3);
+    step(std::integral_constant<int, 1>{}, u + 1);
+    step(std::integral_constant<int, 2>{}, u + 2);
+    step(std::integral_constant<int, 3>{}, u + 3);
   }
 
   // row L2 normalise (x / max(||x||, 1e-12)), round to the input dtype: the

@@ -661,6 +661,56 @@ def wl_fused_head(args):
             "roofline": None}
 
 
+def wl_head(args):
+    """maxsim_from_hidden inference on the largest reference fused-head shape
+    (lateon-code-Nd1024-Ld2k: 1 query x 32 tokens, 1024 docs x 2048 tokens of
+    768-dim hidden states, d_out 128, bias, normalize=True, bf16): the fused
+    projection + MaxSim kernel (lik_maxsim_from_hidden). HBM-bound: the
+    algorithmic bytes are the hidden states read once (plus W, Q, scores).
+    ``roofline.kernel_ms`` is the whole call (head_tile_kernel + the small
+    head_finish_kernel) timed with events on the launch stream."""
+    import torch
+
+    from late_interaction_kernels.autograd import _score
+    from late_interaction_kernels.fused_head import maxsim_from_hidden
+
+    Nq, Nd, Lq, Ld, dm_, do = 1, 1024, 32, 2048, 768, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    H = torch.randn(Nd, Ld, dm_, generator=g, device="cuda", dtype=torch.bfloat16)
+    W = torch.randn(do, dm_, generator=g, device="cuda", dtype=torch.bfloat16) * dm_**-0.5
+    b = torch.randn(do, generator=g, device="cuda", dtype=torch.bfloat16) * 0.01
+    Q = _normed((Nq, Lq, do), g, torch.bfloat16)
+
+    def step():
+        with torch.no_grad():
+            return maxsim_from_hidden(Q, H, W, b, normalize=True)
+
+    def projected():
+        with torch.no_grad():
+            return _score(Q, torch.nn.functional.linear(H, W, b), None, None, normalize=2)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    ms_proj = _time_steps(projected, args.steps, args.warmup)
+    nbytes = float(H.numel() * 2 + W.numel() * 2 + Q.numel() * 2 + Nq * Nd * 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "maxsim_from_hidden inference GB/s of hidden states", "value": round(gbs, 1), "unit": "GB/s",
+        "ms_per_step": round(ms, 4), "dtype": "bf16",
+        "config": {"workload": "fused projection head, lateon-code-Nd1024-Ld2k (docs/benchmarks.md:239-247)",
+                   "Nq": Nq, "Lq": Lq, "Nd": Nd, "Ld": Ld, "d_model": dm_, "d_out": do,
+                   "bytes_per_step": nbytes, "project_first_ms": round(ms_proj, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm"], "unit": "GB/s",
+                     "frac": round(gbs / PEAK["hbm"], 4), "traffic": _traffic("head"), "kernel_ms": round(ms, 4)},
+    }
+
+
+def _traffic(workload: str):
+    """HBM bytes per launch of the workload's main kernel (profiles/traffic.json), or None."""
+    tf = ROOT / "profiles" / "traffic.json"
+    t = json.loads(tf.read_text()).get(workload) if tf.exists() else None
+    return t["hbm_bytes_per_launch"] if t else None
+
+
 def wl_hbm_copy(args):
     """Calibration: a plain 2 GiB device copy (torch's copy kernel). Its GB/s is the
     achievable HBM rate on this box, and its rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -698,6 +748,7 @@ WORKLOADS = {
     "ref_shapes": wl_ref_shapes,
     "train_shapes": wl_train_shapes,
     "fused_head": wl_fused_head,
+    "head": wl_head,
     "plaid_decode": wl_plaid_decode,
     "inbatch": wl_inbatch,
     "inbatch_norm": lambda a: wl_inbatch(a, normalize=True),

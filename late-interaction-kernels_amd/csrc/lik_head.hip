@@ -13,11 +13,12 @@
 //  * Projection as P^T = W . H^T on 32x32x16 MFMAs: W (A operand, 32 output
 //    dims per lane row) is staged in LDS one k-unit (64 model dims) at a time,
 //    double-buffered and shared by the 8 wavefronts; H (B operand, one doc
-//    token per lane row) is read straight from HBM into registers, each lane
-//    64 contiguous bytes of its token per unit, two units ahead of the MFMAs.
-//    Within a unit, lane half h supplies model dims [32 h, 32 h + 32) and k-step
-//    kk the 8 dims at 8 kk of them: the same order for W and H, so the
-//    contraction runs over the same dims whatever the pairing.
+//    token per lane row) is read with coalesced, non-temporal buffer loads
+//    (8 lanes x 16 bytes per 128-byte row segment) into registers three units
+//    ahead of the MFMAs, and turned into B fragments through the wavefront's
+//    LDS tile. Within a unit, lane half h supplies model dims [32 h, 32 h + 32)
+//    and k-step kk the 8 dims at 8 kk of them: the same order for W and H, so
+//    the contraction runs over the same dims whatever the pairing.
 //  * The accumulators start at the bias. Element e of lane (l32, h) holds
 //    output dim 32 n + 8 (e / 4) + 4 h + e % 4 of doc token l32, so a token's
 //    squared norm is the lane's sum plus its partner lane's (l32 + 32).
@@ -37,13 +38,10 @@ namespace lik {
 
 namespace {
 
-#ifndef LIK_HEAD_AUX
-#define LIK_HEAD_AUX 2
-#endif
-#ifndef LIK_HEAD_NW
-#define LIK_HEAD_NW 8
-#endif
-constexpr int HEAD_WAVES = LIK_HEAD_NW;     // wavefronts per workgroup
+// 8 wavefronts per workgroup measured faster than 4 (two workgroups per CU)
+constexpr int HEAD_WAVES = 8;
+// cache policy of the H loads: 2 = non-temporal (each byte of H is read once)
+constexpr int HEAD_H_AUX = 2;
 constexpr int HEAD_THREADS = 64 * HEAD_WAVES;
 constexpr int HEAD_ROWS = 32 * HEAD_WAVES;  // doc tokens per workgroup
 constexpr int HEAD_MAXCOL = 256;            // query tokens (Nq * Lq) per call
@@ -177,7 +175,7 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_tile_kernel(const HeadParam
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       dst[c] = __builtin_amdgcn_raw_buffer_load_b128(rh, (inrow && coff[c] != kHeadOOB) ? coff[c] + ub : kHeadOOB, 0,
-                                                     LIK_HEAD_AUX);
+                                                     HEAD_H_AUX);
   };
   u32x4* tile = s_h + wave * (32 * 9);  // 32 rows x 9 slots of 16 bytes
   auto frag_h = [&](const u32x4* g, u32x4* bf) {

@@ -555,6 +555,84 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
   }
 }
 
+// KD layout (padded docs and queries, Lq <= 64): doc j belongs to query
+// i = j / K alone, so its gradient rows are the (at most Lq) rows that won one
+// of query i's tokens. One workgroup of 4 wavefronts per doc: in each, lane s
+// holds token s's winner; distinct winning row number k (in order of first
+// token) is summed by wavefront k % 4, adding its tokens' scaled query rows in
+// increasing s (the order of grad_d_kernel's scan, so the same sums), then
+// takes the normalise Jacobian and is stored. The doc's other rows are
+// written as zeros by the whole workgroup (each wavefront builds the bitmap of
+// winning rows in its own LDS words). No per-block rescans of the pairs, one
+// streaming pass of stores over the doc.
+constexpr int KD_GD_MAXLD = 8192;
+template <int EK, int DPL>
+__global__ void __launch_bounds__(256) grad_d_kd_kernel(const BwdParams bp) {
+  __shared__ uint32_t s_hit[4][KD_GD_MAXLD / 32];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t j = blockIdx.x;
+  const int64_t i = j / bp.ndoc_pg, jl = j - i * bp.ndoc_pg;
+  const int nwords = (int)((bp.ld + 31) / 32);
+  for (int w = lane; w < nwords; w += 64) s_hit[wv][w] = 0u;
+  const float gij = bp.grad[i * bp.ld_g + jl];
+  int a = -1;
+  float sc = 0.f;
+  if (lane < bp.lq && gij != 0.f) {
+    a = bp.amax[j * bp.lq + lane];
+    if (bp.qmask && bp.qmask[i * bp.qm_sn + lane * bp.qm_sl] == 0) a = -1;
+    sc = bp.qinv ? gij * bp.qinv[i * bp.lq + lane] : gij;
+  }
+  const int64_t esz = sizeof_ek<EK>();
+  const int64_t rowb = (int64_t)bp.dim * esz;
+  char* gdoc = bp.gd + j * bp.ld * rowb;
+  uint64_t todo = __ballot(a >= 0);
+  for (int k = 0; todo; ++k) {
+    const int t = __builtin_amdgcn_readlane(a, __builtin_ctzll(todo));
+    uint64_t same = __ballot(a == t);
+    todo &= ~same;
+    if (lane == 0) s_hit[wv][t >> 5] |= 1u << (t & 31);
+    if ((k & 3) != wv) continue;
+    float gh[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) gh[e] = 0.f;
+    while (same) {
+      const int l = __builtin_ctzll(same);
+      same &= same - 1;
+      const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
+      const char* qrow = bp.q + i * bp.q_sn + (int64_t)l * bp.q_sl;
+      axpy_lane<EK, DPL>(gh, qrow, lane * DPL, bp.dim, c);
+    }
+    if (bp.dinv) {
+      const float di = bp.dinv[j * bp.ld + t];
+      const char* drow = bp.d + j * bp.d_sn + (int64_t)t * bp.d_sl;
+      float xh[DPL], dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        const int el = lane * DPL + e;
+        xh[e] = el < bp.dim ? load_elem<EK>(drow, el) * di : 0.f;
+        dot = fmaf(gh[e], xh[e], dot);
+      }
+      dot = wave_sum(dot);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) gh[e] = (gh[e] - dot * xh[e]) * di;
+    }
+    char* out = gdoc + (int64_t)t * rowb;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      const int el = lane * DPL + e;
+      if (el < bp.dim) store_elem<EK>(out, el, gh[e]);
+    }
+  }
+  // the rows no token won: zeros, 16 bytes per thread per store (LDS
+  // operations of one wavefront complete in order: its bitmap is final)
+  const int64_t nchunk = bp.ld * rowb / 16;
+  const int64_t cpr = rowb / 16;
+  for (int64_t c = threadIdx.x; c < nchunk; c += 256) {
+    const int64_t t = c / cpr;
+    if (!((s_hit[wv][t >> 5] >> (t & 31)) & 1u)) *(u32x4*)(gdoc + c * 16) = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
 template <int EK, int DPL>
 int launch_bwd(const BwdParams& bp, hipStream_t s) {
   constexpr int RB = grad_d_rows<DPL>();
@@ -566,6 +644,12 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
       hipLaunchKernelGGL((grad_q_finish_kernel<EK, DPL>), dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, s, bp);
       if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
     }
+  }
+  if (bp.gd && bp.kd && !bp.q_ptr && !bp.q_cu && !bp.d_cu && bp.lq <= 64 && bp.ld <= KD_GD_MAXLD &&
+      ((int64_t)bp.dim * sizeof_ek<EK>()) % 16 == 0 && ((uintptr_t)bp.gd) % 16 == 0) {
+    if (bp.nd > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((grad_d_kd_kernel<EK, DPL>), dim3((unsigned)bp.nd), dim3(256), 0, s, bp);
+    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   }
   // packed docs: sum of lengths <= nd * ld, so nd * ld / RB blocks cover them
   const int64_t nb = !bp.gd ? 0 : bp.d_cu ? (bp.nd * bp.ld + RB - 1) / RB : bp.nd * ((bp.ld + RB - 1) / RB);

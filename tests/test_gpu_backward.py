@@ -115,6 +115,31 @@ def test_grad_q_doc_splits(Nq, kd):
     assert torch.equal(gq, gq2)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_kd_grad_d_matches_per_query_cross_product(dtype):
+    """KD-layout grad_D (one wavefront per doc: its winning rows summed in
+    token order, the rest written as zeros) equals, bitwise, grad_D of each
+    query scored alone against its K docs on the cross-product path (the
+    row-block kernel, same token order), given the same winners; long docs
+    (Ld 700) and masks."""
+    from late_interaction_kernels._core import dense_maxsim_train, maxsim_backward
+
+    _case(f"kd grad_d vs per-query cross product {dtype}")
+    Nq, K, Lq, Ld, d = 3, 5, 32, 700, 128
+    Q, D, qm, dm = _inputs(Nq, Nq * K, Lq, Ld, d, dtype, 17)
+    G = torch.randn(Nq, K, generator=torch.Generator().manual_seed(2))
+    _, am, Qp, Dp, qmi = dense_maxsim_train(Q.cuda(), D.cuda(), qm.cuda(), dm.cuda(), norm=3, kd=True)
+    gq, gd = maxsim_backward(G.cuda(), Qp, Dp, am, qmi, norm=3, kd=True)
+    assert torch.all(gd[0] == 0)  # fully masked doc
+    for i in range(Nq):
+        sl = slice(i * K, (i + 1) * K)
+        _, am1, Qp1, Dp1, qm1 = dense_maxsim_train(Q[i:i + 1].cuda(), D[sl].cuda(), qm[i:i + 1].cuda(),
+                                                   dm[sl].cuda(), norm=3, kd=False)
+        assert torch.equal(am1.view(K, Lq), am.view(Nq, K, Lq)[i])
+        gq1, gd1 = maxsim_backward(G[i:i + 1].cuda(), Qp1, Dp1, am1, qm1, norm=3, kd=False)
+        assert torch.equal(gd1, gd[sl])
+
+
 def _torch_ref(Q, D, qm, dm, normalize):
     """Plain fp32 autograd restatement of the forward (reference.py:26-98)."""
     if normalize:

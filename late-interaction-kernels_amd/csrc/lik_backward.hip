@@ -87,6 +87,10 @@ struct BwdParams {
   float* gq_part;
   int64_t qchunk;
   int qsplit;
+  // cross-product grad_D from winner entries sorted by doc row (null: the
+  // row-block kernel): entries row_vals[row_ptr[r] .. row_ptr[r + 1]) of row r
+  const int32_t* row_ptr;
+  const int32_t* row_vals;
 };
 
 // inv[r] = 1 / max(||row r||, 1e-12) for rows r = i*L + t of a [n, L, dim]
@@ -633,6 +637,76 @@ __global__ void __launch_bounds__(256) grad_d_kd_kernel(const BwdParams bp) {
   }
 }
 
+// Cross-product layout with many (query, token) pairs per doc: instead of
+// row blocks that each rescan all Nq * Lq pairs, the winner entries
+// f = (i * Nd + j) * Lq + s are sorted once by doc row j * Ld + a (a stable
+// radix sort, so a row's entries stay in increasing (i, s): the row-block
+// kernel's scan order, hence the same sums). Entries that add nothing (no
+// winner, G = 0, a masked query token) get the key Nd * Ld and sort last.
+__global__ void __launch_bounds__(256) row_keys_kernel(const BwdParams bp, int64_t n, int32_t* keys, int32_t* vals) {
+  const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (f >= n) return;
+  const int64_t s = f % bp.lq, ij = f / bp.lq;
+  const int64_t j = ij % bp.nd, i = ij / bp.nd;
+  const int a = bp.amax[f];
+  const bool keep = a >= 0 && bp.grad[i * bp.ld_g + j] != 0.f && (!bp.qmask || bp.qmask[i * bp.qm_sn + s * bp.qm_sl] != 0);
+  keys[f] = keep ? (int32_t)(j * bp.ld + a) : (int32_t)(bp.nd * bp.ld);
+  vals[f] = (int32_t)f;
+}
+
+// One wavefront per doc row: its sorted entries added in order (scaled query
+// rows, as grad_d_kernel adds them), the normalise Jacobian, the store; a row
+// without entries is stored as zeros.
+template <int EK, int DPL>
+__global__ void __launch_bounds__(256) grad_d_sorted_kernel(const BwdParams bp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  if (r >= bp.nd * bp.ld) return;
+  const int64_t j = r / bp.ld, t = r - j * bp.ld;
+  const int b = bp.row_ptr[r], e = bp.row_ptr[r + 1];
+  float gh[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) gh[k] = 0.f;
+  for (int k0 = b; k0 < e; k0 += 64) {
+    float sc = 0.f;
+    int64_t qoff = 0;
+    if (k0 + lane < e) {
+      const int64_t f = bp.row_vals[k0 + lane];
+      const int64_t s = f % bp.lq, i = f / bp.lq / bp.nd;
+      const float gij = bp.grad[i * bp.ld_g + j];
+      sc = bp.qinv ? gij * bp.qinv[i * bp.lq + s] : gij;
+      qoff = i * bp.q_sn + s * bp.q_sl;
+    }
+    const int m = e - k0 < 64 ? e - k0 : 64;
+    for (int l = 0; l < m; ++l) {
+      const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)qoff, l);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)qoff >> 32), l);
+      axpy_lane<EK, DPL>(gh, bp.q + (int64_t)(((uint64_t)hi << 32) | lo), lane * DPL, bp.dim, c);
+    }
+  }
+  if (bp.dinv && e > b) {
+    const float di = bp.dinv[r];
+    const char* drow = bp.d + j * bp.d_sn + t * bp.d_sl;
+    float xh[DPL], dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+      const int el = lane * DPL + k;
+      xh[k] = el < bp.dim ? load_elem<EK>(drow, el) * di : 0.f;
+      dot = fmaf(gh[k], xh[k], dot);
+    }
+    dot = wave_sum(dot);
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) gh[k] = (gh[k] - dot * xh[k]) * di;
+  }
+  char* out = bp.gd + r * bp.dim * (int64_t)sizeof_ek<EK>();
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) {
+    const int el = lane * DPL + k;
+    if (el < bp.dim) store_elem<EK>(out, el, gh[k]);
+  }
+}
+
 template <int EK, int DPL>
 int launch_bwd(const BwdParams& bp, hipStream_t s) {
   constexpr int RB = grad_d_rows<DPL>();
@@ -644,6 +718,11 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
       hipLaunchKernelGGL((grad_q_finish_kernel<EK, DPL>), dim3((unsigned)((nw + 3) / 4)), dim3(256), 0, s, bp);
       if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
     }
+  }
+  if (bp.gd && bp.row_ptr) {
+    const int64_t nr = bp.nd * bp.ld;
+    hipLaunchKernelGGL((grad_d_sorted_kernel<EK, DPL>), dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, bp);
+    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   }
   if (bp.gd && bp.kd && !bp.q_ptr && !bp.q_cu && !bp.d_cu && bp.lq <= 64 && bp.ld <= KD_GD_MAXLD &&
       ((int64_t)bp.dim * sizeof_ek<EK>()) % 16 == 0 && ((uintptr_t)bp.gd) % 16 == 0) {
@@ -797,6 +876,41 @@ static size_t grad_q_part_bytes(const lik_seqs_t* Q, const lik_seqs_t* D, uint32
   return (size_t)(split * Q->n * Q->len * 64 * dpl) * sizeof(float);
 }
 
+// Sorted-entry grad_D (cross product, padded, many pairs per doc): keys and
+// values in and out, the row pointers, the sort's temporary storage.
+struct RowWs {
+  size_t kin, vin, kout, vout, ptr, temp, temp_bytes, total;
+  int64_t n, rows;
+};
+static RowWs row_ws_layout(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
+  RowWs w{};
+  if ((flags & LIK_KD_LAYOUT) || Q->cu_seqlens || D->cu_seqlens || Q->n <= 0 || D->n <= 0 || Q->len <= 0 ||
+      D->len <= 0)
+    return w;
+  const int64_t n = Q->n * D->n * Q->len, rows = D->n * D->len;
+  // worth it when a row block would rescan many pairs (measured: 8192 pairs
+  // per doc 0.92 -> 0.81 ms, 65,920 2.65 -> 2.21 ms, but 4096 pairs over
+  // 1030-token docs 0.45 -> 0.50 ms); 32-bit entry and row ids
+  if (Q->n * Q->len < 8192 || n >= ((int64_t)1 << 31) || rows >= ((int64_t)1 << 31) - 1) return w;
+  size_t o = 0;
+  const size_t a = align256((size_t)n * 4);
+  w.kin = o; o += a;
+  w.vin = o; o += a;
+  w.kout = o; o += a;
+  w.vout = o; o += a;
+  w.ptr = o; o += align256((size_t)(rows + 1) * 4);
+  size_t tb = 0;
+  hipcub::DeviceRadixSort::SortPairs(nullptr, tb, (const int32_t*)nullptr, (int32_t*)nullptr,
+                                     (const int32_t*)nullptr, (int32_t*)nullptr, (int)n, 0, end_bit_for(rows));
+  w.temp = o;
+  w.temp_bytes = tb;
+  o += align256(tb);
+  w.total = o;
+  w.n = n;
+  w.rows = rows;
+  return w;
+}
+
 // float entries of the inverse-norm arrays at the start of the workspace
 static size_t bwd_norm_floats(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
   size_t n = 0;
@@ -807,7 +921,8 @@ static size_t bwd_norm_floats(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t
 
 size_t lik_maxsim_backward_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags) {
   if (!Q || !D || Q->n < 0 || D->n < 0 || Q->len < 0 || D->len < 0) return 0;
-  const size_t b = align256(bwd_norm_floats(Q, D, flags) * sizeof(float)) + grad_q_part_bytes(Q, D, flags);
+  const size_t b = align256(bwd_norm_floats(Q, D, flags) * sizeof(float)) + align256(grad_q_part_bytes(Q, D, flags)) +
+                   row_ws_layout(Q, D, flags).total;
   return b ? b + 256 : 0;
 }
 
@@ -890,11 +1005,30 @@ int lik_maxsim_backward(const float* grad, int64_t grad_ld, const lik_seqs_t* Q,
       return rc;
     }
   }
+  char* wcur = (char*)workspace + align256(bwd_norm_floats(Q, D, flags) * sizeof(float));
   if (grad_q_part_bytes(Q, D, flags)) {
     int64_t split;
     grad_q_split(Q, D, flags, &split, &bp.qchunk);
     bp.qsplit = (int)split;
-    bp.gq_part = (float*)((char*)workspace + align256(bwd_norm_floats(Q, D, flags) * sizeof(float)));
+    bp.gq_part = (float*)wcur;
+  }
+  wcur += align256(grad_q_part_bytes(Q, D, flags));
+  const RowWs rw = grad_d ? row_ws_layout(Q, D, flags) : RowWs{};
+  if (rw.total) {
+    char* ws = (char*)(((uintptr_t)wcur + 255) & ~(uintptr_t)255);
+    auto I = [&](size_t off) { return (int32_t*)(ws + off); };
+    hipLaunchKernelGGL(row_keys_kernel, dim3((unsigned)((rw.n + 255) / 256)), dim3(256), 0, s, bp, rw.n, I(rw.kin),
+                       I(rw.vin));
+    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+    size_t tb = rw.temp_bytes;
+    if (hipcub::DeviceRadixSort::SortPairs(ws + rw.temp, tb, I(rw.kin), I(rw.kout), I(rw.vin), I(rw.vout), (int)rw.n,
+                                           0, end_bit_for(rw.rows), s) != hipSuccess)
+      return LIK_ERR_LAUNCH;
+    hipLaunchKernelGGL(bucket_ptr_kernel, dim3((unsigned)((rw.rows + 1 + 255) / 256)), dim3(256), 0, s, I(rw.kout),
+                       rw.n, rw.rows, I(rw.ptr));
+    if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+    bp.row_ptr = I(rw.ptr);
+    bp.row_vals = I(rw.vout);
   }
   switch (Q->dtype) {
     case LIK_BF16: return launch_bwd_dpl<EK_BF16>(bp, s);

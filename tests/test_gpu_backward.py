@@ -115,6 +115,31 @@ def test_grad_q_doc_splits(Nq, kd):
     assert torch.equal(gq, gq2)
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_grad_d_sorted_entries(dtype, tol, normalize):
+    """Cross product with many (query, token) pairs per doc (Nq * Lq >= 8192):
+    grad_D from the winner entries sorted by doc row, against the oracle given
+    the kernel's winners; masked query tokens, a fully masked doc, holes;
+    bitwise equal on a second run."""
+    from late_interaction_kernels._core import dense_maxsim_train, maxsim_backward
+
+    _case(f"bwd sorted grad_d {dtype} norm={normalize}")
+    Nq, Lq, Nd, Ld, d = 256, 32, 5, 40, 64
+    Q, D, qm, dm = _inputs(Nq, Nd, Lq, Ld, d, dtype, 31 + normalize)
+    norm = 3 if normalize else 0
+    _, am, Qp, Dp, qmi = dense_maxsim_train(Q.cuda(), D.cuda(), qm.cuda(), dm.cuda(), norm=norm, kd=False)
+    G = torch.randn(Nq, Nd, generator=torch.Generator().manual_seed(5))
+    G[3, 4] = 0.0  # a zero upstream gradient drops its pairs
+    gq, gd = maxsim_backward(G.cuda(), Qp, Dp, am, qmi, norm=norm, kd=False)
+    rq, rd = O.maxsim_grads(G.numpy(), _np(Q), _np(D), am.cpu().numpy(), qm.numpy(), normalize=normalize, kd=False)
+    assert rel_err(_np(gq), rq) < tol
+    assert rel_err(_np(gd), rd) < tol
+    assert np.all(_np(gd)[0] == 0)
+    gq2, gd2 = maxsim_backward(G.cuda(), Qp, Dp, am, qmi, norm=norm, kd=False)
+    assert torch.equal(gd, gd2) and torch.equal(gq, gq2)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_kd_grad_d_matches_per_query_cross_product(dtype):
     """KD-layout grad_D (one wavefront per doc: its winning rows summed in

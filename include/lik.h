@@ -181,8 +181,9 @@ size_t lik_maxsim_from_hidden_workspace_size(const lik_seqs_t* Q, const lik_seqs
  * LIK_NORMALIZE (both sides), LIK_NORMALIZE_Q or LIK_NORMALIZE_D the
  * gradients are taken through x / max(||x||, 1e-12) on those sides. The
  * caller passes lik_maxsim_backward_workspace_size() bytes of workspace
- * (inverse norms, and the partial grad_q rows when few query tokens split
- * their docs over several wavefronts; may be 0).
+ * (inverse norms, the partial grad_q rows when few query tokens split their
+ * docs over several wavefronts, the sorted winner entries when many query
+ * tokens share each doc; may be 0).
  * Deterministic: fixed summation order, no atomics.
  * Replaces backward/unified.py:maxsim_backward_unified and
  * backward/lowmem.py:maxsim_backward_lowmem (+ the normalise Jacobian of

@@ -566,8 +566,9 @@ __global__ void __launch_bounds__(64) grad_d_kernel(const BwdParams bp) {
 
 // KD layout (padded docs and queries, Lq <= 64): doc j belongs to query
 // i = j / K alone, so its gradient rows are the (at most Lq) rows that won one
-// of query i's tokens. One workgroup of 4 wavefronts per doc: in each, lane s
-// holds token s's winner; distinct winning row number k (in order of first
+// of query i's tokens; likewise a cross product with Nq * Lq <= 64 (a doc's
+// winners come from those <= 64 pairs). One workgroup of 4 wavefronts per
+// doc: in each, lane s holds pair s's winner; distinct winning row number k (in order of first
 // token) is summed by wavefront k % 4, adding its tokens' scaled query rows in
 // increasing s (the order of grad_d_kernel's scan, so the same sums), then
 // takes the normalise Jacobian and is stored. The doc's other rows are
@@ -580,16 +581,25 @@ __global__ void __launch_bounds__(256) grad_d_kd_kernel(const BwdParams bp) {
   __shared__ uint32_t s_hit[4][KD_GD_MAXLD / 32];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t j = blockIdx.x;
-  const int64_t i = j / bp.ndoc_pg, jl = j - i * bp.ndoc_pg;
   const int nwords = (int)((bp.ld + 31) / 32);
   for (int w = lane; w < nwords; w += 64) s_hit[wv][w] = 0u;
-  const float gij = bp.grad[i * bp.ld_g + jl];
+  // lane f: KD, token f of doc j's query; cross product (Nq * Lq <= 64), the
+  // pair (i, s) = (f / Lq, f % Lq) (the row-block kernel's scan order)
+  const int64_t i = bp.kd ? j / bp.ndoc_pg : lane / bp.lq;
+  const int64_t jl = bp.kd ? j - i * bp.ndoc_pg : j;
+  const int64_t sl = bp.kd ? lane : lane - i * bp.lq;
+  const int64_t npair = bp.kd ? bp.lq : bp.nq * bp.lq;
   int a = -1;
   float sc = 0.f;
-  if (lane < bp.lq && gij != 0.f) {
-    a = bp.amax[j * bp.lq + lane];
-    if (bp.qmask && bp.qmask[i * bp.qm_sn + lane * bp.qm_sl] == 0) a = -1;
-    sc = bp.qinv ? gij * bp.qinv[i * bp.lq + lane] : gij;
+  int64_t qoff = 0;
+  if (lane < npair) {
+    const float gij = bp.grad[i * bp.ld_g + jl];
+    if (gij != 0.f) {
+      a = bp.amax[(i * bp.ndoc_pg + jl) * bp.lq + sl];
+      if (bp.qmask && bp.qmask[i * bp.qm_sn + sl * bp.qm_sl] == 0) a = -1;
+      sc = bp.qinv ? gij * bp.qinv[i * bp.lq + sl] : gij;
+      qoff = i * bp.q_sn + sl * bp.q_sl;
+    }
   }
   const int64_t esz = sizeof_ek<EK>();
   const int64_t rowb = (int64_t)bp.dim * esz;
@@ -608,8 +618,9 @@ __global__ void __launch_bounds__(256) grad_d_kd_kernel(const BwdParams bp) {
       const int l = __builtin_ctzll(same);
       same &= same - 1;
       const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), l));
-      const char* qrow = bp.q + i * bp.q_sn + (int64_t)l * bp.q_sl;
-      axpy_lane<EK, DPL>(gh, qrow, lane * DPL, bp.dim, c);
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)qoff, l);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)qoff >> 32), l);
+      axpy_lane<EK, DPL>(gh, bp.q + (int64_t)(((uint64_t)hi << 32) | lo), lane * DPL, bp.dim, c);
     }
     if (bp.dinv) {
       const float di = bp.dinv[j * bp.ld + t];
@@ -729,7 +740,8 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
     hipLaunchKernelGGL((grad_d_sorted_kernel<EK, DPL>), dim3((unsigned)((nr + 3) / 4)), dim3(256), 0, s, bp);
     return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   }
-  if (bp.gd && bp.kd && !bp.q_ptr && !bp.q_cu && !bp.d_cu && bp.lq <= 64 && bp.ld <= KD_GD_MAXLD &&
+  if (bp.gd && !bp.q_ptr && !bp.q_cu && !bp.d_cu && (bp.kd ? bp.lq <= 64 : bp.nq * bp.lq <= 64) &&
+      bp.ld <= KD_GD_MAXLD &&
       ((int64_t)bp.dim * sizeof_ek<EK>()) % 16 == 0 && ((uintptr_t)bp.gd) % 16 == 0) {
     if (bp.nd > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
     hipLaunchKernelGGL((grad_d_kd_kernel<EK, DPL>), dim3((unsigned)bp.nd), dim3(256), 0, s, bp);

@@ -141,6 +141,29 @@ def test_grad_d_sorted_entries(dtype, tol, normalize):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_small_cross_product_grad_d_matches_row_blocks(dtype):
+    """A cross product with Nq * Lq <= 64 takes the per-doc grad_D kernel; the
+    same problem with one masked query token more (66 pairs) takes the
+    row-block kernel: grad_D bitwise equal (same pairs, same order)."""
+    from late_interaction_kernels._core import dense_maxsim_train, maxsim_backward
+
+    _case(f"small cross grad_d vs row blocks {dtype}")
+    Nq, Lq, Nd, Ld, d = 2, 32, 7, 600, 128
+    Q, D, qm, dm = _inputs(Nq, Nd, Lq, Ld, d, dtype, 23)
+    G = torch.randn(Nq, Nd, generator=torch.Generator().manual_seed(3))
+    Q2 = torch.cat([Q, torch.randn(Nq, 1, d).to(dtype)], dim=1)
+    qm2 = torch.cat([qm, torch.zeros(Nq, 1, dtype=torch.bool)], dim=1)
+    outs = []
+    for Qx, qmx in ((Q, qm), (Q2, qm2)):
+        _, am, Qp, Dp, qmi = dense_maxsim_train(Qx.cuda(), D.cuda(), qmx.cuda(), dm.cuda(), norm=3, kd=False)
+        outs.append((am.view(Nq, Nd, -1)[..., :Lq], maxsim_backward(G.cuda(), Qp, Dp, am, qmi, norm=3, kd=False)[1]))
+    (am1, gd1), (am2, gd2) = outs
+    keep = qm.cuda()[:, None, :].expand(Nq, Nd, Lq)
+    assert torch.equal(am1[keep], am2[keep])
+    assert torch.equal(gd1, gd2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_kd_grad_d_matches_per_query_cross_product(dtype):
     """KD-layout grad_D (one wavefront per doc: its winning rows summed in
     token order, the rest written as zeros) equals, bitwise, grad_D of each

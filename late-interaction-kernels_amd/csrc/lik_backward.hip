@@ -25,8 +25,9 @@
 //   Packed docs (cu_seqlens): a block is RB consecutive packed rows and may
 //   span several docs; it scans each of them in doc order.
 //   Two layouts take other grad_D kernels with the same sums (same order):
-//   the KD layout (grad_d_kd_kernel: a doc's winners are its one query's
-//   tokens, so one workgroup per doc) and cross products with >= 8192
+//   the KD layout and cross products with <= 64 (query, token) pairs
+//   (grad_d_kd_kernel: a doc's winners come from <= 64 pairs, so one
+//   workgroup per doc) and cross products with >= 8192
 //   (query, token) pairs (grad_d_sorted_kernel over the winner entries
 //   radix-sorted by doc row).
 // Packed queries: the wave of (i, s) exits when s is past query i's length;

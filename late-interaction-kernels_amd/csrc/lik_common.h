@@ -22,7 +22,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // Element kinds of the token embeddings. F32 is computed as three bf16 MFMAs
-// (hi*hi + hi*lo + lo*hi), giving ~16 mantissa bits per product.
+// (hi*hi + hi*lo + lo*hi; split_hi / split_lo), ~1e-5 relative of exact fp32 MaxSim.
 enum { EK_BF16 = 0, EK_F16 = 1, EK_F32 = 2, EK_FP8 = 3 };
 
 // Compile-time layout of one 32-token tile for element kind EK and padded
@@ -139,17 +139,42 @@ __device__ __forceinline__ float chunk_sumsq(const u32x4& v) {
   return s;
 }
 
+// fp32 -> bf16 hi / lo split for the three-product fp32 MaxSim
+// (hi*hi + hi*lo + lo*hi). hi is x truncated toward zero (NaN stays NaN), so
+// lo = x - hi (exact in fp32, then rounded to bf16) has the sign of x: for
+// an infinite operand a, a*hi_b and a*lo_b are infinities of one sign and
+// never add up to inf - inf = NaN where the true product a*b is +-inf. A lo
+// that is zero or subnormal becomes the smallest normal bf16 with x's sign
+// (an exactly representable b would otherwise give inf * 0 = NaN); for
+// finite operands that stand-in moves a product by at most 2^-126 |y|.
+// A non-finite x has lo = that stand-in too. Scores are within ~1e-5
+// relative of exact fp32 MaxSim on N(0,1) data (measured against fp64).
+__device__ __forceinline__ uint32_t split_hi(float x) {
+  return x != x ? 0x7fc0u : (__float_as_uint(x) >> 16);
+}
+__device__ __forceinline__ uint32_t split_lo(uint32_t hbits, float x) {
+  const float r = x - __uint_as_float(hbits << 16);
+  const uint32_t l = __builtin_isfinite(r) ? f32_to_bf16_bits(r) : 0u;
+  return (l & 0x7f80u) ? l : ((hbits & 0x8000u) | 0x0080u);
+}
+
 // Split 4 floats into bf16 hi and lo parts (x ~= hi + lo), packed 2 per u32.
 __device__ __forceinline__ void split4(const u32x4& v, u32x2& hi, u32x2& lo) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const float a = __uint_as_float(v[2 * i]), b = __uint_as_float(v[2 * i + 1]);
-    const uint32_t ha = f32_to_bf16_bits(a), hb = f32_to_bf16_bits(b);
-    const float ra = a - __uint_as_float(ha << 16), rb = b - __uint_as_float(hb << 16);
+    const uint32_t ha = split_hi(a), hb = split_hi(b);
     hi[i] = ha | (hb << 16);
-    lo[i] = f32_to_bf16_bits(ra) | (f32_to_bf16_bits(rb) << 16);
+    lo[i] = split_lo(ha, a) | (split_lo(hb, b) << 16);
   }
 }
+
+// max(a, b) that propagates NaN (IEEE 754-2019 maximum; v_maximum3_f32 on
+// gfx950). Row maxima use it so that a NaN similarity makes the max NaN, which
+// the doc-end test then scores as 0, as torch's max does before the
+// isfinite -> 0 rule (reference.py:83-85). fmaxf would drop the NaN and
+// score the row from its other tokens.
+__device__ __forceinline__ float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 __device__ __forceinline__ float inv_norm(float ss) {
   // F.normalize: x / max(||x||, 1e-12)

@@ -6,7 +6,8 @@
 // 16-bit H and W, bias and row L2-normalise in fp32, the normalised row
 // rounded to the input dtype for the MaxSim product, a doc token that is
 // masked (or past the doc's length) never wins, a query token whose doc has
-// no valid token scores 0 and gets argmax -1, ties go to the lowest doc token.
+// no valid token (or whose max is NaN or +inf) scores 0 and gets argmax -1,
+// ties go to the lowest doc token.
 //
 // head_tile_kernel: one workgroup of 8 wavefronts per (doc j, chunk of 256
 // doc tokens); wavefront w owns tokens [256 c + 32 w, +32).
@@ -274,17 +275,16 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_tile_kernel(const HeadParam
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = 8 * (e >> 2) + 4 * hh + (e & 3);
-        if (((vrow >> r) & 1u) && c[e] > m) {
-          m = c[e];
-          idx = r;
+        if ((vrow >> r) & 1u) {
+          // a NaN similarity makes the max NaN (the token then scores 0)
+          if (c[e] > m) idx = r;
+          m = max_nan(m, c[e]);
         }
       }
       const float om = __shfl_xor(m, 32);
       const int oi = __shfl_xor(idx, 32);
-      if (om > m || (om == m && oi >= 0 && (idx < 0 || oi < idx))) {
-        m = om;
-        idx = oi;
-      }
+      if (om > m || (om == m && oi >= 0 && (idx < 0 || oi < idx))) idx = oi;
+      m = max_nan(m, om);
     }
     if (hh == 0) s_red[wave][cb * 32 + l32] = float2{m, __int_as_float(idx < 0 ? -1 : wave * 32 + idx)};
   }
@@ -294,10 +294,8 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_tile_kernel(const HeadParam
     int idx = -1;
     for (int w = 0; w < HEAD_WAVES; ++w) {
       const float2 v = s_red[w][tid];
-      if (v.x > m) {
-        m = v.x;
-        idx = __float_as_int(v.y);
-      }
+      if (v.x > m) idx = __float_as_int(v.y);
+      m = max_nan(m, v.x);
     }
     p.part[((int64_t)tid * p.nd + j) * p.nchunk + chunk] =
         float2{m, __int_as_float(idx < 0 ? -1 : chunk * HEAD_ROWS + idx)};
@@ -318,12 +316,11 @@ __global__ void __launch_bounds__(256) head_finish_kernel(const HeadParams p) {
     int idx = -1;
     for (int c = 0; c < p.nchunk; ++c) {
       const float2 v = p.part[(col * p.nd + j) * p.nchunk + c];
-      if (v.x > m) {
-        m = v.x;
-        idx = __float_as_int(v.y);
-      }
+      if (v.x > m) idx = __float_as_int(v.y);
+      m = max_nan(m, v.x);
     }
-    const bool any = m > -INFINITY;
+    // no kept token (-inf) or a NaN / +inf max: the token scores 0, argmax -1
+    const bool any = __builtin_isfinite(m);
     sum += any ? m : 0.f;
     if (p.amax) p.amax[(i * p.nd + j) * p.lq + s] = any ? idx : -1;
   }

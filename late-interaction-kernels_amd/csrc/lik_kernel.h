@@ -144,9 +144,9 @@ __global__ void __launch_bounds__(W * 64)
   if constexpr (SRC == SRC_PLAID) {
     for (int i = tid; i < 256; i += NT) s_bw[i] = i < p.pl.nb ? p.pl.bw[i] : 0.f;
   }
-  // Row scales start at 0: the first iteration's epilogue runs on the
-  // -inf-initialised accumulator set, and -inf * 0 (NaN) is ignored by the
-  // max, where stale LDS holding a negative scale would give +inf.
+  // Row scales start at 0 (the first iteration's epilogue runs on the
+  // -inf-initialised accumulator set; the epilogue keeps -inf rows at -inf
+  // whatever their scale).
   for (int i = tid; i < 4 * 32; i += NT) s_rs[i >> 5][i & 31] = 0.f;
 
   // ---------------- document range and tile cursor ----------------
@@ -545,6 +545,12 @@ __global__ void __launch_bounds__(W * 64)
             }
           }
         }
+        if constexpr ((FEAT & F_MASK) != 0) {
+          // rows the mask drops are written as zeros: their -inf bias then
+          // gives -inf whatever the row held (a NaN or inf there would
+          // otherwise turn -inf + x into NaN and poison the max)
+          if (d.holes && !((sm[S] >> (row & 31)) & 1u)) v = (u32x4){0u, 0u, 0u, 0u};
+        }
         if (inr) {
           char* rowp = s_tile[buf][0] + row * T::ROW_B;
           if constexpr (T::SPLIT) {
@@ -771,9 +777,8 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float v = acc[P][sub][4 * j + e];
-            const bool up = v > m[sub];
-            m[sub] = up ? v : m[sub];
-            mi[sub] = up ? r0 + 8 * j + e : mi[sub];
+            mi[sub] = v > m[sub] ? r0 + 8 * j + e : mi[sub];
+            m[sub] = max_nan(m[sub], v);  // a NaN row makes the max NaN (scored 0, argmax -1)
           }
       (void)rslot;
       return;
@@ -788,7 +793,11 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) m[sub] = fmaxf(m[sub], acc[P][sub][4 * j + e] * sc[j][e]);
+            for (int e = 0; e < 4; ++e) {
+              // invalid rows hold -inf and may have a 0 or NaN scale: they stay -inf
+              const float a = acc[P][sub][4 * j + e];
+              m[sub] = max_nan(m[sub], a == NEG_INF ? NEG_INF : a * sc[j][e]);
+            }
         return;
       }
     }
@@ -796,7 +805,7 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) m[sub] = fmaxf(m[sub], acc[P][sub][e]);
+      for (int e = 0; e < 16; ++e) m[sub] = max_nan(m[sub], acc[P][sub][e]);
   };
 
   // The previous tile was the last of doc k: park the per-column maxima.
@@ -821,7 +830,7 @@ __global__ void __launch_bounds__(W * 64)
           const int64_t q = u / p.nc;
           const int64_t tok = p.q_tok0 + (u - q * p.nc) * p.LU + (col - ul * p.LU);
           if (u < p.nunits && tok < p.amax_ld)
-            p.amax[(q * p.amax_qs + jl0 + k) * p.amax_ld + tok] = __builtin_isfinite(fmaxf(v0, v1)) ? win : -1;
+            p.amax[(q * p.amax_qs + jl0 + k) * p.amax_ld + tok] = __builtin_isfinite(max_nan(v0, v1)) ? win : -1;
         }
         mi[sub] = -1;
       }
@@ -829,7 +838,7 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
     for (int sub = 0; sub < NSUB; ++sub) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
-      const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over lanes l, l^32
+      const float mm = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over lanes l, l^32
       if (h == 0) s_colb[sl][(wv * NSUB + sub) * 32 + l32] = __builtin_isfinite(mm) ? (kQsc ? mm * qsc[kQsc ? sub : 0] : mm) : 0.f;
       m[sub] = NEG_INF;
     }

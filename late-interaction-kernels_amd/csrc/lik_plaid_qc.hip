@@ -335,7 +335,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
 #pragma unroll
     for (int sub = 0; sub < QN; ++sub) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
-      const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const float mm = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
       const float v = __builtin_isfinite(mm) ? mm : 0.f;
       auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
       // the tile kernel's flush order (query g at place g of its group of 4:
@@ -398,7 +398,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
           const float v0 = fma_mix(acc[sub][e], qsc[sub], rg.qv[sub][e >> 1], std::false_type{}) * rg.inv[e >> 2][e & 3];
           const float v1 = fma_mix(acc[sub][e + 1], qsc[sub], rg.qv[sub][e >> 1], std::true_type{}) *
                            rg.inv[(e + 1) >> 2][(e + 1) & 3];
-          m[sub] = fmaxf(m[sub], fmaxf(v0, v1));
+          m[sub] = max_nan(m[sub], max_nan(v0, v1));
         }
       return;
     }
@@ -416,7 +416,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
           const float v1 = fma_mix(acc[sub][e + 1], qsc[sub], rg.qv[sub][e >> 1], std::true_type{}) *
                            rg.inv[(e + 1) >> 2][(e + 1) & 3];
           const int r0 = 8 * (e >> 2) + (e & 3);
-          m[sub] = fmaxf(m[sub], fmaxf((r0 >= la && r0 < lb) ? v0 : NEG_INF, (r0 + 1 >= la && r0 + 1 < lb) ? v1 : NEG_INF));
+          m[sub] = max_nan(m[sub], max_nan((r0 >= la && r0 < lb) ? v0 : NEG_INF, (r0 + 1 >= la && r0 + 1 < lb) ? v1 : NEG_INF));
         }
       if (ec - T > 32 || jc >= nd) break;  // doc jc continues in the next tile
       doc_end();

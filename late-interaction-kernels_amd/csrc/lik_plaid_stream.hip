@@ -257,13 +257,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) m[sub] = fmaxf(m[sub], acc[sub][e]);
+        for (int e = 0; e < 16; ++e) m[sub] = max_nan(m[sub], acc[sub][e]);
     } else {
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          if (8 * (e >> 2) + 4 * h + (e & 3) < d.nv) m[sub] = fmaxf(m[sub], acc[sub][e]);
+          if (8 * (e >> 2) + 4 * h + (e & 3) < d.nv) m[sub] = max_nan(m[sub], acc[sub][e]);
     }
     if ((int64_t)(d.t + 1) * 32 >= dlen(d.j)) {
       // doc end: column maxima over both halves, scaled, summed over the
@@ -271,7 +271,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
-        const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        const float mm = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
         const float v = __builtin_isfinite(mm) ? mm * qsc[sub] : 0.f;
         auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
         // the tile kernel's flush order: that kernel puts up to 4 queries of
@@ -369,7 +369,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
   constexpr int LUTW = SPLIT ? 2 * 256 : FPB * 256;
   __shared__ __attribute__((aligned(16))) float s_lut[LUTW];
   __shared__ __attribute__((aligned(1024))) char s_st[4][STB];
-  __shared__ __attribute__((aligned(16))) float s_sc[4][SPLIT ? 64 : 1];
+  __shared__ __attribute__((aligned(16))) float s_sc[4][SPLIT ? 32 : 1];
   __shared__ float s_r2[SPLIT ? 256 : 1];
   if constexpr (SPLIT) {
     for (int v = threadIdx.x; v < 256; v += 256) {
@@ -607,7 +607,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
         acc[sub] = mfma32<EK>(acc[sub], &ra, &bq[sub][ks]);
       }
     }
-    // row l32's scale and mask bias (-inf past the tile's end) to the
+    // row l32's scale to the
     // accumulator layout: element i of lane l is row 8 (i / 4) + 4 h + i % 4
     float sc = 1.f;
     if (f_norm_d) {
@@ -616,18 +616,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
       ss = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
       sc = __builtin_amdgcn_rsqf(fmaxf(ss, 1e-24f));  // 1 / max(||x||, 1e-12)
     }
-    if (h == 0) {
-      s_sc[wl][l32] = sc;
-      s_sc[wl][32 + l32] = l32 < d.nv ? 0.f : NEG_INF;
-    }
+    if (h == 0) s_sc[wl][l32] = sc;
+    // rows past the tile's end are set to -inf by a select (in partial tiles
+    // only): their staged data is not the tile's and may hold NaN, which an
+    // added -inf bias would keep
+    const bool part = d.nv < 32;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f32x4 sc4 = *(const f32x4*)&s_sc[wl][8 * j + 4 * h];
-      const f32x4 b4 = *(const f32x4*)&s_sc[wl][32 + 8 * j + 4 * h];
 #pragma unroll
       for (int sub = 0; sub < QN; ++sub)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[sub][4 * j + t] = fmaf(acc[sub][4 * j + t], sc4[t], b4[t]);
+        for (int t = 0; t < 4; ++t) {
+          const float v = acc[sub][4 * j + t] * sc4[t];
+          acc[sub][4 * j + t] = (part && 8 * j + 4 * h + t >= d.nv) ? NEG_INF : v;
+        }
     }
   };
   auto compute = [&](const Tile& d, const Regs& rg) {
@@ -699,18 +702,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DPAD >
     for (int sub = 0; sub < QN; ++sub) {
       if (SPLIT || d.nv == 32) {  // split form: rows past the end are already -inf
 #pragma unroll
-        for (int e = 0; e < 16; ++e) m[sub] = fmaxf(m[sub], acc[sub][e]);
+        for (int e = 0; e < 16; ++e) m[sub] = max_nan(m[sub], acc[sub][e]);
       } else {
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          if (8 * (e >> 2) + 4 * h + (e & 3) < d.nv) m[sub] = fmaxf(m[sub], acc[sub][e]);
+          if (8 * (e >> 2) + 4 * h + (e & 3) < d.nv) m[sub] = max_nan(m[sub], acc[sub][e]);
       }
     }
     if ((int64_t)(d.t + 1) * 32 >= dlen(d.j)) {
 #pragma unroll
      for (int sub = 0; sub < QN; ++sub) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[sub]), __float_as_uint(m[sub]), false, false);
-      const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const float mm = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
       const float v = __builtin_isfinite(mm) ? mm * qsc[sub] : 0.f;
       auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
       // the tile kernel's flush order (query g at place g of its group of 4:

@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
   // the tile kernel's flush order, written by lane 0
   auto doc_end = [&](int k) {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    const float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    const float mm = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
     const float v = __builtin_isfinite(mm) ? (NORMQ ? mm * qsc : mm) : 0.f;
     auto col = [&](int c) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), c)); };
     for (int t = 0; t < p.QPG; ++t) {
@@ -263,7 +263,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
           if (8 * (e >> 2) + (e & 3) >= lim) acc[e] = NEG_INF;
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) m = fmaxf(m, acc[e]);
+      for (int e = 0; e < 16; ++e) m = max_nan(m, acc[e]);
       if (d.docend) doc_end(d.k);
     }
     return dn;

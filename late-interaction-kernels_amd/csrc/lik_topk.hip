@@ -292,10 +292,11 @@ __global__ void __launch_bounds__(256)
       for (int64_t t = 0; t < len; ++t) {
         int64_t code = codes[b * cs + t];
         code = (code >= 0 && code < ncent) ? code : 0;
-        m = fmaxf(m, qcs[code * sc + s * sl]);
+        m = max_nan(m, qcs[code * sc + s * sl]);
       }
     }
-    float v = (s < lq && m != -__builtin_huge_valf()) ? m : 0.f;
+    // a non-finite max (empty doc, NaN or +inf score) contributes 0 (reference.py:119-120)
+    float v = (s < lq && __builtin_isfinite(m)) ? m : 0.f;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
     total += v;

@@ -82,11 +82,12 @@ __global__ void __launch_bounds__(256) maxsim_wide_kernel(const Params p) {
       if constexpr (EK == EK_F16) {
         hi[k] = f32_to_f16_bits(v[2 * k]) | (f32_to_f16_bits(v[2 * k + 1]) << 16);
       } else {
-        const uint32_t a = f32_to_bf16_bits(v[2 * k]), b = f32_to_bf16_bits(v[2 * k + 1]);
-        hi[k] = a | (b << 16);
         if constexpr (EK == EK_F32) {
-          const float ra = v[2 * k] - __uint_as_float(a << 16), rb = v[2 * k + 1] - __uint_as_float(b << 16);
-          lo[k] = f32_to_bf16_bits(ra) | (f32_to_bf16_bits(rb) << 16);
+          const uint32_t a = split_hi(v[2 * k]), b = split_hi(v[2 * k + 1]);
+          hi[k] = a | (b << 16);
+          lo[k] = split_lo(a, v[2 * k]) | (split_lo(b, v[2 * k + 1]) << 16);
+        } else {
+          hi[k] = f32_to_bf16_bits(v[2 * k]) | (f32_to_bf16_bits(v[2 * k + 1]) << 16);
         }
       }
     }
@@ -142,20 +143,16 @@ __global__ void __launch_bounds__(256) maxsim_wide_kernel(const Params p) {
         for (int t = 0; t < 4; ++t) {
           const float sc = sc4[t];
           const float v = sc == NEG_INF ? NEG_INF : acc[4 * jj + t] * sc;
-          if (arow) {
-            if (v > m) {
-              m = v;
-              mi = (int)(t0 + 8 * jj + 4 * h + t);
-            }
-          } else {
-            m = fmaxf(m, v);
-          }
+          // NaN propagates into m (the row then scores 0); the winner
+          // index moves only on a strictly larger value
+          if (arow && v > m) mi = (int)(t0 + 8 * jj + 4 * h + t);
+          m = max_nan(m, v);
         }
       }
     }
     // column l32: max over both halves' rows, query scale, validity, sum
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    float mm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    float mm = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
     if (arow) {
       // winner over lanes l, l^32: larger value, equal values the lower row;
       // -1 where the max is not finite (the row contributes 0)

@@ -192,8 +192,21 @@ def maxsim_kd(Q, D, q_mask=None, d_mask=None, *, normalize=False, dtype=np.float
     return out
 
 
+def _row_max_sum(S):
+    """sum over query tokens of max over doc tokens, a non-finite max scoring 0.
+
+    reference.py:83-85 applies the isfinite -> 0 rule in maxsim_reference; its
+    packed / pair / padded loops (reference.py:236-306) sum the raw maxima, which
+    differ only on non-finite inputs (a NaN or +inf similarity). Every entry point
+    here scores like maxsim_reference, so that packed and padded inputs holding the
+    same tokens give the same scores."""
+    m = S.max(axis=1)
+    return np.where(np.isfinite(m), m, 0.0).sum()
+
+
 def maxsim_varlen(Qp, Dp, cu_q, cu_d, *, dtype=np.float64):
-    """Packed MaxSim (reference.py:213-245): empty query or doc -> 0."""
+    """Packed MaxSim (reference.py:213-245): empty query or doc -> 0; a non-finite
+    row max scores 0 (reference.py:83-85, see _row_max_sum)."""
     Qp = np.asarray(Qp, dtype=dtype)
     Dp = np.asarray(Dp, dtype=dtype)
     cu_q = np.asarray(cu_q, dtype=np.int64)
@@ -208,7 +221,7 @@ def maxsim_varlen(Qp, Dp, cu_q, cu_d, *, dtype=np.float64):
             dj = Dp[cu_d[j] : cu_d[j + 1]]
             if dj.shape[0] == 0:
                 continue
-            out[i, j] = (qi @ dj.T).max(axis=1).sum()
+            out[i, j] = _row_max_sum(qi @ dj.T)
     return out
 
 
@@ -224,7 +237,7 @@ def maxsim_pairs(Qp, Dp, cu_q, cu_d, pair_q, pair_d, *, dtype=np.float64):
         dj = Dp[cu_d[j] : cu_d[j + 1]]
         if qi.shape[0] == 0 or dj.shape[0] == 0:
             continue
-        out[k] = (qi @ dj.T).max(axis=1).sum()
+        out[k] = _row_max_sum(qi @ dj.T)
     return out
 
 
@@ -242,7 +255,7 @@ def maxsim_padded(queries, documents, query_lengths, doc_lengths, *, dtype=np.fl
             dd = D[b, c, : dl[b, c]]
             if q.shape[0] == 0 or dd.shape[0] == 0:
                 continue
-            out[b, c] = (q @ dd.T).max(axis=1).sum()
+            out[b, c] = _row_max_sum(q @ dd.T)
     return out
 
 

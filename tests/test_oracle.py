@@ -231,6 +231,121 @@ def test_oracle_topk_matches_sorted_and_chunking(largest):
         np.testing.assert_array_equal(got[0], full[0])
 
 
+def _torch_max(vals):
+    """torch.max over a row: NaN if any element is NaN (torch propagates it), else the max."""
+    best = -np.inf
+    for v in vals:
+        if v != v:
+            return float("nan")
+        best = max(best, v)
+    return best
+
+
+def brute_nonfinite(Q, D, qm=None, dm=None):
+    """reference.py:75-94 step by step with IEEE scalar arithmetic: masked doc
+    tokens are -inf, the row max propagates NaN, a non-finite max scores 0,
+    masked query tokens are multiplied by 0 after that."""
+    Nq, Lq, _ = Q.shape
+    Nd, Ld, _ = D.shape
+    out = np.zeros((Nq, Nd))
+    with np.errstate(invalid="ignore", over="ignore"):
+        for i in range(Nq):
+            for j in range(Nd):
+                tot = 0.0
+                for s in range(Lq):
+                    row = []
+                    for t in range(Ld):
+                        acc = 0.0
+                        for a, b in zip(Q[i, s], D[j, t]):
+                            acc += float(a) * float(b)
+                        row.append(acc if dm is None or dm[j, t] else -np.inf)
+                    best = _torch_max(row)
+                    best = best if np.isfinite(best) else 0.0
+                    tot += best * (1.0 if qm is None or qm[i, s] else 0.0)
+                out[i, j] = tot
+    return out
+
+
+@pytest.mark.parametrize("normalize", [False, True])
+def test_oracle_nonfinite_inputs(normalize):
+    """NaN / +inf / -inf tokens in Q and D (masked and kept): the oracle follows
+    torch's semantics (reference.py:83-85), pinned by a scalar loop."""
+    rng = np.random.default_rng(11)
+    Q = rng.standard_normal((3, 5, 8))
+    D = rng.standard_normal((5, 7, 8))
+    Q[0, 1, 3] = np.nan
+    Q[1, 2, 0] = np.inf
+    Q[2, 4, 5] = -np.inf
+    Q[2, 0, 1] = np.nan  # masked below: contributes 0
+    D[0, 2, 4] = np.nan
+    D[1, 0, 0] = np.inf
+    D[2, 6, 7] = -np.inf
+    D[3, 3, 2] = np.nan  # masked below: ignored
+    D[4, 1, 1] = -np.inf
+    D[4, 5, 6] = np.inf  # masked below
+    qm = np.ones((3, 5), bool)
+    qm[2, 0] = False
+    dm = np.ones((5, 7), bool)
+    dm[3, 3] = False
+    dm[4, 5] = False
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        got = O.maxsim(Q, D, qm, dm, normalize=normalize)
+        Qb = Q / np.linalg.norm(Q, axis=-1, keepdims=True) if normalize else Q
+        Db = D / np.linalg.norm(D, axis=-1, keepdims=True) if normalize else D
+    want = brute_nonfinite(Qb, Db, qm, dm)
+    assert np.all(np.isfinite(got))
+    np.testing.assert_allclose(got, want, atol=1e-12)
+    # the NaN doc token poisons every query token's max over doc 0
+
+
+def test_oracle_packed_entry_points_nonfinite():
+    """varlen / pairs / padded / KD on poisoned tokens score like the scalar loop
+    (and like each other): one isfinite rule for every entry point."""
+    rng = np.random.default_rng(12)
+    Q = rng.standard_normal((3, 4, 8))
+    D = rng.standard_normal((4, 6, 8))
+    Q[0, 1, 3] = np.nan
+    Q[1, 2, 0] = np.inf
+    D[0, 2, 4] = np.nan
+    D[2, 5, 1] = -np.inf
+    D[3, 0, 0] = np.inf
+    lens = np.array([6, 3, 6, 5])
+    dm = np.arange(6)[None] < lens[:, None]
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = brute_nonfinite(Q, D, None, dm)
+        Dp = np.concatenate([D[j, : lens[j]] for j in range(4)])
+        cu_d = np.concatenate([[0], np.cumsum(lens)])
+        cu_q = np.arange(4) * 4
+        got_v = O.maxsim_varlen(Q.reshape(-1, 8), Dp, cu_q, cu_d)
+        pq, pd = np.repeat(np.arange(3), 4), np.tile(np.arange(4), 3)
+        got_p = O.maxsim_pairs(Q.reshape(-1, 8), Dp, cu_q, cu_d, pq, pd)
+        got_pad = O.maxsim_padded(Q, np.broadcast_to(D[None], (3, 4, 6, 8)), np.full(3, 4), np.tile(lens, (3, 1)))
+        got_kd = O.maxsim_kd(Q, np.broadcast_to(D[None], (3, 4, 6, 8)), None, np.broadcast_to(dm[None], (3, 4, 6)))
+    for got in (got_v, got_p.reshape(3, 4), got_pad, got_kd):
+        assert np.all(np.isfinite(got))
+        np.testing.assert_allclose(got, want, atol=1e-12)
+
+
+def test_oracle_plaid_approx_nonfinite():
+    """A NaN or +inf score in a gathered qcs row makes that query token's max
+    non-finite: it scores 0 (reference.py:118-120); -inf loses the max."""
+    qcs = np.arange(24, dtype=float).reshape(6, 4) / 10.0
+    qcs[2, 1] = np.nan
+    qcs[3, 2] = np.inf
+    qcs[4, 3] = -np.inf
+    codes = np.array([[0, 2, 1], [3, 0, 0], [4, 1, 0], [2, 2, 2]])
+    lens = np.array([3, 2, 1, 0])
+    got = O.plaid_approx_score(qcs, codes, lens)
+    want = []
+    for b in range(4):
+        tot = 0.0
+        for s in range(4):
+            m = _torch_max([qcs[c, s] for c in codes[b, : lens[b]]])
+            tot += m if np.isfinite(m) else 0.0
+        want.append(tot)
+    np.testing.assert_allclose(got, want, atol=1e-12)
+
+
 def test_oracle_plaid_approx():
     rng = np.random.default_rng(8)
     qcs = rng.standard_normal((20, 6))

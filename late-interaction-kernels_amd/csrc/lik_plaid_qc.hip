@@ -52,9 +52,11 @@ constexpr int kQcRMax = 128;  // docs per wavefront of the scan (host caps R)
 // qc[q * qc_qs + c * 32 + s] = fp16(qsc_s * (q_s . c)), for every centroid c
 // and the 32 token slots of query q (0 past its length). One wavefront per
 // (query, 32 centroids).
+// perm: query token s at slot 16 ((s >> 2) & 1) + 4 (s >> 3) + (s & 3) of the
+// row (the element order of plaid_scan_kernel's accumulators), else at slot s.
 template <int EK, int DPAD>
 __global__ void __launch_bounds__(256) centroid_scores_kernel(const Params p, uint16_t* __restrict__ qc,
-                                                              int64_t qc_qs, int64_t ntile) {
+                                                              int64_t qc_qs, int64_t ntile, int perm) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;
   constexpr int HALF = DPAD / 2;
@@ -80,10 +82,11 @@ __global__ void __launch_bounds__(256) centroid_scores_kernel(const Params p, ui
   ss += __shfl_xor(ss, 32);
   const float qsc = valid ? ((p.normalize & 1) ? inv_norm(ss) : 1.f) : 0.f;
   uint16_t* o = qc + q * qc_qs;
+  const int slot = perm ? 16 * ((l32 >> 2) & 1) + 4 * (l32 >> 3) + (l32 & 3) : l32;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t row = tile * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-    if (row < p.pl.ncent) o[row * 32 + l32] = (uint16_t)f32_to_f16_bits(acc[i] * qsc);
+    if (row < p.pl.ncent) o[row * 32 + slot] = (uint16_t)f32_to_f16_bits(acc[i] * qsc);
   }
 }
 
@@ -202,9 +205,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(&s_st[wl][k][0]));
   const uint32_t cs_lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int32_t*)(&s_codes[wl][0][0]));
+  // (s_nop 4: the descriptor words come from v_readlane / v_readfirstlane,
+  // VALU writes of SGPRs that a VMEM instruction may read only 5 wait states
+  // later; the compiler does not count wait states into inline asm)
   auto dma = [&](uint32_t lds, uint32_t voff, const u32x4& desc) {
     uint32_t saved;
     asm volatile(
+        "s_nop 4\n\t"
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
         "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
@@ -216,6 +223,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   auto dma_nt = [&](uint32_t lds, uint32_t voff, const u32x4& desc) {
     uint32_t saved;
     asm volatile(
+        "s_nop 4\n\t"
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
         "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
@@ -315,15 +323,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
         rg.qv[sub][i >> 1][i & 1] = *(const _Float16*)(st + ((i & 1) ? qv_odd : qv_even) + rel);
       }
   };
-  // a * b + (fp16 half of w) in one instruction (the half converted exactly)
+  // a * b + (fp16 half of w), one v_fma_mix_f32 (the half converted
+  // exactly). Written as fmaf on the converted half, not as inline asm: the
+  // operand a comes straight from an MFMA, and only for compiler-visible
+  // instructions does the compiler insert the wait states an MFMA result
+  // needs before a VALU instruction may read it.
   auto fma_mix = [](float a, float b, f16x2 w, auto HI) -> float {
-    float r;
-    const uint32_t wb = __builtin_bit_cast(uint32_t, w);
-    if constexpr (decltype(HI)::value)
-      asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(r) : "v"(a), "v"(b), "v"(wb));
-    else
-      asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,0,1]" : "=v"(r) : "v"(a), "v"(b), "v"(wb));
-    return r;
+    return __builtin_fmaf(a, b, (float)w[decltype(HI)::value ? 1 : 0]);
   };
   // The doc whose tokens continue into the current tile (jc, ending at token
   // ec); its end is known without a table read until it is reached.
@@ -472,6 +478,363 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
     }
 }
 
+// ---------------------------------------------------------------------------
+// plaid_scan_kernel: the same scan with query tokens as the MFMA A rows and
+// doc tokens as the B columns, one doc token per lane (l32), so that every
+// stream lands in registers with plain buffer loads and no LDS staging:
+//   lane (l32, h) of tile t loads token l32's code, its residual bytes of
+//   half h (16 B at d = 128, nbits = 2), its inverse norm, and 32 bytes of
+//   its centroid's table row: the 16 query slots of half h, which the table
+//   stores contiguously (query token s at slot 16 ((s >> 2) & 1) +
+//   4 (s >> 3) + (s & 3), the accumulator order of element e of that half).
+// The accumulator element e of lane (l32, h) is query token
+// 8 (e / 4) + 4 h + e % 4 against doc token l32; the query rows are
+// normalised before they are rounded, so the epilogue is
+//   v[e] = (acc[e] + qc[e]) * inv      (inv: one value per lane)
+// and the running max is elementwise per lane across tiles; a doc's end
+// reduces the 16 maxima of each half over its 32 lanes (a transposing
+// butterfly of permlane16 swaps and DPP moves) and sums the 32 query tokens.
+// Pipeline: tile c + LS's loads are issued after tile c is scored; their
+// codes were loaded LC = 2 LS tiles ahead, right after tile c's loads, so a
+// wait for either never waits for a younger load. The loads are inline asm
+// with explicit vmcnt counts (see load_tile). The loop is unrolled by LC so
+// the register rings have static indices.
+// Measured against the LDS-staged kernel on the C5 corpus at Nq = 1: 2.57
+// against 2.70 ms. What bounds it (counters): the texture address and data
+// units (TA busy 0.92, TD 0.95), i.e. the five vector memory instructions per
+// tile, two of them 64 random 32-byte table reads; with every table read
+// pointed at one row (timing only) the scan takes 2.02 ms.
+// Steps I .. N-1 of one unrolled round (static register indices), stopping
+// at the last tile; false once it stopped.
+template <int I, int N, class F>
+__device__ __forceinline__ bool scan_steps(F& f, int c, int n) {
+  if constexpr (I == N) {
+    return true;
+  } else {
+    if (c + I >= n) return false;
+    f(std::integral_constant<int, I>{}, c + I);
+    return scan_steps<I + 1, N>(f, c, n);
+  }
+}
+
+// LS tiles in flight per wavefront: 3 at three waves per SIMD, 2 at four.
+template <int EK, int DPAD, int NBITS, bool FULLD, bool NORMD, int LS>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 2 ? 4 : 3)))
+    plaid_scan_kernel(const Params p, const uint16_t* __restrict__ qc, int64_t qc_qs, const float* __restrict__ tinv) {
+  using T = KT<EK, DPAD>;
+  constexpr int KS = T::KSTEPS;
+  constexpr int HALF = DPAD / 2;
+  constexpr int RBL = HALF * NBITS / 8;  // residual bytes per lane (8 .. 64)
+  constexpr int RW = RBL / 4;            // ... as dwords
+  constexpr int FPB = 8 / NBITS;
+  constexpr int LC = 2 * LS;
+  constexpr uint32_t NT = 2;  // non-temporal cache policy of the streamed loads
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  static_assert(RW == 2 || RW % 4 == 0, "residual lane bytes");
+
+  __shared__ __attribute__((aligned(16))) float s_lut[2 * 256];
+  __shared__ float s_out[4][kQcRMax];
+  __shared__ int32_t s_cu[4][kQcRMax + 1];
+  for (int v = threadIdx.x; v < 256; v += 256) {
+    uint32_t h16[4] = {0u, 0u, 0u, 0u};
+    for (int k = 0; k < FPB; ++k) {
+      uint32_t bc = ((uint32_t)v >> (k * NBITS)) & ((1u << NBITS) - 1u);
+      bc = bc < (uint32_t)p.pl.nb ? bc : (uint32_t)(p.pl.nb - 1);
+      const float wgt = p.pl.bw[bc];
+      h16[k] = EK == EK_F16 ? f32_to_f16_bits(wgt) : f32_to_bf16_bits(wgt);
+    }
+    uint32_t* e = (uint32_t*)&s_lut[v * 2];
+    e[0] = h16[0] | (h16[1] << 16);
+    e[1] = h16[2] | (h16[3] << 16);
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+  const int wl = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t wv = (int64_t)blockIdx.x * 4 + wl;
+  const int64_t g = wv / p.NR, r = wv - g * p.NR;
+  if (g >= p.ngroups) return;  // wave-uniform, after the only barrier
+
+  // ---- query g: token l32 as the A rows (the B columns of the other
+  // kernels), scaled by its inverse norm before rounding (0 past its length),
+  // so the accumulators are q^.r and the table holds q^.c ----
+  u32x4 aq[KS];
+  {
+    const bool valid = g < p.q.n && l32 < seq_len(p.q, g);
+    const char* rowp = valid ? seq_row0(p.q, g) + (int64_t)l32 * p.q.sl_b : nullptr;
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int e = h * HALF + ks * 8;
+      aq[ks] = (valid && (FULLD || e < p.q.dim)) ? *(const u32x4*)(rowp + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
+      if (p.normalize & 1) ss += chunk_sumsq<EK>(aq[ks]);
+    }
+    ss += __shfl_xor(ss, 32);
+    const float sc = valid ? ((p.normalize & 1) ? inv_norm(ss) : 1.f) : 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t x = aq[ks][w];
+        if constexpr (EK == EK_F16)
+          aq[ks][w] = f32_to_f16_bits(f16_to_f32((uint16_t)(x & 0xffffu)) * sc) |
+                      (f32_to_f16_bits(f16_to_f32((uint16_t)(x >> 16)) * sc) << 16);
+        else
+          aq[ks][w] = f32_to_bf16_bits(bf16lo_to_f32(x) * sc) | (f32_to_bf16_bits(bf16hi_to_f32(x) * sc) << 16);
+      }
+      asm volatile("" : "+v"(aq[ks]));
+    }
+  }
+
+  // ---- this wave's docs [j0, j1): tokens [T0, T0 + span) of the packed corpus ----
+  const int64_t j0 = r * p.R;
+  const int64_t j1 = j0 + p.R < p.pl.n ? j0 + p.R : p.pl.n;
+  const int nd = (int)(j1 - j0);
+  for (int k = lane; k <= nd; k += 64) s_cu[wl][k] = p.pl.cu[j0 + k];
+  __builtin_amdgcn_wave_barrier();
+  const int T0 = __builtin_amdgcn_readfirstlane(s_cu[wl][0]);
+  const int span = __builtin_amdgcn_readfirstlane(s_cu[wl][nd]) - T0;
+  const int ntile = (span + 31) >> 5;
+
+  const int32_t* code_p = p.pl.codes + T0;
+  const char* res_p = (const char*)p.pl.res + (int64_t)T0 * p.pl.res_st;
+  const float* inv_p = NORMD ? tinv + T0 : nullptr;
+  const int64_t res_tile = 32 * p.pl.res_st;
+  const __amdgpu_buffer_rsrc_t rtab = make_rsrc(qc + g * qc_qs, (uint32_t)(p.pl.ncent * 64));
+  const uint32_t res_lane = (uint32_t)(l32 * p.pl.res_st + h * RBL);
+  auto rows_of = [&](int i) {
+    const int rem = span - 32 * i;
+    return rem < 0 ? 0 : (rem < 32 ? rem : 32);
+  };
+  // Loads are inline asm into registers, waited for by explicit vmcnt
+  // counts (loads return in issue order): with compiler-visible loads the
+  // compiler's own wait insertion puts a full vmcnt(0) at the loop head.
+  // A load's destination registers are tied to the stage's previous
+  // contents ("+v"), so each ring slot keeps its physical registers from
+  // one load to the next and the register allocator never moves (reads) a
+  // register whose load is still in flight; each wait names the registers it
+  // guards, so nothing reads a stage before its wait; and the loads of a step
+  // are issued after an ordering point on the running maxima, which every
+  // read of the previous contents feeds. Descriptors: raw, stride 0, untyped.
+  // Each load starts with s_nop 4: its descriptor words come from
+  // v_readfirstlane (a VALU write of SGPRs), which a VMEM instruction may read
+  // only 5 wait states later, and the compiler does not count wait states
+  // into inline asm.
+  auto desc = [](const void* base, uint32_t nbytes) -> u32x4 {
+    const uint64_t b = (uint64_t)base;
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu),
+                 (uint32_t)__builtin_amdgcn_readfirstlane(nbytes), 0x00020000u};
+  };
+  const u32x4 dtab = desc(qc + g * qc_qs, (uint32_t)(p.pl.ncent * 64));
+
+  struct Stage {
+    u32x4 rw[RW == 2 ? 1 : RW / 4];  // residual bytes (RW == 2: the low half of rw[0])
+    float inv;
+    u32x4 tq[2];  // the table's 16 fp16 values of this lane's half, in element order
+  };
+  // loads per tile (residual, inverse norm, table) and per code
+  constexpr int NLT = (RW == 2 ? 1 : RW / 4) + (NORMD ? 1 : 0) + 2;
+  Stage st[LS];
+  uint32_t code[LC];
+#pragma unroll
+  for (int k = 0; k < LS; ++k) {
+#pragma unroll
+    for (int v = 0; v < (RW == 2 ? 1 : RW / 4); ++v) st[k].rw[v] = u32x4{0u, 0u, 0u, 0u};
+    st[k].inv = 1.f;
+    st[k].tq[0] = st[k].tq[1] = u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int k = 0; k < LC; ++k) code[k] = 0u;
+  auto load_code = [&](int t, uint32_t& c) {
+    const u32x4 dc = desc(code_p + 32 * (int64_t)t, (uint32_t)rows_of(t) * 4u);
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, 0 offen nt" : "+v"(c) : "v"((uint32_t)l32 * 4u), "s"(dc));
+  };
+  auto load_tile = [&](int t, uint32_t cd, Stage& s) {
+    const int nv = rows_of(t);
+    const u32x4 dr = desc(res_p + t * res_tile, (uint32_t)nv * (uint32_t)p.pl.res_st);
+    if constexpr (RW == 2) {
+      u32x2 v = {s.rw[0][0], s.rw[0][1]};
+      asm volatile("s_nop 4\n\tbuffer_load_dwordx2 %0, %1, %2, 0 offen nt" : "+v"(v) : "v"(res_lane), "s"(dr));
+      s.rw[0][0] = v[0];
+      s.rw[0][1] = v[1];
+    } else {
+#pragma unroll
+      for (int k = 0; k < RW / 4; ++k)
+        asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3 nt"
+                     : "+v"(s.rw[k]) : "v"(res_lane), "s"(dr), "n"(16 * k));
+    }
+    if constexpr (NORMD) {
+      const u32x4 di = desc(inv_p + 32 * (int64_t)t, (uint32_t)nv * 4u);
+      asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, 0 offen nt" : "+v"(s.inv) : "v"((uint32_t)l32 * 4u), "s"(di));
+    }
+    const uint32_t row = cd < (uint32_t)p.pl.ncent ? cd : 0u;
+    const uint32_t toff = row * 64u + (uint32_t)h * 32u;
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(s.tq[0]) : "v"(toff), "s"(dtab));
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen offset:16" : "+v"(s.tq[1]) : "v"(toff), "s"(dtab));
+  };
+  // wait until at most n loads are in flight, for the registers of stage s
+  auto wait_stage = [](auto NN, Stage& s) {
+    constexpr int n = decltype(NN)::value;
+    asm volatile("s_waitcnt vmcnt(%[n])" : "+v"(s.inv), "+v"(s.tq[0]), "+v"(s.tq[1]) : [n] "n"(n));
+#pragma unroll
+    for (int k = 0; k < (RW == 2 ? 1 : RW / 4); ++k) asm volatile("" : "+v"(s.rw[k]));
+  };
+  auto wait_code = [](auto NN, uint32_t& c) {
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(c) : "n"(decltype(NN)::value));
+  };
+
+  float m[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) m[e] = NEG_INF;
+  int jc = 0;
+  int ec = __builtin_amdgcn_readfirstlane(s_cu[wl][1]) - T0;
+  // doc jc ends: max over its lanes by a transposing butterfly (after the
+  // step over lane bit b each lane keeps half of its values, so 16 values
+  // take 8 + 4 + 2 + 1 + 1 exchanges): bit 4 by v_permlane16_swap, bits 3, 2,
+  // 1, 0 by DPP (row_ror:8, row_half_mirror, quad_perm [3,2,1,0] and
+  // [1,0,3,2]: each pairs lanes that differ in that bit); then the sum of the
+  // 32 query tokens' maxima (non-finite -> 0) by a rotation all-reduce in a
+  // fixed order. No LDS traffic.
+  auto dpp = [](float x, auto CTRL) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(CTRL)::value, 0xf, 0xf, false));
+  };
+  using std::integral_constant;
+  auto doc_end = [&]() {
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // rows 0/1 and 2/3 swap: x[i] gets element i of lanes l, l^16 on even
+      // rows and element i + 8 on odd rows
+      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(m[i]), __float_as_uint(m[i + 8]), false, false);
+      x[i] = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    auto step = [&](int n, int bit, auto CTRL) {
+#pragma unroll
+      for (int i = 0; i < n; ++i) {
+        const float keep = bit ? x[i + n] : x[i];
+        const float send = bit ? x[i] : x[i + n];
+        x[i] = max_nan(keep, dpp(send, CTRL));
+      }
+    };
+    step(4, (l32 >> 3) & 1, integral_constant<int, 0x128>{});  // row_ror:8
+    step(2, (l32 >> 2) & 1, integral_constant<int, 0x141>{});  // row_half_mirror
+    step(1, (l32 >> 1) & 1, integral_constant<int, 0x1b>{});   // quad_perm [3,2,1,0]
+    const float mm = max_nan(x[0], dpp(x[0], integral_constant<int, 0xb1>{}));  // quad_perm [1,0,3,2]
+    float v = ((lane & 1) == 0 && __builtin_isfinite(mm)) ? mm : 0.f;
+    v += dpp(v, integral_constant<int, 0x128>{});  // row_ror:8
+    v += dpp(v, integral_constant<int, 0x124>{});  // row_ror:4
+    v += dpp(v, integral_constant<int, 0x122>{});  // row_ror:2
+    v += dpp(v, integral_constant<int, 0x121>{});  // row_ror:1
+    {
+      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    if (lane == 0) s_out[wl][jc] = v * p.out_scale;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) m[e] = NEG_INF;
+    ++jc;
+    ec = jc < nd ? __builtin_amdgcn_readfirstlane(s_cu[wl][jc + 1]) - T0 : 0x7fffffff;
+  };
+  // a * one + (fp16 half of w): one v_fma_mix_f32 (compiler-visible, so the
+  // MFMA-result wait states before it are the compiler's); `one` is an
+  // opaque 1.0 so that the multiply is not folded into a convert + add
+  float one = 1.f;
+  asm volatile("" : "+s"(one));
+  auto fma_mix = [&](float a, float, uint32_t w, auto HI) -> float {
+    return __builtin_fmaf(a, one, (float)__builtin_bit_cast(f16x2, w)[decltype(HI)::value ? 1 : 0]);
+  };
+  auto compute = [&](int i, const Stage& s) {
+    const int TT = 32 * i;
+    f32x16 acc;
+    auto byte_at = [&](int byte_i) -> uint32_t {
+      return (s.rw[byte_i >> 4][(byte_i >> 2) & 3] >> ((byte_i & 3) * 8)) & 0xffu;
+    };
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 rv;
+      if constexpr (FPB == 4) {
+        const uint2 e0 = *(const uint2*)&s_lut[byte_at(2 * ks) * 2];
+        const uint2 e1 = *(const uint2*)&s_lut[byte_at(2 * ks + 1) * 2];
+        rv = u32x4{e0.x, e0.y, e1.x, e1.y};
+      } else if constexpr (FPB == 2) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) rv[k] = *(const uint32_t*)&s_lut[byte_at(4 * ks + k) * 2];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t b0 = byte_at(8 * ks + 2 * k), b1 = byte_at(8 * ks + 2 * k + 1);
+          rv[k] = (*(const uint32_t*)&s_lut[b0 * 2] & 0xffffu) | (*(const uint32_t*)&s_lut[b1 * 2] << 16);
+        }
+      }
+      if constexpr (!FULLD) {
+        if ((h * HALF + ks * 8) >= p.q.dim) rv = (u32x4){0u, 0u, 0u, 0u};
+      }
+      acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &aq[ks], &rv);
+    }
+    // the tile's scores, in place of the accumulators
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t w = s.tq[e >> 3][(e >> 1) & 3];
+      acc[e] = ((e & 1) ? fma_mix(acc[e], 1.f, w, std::true_type{}) : fma_mix(acc[e], 1.f, w, std::false_type{})) * s.inv;
+    }
+    if (ec - TT > 32) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) m[e] = max_nan(m[e], acc[e]);
+      return;
+    }
+    int a = 0;
+    while (true) {
+      const int b = ec - TT < 32 ? ec - TT : 32;
+      const bool in = l32 >= a && l32 < b;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) m[e] = max_nan(m[e], in ? acc[e] : NEG_INF);
+      if (ec - TT > 32 || jc >= nd) break;
+      doc_end();
+      a = b;
+    }
+  };
+
+  // Prologue: codes of tiles 0 .. LS-1; then for each t < LS tile t's loads
+  // followed by the code of tile t + LS. From here on every tile's loads are
+  // followed by exactly one code load, so at the top of step c tile c's loads
+  // are followed by the code of tile c + LS and by LS - 1 later steps of
+  // NLT + 1 loads each.
+#pragma unroll
+  for (int t = 0; t < LS; ++t) load_code(t, code[t]);
+#pragma unroll
+  for (int t = 0; t < LS; ++t) {
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(code[t]));
+    load_tile(t, code[t], st[t]);
+    load_code(t + LS, code[t + LS]);
+  }
+  constexpr int kWaitTile = 1 + (LS - 1) * (NLT + 1);
+  auto step = [&](auto II, int c) {
+    constexpr int I = decltype(II)::value;  // c % LC
+    wait_stage(integral_constant<int, kWaitTile>{}, st[I % LS]);
+    compute(c, st[I % LS]);
+    // ordering point: the stage's previous contents are all read (they feed m)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(m[e]));
+    // the code of tile c + LS, loaded right after tile c's loads
+    wait_code(integral_constant<int, kWaitTile - 1>{}, code[(I + LS) % LC]);
+    load_tile(c + LS, code[(I + LS) % LC], st[I % LS]);
+    load_code(c + LC, code[I]);
+  };
+  for (int c = 0; c < ntile; c += LC)
+    if (!scan_steps<0, LC>(step, c, ntile)) break;
+  while (jc < nd) doc_end();
+  // no load may still be writing this wave's registers when it exits
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+  for (int k = lane; k < nd; k += 64)
+    if (g < p.q.n) p.out[g * p.osq + (j0 + k) * p.osd] = s_out[wl][k];
+}
+
 template <int EK, int DPAD, int NBITS>
 int launch_qc_scan(int qn, const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s) {
   const int64_t waves = p.ngroups * p.NR;
@@ -487,22 +850,60 @@ int launch_qc_scan(int qn, const Params& p, const uint16_t* qc, int64_t qc_qs, c
   return full ? go(plaid_qc_kernel<EK, DPAD, NBITS, 1, true>) : go(plaid_qc_kernel<EK, DPAD, NBITS, 1, false>);
 }
 
+// Residual rows the register-direct scan takes: its loads land in registers
+// that the compiler must neither spill nor copy while they are in flight, so
+// only instantiations that compile without spills are built (2-bit rows, and
+// 4-bit rows at d <= 64: 16 B of residual per lane); the others keep the
+// LDS-staged scan.
+constexpr int kScanLS = 3;  // (LS = 2 at four waves per SIMD spills at d = 128)
+
+template <int DPAD, int NBITS>
+constexpr bool scan_reg_ok() {
+  return NBITS == 2 || (NBITS == 4 && DPAD == 64);
+}
+
+template <int EK, int DPAD, int NBITS>
+int launch_scan(const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s) {
+  if constexpr (!scan_reg_ok<DPAD, NBITS>()) {
+    return LIK_ERR_UNSUPPORTED;
+  } else {
+  const int64_t waves = p.ngroups * p.NR;
+  const int64_t nb = (waves + 3) / 4;
+  if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(256), 0, s, p, qc, qc_qs, tinv);
+    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+  };
+  const bool full = p.q.dim == DPAD;
+  constexpr int LS = kScanLS;
+  if (tinv)
+    return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, true, LS>)
+                : go(plaid_scan_kernel<EK, DPAD, NBITS, false, true, LS>);
+  return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, false, LS>)
+              : go(plaid_scan_kernel<EK, DPAD, NBITS, false, false, LS>);
+  }
+}
+
 template <int EK, int DPAD>
 int launch_qc(int qn, const Params& p, uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s,
               const lik_launch_opts_t* opts) {
   const int64_t ntile = (p.pl.ncent + 31) / 32;
   const int64_t waves = p.q.n * ntile;
   if ((waves + 3) / 4 > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  // one query per wavefront: the register-direct scan, unless the caller
+  // forces the LDS-staged one (plaid_variant 5)
+  const bool reg = qn == 1 && !(opts && opts->plaid_variant == 5) &&
+                   (p.pl.nbits == 2 || (p.pl.nbits == 4 && DPAD == 64));
   hipLaunchKernelGGL((centroid_scores_kernel<EK, DPAD>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, qc,
-                     qc_qs, ntile);
+                     qc_qs, ntile, reg ? 1 : 0);
   if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
   const bool timed = opts && opts->timing_start && opts->timing_stop;
   if (timed && hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
   int rc;
   switch (p.pl.nbits) {
-    case 2: rc = launch_qc_scan<EK, DPAD, 2>(qn, p, qc, qc_qs, tinv, s); break;
-    case 4: rc = launch_qc_scan<EK, DPAD, 4>(qn, p, qc, qc_qs, tinv, s); break;
-    case 8: rc = launch_qc_scan<EK, DPAD, 8>(qn, p, qc, qc_qs, tinv, s); break;
+    case 2: rc = reg ? launch_scan<EK, DPAD, 2>(p, qc, qc_qs, tinv, s) : launch_qc_scan<EK, DPAD, 2>(qn, p, qc, qc_qs, tinv, s); break;
+    case 4: rc = reg ? launch_scan<EK, DPAD, 4>(p, qc, qc_qs, tinv, s) : launch_qc_scan<EK, DPAD, 4>(qn, p, qc, qc_qs, tinv, s); break;
+    case 8: rc = reg ? launch_scan<EK, DPAD, 8>(p, qc, qc_qs, tinv, s) : launch_qc_scan<EK, DPAD, 8>(qn, p, qc, qc_qs, tinv, s); break;
     default: rc = LIK_ERR_UNSUPPORTED;
   }
   if (rc == LIK_OK && timed && hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;

@@ -92,11 +92,15 @@ typedef struct {
  *       0 = automatic (the streaming kernel picks its own).
  *   plaid_variant (lik_plaid_maxsim_ex): 0 automatic, 1 per-lane stream
  *       decode, 2 exact LDS-gather decode (bitwise equal to the tile
- *       kernel), 3 the tile kernel (no stream kernel).
+ *       kernel), 3 the tile kernel (no stream kernel). lik_plaid_maxsim_qc:
+ *       0 automatic, 5 the LDS-staged scan instead of the register-direct
+ *       one for a single query.
  *   timing_start, timing_stop: hipEvent_t or NULL. When both are set, they
  *       are recorded on the call's stream immediately before and after the
- *       call's main MaxSim launch (the launch that scores the mask-free
- *       documents), so a caller can time that kernel alone.
+ *       call's MaxSim scoring launches: without the pre-passes (mask summary,
+ *       row norms, query-chunk sums), but with both launches of a doc mask
+ *       that has holes (the mask-free documents, then those with holes), so
+ *       a caller can time the scoring kernels alone.
  */
 typedef struct {
   int32_t col_waves;
@@ -303,8 +307,11 @@ int lik_plaid_token_norms(const lik_plaid_docs_t* docs, int64_t tok_begin, int64
  * flags normalise the docs (LIK_NORMALIZE / LIK_NORMALIZE_D) and ignored
  * otherwise. Docs must be packed (docs->cu_seqlens; a lengths-only layout
  * returns LIK_ERR_UNSUPPORTED). The workspace holds the [Q->n, n_centroids,
- * 32] fp16 table (lik_plaid_maxsim_qc_workspace_size bytes). opts:
- * docs_per_wg and the timing events (around the scan kernel) are honoured.
+ * 32] fp16 table (lik_plaid_maxsim_qc_workspace_size bytes): the caller
+ * keeps |q.c| below fp16's 65504 (the Python layer routes larger query or
+ * centroid norms to lik_plaid_maxsim). Q->len == 0 writes zero scores. opts:
+ * docs_per_wg, plaid_variant and the timing events (around the scan kernel)
+ * are honoured.
  */
 size_t lik_plaid_maxsim_qc_workspace_size(const lik_seqs_t* Q, const lik_plaid_docs_t* docs);
 int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* docs, const float* token_inv, uint32_t flags,

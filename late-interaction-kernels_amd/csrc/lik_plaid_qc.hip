@@ -835,6 +835,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     if (g < p.q.n) p.out[g * p.osq + (j0 + k) * p.osd] = s_out[wl][k];
 }
 
+// out[q, j] = 0 for a query batch without tokens (Lq == 0)
+__global__ void __launch_bounds__(256) zero_scores_kernel(float* out, int64_t nq, int64_t nd, int64_t osq,
+                                                          int64_t osd) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < nq * nd) out[(i / nd) * osq + (i % nd) * osd] = 0.f;
+}
+
 template <int EK, int DPAD, int NBITS>
 int launch_qc_scan(int qn, const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s) {
   const int64_t waves = p.ngroups * p.NR;
@@ -942,7 +949,16 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   const bool norm_d = (flags & (LIK_NORMALIZE | LIK_NORMALIZE_D)) != 0;
   if (norm_d && !token_inv) return LIK_ERR_INVALID;
   if (Q->n == 0 || docs->n == 0) return LIK_OK;
-  if (!out || !Q->data || !docs->codes || !docs->residuals || !docs->centroids || docs->n_centroids < 1)
+  if (!out) return LIK_ERR_INVALID;
+  if (Q->len == 0) {
+    // no query tokens: every score is 0 (the scan's column sums assume Lq > 0)
+    const int64_t n = Q->n * docs->n;
+    if ((n + 255) / 256 > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(zero_scores_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, out,
+                       Q->n, docs->n, out_stride_q, out_stride_d);
+    return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+  }
+  if (!Q->data || !docs->codes || !docs->residuals || !docs->centroids || docs->n_centroids < 1)
     return LIK_ERR_INVALID;
   if (((uintptr_t)Q->data) % 16 || (Q->stride_l * 2) % 16 || (Q->stride_n * 2) % 16) return LIK_ERR_UNSUPPORTED;
   if (((uintptr_t)docs->centroids) % 16 != 0 || (docs->cent_stride * 2) % 16 != 0) return LIK_ERR_UNSUPPORTED;

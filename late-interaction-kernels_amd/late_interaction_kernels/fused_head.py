@@ -20,6 +20,12 @@ winners the same way). Projecting first is the faster training route here:
 with the fused forward, the backward has to gather and project the winning
 rows again, and those extra small launches cost more than the fused forward
 saves on the reference's training shapes.
+
+The training route rounds the projection to the input dtype before it is
+normalised (one bf16 GEMM); the inference kernel, like the reference's fused
+kernel (fused_head.py:146-158), projects, adds the bias and normalises in fp32
+and rounds once. Scores of the two routes differ by that rounding
+(tests/test_gpu_fused_head.py compares them within 1e-2).
 """
 
 from __future__ import annotations
@@ -60,7 +66,8 @@ class _FromHiddenFn(torch.autograd.Function):
         g_rows = gd.reshape(Nd * Ld, -1)[rows, :d_out].float()
         grad_h = grad_w = grad_b = None
         if ctx.needs_input_grad[1]:
-            grad_h = torch.zeros_like(H_d)
+            # dense (row-major) whatever H_d's strides: the rows are scattered through a view
+            grad_h = torch.zeros(H_d.shape, dtype=H_d.dtype, device=H_d.device)
             grad_h.view(Nd * Ld, d_model)[rows] = (g_rows @ W.float()).to(H_d.dtype)
         if ctx.needs_input_grad[2]:
             grad_w = (g_rows.t() @ H_d.reshape(Nd * Ld, d_model)[rows].float()).to(W.dtype)

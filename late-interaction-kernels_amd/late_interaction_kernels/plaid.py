@@ -502,8 +502,9 @@ class ResidualIndex:
     and a scan that reads each token's code, residual bytes and norm from HBM
     and one 64-byte table row instead of a 256-byte centroid row. Scores
     match :func:`maxsim_residual_varlen` within bf16 rounding (the centroid
-    term is rounded to fp16). Larger batches, queries needing gradients, and
-    layouts the scan cannot take use :func:`maxsim_residual_varlen`.
+    term is rounded to fp16). Larger batches, queries needing gradients,
+    layouts the scan cannot take, and query / centroid norms whose products
+    could leave fp16's range use :func:`maxsim_residual_varlen`.
 
     The tensors are borrowed: modifying them after construction invalidates
     the precomputed norms.
@@ -523,6 +524,8 @@ class ResidualIndex:
         self.d = d
         self.n_docs = self.cu.numel() - 1
         T = self.codes.numel()
+        # largest centroid norm (one sync, here): bounds |q.c| for the fp16 table
+        self._cent_norm_max = float(self.centroids.float().norm(dim=-1).max()) if self.centroids.shape[0] else 0.0
         self.token_inv = torch.empty(T, device=self.codes.device, dtype=torch.float32)
         if T:
             docs = self._docs()
@@ -541,6 +544,18 @@ class ResidualIndex:
         return (Nq <= 64 and 0 < Lq <= 32 and d <= 128 and self.centroids.dtype == Qp.dtype
                 and self.residuals.shape[-1] % 16 == 0 and self.residuals.data_ptr() % 16 == 0)
 
+    # the scan keeps q.c in an fp16 table: beyond this bound the call takes
+    # maxsim_residual_varlen (fp16's largest finite value is 65504)
+    _TABLE_BOUND = 6.0e4
+
+    def _table_fits(self, Qp: torch.Tensor, normalize: bool) -> bool:
+        """|q.c| <= |q| max|c| stays below the fp16 bound. With normalize the
+        query rows are unit rows (no sync); without, the largest query-token
+        norm is read back (one sync per call). A NaN bound (NaN inputs) passes:
+        the scan propagates NaN like the other routes."""
+        qmax = 1.0 if normalize else float(Qp.float().norm(dim=-1).max()) if Qp.numel() else 0.0
+        return not (qmax * self._cent_norm_max >= self._TABLE_BOUND)
+
     def score(self, Q: torch.Tensor, *, normalize: bool = True) -> torch.Tensor:
         """``[Nq, Nd]`` fp32 scores (``[Nd]`` for 2-D Q), as :func:`maxsim_residual_varlen`."""
         q_squeeze = Q.dim() == 2
@@ -550,7 +565,7 @@ class ResidualIndex:
             raise ValueError(f"Q has d={Q.shape[-1]}, the index d={self.d}")
         _lib.require_gpu(Q)
         Qp = _prep_q(Q)
-        if (torch.is_grad_enabled() and Q.requires_grad) or not self._scan_ok(Qp):
+        if (torch.is_grad_enabled() and Q.requires_grad) or not self._scan_ok(Qp) or not self._table_fits(Qp, normalize):
             out = maxsim_residual_varlen(Q, self.codes, self.residuals, self.cu, self.centroids, self.bucket_weights,
                                          self.nbits, normalize=normalize)
             return out.squeeze(0) if q_squeeze else out

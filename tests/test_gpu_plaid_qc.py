@@ -72,7 +72,9 @@ def test_token_norms_and_scores(nbits, d, cdtype):
             got = idx.score(Q, normalize=normalize)
             with launch_options(plaid_variant=2):
                 exact = maxsim_residual_varlen(Q, *args, normalize=normalize)
-            assert rel_err(got.cpu().numpy(), exact.cpu().numpy()) < 5e-3, (nq, normalize)
+            # the split form against the exact decode route: fp16 q.c and bf16
+            # bucket weights (measured below 2e-3 on these inputs)
+            assert rel_err(got.cpu().numpy(), exact.cpu().numpy()) < 3e-3, (nq, normalize)
             ref = O.maxsim_residual_varlen(Q.double().cpu().numpy(), codes.numpy(), res.numpy(), cu.numpy(),
                                            cent.double().numpy(), bw.numpy(), nbits, normalize=normalize)
             assert rel_err(got.cpu().numpy(), ref) < 1e-2, (nq, normalize)
@@ -174,3 +176,48 @@ def test_docs_split_inside_tiles(nq):
         assert rel_err(base.cpu().numpy(), exact.cpu().numpy()) < 5e-3, normalize
         empty = (lens == 0).nonzero().flatten().cuda()
         assert base[:, empty].abs().max().item() == 0.0
+
+
+def test_table_range_falls_back():
+    """Query / centroid norms whose products could leave fp16's range (the q.c
+    table) take the exact route: the scores equal maxsim_residual_varlen's bits
+    and the oracle's, where the scan's fp16 table would hold inf."""
+    from late_interaction_kernels.plaid import ResidualIndex, maxsim_residual_varlen
+
+    _case("qc fp16 table range")
+    cent, bw, codes, res, cu = _index(60, 50, 128, 2, 9, torch.bfloat16)
+    cent = (cent.float() * 300.0).to(torch.bfloat16)  # |c| = 300
+    args = (codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), 2)
+    idx = ResidualIndex(*args)
+    Q = (torch.nn.functional.normalize(torch.randn(1, 32, 128), dim=-1) * 400.0).to(torch.bfloat16).cuda()
+    got = idx.score(Q, normalize=False)  # |q.c| up to 1.2e5 > 65504
+    assert torch.equal(got, maxsim_residual_varlen(Q, *args, normalize=False))
+    ref = O.maxsim_residual_varlen(Q.double().cpu().numpy(), codes.numpy(), res.numpy(), cu.numpy(),
+                                   cent.double().numpy(), bw.numpy(), 2, normalize=False)
+    assert np.all(np.isfinite(got.cpu().numpy())) and rel_err(got.cpu().numpy(), ref) < 1e-2
+    # normalised queries keep |q.c| <= 300: the scan runs, within its bound
+    got_n = idx.score(Q, normalize=True)
+    ref_n = O.maxsim_residual_varlen(Q.double().cpu().numpy(), codes.numpy(), res.numpy(), cu.numpy(),
+                                     cent.double().numpy(), bw.numpy(), 2, normalize=True)
+    assert rel_err(got_n.cpu().numpy(), ref_n) < 1e-2
+
+
+def test_c_abi_empty_query_tokens():
+    """lik_plaid_maxsim_qc with Q->len == 0 writes zero scores (no scan launch)."""
+    import ctypes
+
+    from late_interaction_kernels import _lib
+    from late_interaction_kernels.plaid import ResidualIndex
+
+    _case("qc C ABI Lq = 0")
+    cent, bw, codes, res, cu = _index(20, 30, 128, 2, 13, torch.bfloat16)
+    idx = ResidualIndex(codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), 2)
+    Q = torch.zeros(2, 0, 128, device="cuda", dtype=torch.bfloat16)
+    out = torch.full((2, 20), 7.0, device="cuda")
+    qs = _lib.seqs(Q, n=2, length=0, stride_n=128, stride_l=128)
+    docs = idx._docs()
+    lib = _lib.load()
+    rc = lib.lik_plaid_maxsim_qc(ctypes.byref(qs), ctypes.byref(docs), idx.token_inv.data_ptr(), _lib.LIK_NORMALIZE,
+                                 out.data_ptr(), out.stride(0), out.stride(1), None, 0, None, _lib.stream_of(out))
+    assert rc == _lib.LIK_OK
+    assert out.abs().max().item() == 0.0

@@ -141,6 +141,13 @@ def _cpu_threads() -> int:
     return os.cpu_count() or 1
 
 
+def _cpu_entry(value: float, unit: str, sample: str) -> dict:
+    """A ``cpu_baseline`` record: the oracle (numpy, the host's BLAS threads) on a
+    bounded sample of the workload, scaled to the metric's unit."""
+    return {"value": value, "unit": unit, "cores": _cpu_threads(), "kind": "port", "cpu_model": _cpu_model(),
+            "host_cpus": os.cpu_count(), "sample": sample}
+
+
 # --------------------------------------------------------------------------- #
 # workloads                                                                   #
 # --------------------------------------------------------------------------- #
@@ -250,13 +257,30 @@ def wl_varlen(args):
     ms = _time_steps(step, args.steps, args.warmup)
     flops = 2.0 * d * Nq * Lq * tot
     tf = flops / (ms * 1e-3) / 1e12
-    return {
+    res = {
         "metric": "MaxSim varlen TFLOP/s", "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
         "dtype": "bf16",
         "config": {"workload": "varlen 65,536 docs log-U[16,2048], 256x32 queries (BASELINE configs[2])",
                    "doc_tokens": tot, "flops_per_step": flops},
         "roofline": _roofline("mfma", flops, "bf16", "varlen"),
     }
+    if args.cpu_baseline:
+        import numpy as np
+
+        import lik_oracle as O
+
+        nq, nd = 32, 4096  # 32 queries x the first 4,096 packed docs (a few seconds)
+        cu_h = cu_d[: nd + 1].cpu().numpy()
+        Ds = Dp[: int(cu_h[-1])].float().cpu().numpy()
+        Qs = Qp[: nq * Lq].float().cpu().numpy()
+        t0 = time.perf_counter()
+        O.maxsim_varlen(Qs, Ds, np.arange(nq + 1) * Lq, cu_h, dtype=np.float32)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = _cpu_entry(round(2.0 * d * nq * Lq * float(cu_h[-1]) / dt / 1e12, 5), "TFLOP/s",
+                                         f"{nq} of {Nq} queries x the first {nd} of {Nd} docs "
+                                         f"({int(cu_h[-1])} tokens; oracle/lik_oracle.maxsim_varlen, numpy fp32), "
+                                         f"{dt:.1f} s")
+    return res
 
 
 def wl_fp8(args):
@@ -281,13 +305,28 @@ def wl_fp8(args):
     ms = _time_steps(step, args.steps, args.warmup)
     flops = 2.0 * d * Nq * Lq * Nd * Ld
     tf = flops / (ms * 1e-3) / 1e12
-    return {
+    res = {
         "metric": "MaxSim fp8 TFLOP/s", "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
         "dtype": "fp8-e4m3",
         "config": {"workload": "ColPali fp8 Q[256,24,128] x D[8192,1030,128] (BASELINE configs[3])",
                    "flops_per_step": flops},
         "roofline": _roofline("mfma", flops, "fp8", "fp8"),
     }
+    if args.cpu_baseline:
+        import numpy as np
+
+        import lik_oracle as O
+
+        nq, nd = 64, 2048  # 64 queries x 2,048 docs, dequantised to fp32 (no fp8 arithmetic on the host)
+        Qs = (Qf[:nq].float() * sq).cpu().numpy()
+        Ds = (D8[:nd].float() * sd).cpu().numpy()
+        t0 = time.perf_counter()
+        O.maxsim(Qs, Ds, dtype=np.float32, q_chunk=1)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = _cpu_entry(round(2.0 * d * nq * Lq * nd * Ld / dt / 1e12, 5), "TFLOP/s",
+                                         f"{nq} of {Nq} queries x {nd} of {Nd} docs, dequantised fp32 "
+                                         f"(oracle/lik_oracle.maxsim, numpy), {dt:.1f} s")
+    return res
 
 
 def wl_plaid(args):
@@ -306,7 +345,7 @@ def wl_plaid(args):
     qps = Nq / (ms * 1e-3)
     flops = 2.0 * d * Nq * Lq * tot
     tf = flops / (ms * 1e-3) / 1e12
-    return {
+    out = {
         "metric": "PLAID retrieve queries/s at top-100", "value": round(qps, 1), "unit": "queries/s",
         "ms_per_step": round(ms, 3), "dtype": "bf16",
         "config": {"workload": f"PLAID {Nd} docs U[30,300], {Nq}x32 queries, nbits=2, top-100, chunk 4096 "
@@ -314,6 +353,28 @@ def wl_plaid(args):
                    "compressed_bytes": tot * (4 + d * nbits // 8)},
         "roofline": _roofline("mfma", flops, "bf16", "plaid"),
     }
+    if args.cpu_baseline:
+        import numpy as np
+
+        import lik_oracle as O
+
+        # 8 queries against the first 8,192 docs: decode + normalise + MaxSim in
+        # fp32, then the chunked top-100 merge; scaled by the corpus's tokens
+        nq, nd = 8, 8192
+        cu_h = cu[: nd + 1].cpu().numpy()
+        ns = int(cu_h[-1])
+        Qs = Q[:nq].float().cpu().numpy()
+        t0 = time.perf_counter()
+        sc = O.maxsim_residual_varlen(Qs, codes[:ns].cpu().numpy(), res[:ns].cpu().numpy(), cu_h,
+                                      cent.float().cpu().numpy(), bw.cpu().numpy(), nbits, dtype=np.float32)
+        O.retrieve_chunked(sc, 100, 4096)
+        dt = time.perf_counter() - t0
+        qps_cpu = nq / (dt * tot / ns)
+        out["cpu_baseline"] = _cpu_entry(round(qps_cpu, 5), "queries/s",
+                                         f"{nq} of {Nq} queries x the first {nd} of {Nd} docs ({ns} tokens; "
+                                         "oracle decode + normalise + maxsim_varlen + chunked top-100, numpy fp32), "
+                                         f"{dt:.1f} s, scaled by {tot} / {ns} tokens")
+    return out
 
 
 def _plaid_index(Nd, seed, ncent=65536, d=128, nbits=2):
@@ -398,6 +459,44 @@ def wl_plaid_q1_prepared(args):
                        "scan_bytes_with_norms": sbytes, "prepare_s": round(prep_s, 3),
                        "queries_per_s": round(1000.0 / ms, 1)},
             "roofline": roof}
+
+
+def wl_plaid_approx(args):
+    """plaid_approx_score (the centroid-only PLAID stage, plaid.py:28-136) on
+    the C5 corpus: its documented input, the query-centroid scores
+    centroids @ Q^T ([65,536, 32] fp32, computed once outside the timed
+    region), over the 1M docs as a padded [1M, 300] int32 code matrix. One
+    step = one launch over all docs; ``value`` = docs scored per second. The
+    roofline counts the streamed bytes (the valid tokens' codes, lengths,
+    scores); the 128 B of query-centroid scores each token gathers come from
+    L2 / MALL (the table is 8 MB)."""
+    import torch
+
+    from late_interaction_kernels.plaid import plaid_approx_score
+
+    Nd, d = args.plaid_docs, 128
+    g, cu, tot, cent, codes, res, bw = _plaid_index(Nd, 4)
+    del res
+    Q = _normed((1, 32, d), g, torch.bfloat16)
+    qcs = cent.float() @ Q[0].float().t()
+    lens = (cu[1:] - cu[:-1]).long()
+    L = 300
+    padded = torch.zeros((Nd, L), device="cuda", dtype=torch.int32)
+    padded[torch.arange(L, device="cuda")[None, :] < lens[:, None]] = codes
+
+    def step():
+        return plaid_approx_score(qcs, padded, lens)
+
+    ms = _time_steps(step, args.steps, args.warmup)
+    nbytes = float(tot) * 4 + Nd * (8 + 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"metric": "PLAID approximate score docs/s (centroid-only stage)", "value": round(Nd / (ms * 1e-3), 1),
+            "unit": "docs/s", "ms_per_step": round(ms, 4), "dtype": "fp32",
+            "config": {"workload": f"plaid_approx_score {Nd} docs U[30,300] padded to 300, 65,536 centroids x "
+                                   "32 query tokens", "doc_tokens": tot, "streamed_bytes": nbytes},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm"], "unit": "GB/s",
+                         "frac": round(gbs / PEAK["hbm"], 4), "traffic": None, "kernel_ms": round(ms, 4),
+                         "kernel_launches_per_step": 1}}
 
 
 def wl_plaid_decode(args):
@@ -750,6 +849,7 @@ WORKLOADS = {
     "fused_head": wl_fused_head,
     "head": wl_head,
     "plaid_decode": wl_plaid_decode,
+    "plaid_approx": wl_plaid_approx,
     "inbatch": wl_inbatch,
     "inbatch_norm": lambda a: wl_inbatch(a, normalize=True),
     "kd": wl_kd,
@@ -805,6 +905,8 @@ def main() -> None:
             parts[name] = {"metric": r["metric"], "value": r["value"], "unit": r["unit"], "dtype": r["dtype"],
                            "steps": sub.steps, "warmup": sub.warmup, "ms_per_step": r["ms_per_step"],
                            "config": r["config"], "roofline": r["roofline"]}
+            if "cpu_baseline" in r:
+                parts[name]["cpu_baseline"] = r["cpu_baseline"]
             print(f"[bench] {name}: {r['value']} {r['unit']}", file=sys.stderr, flush=True)
     out = {
         "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,

@@ -304,6 +304,71 @@ __global__ void __launch_bounds__(256)
   if (lane == 0) out[b] = total;
 }
 
+// The same score for query-centroid rows of at most 32 fp32 values with unit
+// stride and 16-byte aligned rows (the documented qcs = centroids @ Q^T):
+// one wavefront per doc; lane (g = lane / 8, q = lane % 8) keeps the running
+// maxima of slots 4q .. 4q+3 over the doc's tokens t = 8i + g, so one
+// dwordx4 gather instruction reads 8 tokens' whole rows (8 lanes per 128-byte
+// row). Per 64 tokens: one coalesced load of their codes (lane l: token l),
+// 8 ds_bpermute to hand token 8i + g's code to its group, 8 row gathers.
+// At the doc's end the 8 groups' maxima meet (xor 8 by DPP row_ror:8, xor 16
+// and 32 by permlane swaps), a non-finite max scores 0, and the slots are
+// summed (in lane, then over the 8 lanes of a group).
+__global__ void __launch_bounds__(256)
+    plaid_approx_rows_kernel(const float* __restrict__ qcs, int64_t ncent, int lq, int64_t sc,
+                             const int32_t* __restrict__ codes, int64_t B, int64_t L, int64_t cs,
+                             const int64_t* __restrict__ lens, float* __restrict__ out) {
+  // wave-uniform doc index and length (so the buffer descriptors are scalar)
+  const int64_t b = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63, g = lane >> 3, q = lane & 7;
+  if (b >= B) return;
+  int64_t len = lens[b];
+  len = len < 0 ? 0 : (len > L ? L : len);
+  len = __builtin_amdgcn_readfirstlane((int)len);
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  // raw buffers (untyped, byte range checked): reads past them return 0
+  const __amdgpu_buffer_rsrc_t rq =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(qcs), (short)0, (int)(ncent * sc * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(codes + b * cs), (short)0, (int)(len * 4), 0x00020000);
+  float m[4] = {NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+  for (int64_t t0 = 0; t0 < len; t0 += 64) {
+    int32_t c = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, (uint32_t)((t0 + lane) * 4), 0, 0);
+    c = (c >= 0 && c < ncent) ? c : 0;  // out-of-range codes read row 0 (plaid.py:66-67)
+    f32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int ci = __builtin_amdgcn_ds_bpermute((8 * i + g) * 4, c);
+      v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rq, (uint32_t)(ci * sc * 4) + (uint32_t)(q * 16), 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool ok = t0 + 8 * i + g < len;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) m[k] = max_nan(m[k], ok ? v[i][k] : NEG_INF);
+    }
+  }
+  auto dpp_ror8 = [](float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+  };
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float x = max_nan(m[k], dpp_ror8(m[k]));  // groups g, g ^ 1 (lanes l, l ^ 8)
+    auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = max_nan(__uint_as_float(s16[0]), __uint_as_float(s16[1]));  // g ^ 2
+    auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = max_nan(__uint_as_float(s32[0]), __uint_as_float(s32[1]));  // g ^ 4
+    // empty doc (-inf), NaN or +inf: the slot scores 0 (reference.py:119-120)
+    tot += (4 * q + k < lq && __builtin_isfinite(x)) ? x : 0.f;
+  }
+  // sum over the 8 slot quads (lanes q = 0..7 of group 0, fixed order)
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) tot += __shfl_xor(tot, o);
+  if (lane == 0) out[b] = tot;
+}
+
 }  // namespace lik
 
 using namespace lik;
@@ -402,9 +467,18 @@ int lik_plaid_approx_score(const float* qcs, int64_t n_centroids, int64_t lq, in
   if (B < 0 || lq < 0 || n_centroids < 1 || max_len < 0) return LIK_ERR_INVALID;
   if (B == 0) return LIK_OK;
   if (!qcs || !codes || !doc_lengths || !out) return LIK_ERR_INVALID;
-  hipLaunchKernelGGL(plaid_approx_kernel, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, (hipStream_t)stream, qcs,
-                     n_centroids, lq, qcs_stride_c, qcs_stride_l, codes, B, max_len, codes_stride_b, doc_lengths,
-                     out);
+  if ((B + 3) / 4 > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  // rows of <= 32 unit-stride, 16-byte aligned scores: whole rows per gather
+  const bool rows = lq > 0 && lq <= 32 && qcs_stride_l == 1 && qcs_stride_c % 4 == 0 &&
+                    ((uintptr_t)qcs) % 16 == 0 && n_centroids * qcs_stride_c * 4 < (int64_t)0xffffffffLL &&
+                    max_len * 4 < (int64_t)0xffffffffLL;
+  if (rows)
+    hipLaunchKernelGGL(plaid_approx_rows_kernel, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                       qcs, n_centroids, (int)lq, qcs_stride_c, codes, B, max_len, codes_stride_b, doc_lengths, out);
+  else
+    hipLaunchKernelGGL(plaid_approx_kernel, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, (hipStream_t)stream, qcs,
+                       n_centroids, lq, qcs_stride_c, qcs_stride_l, codes, B, max_len, codes_stride_b, doc_lengths,
+                       out);
   return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
 }
 

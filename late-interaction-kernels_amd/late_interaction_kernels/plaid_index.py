@@ -14,8 +14,18 @@ benchmarks/plaid/bench_fastplaid_e2e.py:75-140, reads the same ones):
 ``sum(doclens)`` tokens and copied to the GPU. fast-plaid stores each code's
 bits least-significant first and packs the stream most-significant-bit first
 (``numpy.packbits``), which is the bit-reverse of every byte of the
-little-endian layout the kernels read (``reference.py:124-139``); the
-residuals are converted once on the device with ``lik_residual_reverse_bits``.
+little-endian layout the kernels read (``reference.py:124-139``).
+
+``bit_order`` chooses what the kernels see:
+
+* ``"colbert"`` (default): the residuals are converted once on the device
+  with ``lik_residual_reverse_bits``, so every token decodes to the ColBERTv2
+  embedding the index was built from and the scores equal ``reference.py``'s
+  on those embeddings.
+* ``"raw"``: the bytes are used as stored. This is what the reference's own
+  end-to-end harness does (``bench_fastplaid_e2e.py:75-140`` feeds fast-plaid's
+  bytes to its kernel unconverted; ``bench_decompress_maxsim.py:144-149`` notes
+  the reversed layout), so scores equal that harness's, bit for bit in decode.
 """
 
 from __future__ import annotations
@@ -54,16 +64,19 @@ def load_fastplaid_index(
     device: str | torch.device = "cuda",
     centroid_dtype: torch.dtype = torch.float16,
     d: int | None = None,
+    bit_order: str = "colbert",
 ) -> dict:
     """Read a fast-plaid index directory into the tensors
     :func:`~late_interaction_kernels.plaid.maxsim_residual_varlen` and
     :func:`~late_interaction_kernels.plaid.retrieve_residual_varlen` take.
 
     Returns a dict with the reference loader's keys: ``nbits``, ``centroids``,
-    ``bucket_weights``, ``codes_flat`` (int32 here), ``residuals_flat`` (uint8,
-    converted to the kernels' bit order), ``doc_lengths``, ``cu_seqlens_d``,
-    ``n_docs``, ``total_tokens``, ``d``.
+    ``bucket_weights``, ``codes_flat`` (int32 here), ``residuals_flat`` (uint8;
+    converted to the kernels' bit order unless ``bit_order="raw"``),
+    ``doc_lengths``, ``cu_seqlens_d``, ``n_docs``, ``total_tokens``, ``d``.
     """
+    if bit_order not in ("colbert", "raw"):
+        raise ValueError(f"bit_order must be 'colbert' or 'raw'; got {bit_order!r}")
     with open(os.path.join(index_path, "metadata.json")) as f:
         metadata = json.load(f)
     nbits = int(metadata["nbits"])
@@ -103,7 +116,7 @@ def load_fastplaid_index(
                          f"for {total} document tokens")
     codes_flat = torch.from_numpy(np.ascontiguousarray(codes_all[:total]).astype(np.int32, copy=False)).to(device)
     res_raw = torch.from_numpy(np.array(res_all[:total], dtype=np.uint8, copy=True)).to(device)
-    residuals_flat = reverse_residual_bits(res_raw).view(total, packed_dim)
+    residuals_flat = (reverse_residual_bits(res_raw) if bit_order == "colbert" else res_raw).view(total, packed_dim)
 
     doc_lengths = torch.tensor(doc_lens, device=device, dtype=torch.int64)
     cu = torch.zeros(len(doc_lens) + 1, dtype=torch.int32, device=device)

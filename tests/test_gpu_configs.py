@@ -283,3 +283,28 @@ def test_c5_plaid_1024_queries_top100():
     dj = torch.unique(torch.cat([_sample(1_000_000, 10, 40, 4), i[qi[0], :2].cpu()]))
     ref = _oracle_docs(Q[qi], cu, codes, res, cent, bw, dj)
     assert rel_err(_np(full[qi][:, dj.cuda()]), ref) < 1e-2
+
+
+def test_c5_plaid_approx_score():
+    """plaid_approx_score at C5 scale: its documented input, the query-centroid
+    scores centroids @ Q^T (plaid.py:82-97), computed on the GPU for the
+    65,536 centroids, over the 1M docs as a padded [1M, 300] code matrix.
+    Sampled docs (the shortest and longest included) against the oracle
+    (brute-force pinned), all scores finite, padding past each length ignored."""
+    from late_interaction_kernels.plaid import plaid_approx_score
+
+    _case("C5 plaid_approx_score 1M docs x 65,536 centroids")
+    g, cu, cent, codes, res, bw = _c5_index()
+    Q = _normed((1, 32, 128), g, torch.bfloat16)
+    qcs = cent.float() @ Q[0].float().t()  # [65536, 32]
+    lens = (cu[1:] - cu[:-1]).long()
+    Nd, L = lens.numel(), 300
+    pos = torch.arange(L, device="cuda")[None, :] < lens[:, None]
+    padded = torch.full((Nd, L), 7, device="cuda", dtype=torch.int32)  # junk past each length
+    padded[pos] = codes
+    del res
+    out = plaid_approx_score(qcs, padded, lens)
+    assert out.shape == (Nd,) and bool(torch.isfinite(out).all())
+    dj = torch.unique(torch.cat([_sample(Nd, 11, 200, 8), torch.argmin(lens).cpu()[None], torch.argmax(lens).cpu()[None]]))
+    ref = O.plaid_approx_score(qcs.cpu().numpy(), padded[dj.cuda()].cpu().numpy(), lens[dj.cuda()].cpu().numpy())
+    assert rel_err(_np(out[dj.cuda()]), ref) < 1e-5

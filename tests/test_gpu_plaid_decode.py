@@ -124,8 +124,10 @@ def test_retrieve_decode_route(monkeypatch, budget, chunk):
     np.testing.assert_array_equal(s.cpu().numpy(), ws)
 
 
-def _write_fastplaid_index(path, nbits, merged, seed=3):
-    """A small index directory in fast-plaid's on-disk format (ColBERTv2 bit packing)."""
+def _write_fastplaid_index(path, nbits, merged, seed=3, exact=False):
+    """A small index directory in fast-plaid's on-disk format (ColBERTv2 bit
+    packing). exact: centroids and bucket weights on a 1/16 grid, so every
+    decoded value c + w is exact in bf16."""
     import json
     import os
 
@@ -134,6 +136,9 @@ def _write_fastplaid_index(path, nbits, merged, seed=3):
     doclens = [rng.integers(1, 30, 25).tolist(), rng.integers(1, 30, 17).tolist()]
     cent = rng.standard_normal((n_cent, d)).astype(np.float32)
     bw = np.linspace(-0.2, 0.2, 2**nbits).astype(np.float32)
+    if exact:
+        cent = (rng.integers(-16, 16, (n_cent, d)) / 16).astype(np.float32)
+        bw = ((np.arange(2**nbits) - 2 ** (nbits - 1)) / 16).astype(np.float32)
     codes = [rng.integers(0, n_cent, sum(dl)).astype(np.int64) for dl in doclens]
     bcodes = [rng.integers(0, 2**nbits, (sum(dl), d)) for dl in doclens]
     os.makedirs(path, exist_ok=True)
@@ -176,3 +181,37 @@ def test_fastplaid_index_loader(tmp_path, nbits, merged):
     ref = O.maxsim_residual_varlen(Q.float().cpu().numpy(), codes, O.pack_residuals(bcodes, nbits),
                                    idx["cu_seqlens_d"].cpu().numpy(), cent, bw, nbits)
     assert rel_err(got.cpu().numpy(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("nbits", [2, 4])
+def test_fastplaid_index_loader_raw_bits(tmp_path, nbits):
+    """bit_order="raw" keeps fast-plaid's bytes as stored, as the reference's
+    end-to-end harness does (bench_fastplaid_e2e.py:75-140): decode is bit-exact
+    against the oracle's little-endian unpack of the unconverted bytes, and the
+    scores equal the oracle on those bytes (the harness's result)."""
+    from late_interaction_kernels.plaid import decode_residual_tokens, maxsim_residual_varlen
+    from late_interaction_kernels.plaid_index import load_fastplaid_index
+
+    _case(f"fast-plaid loader raw nbits={nbits}")
+    doclens, cent, bw, codes, bcodes = _write_fastplaid_index(str(tmp_path), nbits, True, exact=True)
+    raw = load_fastplaid_index(str(tmp_path), centroid_dtype=torch.float32, bit_order="raw")
+    stored = O.pack_residuals_colbert(bcodes, nbits)  # the bytes on disk
+    np.testing.assert_array_equal(raw["residuals_flat"].cpu().numpy(), stored)
+    dec = decode_residual_tokens(raw["codes_flat"], raw["residuals_flat"], raw["centroids"], raw["bucket_weights"],
+                                 nbits, normalize=False)
+    want = O.decode_residual_tokens(codes, stored, cent, bw, nbits)
+    np.testing.assert_array_equal(dec.float().cpu().numpy(), want.astype(np.float32))
+    # and the converted ("colbert") load decodes the ColBERTv2 fields
+    conv = load_fastplaid_index(str(tmp_path), centroid_dtype=torch.float32)
+    dec_c = decode_residual_tokens(conv["codes_flat"], conv["residuals_flat"], conv["centroids"],
+                                   conv["bucket_weights"], nbits, normalize=False)
+    want_c = O.decode_residual_tokens(codes, O.pack_residuals(bcodes, nbits), cent, bw, nbits)
+    np.testing.assert_array_equal(dec_c.float().cpu().numpy(), want_c.astype(np.float32))
+    Q = torch.randn(3, 32, 128).to(torch.bfloat16).cuda()
+    got = maxsim_residual_varlen(Q, raw["codes_flat"], raw["residuals_flat"], raw["cu_seqlens_d"], raw["centroids"],
+                                 raw["bucket_weights"], nbits)
+    ref = O.maxsim_residual_varlen(Q.float().cpu().numpy(), codes, stored, raw["cu_seqlens_d"].cpu().numpy(), cent, bw,
+                                   nbits)
+    assert rel_err(got.cpu().numpy(), ref) < 1e-2
+    with pytest.raises(ValueError):
+        load_fastplaid_index(str(tmp_path), bit_order="msb")

@@ -503,7 +503,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
 // against 2.70 ms. What bounds it (counters): the texture address and data
 // units (TA busy 0.92, TD 0.95), i.e. the five vector memory instructions per
 // tile, two of them 64 random 32-byte table reads; with every table read
-// pointed at one row (timing only) the scan takes 2.02 ms.
+// pointed at one row (timing only) the scan takes 2.02 ms, with the texture
+// data unit still busy 0.94 of the cycles. Tried: the streamed bytes through
+// an 8-tile LDS ring (buffer_load ... lds, 2.6x the bytes in flight, 128
+// VGPRs): 2.60 ms, and the same at four waves per SIMD with 6 tiles: 2.75 ms;
+// so latency is not the bound. Codes and inverse norms loaded by 32 lanes
+// instead of 64 (kept): -0.4%.
 // Steps I .. N-1 of one unrolled round (static register indices), stopping
 // at the last tile; false once it stopped.
 template <int I, int N, class F>
@@ -646,9 +651,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   }
 #pragma unroll
   for (int k = 0; k < LC; ++k) code[k] = 0u;
+  // codes and inverse norms: loaded by lanes 0..31 only (EXEC's high half
+  // cleared inside the asm; the loop runs with all lanes active) and copied
+  // to lanes 32..63 by v_permlane32_swap once they have arrived
   auto load_code = [&](int t, uint32_t& c) {
     const u32x4 dc = desc(code_p + 32 * (int64_t)t, (uint32_t)rows_of(t) * 4u);
-    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, 0 offen nt" : "+v"(c) : "v"((uint32_t)l32 * 4u), "s"(dc));
+    uint32_t ex;
+    asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
+                 "buffer_load_dword %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
+                 : "+v"(c), "=&s"(ex) : "v"((uint32_t)l32 * 4u), "s"(dc));
+  };
+  auto bcast = [](uint32_t x) -> uint32_t {
+    return __builtin_amdgcn_permlane32_swap(x, x, false, false)[0];
   };
   auto load_tile = [&](int t, uint32_t cd, Stage& s) {
     const int nv = rows_of(t);
@@ -666,7 +680,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     }
     if constexpr (NORMD) {
       const u32x4 di = desc(inv_p + 32 * (int64_t)t, (uint32_t)nv * 4u);
-      asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, 0 offen nt" : "+v"(s.inv) : "v"((uint32_t)l32 * 4u), "s"(di));
+      uint32_t ex;
+      asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
+                   "buffer_load_dword %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
+                   : "+v"(s.inv), "=&s"(ex) : "v"((uint32_t)l32 * 4u), "s"(di));
     }
     const uint32_t row = cd < (uint32_t)p.pl.ncent ? cd : 0u;
     const uint32_t toff = row * 64u + (uint32_t)h * 32u;
@@ -809,20 +826,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
 #pragma unroll
   for (int t = 0; t < LS; ++t) {
     asm volatile("s_waitcnt vmcnt(0)" : "+v"(code[t]));
-    load_tile(t, code[t], st[t]);
+    load_tile(t, bcast(code[t]), st[t]);
     load_code(t + LS, code[t + LS]);
   }
   constexpr int kWaitTile = 1 + (LS - 1) * (NLT + 1);
   auto step = [&](auto II, int c) {
     constexpr int I = decltype(II)::value;  // c % LC
     wait_stage(integral_constant<int, kWaitTile>{}, st[I % LS]);
-    compute(c, st[I % LS]);
+    {
+      Stage cur = st[I % LS];
+      cur.inv = __uint_as_float(bcast(__float_as_uint(cur.inv)));
+      compute(c, cur);
+    }
     // ordering point: the stage's previous contents are all read (they feed m)
 #pragma unroll
     for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(m[e]));
     // the code of tile c + LS, loaded right after tile c's loads
     wait_code(integral_constant<int, kWaitTile - 1>{}, code[(I + LS) % LC]);
-    load_tile(c + LS, code[(I + LS) % LC], st[I % LS]);
+    load_tile(c + LS, bcast(code[(I + LS) % LC]), st[I % LS]);
     load_code(c + LC, code[I]);
   };
   for (int c = 0; c < ntile; c += LC)

@@ -114,6 +114,21 @@ __global__ void __launch_bounds__(W * 64)
   __shared__ int32_t s_dlen[kRMax];  // length | holes << 31
   __shared__ __attribute__((aligned(16))) i32x4 s_nz[kRMax + 1];  // {k, length | holes << 31, start lo, hi}; [nnz] = sentinel
   __shared__ int s_nnz, s_ntiles;
+  // Flat tiles (DMA kernel, every non-empty doc of the range at least 32
+  // tokens long): the tiles are 32-row windows of the range's docs laid end to
+  // end, so a doc's last tile is not padded to 32 rows; a doc may end inside a
+  // tile and the next one start there (one doc end per tile at most).
+  // s_sst[m]: position of non-empty doc m's token 0 in that sequence ([nnz]:
+  // the total, [nnz + 1]: INT_MAX); s_rb[m]: byte offset of its token 0 from
+  // non-empty doc 0's, minus s_sst[m] row strides (mod 2^32), so the row at
+  // position P of doc m is at s_rb[m] + P * row stride.
+#ifndef LIK_FLAT_TILES
+#define LIK_FLAT_TILES 1
+#endif
+  constexpr bool kFlatOK = LIK_FLAT_TILES && kDMA && SRC == SRC_DENSE;
+  __shared__ int32_t s_sst[kFlatOK ? kRMax + 2 : 1];
+  __shared__ uint32_t s_rb[kFlatOK ? kRMax + 1 : 1];
+  __shared__ int s_flat;
 
   const bool f_mask = (FEAT & F_MASK) && p.d.mask != nullptr;
   const bool f_ts = (FEAT & F_TS) && p.d.ts != nullptr;
@@ -211,7 +226,7 @@ __global__ void __launch_bounds__(W * 64)
   }
   __syncthreads();
   if (wv == 0) {
-    int base = 0, ntl = 0;
+    int base = 0, ntl = 0, run = 0;
     for (int k0 = 0; k0 < nloc; k0 += 64) {
       const int k = k0 + lane;
       const int v = k < nloc ? s_dlen[k] : 0;
@@ -225,17 +240,54 @@ __global__ void __launch_bounds__(W * 64)
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) nt += __shfl_xor(nt, o);
       ntl += nt;
+      if constexpr (kFlatOK) {
+        // positions of the non-empty docs in the flat sequence (exclusive scan)
+        int sc = L;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int t = __shfl_up(sc, o);
+          if (lane >= o) sc += t;
+        }
+        if (nz) s_sst[pos] = run + sc - L;
+        run += __shfl(sc, 63);
+      }
     }
     if (lane == 0) {
       s_nnz = base;
       s_ntiles = ntl;
       s_nz[base] = (i32x4){0, 0, 0, 0};  // sentinel: an empty doc past the last one
+      if constexpr (kFlatOK) {
+        s_sst[base] = run;
+        s_sst[base + 1] = 0x7fffffff;
+        s_rb[base] = 0u;
+      }
     }
   }
   __syncthreads();
   const int nnz = __builtin_amdgcn_readfirstlane(s_nnz);
-  const int ntiles = __builtin_amdgcn_readfirstlane(s_ntiles);
   if (nnz == 0) return;
+  if constexpr (kFlatOK) {
+    // flat tiles need every doc >= 32 tokens (one doc end per tile) and every
+    // row within 4 GiB after non-empty doc 0's first row (32-bit DMA offsets)
+    if (wv == 0) {
+      const int64_t off0 = (int64_t)(uint32_t)s_nz[0][2] | ((int64_t)s_nz[0][3] << 32);
+      const int64_t sl = p.d.sl_b;
+      bool ok = true;
+      for (int m = lane; m < nnz; m += 64) {
+        const i32x4 e = s_nz[m];
+        const int64_t L = e[1] & 0x7fffffff;
+        const int64_t rel = ((int64_t)(uint32_t)e[2] | ((int64_t)e[3] << 32)) - off0;
+        ok = ok && L >= 32 && rel >= 0 && rel + (L - 1) * sl + 256 <= 0xffff0000LL;
+        s_rb[m] = (uint32_t)rel - (uint32_t)s_sst[m] * (uint32_t)sl;
+      }
+      const bool all = __ballot(!ok) == 0ull;
+      if (lane == 0) s_flat = (all && sl > 0) ? 1 : 0;
+    }
+    __syncthreads();
+  }
+  const bool flat = kFlatOK && __builtin_amdgcn_readfirstlane(s_flat) != 0;
+  const int ntiles = flat ? (__builtin_amdgcn_readfirstlane(s_sst[nnz]) + 31) >> 5
+                          : __builtin_amdgcn_readfirstlane(s_ntiles);
 
   // ---------------- query block -> B fragments in VGPRs ----------------
   u32x4 bq[NSUB][KS][FV];
@@ -391,6 +443,10 @@ __global__ void __launch_bounds__(W * 64)
   uint32_t dmaoff[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) dmaoff[i] = lrow[i] < 32 ? loff[i] : kOOB;
+  // flat tiles: offset of this lane's chunk within its row (kOOB: padding chunk)
+  uint32_t dmacc[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) dmacc[i] = lrow[i] < 32 ? (uint32_t)lcc[i] * 16u : kOOB;
 
   // PLAID phase A: centroid codes of tile d
   auto fetch_codes = [&](auto SS, const Desc& d) {
@@ -413,6 +469,21 @@ __global__ void __launch_bounds__(W * 64)
   // The buffer descriptor starts at the tile's first row and ends with its
   // last valid row, so rows past the doc end fall out of range (and read 0)
   // with no per-lane test: the lane offsets are loop constants (dmaoff).
+  auto dma_issue = [&](int buf, int i, uint32_t voff, const u32x4& desc) {
+    const int wu = __builtin_amdgcn_readfirstlane(wv);
+    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(s_tile[buf][0] + (wu * NCH + i) * 1024));
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"  // an M0 write needs one wait state before an LDS DMA reads it
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(desc)
+        : "memory");
+  };
   auto fetch_dma = [&](const Cur& c, const Desc& d, int buf) {
     if constexpr (kDMA) {
       const uint32_t sl = (uint32_t)p.d.sl_b;
@@ -422,22 +493,30 @@ __global__ void __launch_bounds__(W * 64)
       const u32x4 desc = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
                           (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu),
                           (uint32_t)__builtin_amdgcn_readfirstlane(span), 0x00020000u};
-      const int wu = __builtin_amdgcn_readfirstlane(wv);
 #pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane(
-            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(s_tile[buf][0] + (wu * NCH + i) * 1024));
-        const uint32_t voff = dmaoff[i];
-        uint32_t saved;
-        asm volatile(
-            "s_mov_b32 %0, m0\n\t"
-            "s_mov_b32 m0, %1\n\t"
-            "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
-            "s_mov_b32 m0, %0"
-            : "=&s"(saved)
-            : "s"(lds), "v"(voff), "s"(desc)
-            : "memory");
+      for (int i = 0; i < NCH; ++i) dma_issue(buf, i, dmaoff[i], desc);
+    }
+  };
+  // DMA offsets of the flat tile at position P. Lane row l32 of the tile is
+  // position P + l32; (lm, lE, lb) track the non-empty doc that position is
+  // in (its index, end position and s_rb entry): positions advance by 32 per
+  // tile and docs are >= 32 tokens, so a lane crosses at most one doc end per
+  // tile. Positions past the last doc read 0 (offset kOOB). The offsets are
+  // computed one step ahead of their DMA, which then needs no LDS read or
+  // wait and can issue among the tile's MFMAs; the DMA uses the raw
+  // descriptor dflat at non-empty doc 0's first row (range 0xfffffff0).
+  auto flat_offsets = [&](int P, int& lm, int& lE, uint32_t& lb, int total, uint32_t (&vo)[NCH]) {
+    if constexpr (kFlatOK) {
+      const int pr = P + l32;
+      if (pr >= lE) {
+        lm += 1;
+        lE = s_sst[lm + 1];
+        lb = s_rb[lm];
       }
+      const bool live = pr < total;
+      const uint32_t roff = lb + (uint32_t)pr * (uint32_t)p.d.sl_b;
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) vo[i] = (live && dmacc[i] != kOOB) ? roff + dmacc[i] : kOOB;
     }
   };
   auto fetch_dense = [&](auto SS, const Cur& c, const Desc& d) {
@@ -846,6 +925,73 @@ __global__ void __launch_bounds__(W * 64)
     ++nend;
   };
 
+  // Flat tiles (one accumulator set): rows [0, b) of tile d end non-empty doc
+  // d.k when b = d.nv <= 32, and rows [b, 32) are the first rows of the next
+  // one (none past the last doc): their max goes to mn, the next doc's
+  // running max once doc d.k is parked. Accumulator element 4 j + r of lane
+  // half h is row 8 j + 4 h + r, so for b < 32 only the element group
+  // js = b / 8 straddles the boundary (element r below it when
+  // r < b - 8 js - 4 h); the groups before it go whole to m, those after it
+  // whole to mn, and js is uniform: one unrolled body per value.
+  auto epilogue_flat = [&](const Desc& d, float (&mn)[NSUB]) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) mn[sub] = NEG_INF;
+    if (!d.docend || d.nv >= 32) {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m[sub] = max_nan(m[sub], acc[0][sub][e]);
+      return;
+    }
+    const int b = d.nv;
+    const int js = b >> 3;
+    const int ch = b - 8 * js - 4 * h;
+    bool lo[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lo[r] = r < ch;
+    auto split = [&](auto JS) {
+      constexpr int J = decltype(JS)::value;
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) {
+        float a = m[sub], c = NEG_INF;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x[4] = {acc[0][sub][4 * j], acc[0][sub][4 * j + 1], acc[0][sub][4 * j + 2], acc[0][sub][4 * j + 3]};
+          if (j < J) {
+            a = max_nan(a, max_nan(x[0], x[1]));
+            a = max_nan(a, max_nan(x[2], x[3]));
+          } else if (j > J) {
+            c = max_nan(c, max_nan(x[0], x[1]));
+            c = max_nan(c, max_nan(x[2], x[3]));
+          } else {
+            float lv[4], hv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              lv[r] = lo[r] ? x[r] : NEG_INF;
+              hv[r] = lo[r] ? NEG_INF : x[r];
+            }
+            a = max_nan(a, max_nan(lv[0], lv[1]));
+            a = max_nan(a, max_nan(lv[2], lv[3]));
+            c = max_nan(c, max_nan(hv[0], hv[1]));
+            c = max_nan(c, max_nan(hv[2], hv[3]));
+          }
+        }
+        m[sub] = a;
+        mn[sub] = c;
+      }
+    };
+    switch (js) {
+      case 0: split(std::integral_constant<int, 0>{}); break;
+      case 1: split(std::integral_constant<int, 1>{}); break;
+      case 2: split(std::integral_constant<int, 2>{}); break;
+      default: split(std::integral_constant<int, 3>{}); break;
+    }
+    if (d.k + 1 >= nnz) {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) mn[sub] = NEG_INF;
+    }
+  };
+
   // ---------------- prologue ----------------
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -855,13 +1001,60 @@ __global__ void __launch_bounds__(W * 64)
   // staging slot: tile i+3).
   // Descriptor queue: qm1 = tile i-1, q0 = i, q1 = i+1, q2 = i+2, q3 = i+3
   // (PLAID also q4 = i+4); the cursor produces the newest tile.
+  auto run = [&](auto FL) {
+  constexpr bool FLAT = decltype(FL)::value;
   Cur cur;
   cur_entry(cur, 0);
+  // flat tiles: cursor (position of the newest tile, non-empty doc holding
+  // its row 0, that doc's end position) and the lanes' row cursors
+  int fP = 0, fm = 0, fend = 0, lm = 0, lE = 0, total = 0;
+  uint32_t lb = 0u, fvo[NCH];
+  u32x4 dflat = {0u, 0u, 0u, 0u};
+  if constexpr (FLAT) {
+    fend = __builtin_amdgcn_readfirstlane(s_sst[1]);
+    lE = s_sst[1];
+    lb = s_rb[0];
+    total = __builtin_amdgcn_readfirstlane(s_sst[nnz]);
+    const uint64_t base = (uint64_t)(p.d.data + ((int64_t)(uint32_t)s_nz[0][2] | ((int64_t)s_nz[0][3] << 32)));
+    dflat = u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
+                  (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu), 0xfffffff0u, 0x00020000u};
+  }
+  auto fproduce = [&]() -> Desc {
+    Desc d{};
+    d.k = fm;
+    d.nv = fend - fP;  // rows of doc fm from the tile's row 0 (<= 32: it ends in the tile)
+    d.docend = fm < nnz && d.nv <= 32;
+    return d;
+  };
+  auto fadv = [&]() {
+    fP += 32;
+    if (fend <= fP) {
+      fm += 1;
+      fend = __builtin_amdgcn_readfirstlane(s_sst[fm + 1]);
+    }
+  };
+  float mnext[NSUB];
+#pragma unroll
+  for (int sub = 0; sub < NSUB; ++sub) mnext[sub] = NEG_INF;
   Desc qm1{}, q0, q1, q2, q3, q4{};
   // mask words of tiles i, i+1, i+2 (dense + mask; taken from the staged loads at commit)
   uint32_t vw0 = 0xffffffffu, vw1 = 0xffffffffu, vw2 = 0xffffffffu;
-  q0 = produce(cur);
-  if constexpr (SRC == SRC_DENSE && kDMA) {
+  q0 = FLAT ? fproduce() : produce(cur);
+  if constexpr (FLAT) {
+    auto pro = [&](int t) {
+      flat_offsets(fP, lm, lE, lb, total, fvo);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) dma_issue(t, c, fvo[c], dflat);
+      fadv();
+    };
+    pro(0);
+    q1 = fproduce();
+    pro(1);
+    q2 = fproduce();
+    pro(2);
+    flat_offsets(fP, lm, lE, lb, total, fvo);  // tile 3, issued in step 0
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  } else if constexpr (SRC == SRC_DENSE && kDMA) {
     // tiles 0, 1, 2 into buffers 0, 1, 2; the cursor runs three tiles ahead
     // of the MFMA
     fetch_dma(cur, q0, 0);
@@ -942,7 +1135,7 @@ __global__ void __launch_bounds__(W * 64)
       flush(flush_half * HSLOT, HSLOT);
       flush_half = -1;
     }
-    {
+    if constexpr (!FLAT) {
       // row validity of tile i (uniform): rows past the doc end, and rows the
       // mask drops in docs with holes
       uint32_t vb = q0.nv >= 32 ? 0xffffffffu : ((1u << q0.nv) - 1u);
@@ -959,13 +1152,16 @@ __global__ void __launch_bounds__(W * 64)
     }
     // one block: MFMA tile i, read A of tile i+1, max of tile i-1, commit
     // tile i+2, fetch tile i+4
-    const Desc qn = produce(cur);
+    const Desc qn = FLAT ? fproduce() : produce(cur);
     const int bx = kDMA ? (i & 3) : buf_x;
     if constexpr (NACC == 2) {
       mma_tile(IP{}, IP{}, bx);
       epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
     } else {
-      epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
+      if constexpr (FLAT)
+        epilogue_flat(qm1, mnext);
+      else
+        epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
       mma_tile(IP{}, IP{}, bx);
       // the max stays with the MFMAs that overwrite its accumulators (sunk
       // below the branches that follow, it would keep two sets live)
@@ -975,7 +1171,10 @@ __global__ void __launch_bounds__(W * 64)
     if constexpr (kPrefetchA) load_a(IQ{}, buf_a);
     if constexpr (!kDMA) commit(IP{}, q2, buf_c, (i + 2) & 3);
     if constexpr (SRC == SRC_DENSE && (FEAT & F_MASK) != 0) vw2 = sm[P];
-    if constexpr (SRC == SRC_DENSE && kDMA) {
+    if constexpr (FLAT) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) dma_issue((i + 3) & 3, c, fvo[c], dflat);
+    } else if constexpr (SRC == SRC_DENSE && kDMA) {
       fetch_dma(cur, qn, (i + 3) & 3);  // tile i+3 straight into its LDS buffer
     } else if constexpr (SRC == SRC_DENSE) {
       fetch_dense(IP{}, cur, qn);  // tile i+4 into slot (i+4)%2 (one slot: tile i+3, after the commit)
@@ -983,7 +1182,12 @@ __global__ void __launch_bounds__(W * 64)
       fetch_plaid(IP{}, q4);       // tile i+4, codes from slot (i+4)%2
       fetch_codes(IQ{}, qn);       // codes of tile i+5 into slot (i+5)%2
     }
-    cur_adv(cur);
+    if constexpr (FLAT) {
+      fadv();
+      flat_offsets(fP, lm, lE, lb, total, fvo);  // the next step's tile
+    } else {
+      cur_adv(cur);
+    }
     if constexpr (SRC == SRC_DENSE && NACC == 2) {
       // Interleave the block: each MFMA is followed by a few VALU / SALU
       // instructions (epilogue max, commit, fetch addressing, cursor), an LDS
@@ -1003,7 +1207,13 @@ __global__ void __launch_bounds__(W * 64)
       }
     }
     if (i >= 1 && qm1.docend) {
-      doc_end(qm1.k);
+      if constexpr (FLAT) {
+        doc_end(__builtin_amdgcn_readfirstlane(s_nz[qm1.k][0]));
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub) m[sub] = mnext[sub];
+      } else {
+        doc_end(qm1.k);
+      }
       if ((nend % HSLOT) == 0) flush_half = ((nend / HSLOT) - 1) & 1;
     }
     qm1 = q0;
@@ -1047,6 +1257,15 @@ __global__ void __launch_bounds__(W * 64)
   // remaining finished docs: the due half (if any) and the partial half
   if (flush_half >= 0) flush(flush_half * HSLOT, HSLOT);
   if (nend % HSLOT) flush(nend - nend % HSLOT, nend % HSLOT);
+  };
+  if constexpr (kFlatOK) {
+    if (flat)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
+  } else {
+    run(std::false_type{});
+  }
   // no DMA may still be writing this workgroup's LDS when it exits
   if constexpr (kDMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }

@@ -214,6 +214,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
         "s_nop 4\n\t"
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"  // an M0 write needs one wait state before an LDS DMA reads it
         "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
@@ -226,6 +227,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
         "s_nop 4\n\t"
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"  // an M0 write needs one wait state before an LDS DMA reads it
         "buffer_load_dwordx4 %2, %3, 0 offen nt lds\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)

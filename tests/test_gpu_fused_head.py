@@ -90,6 +90,11 @@ CASES = [
     (3, 5, 6, 255, 8, 40),
     (8, 32, 5, 65, 128, 32),
     (1, 1, 4, 1, 64, 128),
+    # more (doc, 256-token chunk) items than CUs: the persistent kernel's
+    # workgroups take several items each (its load pipeline runs across items;
+    # d_model 64 is one unit per item, so it runs two items ahead)
+    (1, 32, 300, 600, 384, 128),
+    (2, 16, 700, 100, 64, 64),
 ]
 
 

@@ -114,10 +114,13 @@ __global__ void __launch_bounds__(W * 64)
   __shared__ int32_t s_dlen[kRMax];  // length | holes << 31
   __shared__ __attribute__((aligned(16))) i32x4 s_nz[kRMax + 1];  // {k, length | holes << 31, start lo, hi}; [nnz] = sentinel
   __shared__ int s_nnz, s_ntiles;
-  // Flat tiles (DMA kernel, every non-empty doc of the range at least 32
-  // tokens long): the tiles are 32-row windows of the range's docs laid end to
-  // end, so a doc's last tile is not padded to 32 rows; a doc may end inside a
-  // tile and the next one start there (one doc end per tile at most).
+  // Flat tiles (DMA kernel): the tiles are 32-row windows of the range's docs
+  // laid end to end, so a doc's last tile is not padded to 32 rows; a doc may
+  // end inside a tile and the next one start there. Packed docs (F_CU, rows
+  // contiguous in memory) take it when every non-empty doc of the range has
+  // at least 16 tokens (two doc ends per tile at most); strided docs when
+  // every one has at least 32 (one end per tile; each lane tracks the doc of
+  // its row).
   // s_sst[m]: position of non-empty doc m's token 0 in that sequence ([nnz]:
   // the total, [nnz + 1]: INT_MAX); s_rb[m]: byte offset of its token 0 from
   // non-empty doc 0's, minus s_sst[m] row strides (mod 2^32), so the row at
@@ -126,6 +129,8 @@ __global__ void __launch_bounds__(W * 64)
 #define LIK_FLAT_TILES 1
 #endif
   constexpr bool kFlatOK = LIK_FLAT_TILES && kDMA && SRC == SRC_DENSE;
+  constexpr bool kTwoEnd = (FEAT & F_CU) != 0;  // packed docs: two doc ends per tile
+  constexpr int kFlatMinLen = kTwoEnd ? 16 : 32;
   __shared__ int32_t s_sst[kFlatOK ? kRMax + 2 : 1];
   __shared__ uint32_t s_rb[kFlatOK ? kRMax + 1 : 1];
   __shared__ int s_flat;
@@ -267,21 +272,28 @@ __global__ void __launch_bounds__(W * 64)
   const int nnz = __builtin_amdgcn_readfirstlane(s_nnz);
   if (nnz == 0) return;
   if constexpr (kFlatOK) {
-    // flat tiles need every doc >= 32 tokens (one doc end per tile) and every
+    // flat tiles need every doc >= kFlatMinLen tokens and every
     // row within 4 GiB after non-empty doc 0's first row (32-bit DMA offsets)
     if (wv == 0) {
       const int64_t off0 = (int64_t)(uint32_t)s_nz[0][2] | ((int64_t)s_nz[0][3] << 32);
       const int64_t sl = p.d.sl_b;
       bool ok = true;
+      int nshort = 0;  // docs under 32 tokens (tiles that hold two doc ends)
       for (int m = lane; m < nnz; m += 64) {
         const i32x4 e = s_nz[m];
         const int64_t L = e[1] & 0x7fffffff;
         const int64_t rel = ((int64_t)(uint32_t)e[2] | ((int64_t)e[3] << 32)) - off0;
-        ok = ok && L >= 32 && rel >= 0 && rel + (L - 1) * sl + 256 <= 0xffff0000LL;
+        ok = ok && L >= kFlatMinLen && rel >= 0 && rel + (L - 1) * sl + 256 <= 0xffff0000LL;
+        nshort += L < 32 ? 1 : 0;
         s_rb[m] = (uint32_t)rel - (uint32_t)s_sst[m] * (uint32_t)sl;
       }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) nshort += __shfl_xor(nshort, o);
       const bool all = __ballot(!ok) == 0ull;
-      if (lane == 0) s_flat = (all && sl > 0) ? 1 : 0;
+      // two-end tiles cost a second split and an early doc end: with many of
+      // them (C3's log-uniform lengths: 14% of docs under 32 tokens) per-doc
+      // tiles measure faster, so flat tiles need at most 1 in 16 short docs
+      if (lane == 0) s_flat = (all && sl > 0 && nshort * 16 <= nnz) ? 1 : 0;
     }
     __syncthreads();
   }
@@ -498,23 +510,26 @@ __global__ void __launch_bounds__(W * 64)
     }
   };
   // DMA offsets of the flat tile at position P. Lane row l32 of the tile is
-  // position P + l32; (lm, lE, lb) track the non-empty doc that position is
-  // in (its index, end position and s_rb entry): positions advance by 32 per
-  // tile and docs are >= 32 tokens, so a lane crosses at most one doc end per
-  // tile. Positions past the last doc read 0 (offset kOOB). The offsets are
+  // position P + l32: for packed docs at (P + l32) row strides from non-empty
+  // doc 0's first row; else (lm, lE, lb) track the non-empty doc that
+  // position is in (its index, end position and s_rb entry): positions
+  // advance by 32 per tile and such docs are >= 32 tokens, so a lane crosses
+  // at most one doc end per tile. Positions past the last doc read 0 (offset kOOB). The offsets are
   // computed one step ahead of their DMA, which then needs no LDS read or
   // wait and can issue among the tile's MFMAs; the DMA uses the raw
   // descriptor dflat at non-empty doc 0's first row (range 0xfffffff0).
   auto flat_offsets = [&](int P, int& lm, int& lE, uint32_t& lb, int total, uint32_t (&vo)[NCH]) {
     if constexpr (kFlatOK) {
       const int pr = P + l32;
-      if (pr >= lE) {
-        lm += 1;
-        lE = s_sst[lm + 1];
-        lb = s_rb[lm];
+      if constexpr (!kTwoEnd) {
+        if (pr >= lE) {
+          lm += 1;
+          lE = s_sst[lm + 1];
+          lb = s_rb[lm];
+        }
       }
       const bool live = pr < total;
-      const uint32_t roff = lb + (uint32_t)pr * (uint32_t)p.d.sl_b;
+      const uint32_t roff = (kTwoEnd ? 0u : lb) + (uint32_t)pr * (uint32_t)p.d.sl_b;
 #pragma unroll
       for (int i = 0; i < NCH; ++i) vo[i] = (live && dmacc[i] != kOOB) ? roff + dmacc[i] : kOOB;
     }
@@ -824,8 +839,12 @@ __global__ void __launch_bounds__(W * 64)
         for (int j = 0; j < p.LU; ++j) sum += cv[j];
       }
       // global (not generic) store: a flat store would also count in the LDS
-      // wait counter and force full waits on the A-fragment reads
-      auto* o = &((__attribute__((address_space(1))) float*)orow)[s_slotk[sl] * p.osd];
+      // wait counter and force full waits on the A-fragment reads. (The slot's
+      // doc index is checked against the range: a slot the ring logic never
+      // filled must not turn into a store outside the output.)
+      const int kd = s_slotk[sl];
+      if ((unsigned)kd >= (unsigned)nloc) continue;
+      auto* o = &((__attribute__((address_space(1))) float*)orow)[kd * p.osd];
       *o = p.accumulate ? sum * osc + *o : sum * osc;
     }
   };
@@ -933,18 +952,12 @@ __global__ void __launch_bounds__(W * 64)
   // js = b / 8 straddles the boundary (element r below it when
   // r < b - 8 js - 4 h); the groups before it go whole to m, those after it
   // whole to mn, and js is uniform: one unrolled body per value.
-  auto epilogue_flat = [&](const Desc& d, float (&mn)[NSUB]) {
-#pragma unroll
-    for (int sub = 0; sub < NSUB; ++sub) mn[sub] = NEG_INF;
-    if (!d.docend || d.nv >= 32) {
-#pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) m[sub] = max_nan(m[sub], acc[0][sub][e]);
-      return;
-    }
-    const int b = d.nv;
-    const int js = b >> 3;
+  // Packed docs: when the next doc ends in the tile too (at row d.t > 0, a doc
+  // shorter than 32 tokens), doc d.k is parked here, its rows are set to
+  // -inf, and the same split at d.t gives the next doc's max (m) and the rows
+  // after it (mn); the caller then parks doc d.k + 1.
+  auto split_at = [&](int b, float (&mn)[NSUB]) {
+    const int js = b < 32 ? b >> 3 : 3;  // (b = 32: everything below, through group 3)
     const int ch = b - 8 * js - 4 * h;
     bool lo[4];
 #pragma unroll
@@ -986,6 +999,34 @@ __global__ void __launch_bounds__(W * 64)
       case 2: split(std::integral_constant<int, 2>{}); break;
       default: split(std::integral_constant<int, 3>{}); break;
     }
+  };
+  auto epilogue_flat = [&](const Desc& d, float (&mn)[NSUB]) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; ++sub) mn[sub] = NEG_INF;
+    if (kTwoEnd && d.docend && d.t > 0) {
+      split_at(d.nv, mn);  // m: doc d.k complete (mn unused)
+      doc_end(__builtin_amdgcn_readfirstlane(s_nz[d.k][0]));  // (the caller checks the slot ring)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const bool lo = 8 * (e >> 2) + 4 * h + (e & 3) < d.nv;
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub) acc[0][sub][e] = lo ? NEG_INF : acc[0][sub][e];
+      }
+      split_at(d.t, mn);  // m: doc d.k + 1 complete, mn: the rows after it
+      if (d.k + 2 >= nnz) {
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub) mn[sub] = NEG_INF;
+      }
+      return;
+    }
+    if (!d.docend || d.nv >= 32) {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m[sub] = max_nan(m[sub], acc[0][sub][e]);
+      return;
+    }
+    split_at(d.nv, mn);
     if (d.k + 1 >= nnz) {
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) mn[sub] = NEG_INF;
@@ -1007,11 +1048,12 @@ __global__ void __launch_bounds__(W * 64)
   cur_entry(cur, 0);
   // flat tiles: cursor (position of the newest tile, non-empty doc holding
   // its row 0, that doc's end position) and the lanes' row cursors
-  int fP = 0, fm = 0, fend = 0, lm = 0, lE = 0, total = 0;
+  int fP = 0, fm = 0, fend = 0, fend2 = 0, lm = 0, lE = 0, total = 0;
   uint32_t lb = 0u, fvo[NCH];
   u32x4 dflat = {0u, 0u, 0u, 0u};
   if constexpr (FLAT) {
     fend = __builtin_amdgcn_readfirstlane(s_sst[1]);
+    fend2 = __builtin_amdgcn_readfirstlane(s_sst[nnz >= 1 ? 2 : 1]);
     lE = s_sst[1];
     lb = s_rb[0];
     total = __builtin_amdgcn_readfirstlane(s_sst[nnz]);
@@ -1019,18 +1061,25 @@ __global__ void __launch_bounds__(W * 64)
     dflat = u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base),
                   (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32) & 0xffffu), 0xfffffff0u, 0x00020000u};
   }
+  // (fend, fend2: end positions of docs fm and fm + 1; s_sst[nnz + 1] is INT_MAX)
   auto fproduce = [&]() -> Desc {
     Desc d{};
     d.k = fm;
     d.nv = fend - fP;  // rows of doc fm from the tile's row 0 (<= 32: it ends in the tile)
     d.docend = fm < nnz && d.nv <= 32;
+    // the next doc ends in the tile too (at row d.t)
+    d.t = (kTwoEnd && d.docend && d.nv < 32 && fm + 1 < nnz && fend2 - fP <= 32) ? fend2 - fP : 0;
     return d;
   };
   auto fadv = [&]() {
     fP += 32;
-    if (fend <= fP) {
-      fm += 1;
-      fend = __builtin_amdgcn_readfirstlane(s_sst[fm + 1]);
+#pragma unroll
+    for (int x = 0; x < (kTwoEnd ? 2 : 1); ++x) {
+      if (fend <= fP) {
+        fm += 1;
+        fend = fend2;
+        fend2 = __builtin_amdgcn_readfirstlane(s_sst[fm + 2 <= nnz + 1 ? fm + 2 : nnz + 1]);
+      }
     }
   };
   float mnext[NSUB];
@@ -1158,10 +1207,12 @@ __global__ void __launch_bounds__(W * 64)
       mma_tile(IP{}, IP{}, bx);
       epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
     } else {
-      if constexpr (FLAT)
+      if constexpr (FLAT) {
         epilogue_flat(qm1, mnext);
-      else
+        if (kTwoEnd && qm1.docend && qm1.t > 0 && (nend % HSLOT) == 0) flush_half = ((nend / HSLOT) - 1) & 1;
+      } else {
         epilogue(IQ{}, (i + 3) & 3, qm1.t * 32);
+      }
       mma_tile(IP{}, IP{}, bx);
       // the max stays with the MFMAs that overwrite its accumulators (sunk
       // below the branches that follow, it would keep two sets live)
@@ -1208,7 +1259,9 @@ __global__ void __launch_bounds__(W * 64)
     }
     if (i >= 1 && qm1.docend) {
       if constexpr (FLAT) {
-        doc_end(__builtin_amdgcn_readfirstlane(s_nz[qm1.k][0]));
+        // (a tile with two doc ends parked the first in its epilogue; two
+        // ends in one step cross at most one half of the slot ring)
+        doc_end(__builtin_amdgcn_readfirstlane(s_nz[qm1.k + (qm1.t > 0 ? 1 : 0)][0]));
 #pragma unroll
         for (int sub = 0; sub < NSUB; ++sub) m[sub] = mnext[sub];
       } else {

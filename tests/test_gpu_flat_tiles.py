@@ -1,13 +1,15 @@
 """GPU parity of the tile kernel's flat tiles.
 
 In the two-workgroup DMA kernel (bf16 / fp16, d = 128, 4 waves x 4 column
-blocks), a workgroup whose non-empty docs are all >= 32 tokens walks them as
-32-row windows laid end to end: a doc ends inside a tile and the next doc
-starts there. These cases put the boundary at every row of a tile (doc
-lengths 32 + 7 k cover every residue mod 32), put a workgroup's last doc end
-exactly on a tile end, mix workgroups that take flat tiles with workgroups
-that hold a short doc (per-doc tiles), and put NaN / inf tokens on both sides
-of a boundary (reference.py:83-85: a NaN row max scores the doc 0). Each is
+blocks), a workgroup whose non-empty docs are all >= 32 tokens (packed docs:
+>= 16, at most 1 in 16 under 32) walks them as 32-row windows laid end to
+end: a doc ends inside a tile and the next doc starts there. These cases put
+the boundary at every row of a tile (doc lengths 32 + 7 k cover every residue
+mod 32), put a workgroup's last doc end exactly on a tile end, put two doc
+ends in one tile (the second also exactly at its end), mix workgroups that
+take flat tiles with workgroups that hold a short doc (per-doc tiles), and
+put NaN / inf tokens on both sides of a boundary (reference.py:83-85: a NaN
+row max scores the doc 0). Each is
 compared with the oracle (oracle/lik_oracle.py) within the bf16 tolerance.
 """
 
@@ -65,15 +67,51 @@ def test_flat_tiles_padded(dtype, docs_per_wg, short):
     assert rel_err(gn, ref) < 1e-2
 
 
-@pytest.mark.parametrize("docs_per_wg", [2, 5, 64])
-def test_flat_tiles_varlen(docs_per_wg):
+def _rare_short_lengths(n):
+    """Mostly 40..239 tokens, every 17th doc 16..31 (under 1 in 16, so packed
+    ranges keep flat tiles): some tiles hold two doc ends, some of them with
+    the second exactly at the tile's end (checked in the test)."""
+    return [16 + (3 * k + 3) % 16 if k % 17 == 5 else 40 + (7 * k) % 200 for k in range(n)]
+
+
+def _two_end_tiles(lens, r):
+    """(two-end tiles, of them with the second end at row 32) over the ranges
+    of r docs that take flat tiles (docs >= 16 tokens, at most 1 in 16 under 32)."""
+    two = at32 = 0
+    for w0 in range(0, len(lens), r):
+        ls = lens[w0:w0 + r]
+        if min(ls) < 16 or 16 * sum(x < 32 for x in ls) > len(ls):
+            continue
+        ends, pos = {}, 0
+        for x in ls:
+            pos += x
+            ends.setdefault((pos - 1) // 32, []).append(pos - 32 * ((pos - 1) // 32))
+        for bs in ends.values():
+            if len(bs) >= 2:
+                two += 1
+                at32 += bs[1] == 32
+    return two, at32
+
+
+@pytest.mark.parametrize("docs_per_wg", [2, 5, 37, 64])
+@pytest.mark.parametrize("short", [False, True])
+def test_flat_tiles_varlen(docs_per_wg, short):
+    """Packed docs take flat tiles down to 16 tokens: a doc of 16..31 tokens
+    can sit entirely inside a tile, which then holds two doc ends."""
     from late_interaction_kernels import maxsim_varlen
 
-    _case(f"flat varlen R={docs_per_wg}")
-    g = torch.Generator().manual_seed(docs_per_wg)
+    _case(f"flat varlen R={docs_per_wg} short={short}")
+    g = torch.Generator().manual_seed(docs_per_wg + 100 * short)
     d, nq = 128, 16
     q_lens = torch.full((nq,), 32)
-    d_lens = _lengths(80)
+    if short:
+        lens = _rare_short_lengths(200)
+        if docs_per_wg in (37, 64):
+            two, at32 = _two_end_tiles(lens, docs_per_wg)
+            assert two > 0 and at32 > 0  # the cases this test is for
+        d_lens = torch.tensor(lens)
+    else:
+        d_lens = _lengths(80)
     cu_q = torch.zeros(nq + 1, dtype=torch.int32)
     cu_q[1:] = torch.cumsum(q_lens, 0)
     cu_d = torch.zeros(len(d_lens) + 1, dtype=torch.int32)

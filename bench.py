@@ -760,13 +760,17 @@ def wl_fused_head(args):
             "roofline": None}
 
 
+HEAD_MIN_WARMUP = 100  # calls of the fused head before its timed region (see wl_head)
+
+
 def wl_head(args):
     """maxsim_from_hidden inference on the largest reference fused-head shape
     (lateon-code-Nd1024-Ld2k: 1 query x 32 tokens, 1024 docs x 2048 tokens of
     768-dim hidden states, d_out 128, bias, normalize=True, bf16): the fused
     projection + MaxSim kernel (lik_maxsim_from_hidden). HBM-bound: the
     algorithmic bytes are the hidden states read once (plus W, Q, scores).
-    ``roofline.kernel_ms`` is the whole call (head_tile_kernel + the small
+    ``roofline.kernel_ms`` is the whole call (the validity pre-pass
+    head_valid_kernel, the persistent head_persist_kernel and the small
     head_finish_kernel) timed with events on the launch stream."""
     import torch
 
@@ -788,8 +792,13 @@ def wl_head(args):
         with torch.no_grad():
             return _score(Q, torch.nn.functional.linear(H, W, b), None, None, normalize=2)
 
-    ms = _time_steps(step, args.steps, args.warmup)
-    ms_proj = _time_steps(projected, args.steps, args.warmup)
+    # A fresh process runs the first few dozen calls of this kernel ~15% slower
+    # (0.80 against 0.68 ms per call; the MFMA- and HBM-bound kernels of the
+    # other workloads show no such ramp), so the warmup is at least 100 calls
+    # (~70 ms), and the steady state is what is timed.
+    warm = max(args.warmup, HEAD_MIN_WARMUP)
+    ms = _time_steps(step, args.steps, warm)
+    ms_proj = _time_steps(projected, args.steps, warm)
     nbytes = float(H.numel() * 2 + W.numel() * 2 + Q.numel() * 2 + Nq * Nd * 4)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {
@@ -797,7 +806,7 @@ def wl_head(args):
         "ms_per_step": round(ms, 4), "dtype": "bf16",
         "config": {"workload": "fused projection head, lateon-code-Nd1024-Ld2k (docs/benchmarks.md:239-247)",
                    "Nq": Nq, "Lq": Lq, "Nd": Nd, "Ld": Ld, "d_model": dm_, "d_out": do,
-                   "bytes_per_step": nbytes, "project_first_ms": round(ms_proj, 4)},
+                   "bytes_per_step": nbytes, "project_first_ms": round(ms_proj, 4), "warmup_calls": warm},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK["hbm"], "unit": "GB/s",
                      "frac": round(gbs / PEAK["hbm"], 4), "traffic": _traffic("head"), "kernel_ms": round(ms, 4)},
     }
@@ -840,7 +849,66 @@ def wl_hbm_copy(args):
                          "frac": round(gbs / PEAK["hbm"], 4), "traffic": 4.0 * n}}
 
 
+def wl_input_entropy(args):
+    """Diagnostic, not part of the metric: the same kernels on the same shapes
+    and masks with inputs of different bit entropy. The in-batch MaxSim call
+    (C2) and the fused projection head (lateon-code-Nd1024-Ld2k) are timed on
+    N(0,1) rows (the benched inputs), on one constant value, and on random
+    signs of one constant (only the sign bits vary). The instruction stream,
+    the memory traffic and the tile counts are identical across the three; a
+    kernel whose time still moves with the data is limited by the power the
+    matrix cores draw (the clock drops under switching load), not by issue
+    slots or bandwidth."""
+    import torch
+
+    from late_interaction_kernels import maxsim
+    from late_interaction_kernels.fused_head import maxsim_from_hidden
+
+    def variants(shape, g, scale):
+        rnd = _normed(shape, g, torch.bfloat16) if scale is None else (
+            torch.randn(*shape, generator=g, device="cuda") * scale).to(torch.bfloat16)
+        c = 1.0 / shape[-1] ** 0.5 if scale is None else scale
+        const = torch.full(shape, c, device="cuda", dtype=torch.bfloat16)
+        signs = (torch.sign(torch.randn(*shape, generator=g, device="cuda")) * c).to(torch.bfloat16)
+        return {"random": rnd, "constant": const, "random_signs": signs}
+
+    Nq, Lq, Nd, Ld, d = 512, 32, 4096, 300, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    dlen = torch.randint(50, Ld + 1, (Nd,), generator=g, device="cuda")
+    dm = torch.arange(Ld, device="cuda")[None] < dlen[:, None]
+    flops = 2.0 * d * (Nq * Lq) * float(dlen.sum().item())
+    Qv, Dv = variants((Nq, Lq, d), g, None), variants((Nd, Ld, d), g, None)
+    inbatch = {}
+    for k in list(Qv):
+        ms = _time_steps(lambda: maxsim(Qv[k], Dv[k], d_mask=dm), args.steps, args.warmup)
+        inbatch[k] = {"ms_per_call": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                      "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK["bf16"], 4)}
+        del Qv[k], Dv[k]
+        torch.cuda.empty_cache()
+    hNd, hLd, dm_, do = 1024, 2048, 768, 128
+    Hv = variants((hNd, hLd, dm_), g, 1.0)
+    Wv = variants((do, dm_), g, dm_ ** -0.5)
+    Q = _normed((1, 32, do), g, torch.bfloat16)
+    hbytes = float(hNd * hLd * dm_ * 2)
+    head = {}
+    for k in list(Hv):
+        with torch.no_grad():
+            ms = _time_steps(lambda: maxsim_from_hidden(Q, Hv[k], Wv[k], None, normalize=True), args.steps,
+                             max(args.warmup, HEAD_MIN_WARMUP))
+        head[k] = {"ms_per_call": round(ms, 4), "gbs_hidden": round(hbytes / (ms * 1e-3) / 1e9, 1),
+                   "frac_hbm": round(hbytes / (ms * 1e-3) / 1e9 / PEAK["hbm"], 4)}
+        del Hv[k]
+        torch.cuda.empty_cache()
+    return {"metric": "kernel time by input bit entropy (diagnostic)", "value": inbatch["random"]["ms_per_call"],
+            "unit": "ms", "higher_is_better": False, "ms_per_step": inbatch["random"]["ms_per_call"],
+            "dtype": "bf16", "data": "synthetic: seeded N(0,1) rows, one constant, random signs of one constant",
+            "config": {"workload": "C2 in-batch maxsim and fused head Nd1024-Ld2k on N(0,1) / constant / "
+                                   "random-sign inputs", "inbatch": inbatch, "head": head},
+            "roofline": None}
+
+
 WORKLOADS = {
+    "input_entropy": wl_input_entropy,
     "hbm_copy": wl_hbm_copy,
     "plaid_q1": wl_plaid_q1,
     "plaid_q1_prepared": wl_plaid_q1_prepared,
@@ -910,8 +978,9 @@ def main() -> None:
             print(f"[bench] {name}: {r['value']} {r['unit']}", file=sys.stderr, flush=True)
     out = {
         "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": res["dtype"], "data": "synthetic (seeded N(0,1), L2-normalised)",
+        "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": res.get("higher_is_better", True),
+        "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
+        "data": res.get("data", "synthetic (seeded N(0,1), L2-normalised)"),
         "config": res["config"], "roofline": res["roofline"],
     }
     if "cpu_baseline" in res:

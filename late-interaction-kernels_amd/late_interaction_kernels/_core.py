@@ -387,8 +387,9 @@ def from_hidden_forward(Q, H, W, b, d_mask, *, normalize: bool, want_argmax: boo
         return None
     Nq, Lq, d_out = Q.shape
     Nd, Ld, _ = H.shape
-    out = torch.zeros(Nq, Nd, device=Q.device, dtype=torch.float32)
-    argmax = torch.full((Nq * Nd, Lq), -1, device=Q.device, dtype=torch.int32) if want_argmax else None
+    # head_finish_kernel writes every score (and every argmax entry)
+    out = torch.empty(Nq, Nd, device=Q.device, dtype=torch.float32)
+    argmax = torch.empty((Nq * Nd, Lq), device=Q.device, dtype=torch.int32) if want_argmax else None
     Qc = Q.detach().contiguous()
     Hc = H.detach()
     if Hc.stride(-1) != 1 or Hc.data_ptr() % 16 or any(s % 8 for s in Hc.stride()[:-1]):

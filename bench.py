@@ -58,10 +58,12 @@ KERNEL_MS = {}  # filled by _time_steps: summed duration and count of the MaxSim
 def _time_steps(fn, steps: int, warmup: int) -> float:
     """ms per step: W untimed steps, then K steps between events on the current
     stream (the stream every op launches on). Inside the timed region each
-    scoring call also records a pair of HIP events on that stream around its
-    MaxSim tile-kernel launch (``_lib.launch_options(timer=...)`` hands them
-    to the C ABI per call through ``lik_launch_opts_t``); their summed
-    duration is what ``roofline.achieved`` divides by."""
+    scoring call also times its MaxSim tile-kernel launches with a pair of
+    HIP events (``_lib.launch_options(timer=...)`` hands them to the C ABI
+    per call through ``lik_launch_opts_t``); the library passes them to the
+    launches themselves (hipExtLaunchKernel), so no event packet sits between
+    kernels and the timed steps run as untimed ones. Their summed duration is
+    what ``roofline.achieved`` divides by."""
     import torch
 
     from late_interaction_kernels import _lib

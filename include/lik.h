@@ -95,12 +95,16 @@ typedef struct {
  *       kernel), 3 the tile kernel (no stream kernel). lik_plaid_maxsim_qc:
  *       0 automatic, 5 the LDS-staged scan instead of the register-direct
  *       one for a single query.
- *   timing_start, timing_stop: hipEvent_t or NULL. When both are set, they
- *       are recorded on the call's stream immediately before and after the
- *       call's MaxSim scoring launches: without the pre-passes (mask summary,
- *       row norms, query-chunk sums), but with both launches of a doc mask
- *       that has holes (the mask-free documents, then those with holes), so
- *       a caller can time the scoring kernels alone.
+ *   timing_start, timing_stop: hipEvent_t or NULL. When both are set, the
+ *       call's MaxSim scoring launches carry them in their own dispatches
+ *       (hipExtLaunchKernel): timing_start records the start of the first
+ *       scoring kernel, timing_stop the end of the last one. That spans both
+ *       launches of a doc mask that has holes (the mask-free documents, then
+ *       those with holes) but none of the pre-passes (mask summary, row
+ *       norms, query-chunk sums), so a caller can time the scoring kernels
+ *       alone; no event packet is queued between launches, so a timed call
+ *       runs as an untimed one does. A call that launches no scoring kernel
+ *       records both events back to back (zero duration).
  */
 typedef struct {
   int32_t col_waves;

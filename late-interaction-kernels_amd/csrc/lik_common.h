@@ -1,5 +1,6 @@
 // Shared device-side definitions for the gfx950 MaxSim kernels.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -20,6 +21,63 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Timing of a call's main launches with the caller's HIP events
+// (lik_launch_opts_t::timing_start / timing_stop). While a TimingScope is open
+// on the calling host thread, every launch made through launch_kernel carries
+// the events in its own dispatch (hipExtLaunchKernelGGL): the first records
+// timing_start when it starts, each records timing_stop when it ends. No
+// event packets are queued between launches, so timed calls run back to back
+// like untimed ones (separate hipEventRecord packets left gaps of several us
+// around each launch, and a power-limited kernel runs faster after a gap).
+struct LaunchTiming {
+  hipEvent_t start, stop;
+  bool start_pending;
+};
+inline thread_local LaunchTiming* g_launch_timing = nullptr;
+
+template <typename K, typename... A>
+inline void launch_kernel(K kern, dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, A... args) {
+  if (LaunchTiming* t = g_launch_timing) {
+    hipExtLaunchKernelGGL(kern, grid, block, shmem, s, t->start_pending ? t->start : nullptr, t->stop, 0u, args...);
+    t->start_pending = false;
+  } else {
+    hipLaunchKernelGGL(kern, grid, block, shmem, s, args...);
+  }
+}
+
+class TimingScope {
+ public:
+  explicit TimingScope(const lik_launch_opts_t* o) {
+    if (o && o->timing_start && o->timing_stop) {
+      t_ = LaunchTiming{(hipEvent_t)o->timing_start, (hipEvent_t)o->timing_stop, true};
+      prev_ = g_launch_timing;
+      g_launch_timing = &t_;
+      on_ = true;
+    }
+  }
+  TimingScope(const TimingScope&) = delete;
+  TimingScope& operator=(const TimingScope&) = delete;
+  // Ends the scope. A scope whose call launched nothing records both events
+  // here, back to back (zero duration), so the caller can always read them.
+  int close(hipStream_t s) {
+    if (!on_) return LIK_OK;
+    g_launch_timing = prev_;
+    on_ = false;
+    if (t_.start_pending &&
+        (hipEventRecord(t_.start, s) != hipSuccess || hipEventRecord(t_.stop, s) != hipSuccess))
+      return LIK_ERR_LAUNCH;
+    return LIK_OK;
+  }
+  ~TimingScope() {
+    if (on_) g_launch_timing = prev_;
+  }
+
+ private:
+  LaunchTiming t_{};
+  LaunchTiming* prev_ = nullptr;
+  bool on_ = false;
+};
 
 // Element kinds of the token embeddings. F32 is computed as three bf16 MFMAs
 // (hi*hi + hi*lo + lo*hi; split_hi / split_lo), ~1e-5 relative of exact fp32 MaxSim.

@@ -1329,7 +1329,7 @@ int launch_one(const Params& p, int64_t nblocks, hipStream_t s) {
   } else {
     if (nblocks <= 0) return LIK_OK;
     if (nblocks > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((maxsim_kernel<EK, DPAD, W, NSUB, SRC, CD, FEAT>), dim3((unsigned)nblocks), dim3(W * 64), 0, s, p);
+    launch_kernel(maxsim_kernel<EK, DPAD, W, NSUB, SRC, CD, FEAT>, dim3((unsigned)nblocks), dim3(W * 64), 0, s, p);
     return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   }
 }

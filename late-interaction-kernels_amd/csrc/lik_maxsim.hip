@@ -73,6 +73,78 @@ __global__ void __launch_bounds__(256) doc_extent_kernel(const int8_t* mask, int
   }
 }
 
+// The same summary for masks whose token bytes are contiguous (stride 1),
+// with 4-byte-aligned rows, L <= 1024 and the whole mask under 4 GB. The
+// byte-per-lane form spends ~90 instructions of a 64-lane wavefront per doc
+// (and one load round trip per doc); here 16 lanes take a doc, 4 docs per
+// wavefront, and lane q reads tokens 16 q .. 16 q + 15 of each 256-token pass
+// as four dwords, all of a wavefront's loads issued before any is used. The
+// nonzero bytes of a dword become 4 bits by an or-fold and one multiply. The
+// loads go through a buffer resource that ends at the mask's last byte (a
+// dword past it reads as 0; bytes past a doc's length are dropped by the
+// length test).
+__device__ __forceinline__ uint32_t nonzero_bytes4(uint32_t x) {
+  uint32_t y = x | (x >> 4);
+  y |= y >> 2;
+  y |= y >> 1;
+  y &= 0x01010101u;  // bit 8 k: byte k is nonzero
+  // bit 8 k -> bit 24 + k (the other products land below bit 24 without carries)
+  return ((y * 0x01020408u) >> 24) & 0xfu;
+}
+
+__global__ void __launch_bounds__(256) doc_extent_w4_kernel(const int8_t* mask, int64_t msn, uint32_t mbytes,
+                                                            int64_t n, int L, const int32_t* lengths,
+                                                            int32_t* extent, uint8_t* holes, uint32_t* tbits,
+                                                            int tbits_sn) {
+  constexpr int NP = 4;  // 256-token passes (L <= 1024)
+  const int lane = threadIdx.x & 63, q = lane & 15;
+  const int64_t j = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  const int np = (L + 255) >> 8;  // passes that hold tokens (uniform)
+  int Lj = j < n ? L : 0;
+  if (lengths && j < n) {
+    const int l = lengths[j];
+    Lj = l < 0 ? 0 : (l > L ? L : l);
+  }
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(mask), (short)0, (int)mbytes, 0x00020000);
+  const uint32_t row = j < n ? (uint32_t)(j * msn) : 0u;
+  uint32_t w[NP][4];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = p * 256 + q * 16 + 4 * i;
+      w[p][i] = (p < np && t < Lj) ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, row + (uint32_t)t, 0, 0) : 0u;
+    }
+  }
+  int last = -1, cnt = 0;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    if (p >= np) break;
+    const int t = p * 256 + q * 16;
+    uint32_t m = nonzero_bytes4(w[p][0]) | (nonzero_bytes4(w[p][1]) << 4) | (nonzero_bytes4(w[p][2]) << 8) |
+                 (nonzero_bytes4(w[p][3]) << 12);
+    const int room = Lj - t;  // tokens of this lane's sixteen that lie inside the doc
+    m &= room >= 16 ? 0xffffu : (room <= 0 ? 0u : (1u << room) - 1u);
+    if (m) last = t + 31 - __builtin_clz(m);
+    cnt += __builtin_popcount(m);
+    // tile p * 8 + q / 2 (32 tokens) = the 16-bit groups of lanes q, q ^ 1
+    uint32_t v = m << (16 * (q & 1));
+    v |= __shfl_xor(v, 1);
+    const int tile = p * 8 + (q >> 1);
+    if (j < n && (q & 1) == 0 && tile < tbits_sn) tbits[j * tbits_sn + tile] = v;
+  }
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) {
+    last = max(last, __shfl_xor(last, o));
+    cnt += __shfl_xor(cnt, o);
+  }
+  if (j < n && q == 0) {
+    extent[j] = last + 1;
+    holes[j] = (uint8_t)(cnt != last + 1);
+  }
+}
+
 // a[i] = v for i < n (used to mark argmax entries "no winner" before a training forward).
 __global__ void __launch_bounds__(256) fill_i32_kernel(int32_t* a, int64_t n, int32_t v) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -350,15 +422,14 @@ int norm_bits(uint32_t flags) {
   return ((flags & (LIK_NORMALIZE | LIK_NORMALIZE_Q)) ? 1 : 0) | ((flags & (LIK_NORMALIZE | LIK_NORMALIZE_D)) ? 2 : 0);
 }
 
-// Brackets the call's main tile-kernel launch with the caller's HIP events
+// Times the call's main tile-kernel launches with the caller's HIP events
 // (lik_launch_opts_t::timing_start / timing_stop), when both are given.
 template <typename F>
 int timed_launch(hipStream_t s, const lik_launch_opts_t* opts, F&& launch) {
-  if (!opts || !opts->timing_start || !opts->timing_stop) return launch();
-  if (hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
+  TimingScope ts(opts);
   const int rc = launch();
-  if (hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;
-  return rc;
+  const int rc2 = ts.close(s);
+  return rc != LIK_OK ? rc : rc2;
 }
 
 struct WsLayout {
@@ -536,10 +607,18 @@ int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float 
     p.holes = (const uint8_t*)(ws + wl.holes_off);
     p.tbits = (const uint32_t*)(ws + wl.tbits_off);
     p.tbits_sn = (D->len + 31) / 32;
-    hipLaunchKernelGGL(doc_extent_kernel, dim3((unsigned)((D->n + 3) / 4)), dim3(256), 0, s, D->mask,
-                       D->mask_stride_n, D->mask_stride_l, D->n, D->len, D->lengths,
-                       (int32_t*)(ws + wl.extent_off), (uint8_t*)(ws + wl.holes_off),
-                       (uint32_t*)(ws + wl.tbits_off), p.tbits_sn);
+    const int64_t mend = (D->n - 1) * D->mask_stride_n + D->len;  // one past the mask's last byte
+    if (D->mask_stride_l == 1 && D->mask_stride_n >= 0 && D->mask_stride_n % 4 == 0 &&
+        (uintptr_t)D->mask % 4 == 0 && D->len <= 1024 && mend < 0x7fffffffLL)
+      hipLaunchKernelGGL(doc_extent_w4_kernel, dim3((unsigned)((D->n + 15) / 16)), dim3(256), 0, s, D->mask,
+                         D->mask_stride_n, (uint32_t)mend, D->n, (int)D->len, D->lengths,
+                         (int32_t*)(ws + wl.extent_off), (uint8_t*)(ws + wl.holes_off),
+                         (uint32_t*)(ws + wl.tbits_off), (int)p.tbits_sn);
+    else
+      hipLaunchKernelGGL(doc_extent_kernel, dim3((unsigned)((D->n + 3) / 4)), dim3(256), 0, s, D->mask,
+                         D->mask_stride_n, D->mask_stride_l, D->n, D->len, D->lengths,
+                         (int32_t*)(ws + wl.extent_off), (uint8_t*)(ws + wl.holes_off),
+                         (uint32_t*)(ws + wl.tbits_off), p.tbits_sn);
     if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
   }
   if (wl.need_part) {
@@ -583,16 +662,18 @@ int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float 
     return launch_dense(Q->dtype, pl, ps, nb, s);
   };
 
-  const bool timed = opts && opts->timing_start && opts->timing_stop;
   if (!wl.need_dnorm) {
-    if (timed && hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
+    TimingScope ts(opts);
     if ((rc = score_docs(p, 0, p.ndocs_pg)) != LIK_OK) return rc;
-    if (timed && hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;
+    if ((rc = ts.close(s)) != LIK_OK) return rc;
   } else {
     // padded cross-product docs, normalised and scored slice by slice through
     // one bounded copy; the tile kernel then normalises only its query block
     char* dn = ws + wl.dnorm_off;
     const int eb = elem_bytes(D->dtype);
+    // the events span the slices' tile kernels: from the first one's start to
+    // the last one's end (the later slices' normalisation passes included)
+    TimingScope ts(opts);
     for (int64_t j0 = 0; j0 < D->n; j0 += wl.dnorm_docs) {
       const int64_t n = D->n - j0 < wl.dnorm_docs ? D->n - j0 : wl.dnorm_docs;
       if ((rc = launch_norm_rows(D, pl.dpad, j0, n, dn, s)) != LIK_OK) return rc;
@@ -601,10 +682,9 @@ int maxsim_impl(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, float 
       ps.d.sn_b = D->len * (int64_t)D->dim * eb;
       ps.d.sl_b = (int64_t)D->dim * eb;
       ps.normalize &= 1;
-      if (timed && j0 == 0 && hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
       if ((rc = score_docs(ps, j0, n)) != LIK_OK) return rc;
     }
-    if (timed && hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;
+    if ((rc = ts.close(s)) != LIK_OK) return rc;
   }
   if (wl.need_part) {
     const int64_t tot = Q->n * p.ndocs_pg;

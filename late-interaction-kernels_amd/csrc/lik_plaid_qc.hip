@@ -871,7 +871,7 @@ int launch_qc_scan(int qn, const Params& p, const uint16_t* qc, int64_t qc_qs, c
   const int64_t nb = (waves + 3) / 4;
   if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(256), 0, s, p, qc, qc_qs, tinv);
+    launch_kernel(kern, dim3((unsigned)nb), dim3(256), 0, s, p, qc, qc_qs, tinv);
     return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   };
   const bool full = p.q.dim == DPAD;
@@ -901,7 +901,7 @@ int launch_scan(const Params& p, const uint16_t* qc, int64_t qc_qs, const float*
   const int64_t nb = (waves + 3) / 4;
   if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(256), 0, s, p, qc, qc_qs, tinv);
+    launch_kernel(kern, dim3((unsigned)nb), dim3(256), 0, s, p, qc, qc_qs, tinv);
     return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   };
   const bool full = p.q.dim == DPAD;
@@ -927,8 +927,7 @@ int launch_qc(int qn, const Params& p, uint16_t* qc, int64_t qc_qs, const float*
   hipLaunchKernelGGL((centroid_scores_kernel<EK, DPAD>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, qc,
                      qc_qs, ntile, reg ? 1 : 0);
   if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
-  const bool timed = opts && opts->timing_start && opts->timing_stop;
-  if (timed && hipEventRecord((hipEvent_t)opts->timing_start, s) != hipSuccess) return LIK_ERR_LAUNCH;
+  TimingScope ts(opts);
   int rc;
   switch (p.pl.nbits) {
     case 2: rc = reg ? launch_scan<EK, DPAD, 2>(p, qc, qc_qs, tinv, s) : launch_qc_scan<EK, DPAD, 2>(qn, p, qc, qc_qs, tinv, s); break;
@@ -936,8 +935,8 @@ int launch_qc(int qn, const Params& p, uint16_t* qc, int64_t qc_qs, const float*
     case 8: rc = reg ? launch_scan<EK, DPAD, 8>(p, qc, qc_qs, tinv, s) : launch_qc_scan<EK, DPAD, 8>(qn, p, qc, qc_qs, tinv, s); break;
     default: rc = LIK_ERR_UNSUPPORTED;
   }
-  if (rc == LIK_OK && timed && hipEventRecord((hipEvent_t)opts->timing_stop, s) != hipSuccess) return LIK_ERR_LAUNCH;
-  return rc;
+  const int rc2 = ts.close(s);
+  return rc != LIK_OK ? rc : rc2;
 }
 
 }  // namespace lik

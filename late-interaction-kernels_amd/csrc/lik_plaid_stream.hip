@@ -777,7 +777,7 @@ int launch_stream_nsub(int nsub, const Params& p, int64_t nblocks, hipStream_t s
   if (p.gather) {
     const bool full = p.q.dim == DPAD;
     auto go = [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(256), 0, s, p);
+      launch_kernel(kern, dim3((unsigned)nblocks), dim3(256), 0, s, p);
       return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
     };
     if constexpr (CD == EK) {
@@ -792,9 +792,9 @@ int launch_stream_nsub(int nsub, const Params& p, int64_t nblocks, hipStream_t s
                 : go(plaid_gather_kernel<EK, DPAD, CD, NBITS, false, false, 1>);
   }
   if (p.q.dim == DPAD)
-    hipLaunchKernelGGL((plaid_stream_kernel<EK, DPAD, CD, NBITS, 1, true>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+    launch_kernel(plaid_stream_kernel<EK, DPAD, CD, NBITS, 1, true>, dim3((unsigned)nblocks), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((plaid_stream_kernel<EK, DPAD, CD, NBITS, 1, false>), dim3((unsigned)nblocks), dim3(256), 0, s, p);
+    launch_kernel(plaid_stream_kernel<EK, DPAD, CD, NBITS, 1, false>, dim3((unsigned)nblocks), dim3(256), 0, s, p);
   return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
 }
 

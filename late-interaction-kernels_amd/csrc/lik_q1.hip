@@ -322,7 +322,7 @@ int launch_q1_t(const Params& p, bool normq, hipStream_t s) {
   if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
   const bool full = p.d.dim == DPAD && p.q.dim == DPAD;
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(256), 0, s, p);
+    launch_kernel(kern, dim3((unsigned)nb), dim3(256), 0, s, p);
     return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   };
   if (full)

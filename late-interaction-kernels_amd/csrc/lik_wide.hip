@@ -182,11 +182,11 @@ int launch_maxsim_wide(int dtype, const Params& p, hipStream_t s) {
   const int64_t nb = (waves + 3) / 4;
   if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
   if (dtype == LIK_BF16)
-    hipLaunchKernelGGL(maxsim_wide_kernel<EK_BF16>, dim3((unsigned)nb), dim3(256), 0, s, p);
+    launch_kernel(maxsim_wide_kernel<EK_BF16>, dim3((unsigned)nb), dim3(256), 0, s, p);
   else if (dtype == LIK_F16)
-    hipLaunchKernelGGL(maxsim_wide_kernel<EK_F16>, dim3((unsigned)nb), dim3(256), 0, s, p);
+    launch_kernel(maxsim_wide_kernel<EK_F16>, dim3((unsigned)nb), dim3(256), 0, s, p);
   else if (dtype == LIK_F32)
-    hipLaunchKernelGGL(maxsim_wide_kernel<EK_F32>, dim3((unsigned)nb), dim3(256), 0, s, p);
+    launch_kernel(maxsim_wide_kernel<EK_F32>, dim3((unsigned)nb), dim3(256), 0, s, p);
   else
     return LIK_ERR_UNSUPPORTED;
   return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;

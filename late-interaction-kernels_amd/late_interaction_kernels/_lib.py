@@ -297,29 +297,61 @@ def version() -> str:
 _OPTS: contextvars.ContextVar[dict | None] = contextvars.ContextVar("lik_launch_opts", default=None)
 
 
+_HIP = None
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime that torch already loaded (libamdhip64), for event calls."""
+    global _HIP
+    if _HIP is None:
+        for name in ("libamdhip64.so", "libamdhip64.so.7", "/opt/rocm/lib/libamdhip64.so"):
+            try:
+                h = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
+        else:
+            raise RuntimeError("libamdhip64 not found (HIP runtime)")
+        h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        _HIP = h
+    return _HIP
+
+
 class LaunchTimer:
-    """Collects a pair of HIP events around the main MaxSim launch of every
-    scoring call made while it is active (see :func:`launch_options`)."""
+    """Collects a pair of HIP events for the MaxSim scoring launches of every
+    call made while it is active (see :func:`launch_options`). The events are
+    created with hipEventCreate (a host call: nothing is queued on the
+    stream); the library records them with the launches themselves."""
 
     def __init__(self) -> None:
-        self.pairs: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+        self.pairs: list[tuple[int, int]] = []
 
     def new_pair(self) -> tuple[int, int]:
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        # materialise the HIP events (torch creates them lazily on first record)
-        a.record()
-        b.record()
-        self.pairs.append((a, b))
-        return a.cuda_event, b.cuda_event
+        hip = _hip_runtime()
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        if hip.hipEventCreate(ctypes.byref(a)) != 0 or hip.hipEventCreate(ctypes.byref(b)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        self.pairs.append((a.value, b.value))
+        return a.value, b.value
 
     def total_ms(self) -> tuple[float, int]:
         """Wait for the recorded launches; return (summed ms, launch count)."""
+        hip = _hip_runtime()
         tot = 0.0
+        ms = ctypes.c_float()
         for a, b in self.pairs:
-            b.synchronize()
-            tot += a.elapsed_time(b)
-        return tot, len(self.pairs)
+            if hip.hipEventSynchronize(b) != 0 or hip.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+                raise RuntimeError("timing events were not recorded")
+            tot += ms.value
+        n = len(self.pairs)
+        for a, b in self.pairs:
+            hip.hipEventDestroy(a)
+            hip.hipEventDestroy(b)
+        self.pairs = []
+        return tot, n
 
 
 @contextlib.contextmanager

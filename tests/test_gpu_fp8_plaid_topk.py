@@ -338,6 +338,38 @@ def test_plaid_retrieve():
     np.testing.assert_array_equal(s.cpu().numpy(), ws)
 
 
+@pytest.mark.parametrize("chunk", [1, 7, 256, 1000])
+@pytest.mark.parametrize("piece_tokens", [0, 300])
+def test_plaid_retrieve_decode_route(chunk, piece_tokens, monkeypatch):
+    """The decode-once route (forced): each chunk is decoded in pieces of at
+    most _DECODE_TOKENS tokens into one reused buffer, scored by the tile
+    kernel, and merged into the running top-k. Chunks of 1, 7, 256 docs and
+    one chunk for the whole corpus; piece_tokens = 300 splits chunks into
+    several decode pieces (a doc longer than that is a piece of its own);
+    docs 0 and 20..27 are empty, so one 7-doc chunk holds no token. The
+    result equals a stable top-k of the full score matrix bit for bit."""
+    from late_interaction_kernels import plaid
+    from late_interaction_kernels.plaid import maxsim_residual_varlen, retrieve_residual_varlen
+
+    _case(f"plaid retrieve decode route chunk={chunk} piece_tokens={piece_tokens}")
+    if piece_tokens:
+        monkeypatch.setattr(plaid, "_DECODE_TOKENS", piece_tokens)
+    cent, bw, lens, codes, res = _index(700, 40, 128, 128, 2, 78)
+    lens[20:28] = 0
+    keep = torch.arange(40)[None] < lens[:, None]
+    cu = torch.zeros(701, dtype=torch.int32)
+    cu[1:] = lens.cumsum(0).to(torch.int32)
+    args = (codes[keep].cuda(), res[keep].cuda(), cu.cuda(), cent.cuda(), bw.cuda(), 2)
+    g = torch.Generator().manual_seed(9)
+    Q = torch.randn(5, 32, 128, generator=g).to(torch.bfloat16).cuda()
+    with launch_options(plaid_route="decode"):
+        full = maxsim_residual_varlen(Q, *args)
+        s, i = retrieve_residual_varlen(Q, *args, 100, chunk=chunk)
+    ws, wi = O.topk_stable(full.cpu().numpy(), 100)
+    np.testing.assert_array_equal(i.cpu().numpy(), wi)
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
+
+
 def test_plaid_approx_score_gpu():
     from late_interaction_kernels.plaid import plaid_approx_score
 

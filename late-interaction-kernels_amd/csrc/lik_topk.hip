@@ -84,8 +84,9 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(TopkArgs a) {
   uint64_t* const s_sel = C::INPLACE ? s_keys : s_sel_own;
   __shared__ uint32_t s_hist[256];
   __shared__ uint64_t s_prefix, s_pmask;
-  __shared__ int s_kk, s_done, s_cnt, s_real;
+  __shared__ int s_kk, s_done, s_cnt, s_real, s_fcnt;
   __shared__ int s_wcnt[TK_THREADS / 64];
+  __shared__ uint64_t s_wmin[TK_THREADS / 64];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t row = blockIdx.x / a.groups;
@@ -94,7 +95,45 @@ __global__ void __launch_bounds__(TK_THREADS) topk_select_kernel(TopkArgs a) {
   __syncthreads();
 
   int total;
-  if (!FROM_KEYS) {
+  if (!FROM_KEYS && g == 0 && a.groups == 1 && a.pk > 0 && a.pk == a.k) {
+    // A running merge whose list is full: every one of the k list keys is at
+    // least the list's smallest key T, so a chunk key below T cannot be among
+    // the k best of the union. Only chunk keys above T join the list's keys:
+    // the same k winners, usually from ~k keys instead of k + n. (The list
+    // need not be sorted; T is its minimum.)
+    const int pk = (int)a.pk;
+    uint64_t mn = ~0ull;
+    for (int i = tid; i < pk; i += TK_THREADS) {
+      const uint64_t key = make_key(a.prev_s[row * a.pld + i], (uint32_t)a.prev_i[row * a.pld + i], a.largest);
+      s_keys[i] = key;
+      mn = key < mn ? key : mn;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint64_t v = __shfl_xor(mn, o);
+      mn = v < mn ? v : mn;
+    }
+    if (lane == 0) s_wmin[wv] = mn;
+    if (tid == 0) s_fcnt = 0;
+    __syncthreads();
+    uint64_t T = s_wmin[0];
+#pragma unroll
+    for (int w = 1; w < TK_THREADS / 64; ++w) T = s_wmin[w] < T ? s_wmin[w] : T;
+    const int nn = (int)min(a.per_group, a.n);
+    for (int i0 = 0; i0 < nn; i0 += TK_THREADS) {
+      const int i = i0 + tid;
+      const uint64_t key = i < nn ? make_key(a.scores[row * a.ld + i], (uint32_t)(a.idx_base + i), a.largest) : 0;
+      const bool win = i < nn && key > T;
+      const uint64_t bal = __ballot(win);
+      int base = 0;
+      if (lane == 0 && bal) base = atomicAdd(&s_fcnt, (int)__popcll(bal));
+      base = __shfl(base, 0);
+      if (win) s_keys[pk + base + (int)__popcll(bal & ((1ull << lane) - 1ull))] = key;
+    }
+    __syncthreads();
+    total = pk + s_fcnt;
+    if (tid == 0) s_real = total;
+  } else if (!FROM_KEYS) {
     const int64_t c0 = (int64_t)g * a.per_group;
     const int64_t nn = min(a.per_group, a.n - c0);
     const int pk = g == 0 ? (int)a.pk : 0;

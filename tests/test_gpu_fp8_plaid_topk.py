@@ -277,6 +277,28 @@ def test_topk_merge_bit_exact(largest, n, k, chunk):
     np.testing.assert_array_equal(run_s.cpu().numpy(), ws)
 
 
+@pytest.mark.parametrize("largest", [True, False])
+@pytest.mark.parametrize("n,k,chunk", [(5000, 100, 512), (3000, 7, 1), (9000, 1000, 2048), (4100, 64, 4096)])
+def test_topk_merge_chunks_in_reverse(largest, n, k, chunk):
+    """Chunks merged last-first: once the running list holds k entries, a
+    chunk's scores that tie the list's worst one carry lower doc indices and
+    must win the tie (the merge keeps only chunk keys above the list's worst
+    key); the result is still the stable top-k of the whole row."""
+    from late_interaction_kernels.topk import topk_update
+
+    _case(f"topk reverse {largest} {n} {k} {chunk}")
+    g = torch.Generator().manual_seed(n * 3 + k)
+    s = (torch.randint(0, 20, (5, n), generator=g).float() / 3.0)  # heavy ties
+    s[2, :] = 1.0
+    sc = s.cuda()
+    run_s = run_i = None
+    for st in reversed(range(0, n, chunk)):
+        run_s, run_i = topk_update(sc[:, st:st + chunk], st, run_s, run_i, k, largest)
+    ws, wi = O.topk_stable(s.numpy(), k, largest=largest)
+    np.testing.assert_array_equal(run_i.cpu().numpy(), wi)
+    np.testing.assert_array_equal(run_s.cpu().numpy(), ws)
+
+
 def test_topk_merge_entry_point():
     """lik_topk_merge keeps its one-workgroup-per-row contract (n <= 4096)."""
     from late_interaction_kernels import _lib
@@ -304,6 +326,41 @@ def test_topk_merge_entry_point():
         order = np.lexsort((all_i[r], -all_s[r]))[:80]
         np.testing.assert_array_equal(out_i[r].cpu().numpy(), all_i[r][order])
         np.testing.assert_array_equal(out_s[r].cpu().numpy(), all_s[r][order])
+
+
+@pytest.mark.parametrize("largest", [1, 0])
+def test_topk_merge_full_unsorted_list_aliased(largest):
+    """lik_topk_merge with a full running list (prev_k == k) given in no
+    particular order and aliased to the output: the merge keeps only chunk
+    scores that beat the list's worst entry (its minimum key, wherever it
+    sits), and writes over the list it read. Heavy ties between the list and
+    the chunk; list indices lie both below and above the chunk's."""
+    from late_interaction_kernels import _lib
+
+    _case(f"topk merge full unsorted aliased largest={largest}")
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(17 + largest)
+    k, n = 80, 4096
+    prev = torch.randint(0, 12, (4, k), generator=g).float()
+    # list indices below and above the chunk's 1000..5095, never inside it
+    pool = torch.cat([torch.arange(0, 1000), torch.arange(6000, 30000)])
+    prev_i = pool[torch.randperm(pool.numel(), generator=g)[: 4 * k]].reshape(4, k).to(torch.int64)
+    s = torch.randint(0, 12, (4, n), generator=g).float()
+    s[3] = 5.0  # a row of one value
+    base = 1000  # chunk indices 1000..5095 overlap the list's range
+    ps, pi, sc = prev.cuda(), prev_i.cuda(), s.cuda()
+    all_s = torch.cat([prev, s], -1).numpy()
+    all_i = torch.cat([prev_i, torch.arange(base, base + n).expand(4, n)], -1).numpy()
+    rc = lib.lik_topk_merge(sc.data_ptr(), 4, n, n, base, ps.data_ptr(), pi.data_ptr(), k, k, k, largest,
+                            ps.data_ptr(), pi.data_ptr(), k, _lib.stream_of(ps))
+    assert rc == _lib.LIK_OK
+    torch.cuda.synchronize()
+    sign = -1 if largest else 1
+    for r in range(4):
+        rs, ri = all_s[r], all_i[r]
+        order = np.lexsort((ri, sign * rs))[:k]
+        np.testing.assert_array_equal(pi[r].cpu().numpy(), ri[order])
+        np.testing.assert_array_equal(ps[r].cpu().numpy(), rs[order])
 
 
 def test_retrieve_matches_oracle_on_gpu_scores():

@@ -276,27 +276,57 @@ def test_non_contiguous_inputs():
     assert rel_err(_np(got), ref) < 1e-2
 
 
-def test_cuda_graph_capture_replay():
-    from late_interaction_kernels import maxsim
+@pytest.mark.parametrize("form", ["dense_normalize", "mask_with_holes", "kd_mask", "varlen"])
+def test_cuda_graph_capture_replay(form):
+    """Captured calls replay to the eager result, with eager work (other
+    shapes) between replays: the dense call, a doc mask with holes (mask
+    summary pre-pass, then the mask-free and the masked launch), the KD
+    layout with a mask (streaming kernel) and packed docs (with
+    max_seqlen_q / max_seqlen_d given: without them the call reads the longest
+    sequence back to the host, as the reference does)."""
+    from late_interaction_kernels import maxsim, maxsim_varlen
 
-    _case("graph")
+    _case(f"graph {form}")
     g = torch.Generator().manual_seed(4)
-    Q = _rand((8, 32, 128), torch.bfloat16, g)
-    D = _rand((64, 100, 128), torch.bfloat16, g)
-    eager = maxsim(Q, D, normalize=True)
+    if form == "varlen":
+        cu_q = torch.tensor([0, 32, 64, 96], dtype=torch.int32).cuda()
+        lens = torch.randint(1, 200, (50,), generator=g)
+        cu_d = torch.zeros(51, dtype=torch.int32)
+        cu_d[1:] = torch.cumsum(lens, 0)
+        cu_d = cu_d.cuda()
+        Qp = _rand((96, 128), torch.bfloat16, g)
+        Dp = _rand((int(cu_d[-1]), 128), torch.bfloat16, g)
+        # with the bounds given there is no host sync (the cover check is an async assert)
+        call = lambda: maxsim_varlen(Qp, Dp, cu_q, cu_d, max_seqlen_q=32, max_seqlen_d=200)
+    elif form == "kd_mask":
+        Q = _rand((8, 32, 128), torch.bfloat16, g)
+        D = _rand((8, 12, 90, 128), torch.bfloat16, g)
+        dm = (torch.arange(90)[None, None] < torch.randint(1, 91, (8, 12), generator=g)[..., None]).cuda()
+        call = lambda: maxsim(Q, D, d_mask=dm)
+    else:
+        Q = _rand((8, 32, 128), torch.bfloat16, g)
+        D = _rand((64, 100, 128), torch.bfloat16, g)
+        if form == "mask_with_holes":
+            dm = (torch.arange(100)[None] < torch.randint(1, 101, (64,), generator=g)[:, None])
+            dm[::5, 3] = False
+            dm = dm.cuda()
+            call = lambda: maxsim(Q, D, d_mask=dm)
+        else:
+            call = lambda: maxsim(Q, D, normalize=True)
+    eager = call()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        maxsim(Q, D, normalize=True)  # warm the allocator
+        call()  # warm the allocator
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out = maxsim(Q, D, normalize=True)
+        out = call()
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
-        _ = maxsim(Q[:2], D[:5], normalize=True)  # eager work between replays
+        _ = maxsim(_rand((2, 16, 128), torch.bfloat16, g), _rand((5, 40, 128), torch.bfloat16, g))
         torch.cuda.synchronize()
 
 

@@ -33,7 +33,9 @@
 // Calls with at most 64 query tokens (the inference case) run
 // head_persist_kernel below instead (the same arithmetic and partial maxima;
 // one persistent workgroup per CU streaming H and W into LDS by DMA), after
-// head_valid_kernel has written the token-validity words it reads.
+// head_valid_kernel has written the token-validity words it reads (with a
+// doc mask or lengths; without, the persistent kernel computes them from the
+// padded length).
 // head_finish_kernel: per (query i, doc j), the chunks in order, then the sum
 // over the query tokens in order: a fixed order, so the bits do not depend on
 // scheduling.
@@ -538,15 +540,27 @@ __global__ void __launch_bounds__(HP_THREADS) head_persist_kernel(const HeadPara
   };
   __syncthreads();  // s_q, s_bias
   reset_acc();
-  auto words_addr = [&](int k) -> const uint32_t* {  // this wavefront's words of item k (item 0 past the last)
+  // Validity words of this wavefront's 64 tokens of item k (item 0 past the
+  // last): loaded from head_valid_kernel's output, or, with no mask and no
+  // lengths (vwords null: every token before the doc's end is kept),
+  // computed from the padded length alone.
+  const bool has_words = vwords != nullptr;
+  auto words_addr = [&](int k) -> const uint32_t* {
     return vwords + (int64_t)(b0 + (k < nk ? k : 0) * G) * 8 + wave * 2;
   };
-  wnext = sload_u64(words_addr(0), 0);
+  auto words_of = [&](int k) -> uint64_t {
+    const int it = b0 + (k < nk ? k : 0) * G;
+    const int chunk = it - (it / p.nchunk) * p.nchunk;
+    const int n = p.ld - (chunk * HEAD_ROWS + wave * 64);  // tokens of the 64 inside the doc
+    return n >= 64 ? ~0ull : (n <= 0 ? 0ull : (1ull << n) - 1ull);
+  };
+  auto words = [&](int k) -> uint64_t { return has_words ? sload_u64(words_addr(k), 0) : words_of(k); };
+  wnext = words(0);
   set_h_item(0);
-  wnext = sload_u64(words_addr(hk + 1), 0);
+  wnext = words(hk + 1);
   issue_h(0);
   issue_w(0);
-  wnext = sload_u64(words_addr(hk + 1), 0);
+  wnext = words(hk + 1);
   issue_h(1);
   // this lane's fragment chunk offsets within 32 rows (row l32, chunk 4 h + kk;
   // (row >> 1) & 7 is (l32 >> 1) & 7 for every 32-row group), for H and W alike
@@ -561,14 +575,24 @@ __global__ void __launch_bounds__(HP_THREADS) head_persist_kernel(const HeadPara
   int k = 0, u = 0;
   const int NU = nk * nunit;
   for (int U = 0; U < NU; ++U) {
-    const uint64_t wa = (uint64_t)words_addr(hk + 1);
-    if (pend && stores) {
-      if (tid < p.ncol) *pdst = pval;
-      asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier"
-                   : "=&s"(wnext) : "s"(wa) : "memory");
+    if (has_words) {
+      const uint64_t wa = (uint64_t)words_addr(hk + 1);
+      if (pend && stores) {
+        if (tid < p.ncol) *pdst = pval;
+        asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier"
+                     : "=&s"(wnext) : "s"(wa) : "memory");
+      } else {
+        asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier"
+                     : "=&s"(wnext) : "s"(wa) : "memory");
+      }
     } else {
-      asm volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier"
-                   : "=&s"(wnext) : "s"(wa) : "memory");
+      if (pend && stores) {
+        if (tid < p.ncol) *pdst = pval;
+        asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+      wnext = words_of(hk + 1);
     }
     pend = false;
     issue_w(U + 1);
@@ -726,8 +750,15 @@ int launch_head(const HeadParams& p, uint32_t* vwords, hipStream_t s) {
       // token-validity words, then one persistent workgroup per CU
       const int64_t nitems = grid;
       if (nitems > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
-      hipLaunchKernelGGL(head_valid_kernel, dim3((unsigned)((nitems * 4 + 3) / 4)), dim3(256), 0, s, p, vwords, nitems);
-      if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+      // without a mask or lengths every token before the doc's end is kept:
+      // the persistent kernel computes those words itself
+      if (p.dmask || p.dlen) {
+        hipLaunchKernelGGL(head_valid_kernel, dim3((unsigned)((nitems * 4 + 3) / 4)), dim3(256), 0, s, p, vwords,
+                           nitems);
+        if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
+      } else {
+        vwords = nullptr;
+      }
       int dev = 0, ncu = 0;
       if (hipGetDevice(&dev) != hipSuccess ||
           hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)

@@ -122,6 +122,27 @@ def test_fused_forward_and_argmax(case, dtype, normalize):
     assert torch.equal(again[0], got[0]) and torch.equal(again[1], got[1])
 
 
+@pytest.mark.parametrize("case", CASES)
+def test_fused_forward_without_mask(case):
+    """No doc mask and no lengths: the persistent kernel computes the token
+    validity words from the padded length itself (no validity pre-pass), so
+    every token before Ld counts, including a last 256-token chunk that is
+    only partly inside the docs (Ld 300, 257, 255, 65, 1, 600, 100)."""
+    from late_interaction_kernels._core import from_hidden_forward
+
+    Nq, Lq, Nd, Ld, dmod, dout = case
+    _case(f"fused head fwd no mask {case}")
+    Q, H, W, b, _ = _inputs(Nq, Lq, Nd, Ld, dmod, dout, torch.bfloat16, sum(case) + 7, holes=False)
+    got = from_hidden_forward(Q.cuda(), H.cuda(), W.cuda(), b.cuda(), None, normalize=True, want_argmax=True)
+    assert got is not None, "the fused kernel must take this shape"
+    s, am = got
+    rs, ram, gap = _ref(Q, H, W, b, torch.ones(Nd, Ld, dtype=torch.bool), True)
+    assert rel_err(_np(s), rs.numpy()) < 2e-3
+    am = am.view(Nq, Nd, Lq).cpu()
+    sep = (gap > 2e-2) | (ram < 0)
+    assert torch.equal(am[sep], ram[sep])
+
+
 @pytest.mark.parametrize("bias", [True, False])
 @pytest.mark.parametrize("shape", [(2, 32, 10, 300, 768, 128), (1, 32, 40, 70, 384, 96)])
 def test_public_routes(shape, bias):

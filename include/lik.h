@@ -120,6 +120,7 @@ typedef struct {
 #define LIK_KD_LAYOUT 2u /* D holds n = Nq*K docs; query i scores docs [i*K, (i+1)*K) */
 #define LIK_NORMALIZE_Q 4u /* normalise query tokens only (docs already unit rows, e.g. decoded PLAID) */
 #define LIK_NORMALIZE_D 8u /* normalise doc tokens only (queries pre-normalised, e.g. a projection head) */
+#define LIK_BIAS_16 16u /* lik_maxsim_from_hidden: bias holds d_out values of Q's 16-bit dtype, not fp32 */
 
 /*
  * score[i, j] = out_scale * sum_{s valid in Q_i} max_{t valid in D_j} <Q_i[s], D_j[t]>
@@ -161,7 +162,9 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
  * Q: padded [Q->n, Q->len, d_out], already projected (and normalised by the
  * caller if wanted), no mask. H: padded [H->n, H->len, d_model] with its mask
  * and lengths marking the doc tokens that can win. W: [d_out, d_model] with
- * row stride w_stride elements; bias: fp32 [d_out] or NULL. bf16 / f16 (Q, H
+ * row stride w_stride elements; bias: fp32 [d_out], or with flag LIK_BIAS_16
+ * [d_out] in the Q / H dtype (widened to fp32 in the kernel, so the caller
+ * needs no conversion pass), or NULL. bf16 / f16 (Q, H
  * and W in one dtype); d_out <= 128; Q->n * Q->len <= 256; d_model, the H
  * strides and w_stride multiples of 8; H and W 16-byte aligned (other shapes:
  * LIK_ERR_UNSUPPORTED, and the caller projects first). argmax (optional)
@@ -171,7 +174,7 @@ int lik_maxsim_argmax(const lik_seqs_t* Q, const lik_seqs_t* D, uint32_t flags, 
  * launching _fused_head_fwd_kernel (fused_head.py:46-189).
  */
 int lik_maxsim_from_hidden(const lik_seqs_t* Q, const lik_seqs_t* H, const void* W, int64_t w_stride,
-                           const float* bias, uint32_t flags, float* out, int64_t out_stride_q,
+                           const void* bias, uint32_t flags, float* out, int64_t out_stride_q,
                            int64_t out_stride_d, int32_t* argmax, void* workspace, size_t workspace_bytes,
                            lik_stream_t stream);
 size_t lik_maxsim_from_hidden_workspace_size(const lik_seqs_t* Q, const lik_seqs_t* H);

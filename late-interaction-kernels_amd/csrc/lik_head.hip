@@ -61,7 +61,8 @@ struct HeadParams {
   int64_t h_sn, h_sl;
   const char* w;  // W rows: w + o * w_sl (bytes)
   int64_t w_sl;
-  const float* bias;  // [d_out] or null
+  const float* bias;       // [d_out] fp32, or null
+  const uint16_t* bias16;  // [d_out] in the Q / H dtype (LIK_BIAS_16), or null
   const int8_t* dmask;  // keep flags, or null
   int64_t dm_sn, dm_sl;
   const int32_t* dlen;  // doc lengths, or null
@@ -77,6 +78,15 @@ constexpr uint32_t kHeadOOB = 0xffffffffu;  // buffer offset past num_records: t
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void* base, uint32_t nbytes) {
   // dword3 0x00020000: raw (untyped) access, stride 0, byte range check
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
+}
+
+// output dim o's bias as fp32 (0 past d_out or without a bias)
+template <int EK>
+__device__ __forceinline__ float head_bias(const HeadParams& p, int o) {
+  if (o >= p.dout) return 0.f;
+  if (p.bias) return p.bias[o];
+  if (p.bias16) return EK == EK_F16 ? f16_to_f32(p.bias16[o]) : bf16lo_to_f32(p.bias16[o]);
+  return 0.f;
 }
 
 template <int EK>
@@ -125,7 +135,7 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_tile_kernel(const HeadParam
     }
     s_q[f] = v;
   }
-  if (tid < 32 * NB) s_bias[tid] = (p.bias && tid < p.dout) ? p.bias[tid] : 0.f;
+  if (tid < 32 * NB) s_bias[tid] = head_bias<EK>(p, tid);
 
   // this lane's doc token and whether it takes part (in the doc, kept)
   const int t = chunk * HEAD_ROWS + wave * 32 + l32;
@@ -407,7 +417,7 @@ __global__ void __launch_bounds__(HP_THREADS) head_persist_kernel(const HeadPara
     }
     s_q[f] = v;
   }
-  if (tid < 32 * NB) s_bias[tid] = (p.bias && tid < p.dout) ? p.bias[tid] : 0.f;
+  if (tid < 32 * NB) s_bias[tid] = head_bias<EK>(p, tid);
 
   auto desc = [](const void* base, uint32_t nbytes) -> u32x4 {
     const uint64_t b = (uint64_t)base;
@@ -831,12 +841,12 @@ size_t lik_maxsim_from_hidden_workspace_size(const lik_seqs_t* Q, const lik_seqs
 }
 
 int lik_maxsim_from_hidden(const lik_seqs_t* Q, const lik_seqs_t* H, const void* W, int64_t w_stride,
-                           const float* bias, uint32_t flags, float* out, int64_t out_stride_q,
+                           const void* bias, uint32_t flags, float* out, int64_t out_stride_q,
                            int64_t out_stride_d, int32_t* argmax, void* workspace, size_t workspace_bytes,
                            lik_stream_t stream) {
   int rc = head_check(Q, H, W, w_stride);
   if (rc != LIK_OK) return rc;
-  if (flags & ~(uint32_t)LIK_NORMALIZE_D) return LIK_ERR_INVALID;
+  if (flags & ~(uint32_t)(LIK_NORMALIZE_D | LIK_BIAS_16)) return LIK_ERR_INVALID;
   if (Q->n == 0 || H->n == 0) return LIK_OK;
   if (!out || !Q->data || (!H->data && H->len > 0) || !W) return LIK_ERR_INVALID;
   const size_t need = lik_maxsim_from_hidden_workspace_size(Q, H);
@@ -850,7 +860,8 @@ int lik_maxsim_from_hidden(const lik_seqs_t* Q, const lik_seqs_t* H, const void*
   p.h_sl = H->stride_l * 2;
   p.w = (const char*)W;
   p.w_sl = w_stride * 2;
-  p.bias = bias;
+  p.bias = (flags & LIK_BIAS_16) ? nullptr : (const float*)bias;
+  p.bias16 = (flags & LIK_BIAS_16) ? (const uint16_t*)bias : nullptr;
   p.dmask = H->mask;
   p.dm_sn = H->mask_stride_n;
   p.dm_sl = H->mask_stride_l;

@@ -395,7 +395,9 @@ def from_hidden_forward(Q, H, W, b, d_mask, *, normalize: bool, want_argmax: boo
     if Hc.stride(-1) != 1 or Hc.data_ptr() % 16 or any(s % 8 for s in Hc.stride()[:-1]):
         Hc = Hc.contiguous()
     Wc = W.detach().contiguous()
-    bias = None if b is None else b.detach().to(torch.float32).contiguous()
+    # a bias in the inputs' 16-bit dtype is read and widened by the kernel
+    bias16 = b is not None and b.dtype == Q.dtype
+    bias = None if b is None else (b.detach().contiguous() if bias16 else b.detach().to(torch.float32).contiguous())
     dm = _mask_i8(d_mask, (Nd, Ld))
     qs = _lib.seqs(Qc, n=Nq, length=Lq, stride_n=Qc.stride(0), stride_l=Qc.stride(1))
     hs = _lib.seqs(Hc, n=Nd, length=Ld, stride_n=Hc.stride(0), stride_l=Hc.stride(1), mask=dm,
@@ -403,7 +405,7 @@ def from_hidden_forward(Q, H, W, b, d_mask, *, normalize: bool, want_argmax: boo
     lib = _lib.load()
     nbytes = lib.lik_maxsim_from_hidden_workspace_size(ctypes.byref(qs), ctypes.byref(hs))
     ws = _lib.workspace(nbytes, Q.device)
-    flags = _lib.LIK_NORMALIZE_D if normalize else 0
+    flags = (_lib.LIK_NORMALIZE_D if normalize else 0) | (_lib.LIK_BIAS_16 if bias16 else 0)
     with torch.cuda.device(Q.device):
         rc = lib.lik_maxsim_from_hidden(ctypes.byref(qs), ctypes.byref(hs), Wc.data_ptr(), Wc.stride(0),
                                         _lib.ptr(bias), flags, out.data_ptr(), out.stride(0), out.stride(1),

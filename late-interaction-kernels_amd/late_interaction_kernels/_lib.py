@@ -29,6 +29,7 @@ LIK_NORMALIZE = 1
 LIK_KD_LAYOUT = 2
 LIK_NORMALIZE_Q = 4
 LIK_NORMALIZE_D = 8
+LIK_BIAS_16 = 16
 
 
 def norm_flags(norm: int) -> int:

@@ -143,6 +143,28 @@ def test_fused_forward_without_mask(case):
     assert torch.equal(am[sep], ram[sep])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1, 32, 12, 300, 768, 128), (3, 20, 9, 130, 384, 96)])
+def test_bias_in_input_dtype(shape, dtype):
+    """A bias in the inputs' 16-bit dtype goes to the kernel as is
+    (LIK_BIAS_16, widened in the kernel); an fp32 bias goes as fp32. The fp32
+    copy of a 16-bit bias holds the same values, so both calls give the same
+    bits. Unknown flag bits are still rejected."""
+    from late_interaction_kernels import _lib
+    from late_interaction_kernels._core import from_hidden_forward
+
+    Nq, Lq, Nd, Ld, dmod, dout = shape
+    _case(f"fused head bias dtype {shape} {dtype}")
+    Q, H, W, b, dm = _inputs(Nq, Lq, Nd, Ld, dmod, dout, dtype, sum(shape) + 3)
+    args = (Q.cuda(), H.cuda(), W.cuda())
+    s16, a16 = from_hidden_forward(*args, b.cuda(), dm.cuda(), normalize=True, want_argmax=True)
+    s32, a32 = from_hidden_forward(*args, b.float().cuda(), dm.cuda(), normalize=True, want_argmax=True)
+    assert torch.equal(s16, s32) and torch.equal(a16, a32)
+    rs, _, _ = _ref(Q, H, W, b, dm, True)
+    assert rel_err(_np(s16), rs.numpy()) < 2e-3
+    assert _lib.LIK_BIAS_16 == 16
+
+
 @pytest.mark.parametrize("bias", [True, False])
 @pytest.mark.parametrize("shape", [(2, 32, 10, 300, 768, 128), (1, 32, 40, 70, 384, 96)])
 def test_public_routes(shape, bias):
@@ -252,7 +274,7 @@ def test_c_abi_checks():
     assert rc == _lib.LIK_ERR_WORKSPACE
     rc = lib.lik_maxsim_from_hidden(ctypes.byref(qs2), ctypes.byref(hs), W2.data_ptr(), 64, None, 4, out.data_ptr(), 2,
                                     1, None, None, 0, _lib.stream_of(out))
-    assert rc == _lib.LIK_ERR_INVALID  # only LIK_NORMALIZE_D
+    assert rc == _lib.LIK_ERR_INVALID  # only LIK_NORMALIZE_D and LIK_BIAS_16
     qs0 = _lib.seqs(Q2, n=0, length=32, stride_n=Q2.stride(0), stride_l=Q2.stride(1))
     rc = lib.lik_maxsim_from_hidden(ctypes.byref(qs0), ctypes.byref(hs), W2.data_ptr(), 64, None, 0, out.data_ptr(), 2,
                                     1, None, None, 0, _lib.stream_of(out))

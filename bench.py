@@ -12,8 +12,10 @@ The default run also measures the rest of BASELINE.json's metric and puts it
 under ``parts`` in the same JSON line: ``kd`` (C2's KD layout, K steps),
 ``varlen`` (C3, K steps), ``fp8`` (C4 ColPali, K steps),
 ``plaid`` (C5 retrieve top-100 over 1M compressed docs, 1,024 queries,
-``--plaid-steps`` steps) and ``plaid_q1`` (the same corpus at one query, the
-HBM-bound case), each with its own roofline. ``--no-parts`` skips them.
+``--plaid-steps`` steps), ``plaid_q1`` / ``plaid_q1_prepared`` (the same corpus at
+one query, the HBM-bound case) and ``head`` (the fused projection head of
+``maxsim_from_hidden`` on the reference's largest fused-head shape, at least
+100 warmup calls), each with its own roofline. ``--no-parts`` skips them.
 
 Other workloads (``--workload``): ``kd`` (D_kd[512, 64, 300, 128], HBM-bound),
 ``varlen`` (65,536 packed docs, log-uniform [16, 2048] tokens, 256 queries),
@@ -961,16 +963,19 @@ def main() -> None:
     if args.workload == "inbatch" and args.parts:
         # The rest of BASELINE.json's metric, each on its own config and with
         # its own roofline: C2's KD layout (HBM), C3 varlen TFLOP/s, C4 fp8
-        # TFLOP/s, C5 PLAID retrieve queries/s at top-100, and the PLAID
-        # kernels' HBM rate at Nq = 1.
+        # TFLOP/s, C5 PLAID retrieve queries/s at top-100, the PLAID
+        # kernels' HBM rate at Nq = 1, and the fused projection head's HBM rate.
         parts = {}
         for name, fn, steps in (("kd", wl_kd, args.steps), ("varlen", wl_varlen, args.steps),
                                 ("fp8", wl_fp8, args.steps), ("plaid", wl_plaid, args.plaid_steps),
                                 ("plaid_q1", wl_plaid_q1, args.steps),
-                                ("plaid_q1_prepared", wl_plaid_q1_prepared, args.steps)):
+                                ("plaid_q1_prepared", wl_plaid_q1_prepared, args.steps),
+                                ("head", wl_head, args.steps)):
             torch.cuda.empty_cache()
             sub = argparse.Namespace(**vars(args))
             sub.steps, sub.warmup = steps, min(args.warmup, 2) if name == "plaid" else args.warmup
+            if name == "head":
+                sub.warmup = max(args.warmup, HEAD_MIN_WARMUP)
             r = fn(sub)
             parts[name] = {"metric": r["metric"], "value": r["value"], "unit": r["unit"], "dtype": r["dtype"],
                            "steps": sub.steps, "warmup": sub.warmup, "ms_per_step": r["ms_per_step"],

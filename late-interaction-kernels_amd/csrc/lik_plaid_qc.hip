@@ -486,9 +486,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
 // stream lands in registers with plain buffer loads and no LDS staging:
 //   lane (l32, h) of tile t loads token l32's code, its residual bytes of
 //   half h (16 B at d = 128, nbits = 2), its inverse norm, and 32 bytes of
-//   its centroid's table row: the 16 query slots of half h, which the table
-//   stores contiguously (query token s at slot 16 ((s >> 2) & 1) +
-//   4 (s >> 3) + (s & 3), the accumulator order of element e of that half).
+//   table rows: the table stores the 16 query slots of half h contiguously
+//   (query token s at slot 16 ((s >> 2) & 1) + 4 (s >> 3) + (s & 3), the
+//   accumulator order of element e of that half), and the lane reads 16 of
+//   them from each of the rows of tokens l32 % 16 and l32 % 16 + 16, so that
+//   the four lanes reading one row in a load sit in one 64-byte request;
+//   v_permlane16_swap then hands each lane its own token's 32 bytes.
 // The accumulator element e of lane (l32, h) is query token
 // 8 (e / 4) + 4 h + e % 4 against doc token l32; the query rows are
 // normalised before they are rounded, so the epilogue is
@@ -504,9 +507,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
 // Measured against the LDS-staged kernel on the C5 corpus at Nq = 1: 2.57
 // against 2.70 ms. What bounds it (counters): the texture address and data
 // units (TA busy 0.92, TD 0.95), i.e. the five vector memory instructions per
-// tile, two of them 64 random 32-byte table reads; with every table read
-// pointed at one row (timing only) the scan takes 2.02 ms, with the texture
-// data unit still busy 0.94 of the cycles. Tried: the streamed bytes through
+// tile, two of them random table reads; with every table read pointed at one
+// row (timing only) the scan takes 2.02 ms, with the texture data unit still
+// busy 0.94 of the cycles. Table reads of 16 rows per load, four lanes per
+// row (above), instead of 32 rows, two lanes per row: 2.57 -> 2.40 ms. Tried: the streamed bytes through
 // an 8-tile LDS ring (buffer_load ... lds, 2.6x the bytes in flight, 128
 // VGPRs): 2.60 ms, and the same at four waves per SIMD with 6 tiles: 2.75 ms;
 // so latency is not the bound. Codes and inverse norms loaded by 32 lanes
@@ -687,10 +691,28 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
                    "buffer_load_dword %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
                    : "+v"(s.inv), "=&s"(ex) : "v"((uint32_t)l32 * 4u), "s"(di));
     }
-    const uint32_t row = cd < (uint32_t)p.pl.ncent ? cd : 0u;
-    const uint32_t toff = row * 64u + (uint32_t)h * 32u;
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(s.tq[0]) : "v"(toff), "s"(dtab));
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen offset:16" : "+v"(s.tq[1]) : "v"(toff), "s"(dtab));
+    // table rows of tokens l32 % 16 (tq[0]) and l32 % 16 + 16 (tq[1]), 16
+    // bytes each at quarter lane / 16 of the row, so four lanes read each row
+    // of a load (16 rows per load instead of 32); unswap_table gives every
+    // lane its own token's 32 bytes
+    const auto cs = __builtin_amdgcn_permlane16_swap(cd, cd, false, false);
+    const uint32_t qoff = (uint32_t)(lane >> 4) * 16u;
+    const uint32_t ta = (cs[0] < (uint32_t)p.pl.ncent ? cs[0] : 0u) * 64u + qoff;
+    const uint32_t tb = (cs[1] < (uint32_t)p.pl.ncent ? cs[1] : 0u) * 64u + qoff;
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(s.tq[0]) : "v"(ta), "s"(dtab));
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(s.tq[1]) : "v"(tb), "s"(dtab));
+  };
+  // Lane (l32, h) holds, of tokens l32 % 16 and l32 % 16 + 16, table quarter
+  // 2 h + l32 / 16; one v_permlane16_swap per dword (odd rows of tq[0] with
+  // even rows of tq[1]) leaves it quarters 2 h and 2 h + 1 of token l32: the
+  // 16 values of its half, in element order.
+  auto unswap_table = [](Stage& s) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const auto sw = __builtin_amdgcn_permlane16_swap(s.tq[0][k], s.tq[1][k], false, false);
+      s.tq[0][k] = sw[0];
+      s.tq[1][k] = sw[1];
+    }
   };
   // wait until at most n loads are in flight, for the registers of stage s
   auto wait_stage = [](auto NN, Stage& s) {
@@ -838,6 +860,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     {
       Stage cur = st[I % LS];
       cur.inv = __uint_as_float(bcast(__float_as_uint(cur.inv)));
+      unswap_table(cur);
       compute(c, cur);
     }
     // ordering point: the stage's previous contents are all read (they feed m)

@@ -121,6 +121,7 @@ typedef struct {
 #define LIK_NORMALIZE_Q 4u /* normalise query tokens only (docs already unit rows, e.g. decoded PLAID) */
 #define LIK_NORMALIZE_D 8u /* normalise doc tokens only (queries pre-normalised, e.g. a projection head) */
 #define LIK_BIAS_16 16u /* lik_maxsim_from_hidden: bias holds d_out values of Q's 16-bit dtype, not fp32 */
+#define LIK_TOKEN_RECORDS 32u /* lik_plaid_maxsim_qc: token_inv points at lik_plaid_token_t records */
 
 /*
  * score[i, j] = out_scale * sum_{s valid in Q_i} max_{t valid in D_j} <Q_i[s], D_j[t]>
@@ -305,6 +306,25 @@ int lik_plaid_token_norms(const lik_plaid_docs_t* docs, int64_t tok_begin, int64
                           lik_stream_t stream);
 
 /*
+ * A prepared token: its code (docs->codes[tok], as stored) and its inverse
+ * norm (as lik_plaid_token_norms computes it). 8 bytes, 8-byte aligned.
+ */
+typedef struct {
+  int32_t code;
+  float inv;
+} lik_plaid_token_t;
+
+/*
+ * The records of tokens [tok_begin, tok_end) (rec indexed by absolute token,
+ * 8-byte aligned). With LIK_TOKEN_RECORDS, lik_plaid_maxsim_qc reads a
+ * token's code and norm from its record with one load instead of two (the
+ * scan is bound by its load instructions; the bytes read are the same). No
+ * counterpart in the reference (as lik_plaid_token_norms).
+ */
+int lik_plaid_token_records(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end, lik_plaid_token_t* rec,
+                            lik_stream_t stream);
+
+/*
  * Few-query PLAID scoring from centroid scores (up to 64 queries of <= 32
  * tokens, bf16 / f16 query and centroids of the same type, d <= 128): the
  * same scores as lik_plaid_maxsim (plaid.py:832-963; within bf16 rounding:
@@ -312,7 +332,9 @@ int lik_plaid_token_norms(const lik_plaid_docs_t* docs, int64_t tok_begin, int64
  * on bucket weights rounded to the query type, both divided by the token's
  * precomputed norm). token_inv (from lik_plaid_token_norms) is required when
  * flags normalise the docs (LIK_NORMALIZE / LIK_NORMALIZE_D) and ignored
- * otherwise. Docs must be packed (docs->cu_seqlens; a lengths-only layout
+ * otherwise; with LIK_TOKEN_RECORDS it is required and points at the
+ * lik_plaid_token_t records of every token (lik_plaid_token_records, from
+ * the same docs), which then supply the codes as well as the norms. Docs must be packed (docs->cu_seqlens; a lengths-only layout
  * returns LIK_ERR_UNSUPPORTED). The workspace holds the [Q->n, n_centroids,
  * 32] fp16 table (lik_plaid_maxsim_qc_workspace_size bytes): the caller
  * keeps |q.c| below fp16's 65504 (the Python layer routes larger query or

@@ -27,7 +27,8 @@ __global__ void __launch_bounds__(256)
     plaid_decode_kernel(const int32_t* __restrict__ codes, const uint8_t* __restrict__ res, int64_t res_st,
                         const char* __restrict__ cent, int64_t cent_sb, int64_t ncent,
                         const float* __restrict__ bw, int nb, int nbits, int dim, int normalize,
-                        uint16_t* __restrict__ out, int64_t out_stride, int64_t ntok, float* __restrict__ inv_out) {
+                        uint16_t* __restrict__ out, int64_t out_stride, int64_t ntok, float* __restrict__ inv_out,
+                        int rec) {
   constexpr int TPB = 256 / LPT;  // tokens per workgroup
   constexpr int CSZ = CD == EK_F32 ? 4 : 2;
   __shared__ float s_bw[256];
@@ -71,9 +72,15 @@ __global__ void __launch_bounds__(256)
   for (int e = 0; e < 8; ++e) ss = fmaf(x8[e], x8[e], ss);
 #pragma unroll
   for (int o = 1; o < LPT; o <<= 1) ss += __shfl_xor(ss, o);
-  // norms-only mode (out == null): the token's inverse norm, 1 / max(||x||, 1e-12)
+  // norms-only mode (out == null): the token's inverse norm, 1 / max(||x||, 1e-12),
+  // alone or after the token's code as an 8-byte (code, norm) record
   if (inv_out) {
-    if (tok_ok && cc == 0) inv_out[tok] = inv_norm(ss);
+    if (tok_ok && cc == 0) {
+      if (rec)
+        *(uint2*)(inv_out + 2 * tok) = uint2{(uint32_t)codes[tok], __float_as_uint(inv_norm(ss))};
+      else
+        inv_out[tok] = inv_norm(ss);
+    }
     return;
   }
   const float sc = normalize ? inv_norm(ss) : 1.f;
@@ -92,28 +99,28 @@ __global__ void __launch_bounds__(256)
 
 template <int LPT, int CD>
 int launch_decode_cd(int outk, const lik_plaid_docs_t* d, const int32_t* codes, const uint8_t* res, int norm,
-                     uint16_t* out, int64_t out_stride, int64_t ntok, float* inv_out, hipStream_t s) {
+                     uint16_t* out, int64_t out_stride, int64_t ntok, float* inv_out, int rec, hipStream_t s) {
   constexpr int TPB = 256 / LPT;
   const int ceb = CD == EK_F32 ? 4 : 2;
   const dim3 grid((unsigned)((ntok + TPB - 1) / TPB));
   if (outk == EK_F16)
     hipLaunchKernelGGL((plaid_decode_kernel<LPT, CD, EK_F16>), grid, dim3(256), 0, s, codes, res, d->res_stride_tok,
                        (const char*)d->centroids, d->cent_stride * ceb, d->n_centroids, d->bucket_weights,
-                       d->n_buckets, d->nbits, d->dim, norm, out, out_stride, ntok, inv_out);
+                       d->n_buckets, d->nbits, d->dim, norm, out, out_stride, ntok, inv_out, rec);
   else
     hipLaunchKernelGGL((plaid_decode_kernel<LPT, CD, EK_BF16>), grid, dim3(256), 0, s, codes, res, d->res_stride_tok,
                        (const char*)d->centroids, d->cent_stride * ceb, d->n_centroids, d->bucket_weights,
-                       d->n_buckets, d->nbits, d->dim, norm, out, out_stride, ntok, inv_out);
+                       d->n_buckets, d->nbits, d->dim, norm, out, out_stride, ntok, inv_out, rec);
   return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
 }
 
 template <int LPT>
 int launch_decode(int outk, const lik_plaid_docs_t* d, const int32_t* codes, const uint8_t* res, int norm,
-                  uint16_t* out, int64_t out_stride, int64_t ntok, float* inv_out, hipStream_t s) {
+                  uint16_t* out, int64_t out_stride, int64_t ntok, float* inv_out, hipStream_t s, int rec = 0) {
   switch (d->centroid_dtype) {
-    case LIK_BF16: return launch_decode_cd<LPT, EK_BF16>(outk, d, codes, res, norm, out, out_stride, ntok, inv_out, s);
-    case LIK_F16: return launch_decode_cd<LPT, EK_F16>(outk, d, codes, res, norm, out, out_stride, ntok, inv_out, s);
-    case LIK_F32: return launch_decode_cd<LPT, EK_F32>(outk, d, codes, res, norm, out, out_stride, ntok, inv_out, s);
+    case LIK_BF16: return launch_decode_cd<LPT, EK_BF16>(outk, d, codes, res, norm, out, out_stride, ntok, inv_out, rec, s);
+    case LIK_F16: return launch_decode_cd<LPT, EK_F16>(outk, d, codes, res, norm, out, out_stride, ntok, inv_out, rec, s);
+    case LIK_F32: return launch_decode_cd<LPT, EK_F32>(outk, d, codes, res, norm, out, out_stride, ntok, inv_out, rec, s);
     default: return LIK_ERR_UNSUPPORTED;
   }
 }
@@ -175,8 +182,12 @@ extern "C" int lik_plaid_decode(const lik_plaid_docs_t* docs, int64_t tok_begin,
   return LIK_ERR_UNSUPPORTED;
 }
 
-extern "C" int lik_plaid_token_norms(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end, float* inv,
-                                     lik_stream_t stream) {
+namespace {
+// inverse norms (rec = 0: 4 bytes per token) or (code, inverse norm) records
+// (rec = 1: 8 bytes per token) of tokens [tok_begin, tok_end), indexed by
+// absolute token
+int token_norms(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end, float* inv, int rec,
+                lik_stream_t stream) {
   if (!docs || tok_begin < 0 || tok_end < tok_begin) return LIK_ERR_INVALID;
   if (docs->nbits != 2 && docs->nbits != 4 && docs->nbits != 8) return LIK_ERR_INVALID;
   if (docs->dim <= 0 || docs->dim % 8 != 0) return LIK_ERR_INVALID;
@@ -191,10 +202,23 @@ extern "C" int lik_plaid_token_norms(const lik_plaid_docs_t* docs, int64_t tok_b
   if (ntok > (int64_t)0x7fffffff * 8) return LIK_ERR_UNSUPPORTED;
   const int32_t* codes = docs->codes + tok_begin;
   const uint8_t* res = docs->residuals + tok_begin * docs->res_stride_tok;
-  float* o = inv + tok_begin;
+  if (rec && ((uintptr_t)inv) % 8) return LIK_ERR_UNSUPPORTED;
+  // (the kernel indexes its output from the range's first token)
+  float* o = inv + (rec ? 2 : 1) * tok_begin;
   hipStream_t s = (hipStream_t)stream;
-  if (docs->dim <= 64) return launch_decode<8>(EK_BF16, docs, codes, res, 1, nullptr, 0, ntok, o, s);
-  if (docs->dim <= 128) return launch_decode<16>(EK_BF16, docs, codes, res, 1, nullptr, 0, ntok, o, s);
-  if (docs->dim <= 256) return launch_decode<32>(EK_BF16, docs, codes, res, 1, nullptr, 0, ntok, o, s);
+  if (docs->dim <= 64) return launch_decode<8>(EK_BF16, docs, codes, res, 1, nullptr, 0, ntok, o, s, rec);
+  if (docs->dim <= 128) return launch_decode<16>(EK_BF16, docs, codes, res, 1, nullptr, 0, ntok, o, s, rec);
+  if (docs->dim <= 256) return launch_decode<32>(EK_BF16, docs, codes, res, 1, nullptr, 0, ntok, o, s, rec);
   return LIK_ERR_UNSUPPORTED;
+}
+}  // namespace
+
+extern "C" int lik_plaid_token_norms(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end, float* inv,
+                                     lik_stream_t stream) {
+  return token_norms(docs, tok_begin, tok_end, inv, 0, stream);
+}
+
+extern "C" int lik_plaid_token_records(const lik_plaid_docs_t* docs, int64_t tok_begin, int64_t tok_end,
+                                       lik_plaid_token_t* rec, lik_stream_t stream) {
+  return token_norms(docs, tok_begin, tok_end, (float*)rec, 1, stream);
 }

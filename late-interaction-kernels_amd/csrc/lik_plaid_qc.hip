@@ -90,9 +90,12 @@ __global__ void __launch_bounds__(256) centroid_scores_kernel(const Params p, ui
   }
 }
 
+// tinv: inverse norms (ist = 4 bytes per token), or (code, inverse norm)
+// records (ist = 8; the codes are still read from p.pl.codes), or null.
 template <int EK, int DPAD, int NBITS, int QN, bool FULLD>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1 ? 2 : 4)))
-    plaid_qc_kernel(const Params p, const uint16_t* __restrict__ qc, int64_t qc_qs, const float* __restrict__ tinv) {
+    plaid_qc_kernel(const Params p, const uint16_t* __restrict__ qc, int64_t qc_qs, const float* __restrict__ tinv,
+                    int ist) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;
   constexpr int HALF = DPAD / 2;
@@ -104,7 +107,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   constexpr int QCT = 32 * 64;                     // table rows of one query per tile
   constexpr int RES0 = QN * QCT;                   // stage offsets
   constexpr int INV0 = RES0 + NRI * 1024;
-  constexpr int STB = INV0 + 128;
+  constexpr int STB = INV0 + 256;  // norms: 32 floats, or 32 records' (4-byte shifted)
   // vector memory instructions issued per iteration: the gather (table rows,
   // residual bytes, norms: G) and one code load, all loads into LDS, which
   // return in issue order, so a fixed count identifies the tile in flight
@@ -248,7 +251,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   };
   const char* code_p = (const char*)(p.pl.codes + T0);  // tile 0
   const char* res_p = (const char*)p.pl.res + (int64_t)T0 * p.pl.res_st;
-  const char* inv_p = (const char*)(tinv ? tinv + T0 : nullptr);
+  // a record's norm is its second word: the norms' stream starts 4 bytes in
+  const char* inv_p = tinv ? (const char*)tinv + (int64_t)T0 * ist + (ist == 8 ? 4 : 0) : nullptr;
+  const int inv_tile = 32 * ist;
   const int64_t res_tile = 32 * p.pl.res_st;
   // codes of tile i (at code_p) into code slot `slot` (lanes 0..7, 16 bytes each)
   auto code_dma = [&](int i, int slot, const char* cp) {
@@ -276,8 +281,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
     const u32x4 dres = rsrc_words(rp, (uint32_t)nv * (uint32_t)p.pl.res_st);
 #pragma unroll
     for (int k = 0; k < NRI; ++k) dma_nt(st_lds[stage] + (uint32_t)(RES0 + k * 1024), (uint32_t)(k * 1024 + lane * 16), dres);
-    const u32x4 dinv = rsrc_words(ip ? (const void*)ip : (const void*)p.pl.res, ip ? (uint32_t)nv * 4u : 0u);
-    if (lane < 8) dma_nt(st_lds[stage] + (uint32_t)INV0, (uint32_t)(lane * 16), dinv);
+    // norms (records: every other word, from 4 bytes in, so the byte count
+    // stops at the last row's norm and nothing past the array is read)
+    const uint32_t inb = nv == 0 ? 0u : (uint32_t)(nv * ist - (ist == 8 ? 4 : 0));
+    const u32x4 dinv = rsrc_words(ip ? (const void*)ip : (const void*)p.pl.res, ip ? inb : 0u);
+    if (lane < 2 * ist) dma_nt(st_lds[stage] + (uint32_t)INV0, (uint32_t)(lane * 16), dinv);
   };
 
   float m[QN];
@@ -315,8 +323,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
       }
     }
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-      rg.inv[jj] = decltype(NORMD)::value ? *(const f32x4*)(st + INV0 + (8 * jj + 4 * h) * 4) : (f32x4){1.f, 1.f, 1.f, 1.f};
+    for (int jj = 0; jj < 4; ++jj) {
+      constexpr int NM = decltype(NORMD)::value;  // 0: none, 1: norms, 2: records
+      if constexpr (NM == 2) {
+        const f32x4 a = *(const f32x4*)(st + INV0 + (8 * jj + 4 * h) * 8);
+        const f32x4 b = *(const f32x4*)(st + INV0 + (8 * jj + 4 * h) * 8 + 16);
+        rg.inv[jj] = (f32x4){a[0], a[2], b[0], b[2]};
+      } else {
+        rg.inv[jj] = NM ? *(const f32x4*)(st + INV0 + (8 * jj + 4 * h) * 4) : (f32x4){1.f, 1.f, 1.f, 1.f};
+      }
+    }
 #pragma unroll
     for (int sub = 0; sub < QN; ++sub)
 #pragma unroll
@@ -442,13 +458,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   gather(0, 0, 0, res_p, inv_p);
   code_dma(2, 2, code_p + 256);
-  gather(1, 1, 1, res_p + res_tile, inv_p ? inv_p + 128 : nullptr);
+  gather(1, 1, 1, res_p + res_tile, inv_p ? inv_p + inv_tile : nullptr);
   code_dma(3, 3, code_p + 384);
   // (two copies of the loop: with and without token inverse norms)
   auto scan = [&](auto NORMD) {
     const char* cp = code_p + 512;                 // tile c + 4
     const char* rp = res_p + 2 * res_tile;         // tile c + 2
-    const char* ip = NORMD ? inv_p + 256 : nullptr;
+    const char* ip = NORMD ? inv_p + 2 * inv_tile : nullptr;
     for (int c = 0; c < ntile; ++c) {
       asm volatile("s_waitcnt vmcnt(%0)" : : "n"(G + 1) : "memory");
       const int stage = c & 1;
@@ -459,13 +475,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
       compute(c, rg);
       cp += 128;
       rp += res_tile;
-      if (NORMD) ip += 128;
+      if (NORMD) ip += inv_tile;
     }
   };
-  if (tinv)
-    scan(std::true_type{});
+  if (tinv && ist == 8)
+    scan(std::integral_constant<int, 2>{});
+  else if (tinv)
+    scan(std::integral_constant<int, 1>{});
   else
-    scan(std::false_type{});
+    scan(std::integral_constant<int, 0>{});
   // docs left (empty docs at the range's end, or an empty range)
   while (jc < nd) doc_end();
   // no gather may still be writing this wave's LDS when it exits
@@ -529,7 +547,9 @@ __device__ __forceinline__ bool scan_steps(F& f, int c, int n) {
 }
 
 // LS tiles in flight per wavefront: 3 at three waves per SIMD, 2 at four.
-template <int EK, int DPAD, int NBITS, bool FULLD, bool NORMD, int LS>
+// REC: tinv points at (code, inverse norm) records of 8 bytes per token
+// (lik_plaid_token_t), read in place of the codes and the norms by one load.
+template <int EK, int DPAD, int NBITS, bool FULLD, bool NORMD, int LS, bool REC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 2 ? 4 : 3)))
     plaid_scan_kernel(const Params p, const uint16_t* __restrict__ qc, int64_t qc_qs, const float* __restrict__ tinv) {
   using T = KT<EK, DPAD>;
@@ -607,9 +627,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   const int span = __builtin_amdgcn_readfirstlane(s_cu[wl][nd]) - T0;
   const int ntile = (span + 31) >> 5;
 
-  const int32_t* code_p = p.pl.codes + T0;
+  // codes (4 bytes per token), or records (8 bytes: code, inverse norm)
+  constexpr uint32_t CB = REC ? 8u : 4u;
+  const char* code_p = REC ? (const char*)(tinv + 2 * (int64_t)T0) : (const char*)(p.pl.codes + T0);
   const char* res_p = (const char*)p.pl.res + (int64_t)T0 * p.pl.res_st;
-  const float* inv_p = NORMD ? tinv + T0 : nullptr;
+  const float* inv_p = (NORMD && !REC) ? tinv + T0 : nullptr;
   const int64_t res_tile = 32 * p.pl.res_st;
   const __amdgpu_buffer_rsrc_t rtab = make_rsrc(qc + g * qc_qs, (uint32_t)(p.pl.ncent * 64));
   const uint32_t res_lane = (uint32_t)(l32 * p.pl.res_st + h * RBL);
@@ -645,9 +667,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     u32x4 tq[2];  // the table's 16 fp16 values of this lane's half, in element order
   };
   // loads per tile (residual, inverse norm, table) and per code
-  constexpr int NLT = (RW == 2 ? 1 : RW / 4) + (NORMD ? 1 : 0) + 2;
+  constexpr int NLT = (RW == 2 ? 1 : RW / 4) + ((NORMD && !REC) ? 1 : 0) + 2;
+  using CodeT = std::conditional_t<REC, u32x2, uint32_t>;
   Stage st[LS];
-  uint32_t code[LC];
+  CodeT code[LC];
 #pragma unroll
   for (int k = 0; k < LS; ++k) {
 #pragma unroll
@@ -656,16 +679,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     st[k].tq[0] = st[k].tq[1] = u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
-  for (int k = 0; k < LC; ++k) code[k] = 0u;
+  for (int k = 0; k < LC; ++k) code[k] = CodeT{};
   // codes and inverse norms: loaded by lanes 0..31 only (EXEC's high half
   // cleared inside the asm; the loop runs with all lanes active) and copied
   // to lanes 32..63 by v_permlane32_swap once they have arrived
-  auto load_code = [&](int t, uint32_t& c) {
-    const u32x4 dc = desc(code_p + 32 * (int64_t)t, (uint32_t)rows_of(t) * 4u);
+  auto load_code = [&](int t, CodeT& c) {
+    const u32x4 dc = desc(code_p + 32 * CB * (int64_t)t, (uint32_t)rows_of(t) * CB);
     uint32_t ex;
-    asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
-                 "buffer_load_dword %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
-                 : "+v"(c), "=&s"(ex) : "v"((uint32_t)l32 * 4u), "s"(dc));
+    if constexpr (REC)
+      asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
+                   "buffer_load_dwordx2 %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
+                   : "+v"(c), "=&s"(ex) : "v"((uint32_t)l32 * 8u), "s"(dc));
+    else
+      asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
+                   "buffer_load_dword %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
+                   : "+v"(c), "=&s"(ex) : "v"((uint32_t)l32 * 4u), "s"(dc));
+  };
+  auto code_of = [](const CodeT& c) -> uint32_t {
+    if constexpr (REC) return c[0]; else return c;
   };
   auto bcast = [](uint32_t x) -> uint32_t {
     return __builtin_amdgcn_permlane32_swap(x, x, false, false)[0];
@@ -684,7 +715,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
         asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3 nt"
                      : "+v"(s.rw[k]) : "v"(res_lane), "s"(dr), "n"(16 * k));
     }
-    if constexpr (NORMD) {
+    if constexpr (NORMD && !REC) {
       const u32x4 di = desc(inv_p + 32 * (int64_t)t, (uint32_t)nv * 4u);
       uint32_t ex;
       asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
@@ -721,7 +752,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
 #pragma unroll
     for (int k = 0; k < (RW == 2 ? 1 : RW / 4); ++k) asm volatile("" : "+v"(s.rw[k]));
   };
-  auto wait_code = [](auto NN, uint32_t& c) {
+  auto wait_code = [](auto NN, CodeT& c) {
     asm volatile("s_waitcnt vmcnt(%1)" : "+v"(c) : "n"(decltype(NN)::value));
   };
 
@@ -850,7 +881,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
 #pragma unroll
   for (int t = 0; t < LS; ++t) {
     asm volatile("s_waitcnt vmcnt(0)" : "+v"(code[t]));
-    load_tile(t, bcast(code[t]), st[t]);
+    load_tile(t, bcast(code_of(code[t])), st[t]);
     load_code(t + LS, code[t + LS]);
   }
   constexpr int kWaitTile = 1 + (LS - 1) * (NLT + 1);
@@ -859,7 +890,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     wait_stage(integral_constant<int, kWaitTile>{}, st[I % LS]);
     {
       Stage cur = st[I % LS];
-      cur.inv = __uint_as_float(bcast(__float_as_uint(cur.inv)));
+      // the inverse norm: from the stage, or from tile c's record (code slot I)
+      if constexpr (REC && NORMD) cur.inv = __uint_as_float(bcast(code[I][1]));
+      else cur.inv = __uint_as_float(bcast(__float_as_uint(cur.inv)));
       unswap_table(cur);
       compute(c, cur);
     }
@@ -868,7 +901,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(m[e]));
     // the code of tile c + LS, loaded right after tile c's loads
     wait_code(integral_constant<int, kWaitTile - 1>{}, code[(I + LS) % LC]);
-    load_tile(c + LS, bcast(code[(I + LS) % LC]), st[I % LS]);
+    load_tile(c + LS, bcast(code_of(code[(I + LS) % LC])), st[I % LS]);
     load_code(c + LC, code[I]);
   };
   for (int c = 0; c < ntile; c += LC)
@@ -889,12 +922,15 @@ __global__ void __launch_bounds__(256) zero_scores_kernel(float* out, int64_t nq
 }
 
 template <int EK, int DPAD, int NBITS>
-int launch_qc_scan(int qn, const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s) {
+int launch_qc_scan(int qn, const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, bool rec, bool norm_d,
+                   hipStream_t s) {
   const int64_t waves = p.ngroups * p.NR;
   const int64_t nb = (waves + 3) / 4;
   if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+  const float* inv = norm_d ? tinv : nullptr;  // records are read for their norms only
+  const int ist = rec ? 8 : 4;
   auto go = [&](auto kern) {
-    launch_kernel(kern, dim3((unsigned)nb), dim3(256), 0, s, p, qc, qc_qs, tinv);
+    launch_kernel(kern, dim3((unsigned)nb), dim3(256), 0, s, p, qc, qc_qs, inv, ist);
     return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
   };
   const bool full = p.q.dim == DPAD;
@@ -916,7 +952,8 @@ constexpr bool scan_reg_ok() {
 }
 
 template <int EK, int DPAD, int NBITS>
-int launch_scan(const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s) {
+int launch_scan(const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, bool rec, bool norm_d,
+                hipStream_t s) {
   if constexpr (!scan_reg_ok<DPAD, NBITS>()) {
     return LIK_ERR_UNSUPPORTED;
   } else {
@@ -929,17 +966,24 @@ int launch_scan(const Params& p, const uint16_t* qc, int64_t qc_qs, const float*
   };
   const bool full = p.q.dim == DPAD;
   constexpr int LS = kScanLS;
-  if (tinv)
-    return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, true, LS>)
-                : go(plaid_scan_kernel<EK, DPAD, NBITS, false, true, LS>);
-  return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, false, LS>)
-              : go(plaid_scan_kernel<EK, DPAD, NBITS, false, false, LS>);
+  if (rec) {
+    if (norm_d)
+      return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, true, LS, true>)
+                  : go(plaid_scan_kernel<EK, DPAD, NBITS, false, true, LS, true>);
+    return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, false, LS, true>)
+                : go(plaid_scan_kernel<EK, DPAD, NBITS, false, false, LS, true>);
+  }
+  if (norm_d)
+    return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, true, LS, false>)
+                : go(plaid_scan_kernel<EK, DPAD, NBITS, false, true, LS, false>);
+  return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, false, LS, false>)
+              : go(plaid_scan_kernel<EK, DPAD, NBITS, false, false, LS, false>);
   }
 }
 
 template <int EK, int DPAD>
-int launch_qc(int qn, const Params& p, uint16_t* qc, int64_t qc_qs, const float* tinv, hipStream_t s,
-              const lik_launch_opts_t* opts) {
+int launch_qc(int qn, const Params& p, uint16_t* qc, int64_t qc_qs, const float* tinv, bool rec, bool norm_d,
+              hipStream_t s, const lik_launch_opts_t* opts) {
   const int64_t ntile = (p.pl.ncent + 31) / 32;
   const int64_t waves = p.q.n * ntile;
   if ((waves + 3) / 4 > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
@@ -953,9 +997,12 @@ int launch_qc(int qn, const Params& p, uint16_t* qc, int64_t qc_qs, const float*
   TimingScope ts(opts);
   int rc;
   switch (p.pl.nbits) {
-    case 2: rc = reg ? launch_scan<EK, DPAD, 2>(p, qc, qc_qs, tinv, s) : launch_qc_scan<EK, DPAD, 2>(qn, p, qc, qc_qs, tinv, s); break;
-    case 4: rc = reg ? launch_scan<EK, DPAD, 4>(p, qc, qc_qs, tinv, s) : launch_qc_scan<EK, DPAD, 4>(qn, p, qc, qc_qs, tinv, s); break;
-    case 8: rc = reg ? launch_scan<EK, DPAD, 8>(p, qc, qc_qs, tinv, s) : launch_qc_scan<EK, DPAD, 8>(qn, p, qc, qc_qs, tinv, s); break;
+    case 2: rc = reg ? launch_scan<EK, DPAD, 2>(p, qc, qc_qs, tinv, rec, norm_d, s)
+                 : launch_qc_scan<EK, DPAD, 2>(qn, p, qc, qc_qs, tinv, rec, norm_d, s); break;
+    case 4: rc = reg ? launch_scan<EK, DPAD, 4>(p, qc, qc_qs, tinv, rec, norm_d, s)
+                 : launch_qc_scan<EK, DPAD, 4>(qn, p, qc, qc_qs, tinv, rec, norm_d, s); break;
+    case 8: rc = reg ? launch_scan<EK, DPAD, 8>(p, qc, qc_qs, tinv, rec, norm_d, s)
+                 : launch_qc_scan<EK, DPAD, 8>(qn, p, qc, qc_qs, tinv, rec, norm_d, s); break;
     default: rc = LIK_ERR_UNSUPPORTED;
   }
   const int rc2 = ts.close(s);
@@ -992,7 +1039,8 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   if ((flags & LIK_KD_LAYOUT) || Q->mask || Q->token_scale || Q->cu_seqlens) return LIK_ERR_INVALID;
   if (Q->len > 32 || Q->n > kQcMaxQueries) return LIK_ERR_UNSUPPORTED;
   const bool norm_d = (flags & (LIK_NORMALIZE | LIK_NORMALIZE_D)) != 0;
-  if (norm_d && !token_inv) return LIK_ERR_INVALID;
+  const bool rec = (flags & LIK_TOKEN_RECORDS) != 0;
+  if ((norm_d || rec) && !token_inv) return LIK_ERR_INVALID;
   if (Q->n == 0 || docs->n == 0) return LIK_OK;
   if (!out) return LIK_ERR_INVALID;
   if (Q->len == 0) {
@@ -1012,7 +1060,7 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   if (((uintptr_t)docs->residuals) % 16 != 0 || docs->res_stride_tok % 16 != 0 || 32 * docs->res_stride_tok > nri * 1024)
     return LIK_ERR_UNSUPPORTED;
   if (docs->res_stride_tok * 8 < (int64_t)docs->dim * docs->nbits) return LIK_ERR_INVALID;
-  if (token_inv && ((uintptr_t)token_inv) % 4) return LIK_ERR_UNSUPPORTED;
+  if (token_inv && ((uintptr_t)token_inv) % (rec ? 8 : 4)) return LIK_ERR_UNSUPPORTED;
   // table rows are gathered with 32-bit byte offsets below kInvRow
   if (docs->n_centroids * 64 >= (int64_t)kInvRow) return LIK_ERR_UNSUPPORTED;
   const size_t need = qc_bytes(Q->n, docs->n_centroids);
@@ -1055,11 +1103,13 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   p.NR = (docs->n + p.R - 1) / p.R;
   uint16_t* qc = (uint16_t*)workspace;
   const int64_t qc_qs = docs->n_centroids * 32;
-  const float* tinv = norm_d ? token_inv : nullptr;
+  // token_inv: inverse norms (used only when the docs are normalised), or
+  // records (codes, and norms when normalised)
+  const float* tinv = rec ? token_inv : norm_d ? token_inv : nullptr;
   hipStream_t s = (hipStream_t)stream;
   if (Q->dtype == LIK_BF16)
-    return dpad == 64 ? launch_qc<EK_BF16, 64>(qn, p, qc, qc_qs, tinv, s, opts)
-                      : launch_qc<EK_BF16, 128>(qn, p, qc, qc_qs, tinv, s, opts);
-  return dpad == 64 ? launch_qc<EK_F16, 64>(qn, p, qc, qc_qs, tinv, s, opts)
-                    : launch_qc<EK_F16, 128>(qn, p, qc, qc_qs, tinv, s, opts);
+    return dpad == 64 ? launch_qc<EK_BF16, 64>(qn, p, qc, qc_qs, tinv, rec, norm_d, s, opts)
+                      : launch_qc<EK_BF16, 128>(qn, p, qc, qc_qs, tinv, rec, norm_d, s, opts);
+  return dpad == 64 ? launch_qc<EK_F16, 64>(qn, p, qc, qc_qs, tinv, rec, norm_d, s, opts)
+                    : launch_qc<EK_F16, 128>(qn, p, qc, qc_qs, tinv, rec, norm_d, s, opts);
 }

@@ -30,6 +30,7 @@ LIK_KD_LAYOUT = 2
 LIK_NORMALIZE_Q = 4
 LIK_NORMALIZE_D = 8
 LIK_BIAS_16 = 16
+LIK_TOKEN_RECORDS = 32
 
 
 def norm_flags(norm: int) -> int:
@@ -69,6 +70,7 @@ EXPORTED_SYMBOLS = (
     "lik_plaid_maxsim_ex",
     "lik_maxsim_noalloc",
     "lik_plaid_token_norms",
+    "lik_plaid_token_records",
     "lik_plaid_maxsim_qc",
     "lik_plaid_maxsim_qc_workspace_size",
 )
@@ -213,6 +215,8 @@ def load() -> ctypes.CDLL:
     lib.lik_maxsim_noalloc.restype = ctypes.c_int
     lib.lik_plaid_token_norms.argtypes = [P(LikPlaidDocs), _i64, _i64, _p, _p]
     lib.lik_plaid_token_norms.restype = ctypes.c_int
+    lib.lik_plaid_token_records.argtypes = [P(LikPlaidDocs), _i64, _i64, _p, _p]
+    lib.lik_plaid_token_records.restype = ctypes.c_int
     lib.lik_plaid_maxsim_qc_workspace_size.argtypes = [P(LikSeqs), P(LikPlaidDocs)]
     lib.lik_plaid_maxsim_qc_workspace_size.restype = ctypes.c_size_t
     lib.lik_plaid_maxsim_qc.argtypes = [P(LikSeqs), P(LikPlaidDocs), _p, ctypes.c_uint32, _p, _i64, _i64, _p,

@@ -495,12 +495,13 @@ class ResidualIndex:
 
     Same inputs as :func:`maxsim_residual_varlen` (``codes_flat``,
     ``residuals_flat``, ``cu_seqlens_d``, ``centroids``, ``bucket_weights``,
-    ``nbits``). Construction computes every token's inverse L2 norm once
-    (``lik_plaid_token_norms``: 4 bytes per token, one decode pass). Scoring
-    up to 64 queries of at most 32 tokens then runs ``lik_plaid_maxsim_qc``:
-    per query a table of query-centroid scores (``[n_centroids, 32]`` fp16),
-    and a scan that reads each token's code, residual bytes and norm from HBM
-    and one 64-byte table row instead of a 256-byte centroid row. Scores
+    ``nbits``). Construction computes every token's inverse L2 norm once and
+    stores it beside the token's code (``lik_plaid_token_records``: an
+    8-byte (code, norm) record per token, one decode pass). Scoring up to 64
+    queries of at most 32 tokens then runs ``lik_plaid_maxsim_qc``: per query
+    a table of query-centroid scores (``[n_centroids, 32]`` fp16), and a scan
+    that reads each token's record and residual bytes from HBM and one 64-byte
+    table row instead of a 256-byte centroid row. Scores
     match :func:`maxsim_residual_varlen` within bf16 rounding (the centroid
     term is rounded to fp16). Larger batches, queries needing gradients,
     layouts the scan cannot take, and query / centroid norms whose products
@@ -526,14 +527,20 @@ class ResidualIndex:
         T = self.codes.numel()
         # largest centroid norm (one sync, here): bounds |q.c| for the fp16 table
         self._cent_norm_max = float(self.centroids.float().norm(dim=-1).max()) if self.centroids.shape[0] else 0.0
-        self.token_inv = torch.empty(T, device=self.codes.device, dtype=torch.float32)
+        # (code, inverse norm) per token, as int32 pairs
+        self.token_rec = torch.empty(T, 2, device=self.codes.device, dtype=torch.int32)
         if T:
             docs = self._docs()
             lib = _lib.load()
             with torch.cuda.device(self.codes.device):
-                rc = lib.lik_plaid_token_norms(ctypes.byref(docs), 0, T, self.token_inv.data_ptr(),
-                                               _lib.stream_of(self.token_inv))
-            _lib.check(rc, "lik_plaid_token_norms")
+                rc = lib.lik_plaid_token_records(ctypes.byref(docs), 0, T, self.token_rec.data_ptr(),
+                                                 _lib.stream_of(self.token_rec))
+            _lib.check(rc, "lik_plaid_token_records")
+
+    @property
+    def token_inv(self) -> torch.Tensor:
+        """``[T]`` fp32 inverse norms of the tokens (a strided view of the records)."""
+        return self.token_rec[:, 1].view(torch.float32)
 
     def _docs(self) -> _lib.LikPlaidDocs:
         return _plaid_docs(self.codes, self.residuals, self.centroids, self.bucket_weights, self.nbits, self.d,
@@ -579,9 +586,9 @@ class ResidualIndex:
             lib = _lib.load()
             nbytes = lib.lik_plaid_maxsim_qc_workspace_size(ctypes.byref(qs), ctypes.byref(docs))
             ws = _lib.workspace(nbytes, Q.device)
-            flags = _lib.LIK_NORMALIZE if normalize else 0
+            flags = (_lib.LIK_NORMALIZE if normalize else 0) | _lib.LIK_TOKEN_RECORDS
             with torch.cuda.device(Q.device):
-                rc = lib.lik_plaid_maxsim_qc(ctypes.byref(qs), ctypes.byref(docs), self.token_inv.data_ptr(), flags,
+                rc = lib.lik_plaid_maxsim_qc(ctypes.byref(qs), ctypes.byref(docs), self.token_rec.data_ptr(), flags,
                                              out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(ws), nbytes,
                                              _lib.call_opts(), _lib.stream_of(out))
             _lib.check(rc, "lik_plaid_maxsim_qc")

@@ -1,5 +1,5 @@
 """GPU parity of the prepared-corpus PLAID scan (plaid.ResidualIndex,
-lik_plaid_token_norms + lik_plaid_maxsim_qc).
+lik_plaid_token_records / lik_plaid_token_norms + lik_plaid_maxsim_qc).
 
 * Token inverse norms equal 1 / max(||centroid + bucket weights||, 1e-12) of
   the oracle's float64 decode (oracle/lik_oracle.decode_residual_tokens,
@@ -16,6 +16,12 @@ lik_plaid_token_norms + lik_plaid_maxsim_qc).
   16 bytes) go to maxsim_residual_varlen and give its result exactly.
 * Docs split inside the scan's 32-token tiles (short and empty docs, 1 to
   128 docs per wavefront): the same bits for every split.
+* Token records (LIK_TOKEN_RECORDS): each record holds the token's code and
+  bitwise lik_plaid_token_norms' value, and scores from the records equal
+  bitwise the scores from the separate codes and norms, on the register scan
+  (one query) and the LDS-staged scan (several queries, or plaid_variant 5),
+  with and without normalisation; the C ABI rejects a missing or misaligned
+  record pointer.
 """
 
 import sys
@@ -217,7 +223,64 @@ def test_c_abi_empty_query_tokens():
     qs = _lib.seqs(Q, n=2, length=0, stride_n=128, stride_l=128)
     docs = idx._docs()
     lib = _lib.load()
-    rc = lib.lik_plaid_maxsim_qc(ctypes.byref(qs), ctypes.byref(docs), idx.token_inv.data_ptr(), _lib.LIK_NORMALIZE,
-                                 out.data_ptr(), out.stride(0), out.stride(1), None, 0, None, _lib.stream_of(out))
+    rc = lib.lik_plaid_maxsim_qc(ctypes.byref(qs), ctypes.byref(docs), idx.token_rec.data_ptr(),
+                                 _lib.LIK_NORMALIZE | _lib.LIK_TOKEN_RECORDS, out.data_ptr(), out.stride(0),
+                                 out.stride(1), None, 0, None, _lib.stream_of(out))
     assert rc == _lib.LIK_OK
     assert out.abs().max().item() == 0.0
+
+
+def _qc_call(idx, Q, token_ptr, flags, opts=None):
+    """lik_plaid_maxsim_qc through the C ABI: (return code, [Nq, Nd] scores)."""
+    import ctypes
+
+    from late_interaction_kernels import _lib
+
+    nq, lq, _ = Q.shape
+    out = torch.full((nq, idx.n_docs), float("nan"), device="cuda")
+    qs = _lib.seqs(Q, n=nq, length=lq, stride_n=Q.stride(0), stride_l=Q.stride(1))
+    docs = idx._docs()
+    lib = _lib.load()
+    nbytes = lib.lik_plaid_maxsim_qc_workspace_size(ctypes.byref(qs), ctypes.byref(docs))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    with launch_options(**(opts or {})):
+        rc = lib.lik_plaid_maxsim_qc(ctypes.byref(qs), ctypes.byref(docs), token_ptr, flags, out.data_ptr(),
+                                     out.stride(0), out.stride(1), ws.data_ptr(), nbytes, _lib.call_opts(),
+                                     _lib.stream_of(out))
+    torch.cuda.synchronize()
+    return rc, out
+
+
+@pytest.mark.parametrize("nbits,d", [(2, 128), (4, 64), (8, 128), (2, 64)])
+def test_token_records_equal_norms_route(nbits, d):
+    import ctypes
+
+    from late_interaction_kernels import _lib
+    from late_interaction_kernels.plaid import ResidualIndex
+
+    _case(f"qc records nbits={nbits} d={d}")
+    cent, bw, codes, res, cu = _index(500, 70, d, nbits, 31 + nbits + d, torch.bfloat16)
+    codes[::97] = -3  # out-of-range codes decode as centroid 0 on every route
+    codes[5::89] = 100000
+    idx = ResidualIndex(codes.cuda(), res.cuda(), cu.cuda(), cent.cuda(), bw.cuda(), nbits)
+    T = codes.numel()
+    inv = torch.empty(T, device="cuda")
+    lib = _lib.load()
+    docs = idx._docs()
+    assert lib.lik_plaid_token_norms(ctypes.byref(docs), 0, T, inv.data_ptr(), _lib.stream_of(inv)) == _lib.LIK_OK
+    torch.cuda.synchronize()
+    assert torch.equal(idx.token_rec[:, 0].cpu(), codes)
+    assert torch.equal(idx.token_rec[:, 1].cpu(), inv.view(torch.int32).cpu())
+    g = torch.Generator().manual_seed(d * nbits)
+    for nq, lq, opts in ((1, 32, {}), (1, 32, {"plaid_variant": 5}), (3, 24, {}), (2, 32, {"docs_per_wg": 3})):
+        Q = torch.randn(nq, lq, d, generator=g).to(torch.bfloat16).cuda()
+        for normalize in (True, False):
+            f = _lib.LIK_NORMALIZE if normalize else 0
+            rc0, base = _qc_call(idx, Q, inv.data_ptr(), f, opts)
+            rc1, got = _qc_call(idx, Q, idx.token_rec.data_ptr(), f | _lib.LIK_TOKEN_RECORDS, opts)
+            assert rc0 == _lib.LIK_OK and rc1 == _lib.LIK_OK
+            assert torch.equal(got, base), (nq, opts, normalize)
+    # the records are required with the flag, and 8-byte aligned
+    Q = torch.randn(1, 32, d, generator=g).to(torch.bfloat16).cuda()
+    assert _qc_call(idx, Q, None, _lib.LIK_TOKEN_RECORDS)[0] == _lib.LIK_ERR_INVALID
+    assert _qc_call(idx, Q, idx.token_rec.data_ptr() + 4, _lib.LIK_TOKEN_RECORDS)[0] == _lib.LIK_ERR_UNSUPPORTED

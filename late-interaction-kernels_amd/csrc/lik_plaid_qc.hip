@@ -628,7 +628,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   const int ntile = (span + 31) >> 5;
 
   // codes (4 bytes per token), or records (8 bytes: code, inverse norm)
-  constexpr uint32_t CB = REC ? 8u : 4u;
   const char* code_p = REC ? (const char*)(tinv + 2 * (int64_t)T0) : (const char*)(p.pl.codes + T0);
   const char* res_p = (const char*)p.pl.res + (int64_t)T0 * p.pl.res_st;
   const float* inv_p = (NORMD && !REC) ? tinv + T0 : nullptr;
@@ -668,9 +667,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   };
   // loads per tile (residual, inverse norm, table) and per code
   constexpr int NLT = (RW == 2 ? 1 : RW / 4) + ((NORMD && !REC) ? 1 : 0) + 2;
-  using CodeT = std::conditional_t<REC, u32x2, uint32_t>;
   Stage st[LS];
-  CodeT code[LC];
+  uint32_t code[LC];  // (without records)
 #pragma unroll
   for (int k = 0; k < LS; ++k) {
 #pragma unroll
@@ -679,24 +677,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     st[k].tq[0] = st[k].tq[1] = u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
-  for (int k = 0; k < LC; ++k) code[k] = CodeT{};
+  for (int k = 0; k < LC; ++k) code[k] = 0u;
   // codes and inverse norms: loaded by lanes 0..31 only (EXEC's high half
   // cleared inside the asm; the loop runs with all lanes active) and copied
   // to lanes 32..63 by v_permlane32_swap once they have arrived
-  auto load_code = [&](int t, CodeT& c) {
-    const u32x4 dc = desc(code_p + 32 * CB * (int64_t)t, (uint32_t)rows_of(t) * CB);
+  auto load_code = [&](int t, uint32_t& c) {
+    const u32x4 dc = desc(code_p + 128 * (int64_t)t, (uint32_t)rows_of(t) * 4u);
     uint32_t ex;
-    if constexpr (REC)
-      asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
-                   "buffer_load_dwordx2 %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
-                   : "+v"(c), "=&s"(ex) : "v"((uint32_t)l32 * 8u), "s"(dc));
-    else
-      asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
-                   "buffer_load_dword %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
-                   : "+v"(c), "=&s"(ex) : "v"((uint32_t)l32 * 4u), "s"(dc));
-  };
-  auto code_of = [](const CodeT& c) -> uint32_t {
-    if constexpr (REC) return c[0]; else return c;
+    asm volatile("s_nop 4\n\ts_mov_b32 %1, exec_hi\n\ts_mov_b32 exec_hi, 0\n\t"
+                 "buffer_load_dword %0, %2, %3, 0 offen nt\n\ts_mov_b32 exec_hi, %1"
+                 : "+v"(c), "=&s"(ex) : "v"((uint32_t)l32 * 4u), "s"(dc));
   };
   auto bcast = [](uint32_t x) -> uint32_t {
     return __builtin_amdgcn_permlane32_swap(x, x, false, false)[0];
@@ -752,7 +742,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
 #pragma unroll
     for (int k = 0; k < (RW == 2 ? 1 : RW / 4); ++k) asm volatile("" : "+v"(s.rw[k]));
   };
-  auto wait_code = [](auto NN, CodeT& c) {
+  auto wait_code = [](auto NN, uint32_t& c) {
     asm volatile("s_waitcnt vmcnt(%1)" : "+v"(c) : "n"(decltype(NN)::value));
   };
 
@@ -871,41 +861,92 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     }
   };
 
-  // Prologue: codes of tiles 0 .. LS-1; then for each t < LS tile t's loads
-  // followed by the code of tile t + LS. From here on every tile's loads are
-  // followed by exactly one code load, so at the top of step c tile c's loads
-  // are followed by the code of tile c + LS and by LS - 1 later steps of
-  // NLT + 1 loads each.
+  if constexpr (REC) {
+    // Records two tiles at a time: one 64-lane load of tiles (u, u + 1), u
+    // even (512 contiguous bytes; lanes 0..31 tile u, 32..63 tile u + 1),
+    // into pair slot (u / 2) % 3. Odd step c issues the pair (c + 5, c + 6)
+    // (into the slot of (c - 1, c), both scored by then) before tile c + 3's
+    // loads. Loads issued after a tile's loads until its step: two steps of
+    // NLT loads and one pair, 2 NLT + 1; after the pair holding tile c + 3's
+    // record until step c issues that tile: 2 NLT + 1 at odd c, 3 NLT + 1 at
+    // even c. The prologue issues what steps -5 .. -1 would have.
+    static_assert(LS == 3 && LC == 6, "record pairs: three stages, a six-step round");
+    u32x2 pr[3];
 #pragma unroll
-  for (int t = 0; t < LS; ++t) load_code(t, code[t]);
+    for (int k = 0; k < 3; ++k) pr[k] = u32x2{0u, 0u};
+    auto load_pair = [&](int u, u32x2& v) {
+      const u32x4 dc = desc(code_p + 256 * (int64_t)u, (uint32_t)(rows_of(u) + rows_of(u + 1)) * 8u);
+      asm volatile("s_nop 4\n\tbuffer_load_dwordx2 %0, %1, %2, 0 offen nt" : "+v"(v) : "v"((uint32_t)lane * 8u), "s"(dc));
+    };
+    // word x of this lane's token in the even (lanes 0..31) or odd tile of a pair
+    auto half = [](uint32_t x, auto ODD) -> uint32_t {
+      const auto sw = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+      return decltype(ODD)::value ? sw[1] : sw[0];
+    };
+    using F = std::false_type;
+    using Tt = std::true_type;
+    load_pair(0, pr[0]);
+    load_pair(2, pr[1]);
+    asm volatile("s_waitcnt vmcnt(1)" : "+v"(pr[0]));
+    load_tile(0, half(pr[0][0], F{}), st[0]);
+    load_tile(1, half(pr[0][0], Tt{}), st[1]);
+    load_pair(4, pr[2]);
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(pr[1]) : "n"(2 * NLT + 1));
+    load_tile(2, half(pr[1][0], F{}), st[2]);
+    auto step = [&](auto II, int c) {
+      constexpr int I = decltype(II)::value;  // c % 6
+      constexpr int J = (I + 3) % 6;           // (c + 3) % 6
+      wait_stage(integral_constant<int, 2 * NLT + 1>{}, st[I % 3]);
+      {
+        Stage cur = st[I % 3];
+        if constexpr (NORMD) cur.inv = __uint_as_float(half(pr[I / 2][1], integral_constant<bool, (I & 1) != 0>{}));
+        unswap_table(cur);
+        compute(c, cur);
+      }
+      // ordering point: the stage's previous contents are all read (they feed m)
 #pragma unroll
-  for (int t = 0; t < LS; ++t) {
-    asm volatile("s_waitcnt vmcnt(0)" : "+v"(code[t]));
-    load_tile(t, bcast(code_of(code[t])), st[t]);
-    load_code(t + LS, code[t + LS]);
-  }
-  constexpr int kWaitTile = 1 + (LS - 1) * (NLT + 1);
-  auto step = [&](auto II, int c) {
-    constexpr int I = decltype(II)::value;  // c % LC
-    wait_stage(integral_constant<int, kWaitTile>{}, st[I % LS]);
-    {
-      Stage cur = st[I % LS];
-      // the inverse norm: from the stage, or from tile c's record (code slot I)
-      if constexpr (REC && NORMD) cur.inv = __uint_as_float(bcast(code[I][1]));
-      else cur.inv = __uint_as_float(bcast(__float_as_uint(cur.inv)));
-      unswap_table(cur);
-      compute(c, cur);
+      for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(m[e]));
+      if constexpr ((I & 1) != 0) load_pair(c + 5, pr[I / 2]);
+      asm volatile("s_waitcnt vmcnt(%1)" : "+v"(pr[J / 2]) : "n"((I & 1) ? 2 * NLT + 1 : 3 * NLT + 1));
+      load_tile(c + 3, half(pr[J / 2][0], integral_constant<bool, (J & 1) != 0>{}), st[I % 3]);
+    };
+    for (int c = 0; c < ntile; c += LC)
+      if (!scan_steps<0, LC>(step, c, ntile)) break;
+  } else {
+    // Prologue: codes of tiles 0 .. LS-1; then for each t < LS tile t's loads
+    // followed by the code of tile t + LS. From here on every tile's loads are
+    // followed by exactly one code load, so at the top of step c tile c's loads
+    // are followed by the code of tile c + LS and by LS - 1 later steps of
+    // NLT + 1 loads each.
+#pragma unroll
+    for (int t = 0; t < LS; ++t) load_code(t, code[t]);
+#pragma unroll
+    for (int t = 0; t < LS; ++t) {
+      asm volatile("s_waitcnt vmcnt(0)" : "+v"(code[t]));
+      load_tile(t, bcast(code[t]), st[t]);
+      load_code(t + LS, code[t + LS]);
     }
-    // ordering point: the stage's previous contents are all read (they feed m)
+    constexpr int kWaitTile = 1 + (LS - 1) * (NLT + 1);
+    auto step = [&](auto II, int c) {
+      constexpr int I = decltype(II)::value;  // c % LC
+      wait_stage(integral_constant<int, kWaitTile>{}, st[I % LS]);
+      {
+        Stage cur = st[I % LS];
+        cur.inv = __uint_as_float(bcast(__float_as_uint(cur.inv)));
+        unswap_table(cur);
+        compute(c, cur);
+      }
+      // ordering point: the stage's previous contents are all read (they feed m)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(m[e]));
-    // the code of tile c + LS, loaded right after tile c's loads
-    wait_code(integral_constant<int, kWaitTile - 1>{}, code[(I + LS) % LC]);
-    load_tile(c + LS, bcast(code_of(code[(I + LS) % LC])), st[I % LS]);
-    load_code(c + LC, code[I]);
-  };
-  for (int c = 0; c < ntile; c += LC)
-    if (!scan_steps<0, LC>(step, c, ntile)) break;
+      for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(m[e]));
+      // the code of tile c + LS, loaded right after tile c's loads
+      wait_code(integral_constant<int, kWaitTile - 1>{}, code[(I + LS) % LC]);
+      load_tile(c + LS, bcast(code[(I + LS) % LC]), st[I % LS]);
+      load_code(c + LC, code[I]);
+    };
+    for (int c = 0; c < ntile; c += LC)
+      if (!scan_steps<0, LC>(step, c, ntile)) break;
+  }
   while (jc < nd) doc_end();
   // no load may still be writing this wave's registers when it exits
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

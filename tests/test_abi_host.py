@@ -94,6 +94,15 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     assert rc == _lib.LIK_ERR_UNSUPPORTED
     rc = L.lik_topk_merge(1, 1, 8193, 8193, 0, None, None, 0, 0, 2000, 1, 1, 1, 2000, None)
     assert rc == _lib.LIK_ERR_UNSUPPORTED
+    # token records: a null descriptor or an inverted range is invalid, an empty
+    # range a no-op; a misaligned record array is refused before any launch
+    assert L.lik_plaid_token_records(None, 0, 1, None, None) == _lib.LIK_ERR_INVALID
+    docs = _lib.LikPlaidDocs()
+    docs.nbits, docs.dim, docs.n_buckets, docs.bucket_weights, docs.res_stride_tok = 2, 128, 4, 8, 32
+    assert L.lik_plaid_token_records(ctypes.byref(docs), 5, 4, None, None) == _lib.LIK_ERR_INVALID
+    assert L.lik_plaid_token_records(ctypes.byref(docs), 4, 4, None, None) == _lib.LIK_OK
+    docs.codes, docs.residuals, docs.centroids, docs.n_centroids = 16, 16, 16, 1
+    assert L.lik_plaid_token_records(ctypes.byref(docs), 0, 4, 4, None) == _lib.LIK_ERR_UNSUPPORTED
 
 
 def test_value_errors_match_the_reference_contract():

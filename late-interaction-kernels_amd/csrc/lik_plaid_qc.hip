@@ -3,7 +3,8 @@
 //
 // A decoded token is x = c + r: c its centroid row, r the bucket weights
 // picked by its residual fields. With the token's inverse norm known ahead
-// (lik_plaid_token_norms, once per corpus), the normalised score of query
+// (lik_plaid_token_records / lik_plaid_token_norms, once per corpus), the
+// normalised score of query
 // token s is
 //     q_s . x / ||x|| = (q_s . c + q_s . r) / ||x||.
 // q_s . c depends on the centroid alone, so for each query it is one
@@ -519,20 +520,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN > 1
 // butterfly of permlane16 swaps and DPP moves) and sums the 32 query tokens.
 // Pipeline: tile c + LS's loads are issued after tile c is scored; their
 // codes were loaded LC = 2 LS tiles ahead, right after tile c's loads, so a
-// wait for either never waits for a younger load. The loads are inline asm
-// with explicit vmcnt counts (see load_tile). The loop is unrolled by LC so
-// the register rings have static indices.
-// Measured against the LDS-staged kernel on the C5 corpus at Nq = 1: 2.57
-// against 2.70 ms. What bounds it (counters): the texture address and data
-// units (TA busy 0.92, TD 0.95), i.e. the five vector memory instructions per
-// tile, two of them random table reads; with every table read pointed at one
-// row (timing only) the scan takes 2.02 ms, with the texture data unit still
-// busy 0.94 of the cycles. Table reads of 16 rows per load, four lanes per
-// row (above), instead of 32 rows, two lanes per row: 2.57 -> 2.40 ms. Tried: the streamed bytes through
-// an 8-tile LDS ring (buffer_load ... lds, 2.6x the bytes in flight, 128
-// VGPRs): 2.60 ms, and the same at four waves per SIMD with 6 tiles: 2.75 ms;
-// so latency is not the bound. Codes and inverse norms loaded by 32 lanes
-// instead of 64 (kept): -0.4%.
+// wait for either never waits for a younger load. With token records (REC)
+// the code and the norm of a token come in one record, and the records of
+// two tiles in one 64-lane load every other step (see the REC branch at the
+// loop). The loads are inline asm with explicit vmcnt counts (see
+// load_tile). The loop is unrolled by LC so the register rings have static
+// indices.
+// Measured on the C5 corpus at Nq = 1: 2.70 ms with the LDS-staged kernel;
+// 2.57 ms register-direct; 2.40 ms with table reads of 16 rows per load
+// (four lanes per row, above) instead of 32 rows by two lanes each; 2.32 ms
+// with records; 2.245 ms with records of two tiles per load. What bounds it
+// (counters): the texture data unit, busy 0.955 of the cycles returning 832
+// dwords per tile to registers (512 of them table rows). Tried: the streamed
+// bytes through an 8-tile LDS ring (buffer_load ... lds, 2.6x the bytes in
+// flight, 128 VGPRs): 2.60 against 2.57 ms, and the same at four waves per
+// SIMD with 6 tiles: 2.75 ms; so latency is not the bound.
 // Steps I .. N-1 of one unrolled round (static register indices), stopping
 // at the last tile; false once it stopped.
 template <int I, int N, class F>

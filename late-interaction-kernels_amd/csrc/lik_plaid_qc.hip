@@ -1137,7 +1137,13 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   p.osq = out_stride_q;
   p.osd = out_stride_d;
   p.LU = (int)Q->len;
-  const int qn = Q->n >= 2 ? 2 : 1;
+  // One query per wavefront on the register-direct scan wherever it applies
+  // (2-bit residuals, or 4-bit at d <= 64; measured faster per query than
+  // two queries per wavefront on the LDS-staged scan: 2.25 against 2.56 ms
+  // at 8 queries, C5 corpus); else two queries per wavefront when there are
+  // several.
+  const bool reg_ok = !(opts && opts->plaid_variant == 5) && (docs->nbits == 2 || (docs->nbits == 4 && dpad == 64));
+  const int qn = (reg_ok || Q->n < 2) ? 1 : 2;
   p.ngroups = (Q->n + qn - 1) / qn;
   // ~16k wavefronts over the corpus, at most kQcRMax docs each
   int64_t R = (docs->n + 16383) / 16384;

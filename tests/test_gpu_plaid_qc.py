@@ -19,7 +19,8 @@ lik_plaid_token_records / lik_plaid_token_norms + lik_plaid_maxsim_qc).
 * Token records (LIK_TOKEN_RECORDS): each record holds the token's code and
   bitwise lik_plaid_token_norms' value, and scores from the records equal
   bitwise the scores from the separate codes and norms, on the register scan
-  (one query) and the LDS-staged scan (several queries, or plaid_variant 5),
+  (one query per wavefront) and the LDS-staged scan (plaid_variant 5, and
+  the residual widths the register scan does not take),
   with and without normalisation; the C ABI rejects a missing or misaligned
   record pointer.
 """
@@ -172,16 +173,19 @@ def test_docs_split_inside_tiles(nq):
     idx = ResidualIndex(*args)
     Q = torch.randn(nq, 32, d, generator=g).to(torch.bfloat16).cuda()
     for normalize in (True, False):
-        base = idx.score(Q, normalize=normalize)
-        for r in (3, 37, 128):
-            with launch_options(docs_per_wg=r):
-                got = idx.score(Q, normalize=normalize)
-            assert torch.equal(got, base), (r, normalize)
         with launch_options(plaid_variant=2):
             exact = maxsim_residual_varlen(Q, *args, normalize=normalize)
-        assert rel_err(base.cpu().numpy(), exact.cpu().numpy()) < 5e-3, normalize
         empty = (lens == 0).nonzero().flatten().cuda()
-        assert base[:, empty].abs().max().item() == 0.0
+        # the register-direct scan (automatic) and the LDS-staged one (variant 5)
+        for variant in (0, 5):
+            with launch_options(plaid_variant=variant):
+                base = idx.score(Q, normalize=normalize)
+            for r in (3, 37, 128):
+                with launch_options(docs_per_wg=r, plaid_variant=variant):
+                    got = idx.score(Q, normalize=normalize)
+                assert torch.equal(got, base), (r, normalize, variant)
+            assert rel_err(base.cpu().numpy(), exact.cpu().numpy()) < 5e-3, (normalize, variant)
+            assert base[:, empty].abs().max().item() == 0.0
 
 
 def test_table_range_falls_back():
@@ -272,7 +276,8 @@ def test_token_records_equal_norms_route(nbits, d):
     assert torch.equal(idx.token_rec[:, 0].cpu(), codes)
     assert torch.equal(idx.token_rec[:, 1].cpu(), inv.view(torch.int32).cpu())
     g = torch.Generator().manual_seed(d * nbits)
-    for nq, lq, opts in ((1, 32, {}), (1, 32, {"plaid_variant": 5}), (3, 24, {}), (2, 32, {"docs_per_wg": 3})):
+    for nq, lq, opts in ((1, 32, {}), (1, 32, {"plaid_variant": 5}), (3, 24, {}), (3, 24, {"plaid_variant": 5}),
+                         (2, 32, {"docs_per_wg": 3})):
         Q = torch.randn(nq, lq, d, generator=g).to(torch.bfloat16).cuda()
         for normalize in (True, False):
             f = _lib.LIK_NORMALIZE if normalize else 0

@@ -17,7 +17,8 @@ lik_plaid_token_records / lik_plaid_token_norms + lik_plaid_maxsim_qc).
 * Docs split inside the scan's 32-token tiles (short and empty docs, 1 to
   128 docs per wavefront): the same bits for every split.
 * Token records (LIK_TOKEN_RECORDS): each record holds the token's code and
-  bitwise lik_plaid_token_norms' value, and scores from the records equal
+  bitwise lik_plaid_token_norms' value (also when written in two token
+  ranges), and scores from the records equal
   bitwise the scores from the separate codes and norms, on the register scan
   (one query per wavefront) and the LDS-staged scan (plaid_variant 5, and
   the residual widths the register scan does not take),
@@ -275,6 +276,13 @@ def test_token_records_equal_norms_route(nbits, d):
     torch.cuda.synchronize()
     assert torch.equal(idx.token_rec[:, 0].cpu(), codes)
     assert torch.equal(idx.token_rec[:, 1].cpu(), inv.view(torch.int32).cpu())
+    # records of two token ranges, written at their absolute indices, equal one call
+    rec2 = torch.full_like(idx.token_rec, -7)
+    half = T // 2 + 3
+    for a, b in ((half, T), (0, half)):
+        assert lib.lik_plaid_token_records(ctypes.byref(docs), a, b, rec2.data_ptr(), _lib.stream_of(rec2)) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(rec2, idx.token_rec)
     g = torch.Generator().manual_seed(d * nbits)
     for nq, lq, opts in ((1, 32, {}), (1, 32, {"plaid_variant": 5}), (3, 24, {}), (3, 24, {"plaid_variant": 5}),
                          (2, 32, {"docs_per_wg": 3})):

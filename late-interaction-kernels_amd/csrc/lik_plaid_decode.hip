@@ -15,12 +15,19 @@
 // dense-MaxSim and fused decode+MaxSim give identical scores.
 //
 // Work: one lane per 8 embedding elements (16 bytes out); a 256-thread
-// workgroup covers 256 / (dpad / 8) tokens. Per token it reads 4 bytes of
+// workgroup covers 4 x 256 / (dpad / 8) tokens (four passes, loads first). Per token it reads 4 bytes of
 // code, dim*nbits/8 bytes of residual and one centroid row (L2 / MALL
 // resident for typical tables), and writes dim*2 bytes: an HBM-bound kernel.
 #include "lik_common.h"
 
 namespace lik {
+
+// Tokens per lane group: a workgroup makes kDecodeTPT passes of 256 / LPT
+// tokens, and issues the loads of all of them (codes, then centroid rows and
+// residual bits) before it decodes the first: with one token per lane group
+// each wave held 1 KB of rows in flight behind two dependent load latencies
+// (code, then row), too little to cover them.
+constexpr int kDecodeTPT = 4;
 
 template <int LPT, int CD, int OUTK>
 __global__ void __launch_bounds__(256)
@@ -29,80 +36,101 @@ __global__ void __launch_bounds__(256)
                         const float* __restrict__ bw, int nb, int nbits, int dim, int normalize,
                         uint16_t* __restrict__ out, int64_t out_stride, int64_t ntok, float* __restrict__ inv_out,
                         int rec) {
-  constexpr int TPB = 256 / LPT;  // tokens per workgroup
+  constexpr int TPB = 256 / LPT;  // tokens per pass
+  constexpr int TPT = kDecodeTPT;
   constexpr int CSZ = CD == EK_F32 ? 4 : 2;
+  constexpr int NCV = CD == EK_F32 ? 2 : 1;
   __shared__ float s_bw[256];
   for (int i = threadIdx.x; i < 256; i += 256) s_bw[i] = i < nb ? bw[i] : 0.f;
   __syncthreads();
   const int cc = threadIdx.x % LPT;  // 8-element chunk of the row
-  const int64_t tok = (int64_t)blockIdx.x * TPB + threadIdx.x / LPT;
-  const bool tok_ok = tok < ntok;
-  const bool live = tok_ok && cc * 8 < dim;
-  float x8[8];
+  const int64_t tok0 = (int64_t)blockIdx.x * (TPB * TPT) + threadIdx.x / LPT;
+  int64_t code[TPT];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) x8[e] = 0.f;
-  if (live) {
-    int64_t code = codes[tok];
-    code = (code < 0 || code >= ncent) ? 0 : code;
-    const char* crow = cent + code * cent_sb + (int64_t)cc * 8 * CSZ;
-    const uint8_t* rrow = res + tok * res_st + (int64_t)cc * nbits;
-    uint64_t bits;
-    if (nbits == 2) bits = *(const uint16_t*)rrow;
-    else if (nbits == 4) bits = *(const uint32_t*)rrow;
-    else bits = *(const uint64_t*)rrow;
-    const uint32_t bmask = (1u << nbits) - 1u;
-    u32x4 cv4[CD == EK_F32 ? 2 : 1];
-    cv4[0] = *(const u32x4*)crow;
-    if constexpr (CD == EK_F32) cv4[1] = *(const u32x4*)(crow + 16);
+  for (int k = 0; k < TPT; ++k) {
+    const int64_t tok = tok0 + (int64_t)k * TPB;
+    int64_t c = tok < ntok ? codes[tok] : 0;
+    code[k] = (c < 0 || c >= ncent) ? 0 : c;
+  }
+  u32x4 cv4[TPT][NCV];
+  uint64_t bits[TPT];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float cv;
-      if constexpr (CD == EK_F32) cv = __uint_as_float(cv4[e >> 2][e & 3]);
-      else if constexpr (CD == EK_BF16)
-        cv = (e & 1) ? bf16hi_to_f32(cv4[0][e >> 1]) : bf16lo_to_f32(cv4[0][e >> 1]);
-      else
-        cv = f16_to_f32((uint16_t)((e & 1) ? (cv4[0][e >> 1] >> 16) : (cv4[0][e >> 1] & 0xffffu)));
-      uint32_t bc = (uint32_t)(bits >> (e * nbits)) & bmask;
-      bc = bc < (uint32_t)nb ? bc : (uint32_t)(nb - 1);
-      x8[e] = (cc * 8 + e) < dim ? cv + s_bw[bc] : 0.f;
+  for (int k = 0; k < TPT; ++k) {
+    const int64_t tok = tok0 + (int64_t)k * TPB;
+    const bool live = tok < ntok && cc * 8 < dim;
+    bits[k] = 0;
+#pragma unroll
+    for (int v = 0; v < NCV; ++v) cv4[k][v] = u32x4{0u, 0u, 0u, 0u};
+    if (live) {
+      const char* crow = cent + code[k] * cent_sb + (int64_t)cc * 8 * CSZ;
+      const uint8_t* rrow = res + tok * res_st + (int64_t)cc * nbits;
+      if (nbits == 2) bits[k] = *(const uint16_t*)rrow;
+      else if (nbits == 4) bits[k] = *(const uint32_t*)rrow;
+      else bits[k] = *(const uint64_t*)rrow;
+      cv4[k][0] = *(const u32x4*)crow;
+      if constexpr (CD == EK_F32) cv4[k][1] = *(const u32x4*)(crow + 16);
     }
   }
-  float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ss = fmaf(x8[e], x8[e], ss);
+  for (int k = 0; k < TPT; ++k) {
+    const int64_t tok = tok0 + (int64_t)k * TPB;
+    const bool tok_ok = tok < ntok;
+    const bool live = tok_ok && cc * 8 < dim;
+    float x8[8];
 #pragma unroll
-  for (int o = 1; o < LPT; o <<= 1) ss += __shfl_xor(ss, o);
-  // norms-only mode (out == null): the token's inverse norm, 1 / max(||x||, 1e-12),
-  // alone or after the token's code as an 8-byte (code, norm) record
-  if (inv_out) {
-    if (tok_ok && cc == 0) {
-      if (rec)
-        *(uint2*)(inv_out + 2 * tok) = uint2{(uint32_t)codes[tok], __float_as_uint(inv_norm(ss))};
-      else
-        inv_out[tok] = inv_norm(ss);
+    for (int e = 0; e < 8; ++e) x8[e] = 0.f;
+    if (live) {
+      const uint32_t bmask = (1u << nbits) - 1u;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float cv;
+        if constexpr (CD == EK_F32) cv = __uint_as_float(cv4[k][e >> 2][e & 3]);
+        else if constexpr (CD == EK_BF16)
+          cv = (e & 1) ? bf16hi_to_f32(cv4[k][0][e >> 1]) : bf16lo_to_f32(cv4[k][0][e >> 1]);
+        else
+          cv = f16_to_f32((uint16_t)((e & 1) ? (cv4[k][0][e >> 1] >> 16) : (cv4[k][0][e >> 1] & 0xffffu)));
+        uint32_t bc = (uint32_t)(bits[k] >> (e * nbits)) & bmask;
+        bc = bc < (uint32_t)nb ? bc : (uint32_t)(nb - 1);
+        x8[e] = (cc * 8 + e) < dim ? cv + s_bw[bc] : 0.f;
+      }
     }
-    return;
-  }
-  const float sc = normalize ? inv_norm(ss) : 1.f;
-  if (live) {
-    u32x4 w;
+    float ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if constexpr (OUTK == EK_F16)
-        w[e] = f32_to_f16_bits(x8[2 * e] * sc) | (f32_to_f16_bits(x8[2 * e + 1] * sc) << 16);
-      else
-        w[e] = f32_to_bf16_bits(x8[2 * e] * sc) | (f32_to_bf16_bits(x8[2 * e + 1] * sc) << 16);
+    for (int e = 0; e < 8; ++e) ss = fmaf(x8[e], x8[e], ss);
+#pragma unroll
+    for (int o = 1; o < LPT; o <<= 1) ss += __shfl_xor(ss, o);
+    // norms-only mode (out == null): the token's inverse norm, 1 / max(||x||, 1e-12),
+    // alone or after the token's code as an 8-byte (code, norm) record
+    if (inv_out) {
+      if (tok_ok && cc == 0) {
+        if (rec)
+          *(uint2*)(inv_out + 2 * tok) = uint2{(uint32_t)codes[tok], __float_as_uint(inv_norm(ss))};
+        else
+          inv_out[tok] = inv_norm(ss);
+      }
+      continue;
     }
-    *(u32x4*)(out + tok * out_stride + cc * 8) = w;
+    const float sc = normalize ? inv_norm(ss) : 1.f;
+    if (live) {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (OUTK == EK_F16)
+          w[e] = f32_to_f16_bits(x8[2 * e] * sc) | (f32_to_f16_bits(x8[2 * e + 1] * sc) << 16);
+        else
+          w[e] = f32_to_bf16_bits(x8[2 * e] * sc) | (f32_to_bf16_bits(x8[2 * e + 1] * sc) << 16);
+      }
+      *(u32x4*)(out + tok * out_stride + cc * 8) = w;
+    }
   }
 }
 
 template <int LPT, int CD>
 int launch_decode_cd(int outk, const lik_plaid_docs_t* d, const int32_t* codes, const uint8_t* res, int norm,
                      uint16_t* out, int64_t out_stride, int64_t ntok, float* inv_out, int rec, hipStream_t s) {
-  constexpr int TPB = 256 / LPT;
+  constexpr int TPW = 256 / LPT * kDecodeTPT;  // tokens per workgroup
   const int ceb = CD == EK_F32 ? 4 : 2;
-  const dim3 grid((unsigned)((ntok + TPB - 1) / TPB));
+  const dim3 grid((unsigned)((ntok + TPW - 1) / TPW));
   if (outk == EK_F16)
     hipLaunchKernelGGL((plaid_decode_kernel<LPT, CD, EK_F16>), grid, dim3(256), 0, s, codes, res, d->res_stride_tok,
                        (const char*)d->centroids, d->cent_stride * ceb, d->n_centroids, d->bucket_weights,

@@ -551,8 +551,10 @@ __device__ __forceinline__ bool scan_steps(F& f, int c, int n) {
 // LS tiles in flight per wavefront: 3 at three waves per SIMD, 2 at four.
 // REC: tinv points at (code, inverse norm) records of 8 bytes per token
 // (lik_plaid_token_t), read in place of the codes and the norms by one load.
-template <int EK, int DPAD, int NBITS, bool FULLD, bool NORMD, int LS, bool REC>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 2 ? 4 : 3)))
+// QN: queries per wavefront (2 with records: both score the same residual
+// bytes and records, each from its own table; two waves per SIMD).
+template <int EK, int DPAD, int NBITS, bool FULLD, bool NORMD, int LS, bool REC, int QN = 1>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(QN == 2 ? 2 : (LS == 2 ? 4 : 3))))
     plaid_scan_kernel(const Params p, const uint16_t* __restrict__ qc, int64_t qc_qs, const float* __restrict__ tinv) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;
@@ -564,9 +566,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   constexpr uint32_t NT = 2;  // non-temporal cache policy of the streamed loads
   constexpr float NEG_INF = -__builtin_huge_valf();
   static_assert(RW == 2 || RW % 4 == 0, "residual lane bytes");
+  static_assert(QN == 1 || (QN == 2 && REC), "two queries per wavefront with records only");
 
   __shared__ __attribute__((aligned(16))) float s_lut[2 * 256];
-  __shared__ float s_out[4][kQcRMax];
+  __shared__ float s_out[4][QN][kQcRMax];
   __shared__ int32_t s_cu[4][kQcRMax + 1];
   for (int v = threadIdx.x; v < 256; v += 256) {
     uint32_t h16[4] = {0u, 0u, 0u, 0u};
@@ -588,19 +591,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   const int64_t g = wv / p.NR, r = wv - g * p.NR;
   if (g >= p.ngroups) return;  // wave-uniform, after the only barrier
 
-  // ---- query g: token l32 as the A rows (the B columns of the other
-  // kernels), scaled by its inverse norm before rounding (0 past its length),
-  // so the accumulators are q^.r and the table holds q^.c ----
-  u32x4 aq[KS];
-  {
-    const bool valid = g < p.q.n && l32 < seq_len(p.q, g);
-    const char* rowp = valid ? seq_row0(p.q, g) + (int64_t)l32 * p.q.sl_b : nullptr;
+  // ---- queries g QN + sub: token l32 as the A rows (the B columns of the
+  // other kernels), scaled by its inverse norm before rounding (0 past its
+  // length), so the accumulators are q^.r and the table holds q^.c ----
+  u32x4 aq[QN][KS];
+#pragma unroll
+  for (int sub = 0; sub < QN; ++sub) {
+    const int64_t q = g * QN + sub;
+    const bool valid = q < p.q.n && l32 < seq_len(p.q, q);
+    const char* rowp = valid ? seq_row0(p.q, q) + (int64_t)l32 * p.q.sl_b : nullptr;
     float ss = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int e = h * HALF + ks * 8;
-      aq[ks] = (valid && (FULLD || e < p.q.dim)) ? *(const u32x4*)(rowp + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
-      if (p.normalize & 1) ss += chunk_sumsq<EK>(aq[ks]);
+      aq[sub][ks] = (valid && (FULLD || e < p.q.dim)) ? *(const u32x4*)(rowp + (int64_t)e * 2) : (u32x4){0u, 0u, 0u, 0u};
+      if (p.normalize & 1) ss += chunk_sumsq<EK>(aq[sub][ks]);
     }
     ss += __shfl_xor(ss, 32);
     const float sc = valid ? ((p.normalize & 1) ? inv_norm(ss) : 1.f) : 0.f;
@@ -608,14 +613,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const uint32_t x = aq[ks][w];
+        const uint32_t x = aq[sub][ks][w];
         if constexpr (EK == EK_F16)
-          aq[ks][w] = f32_to_f16_bits(f16_to_f32((uint16_t)(x & 0xffffu)) * sc) |
-                      (f32_to_f16_bits(f16_to_f32((uint16_t)(x >> 16)) * sc) << 16);
+          aq[sub][ks][w] = f32_to_f16_bits(f16_to_f32((uint16_t)(x & 0xffffu)) * sc) |
+                           (f32_to_f16_bits(f16_to_f32((uint16_t)(x >> 16)) * sc) << 16);
         else
-          aq[ks][w] = f32_to_bf16_bits(bf16lo_to_f32(x) * sc) | (f32_to_bf16_bits(bf16hi_to_f32(x) * sc) << 16);
+          aq[sub][ks][w] = f32_to_bf16_bits(bf16lo_to_f32(x) * sc) | (f32_to_bf16_bits(bf16hi_to_f32(x) * sc) << 16);
       }
-      asm volatile("" : "+v"(aq[ks]));
+      asm volatile("" : "+v"(aq[sub][ks]));
     }
   }
 
@@ -634,7 +639,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   const char* res_p = (const char*)p.pl.res + (int64_t)T0 * p.pl.res_st;
   const float* inv_p = (NORMD && !REC) ? tinv + T0 : nullptr;
   const int64_t res_tile = 32 * p.pl.res_st;
-  const __amdgpu_buffer_rsrc_t rtab = make_rsrc(qc + g * qc_qs, (uint32_t)(p.pl.ncent * 64));
   const uint32_t res_lane = (uint32_t)(l32 * p.pl.res_st + h * RBL);
   auto rows_of = [&](int i) {
     const int rem = span - 32 * i;
@@ -660,15 +664,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
                  (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32) & 0xffffu),
                  (uint32_t)__builtin_amdgcn_readfirstlane(nbytes), 0x00020000u};
   };
-  const u32x4 dtab = desc(qc + g * qc_qs, (uint32_t)(p.pl.ncent * 64));
+  // the queries' tables (a query past the batch reads zeros: record count 0)
+  u32x4 dtab[QN];
+#pragma unroll
+  for (int sub = 0; sub < QN; ++sub) {
+    const int64_t q = g * QN + sub;
+    dtab[sub] = desc(qc + (q < p.q.n ? q : 0) * qc_qs, q < p.q.n ? (uint32_t)(p.pl.ncent * 64) : 0u);
+  }
 
   struct Stage {
     u32x4 rw[RW == 2 ? 1 : RW / 4];  // residual bytes (RW == 2: the low half of rw[0])
     float inv;
-    u32x4 tq[2];  // the table's 16 fp16 values of this lane's half, in element order
+    u32x4 tq[QN][2];  // each table's 16 fp16 values of this lane's half, in element order
   };
-  // loads per tile (residual, inverse norm, table) and per code
-  constexpr int NLT = (RW == 2 ? 1 : RW / 4) + ((NORMD && !REC) ? 1 : 0) + 2;
+  // loads per tile (residual, inverse norm, tables) and per code
+  constexpr int NLT = (RW == 2 ? 1 : RW / 4) + ((NORMD && !REC) ? 1 : 0) + 2 * QN;
   Stage st[LS];
   uint32_t code[LC];  // (without records)
 #pragma unroll
@@ -676,7 +686,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
 #pragma unroll
     for (int v = 0; v < (RW == 2 ? 1 : RW / 4); ++v) st[k].rw[v] = u32x4{0u, 0u, 0u, 0u};
     st[k].inv = 1.f;
-    st[k].tq[0] = st[k].tq[1] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub) st[k].tq[sub][0] = st[k].tq[sub][1] = u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
   for (int k = 0; k < LC; ++k) code[k] = 0u;
@@ -722,8 +733,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     const uint32_t qoff = (uint32_t)(lane >> 4) * 16u;
     const uint32_t ta = (cs[0] < (uint32_t)p.pl.ncent ? cs[0] : 0u) * 64u + qoff;
     const uint32_t tb = (cs[1] < (uint32_t)p.pl.ncent ? cs[1] : 0u) * 64u + qoff;
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(s.tq[0]) : "v"(ta), "s"(dtab));
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(s.tq[1]) : "v"(tb), "s"(dtab));
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub) {
+      asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(s.tq[sub][0]) : "v"(ta), "s"(dtab[sub]));
+      asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "+v"(s.tq[sub][1]) : "v"(tb), "s"(dtab[sub]));
+    }
   };
   // Lane (l32, h) holds, of tokens l32 % 16 and l32 % 16 + 16, table quarter
   // 2 h + l32 / 16; one v_permlane16_swap per dword (odd rows of tq[0] with
@@ -731,16 +745,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   // 16 values of its half, in element order.
   auto unswap_table = [](Stage& s) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const auto sw = __builtin_amdgcn_permlane16_swap(s.tq[0][k], s.tq[1][k], false, false);
-      s.tq[0][k] = sw[0];
-      s.tq[1][k] = sw[1];
-    }
+    for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(s.tq[sub][0][k], s.tq[sub][1][k], false, false);
+        s.tq[sub][0][k] = sw[0];
+        s.tq[sub][1][k] = sw[1];
+      }
   };
   // wait until at most n loads are in flight, for the registers of stage s
   auto wait_stage = [](auto NN, Stage& s) {
     constexpr int n = decltype(NN)::value;
-    asm volatile("s_waitcnt vmcnt(%[n])" : "+v"(s.inv), "+v"(s.tq[0]), "+v"(s.tq[1]) : [n] "n"(n));
+    asm volatile("s_waitcnt vmcnt(%[n])" : "+v"(s.inv), "+v"(s.tq[0][0]), "+v"(s.tq[0][1]) : [n] "n"(n));
+#pragma unroll
+    for (int sub = 1; sub < QN; ++sub) asm volatile("" : "+v"(s.tq[sub][0]), "+v"(s.tq[sub][1]));
 #pragma unroll
     for (int k = 0; k < (RW == 2 ? 1 : RW / 4); ++k) asm volatile("" : "+v"(s.rw[k]));
   };
@@ -748,9 +766,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
     asm volatile("s_waitcnt vmcnt(%1)" : "+v"(c) : "n"(decltype(NN)::value));
   };
 
-  float m[16];
+  float m[QN][16];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) m[e] = NEG_INF;
+  for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) m[sub][e] = NEG_INF;
   int jc = 0;
   int ec = __builtin_amdgcn_readfirstlane(s_cu[wl][1]) - T0;
   // doc jc ends: max over its lanes by a transposing butterfly (after the
@@ -765,12 +785,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   };
   using std::integral_constant;
   auto doc_end = [&]() {
+#pragma unroll
+   for (int sub = 0; sub < QN; ++sub) {
     float x[16];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       // rows 0/1 and 2/3 swap: x[i] gets element i of lanes l, l^16 on even
       // rows and element i + 8 on odd rows
-      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(m[i]), __float_as_uint(m[i + 8]), false, false);
+      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(m[sub][i]), __float_as_uint(m[sub][i + 8]), false, false);
       x[i] = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
     }
     auto step = [&](int n, int bit, auto CTRL) {
@@ -798,9 +820,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
       v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
-    if (lane == 0) s_out[wl][jc] = v * p.out_scale;
+    if (lane == 0) s_out[wl][sub][jc] = v * p.out_scale;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) m[e] = NEG_INF;
+    for (int e = 0; e < 16; ++e) m[sub][e] = NEG_INF;
+   }
     ++jc;
     ec = jc < nd ? __builtin_amdgcn_readfirstlane(s_cu[wl][jc + 1]) - T0 : 0x7fffffff;
   };
@@ -814,7 +837,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   };
   auto compute = [&](int i, const Stage& s) {
     const int TT = 32 * i;
-    f32x16 acc;
+    f32x16 acc[QN];
     auto byte_at = [&](int byte_i) -> uint32_t {
       return (s.rw[byte_i >> 4][(byte_i >> 2) & 3] >> ((byte_i & 3) * 8)) & 0xffu;
     };
@@ -838,17 +861,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
       if constexpr (!FULLD) {
         if ((h * HALF + ks * 8) >= p.q.dim) rv = (u32x4){0u, 0u, 0u, 0u};
       }
-      acc = mfma32<EK>(ks == 0 ? f32x16{} : acc, &aq[ks], &rv);
+#pragma unroll
+      for (int sub = 0; sub < QN; ++sub) acc[sub] = mfma32<EK>(ks == 0 ? f32x16{} : acc[sub], &aq[sub][ks], &rv);
     }
     // the tile's scores, in place of the accumulators
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint32_t w = s.tq[e >> 3][(e >> 1) & 3];
-      acc[e] = ((e & 1) ? fma_mix(acc[e], 1.f, w, std::true_type{}) : fma_mix(acc[e], 1.f, w, std::false_type{})) * s.inv;
-    }
+    for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t w = s.tq[sub][e >> 3][(e >> 1) & 3];
+        acc[sub][e] = ((e & 1) ? fma_mix(acc[sub][e], 1.f, w, std::true_type{})
+                               : fma_mix(acc[sub][e], 1.f, w, std::false_type{})) * s.inv;
+      }
     if (ec - TT > 32) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) m[e] = max_nan(m[e], acc[e]);
+      for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m[sub][e] = max_nan(m[sub][e], acc[sub][e]);
       return;
     }
     int a = 0;
@@ -856,7 +885,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
       const int b = ec - TT < 32 ? ec - TT : 32;
       const bool in = l32 >= a && l32 < b;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) m[e] = max_nan(m[e], in ? acc[e] : NEG_INF);
+      for (int sub = 0; sub < QN; ++sub)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m[sub][e] = max_nan(m[sub][e], in ? acc[sub][e] : NEG_INF);
       if (ec - TT > 32 || jc >= nd) break;
       doc_end();
       a = b;
@@ -907,7 +938,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
       }
       // ordering point: the stage's previous contents are all read (they feed m)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(m[e]));
+      for (int e = 0; e < 16 * QN; ++e) asm volatile("" : "+v"(m[e / 16][e % 16]));
       if constexpr ((I & 1) != 0) load_pair(c + 5, pr[I / 2]);
       asm volatile("s_waitcnt vmcnt(%1)" : "+v"(pr[J / 2]) : "n"((I & 1) ? 2 * NLT + 1 : 3 * NLT + 1));
       load_tile(c + 3, half(pr[J / 2][0], integral_constant<bool, (J & 1) != 0>{}), st[I % 3]);
@@ -940,7 +971,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
       }
       // ordering point: the stage's previous contents are all read (they feed m)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(m[e]));
+      for (int e = 0; e < 16 * QN; ++e) asm volatile("" : "+v"(m[e / 16][e % 16]));
       // the code of tile c + LS, loaded right after tile c's loads
       wait_code(integral_constant<int, kWaitTile - 1>{}, code[(I + LS) % LC]);
       load_tile(c + LS, bcast(code[(I + LS) % LC]), st[I % LS]);
@@ -954,7 +985,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LS == 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_wave_barrier();
   for (int k = lane; k < nd; k += 64)
-    if (g < p.q.n) p.out[g * p.osq + (j0 + k) * p.osd] = s_out[wl][k];
+#pragma unroll
+    for (int sub = 0; sub < QN; ++sub) {
+      const int64_t q = g * QN + sub;
+      if (q < p.q.n) p.out[q * p.osq + (j0 + k) * p.osd] = s_out[wl][sub][k];
+    }
 }
 
 // out[q, j] = 0 for a query batch without tokens (Lq == 0)
@@ -995,7 +1030,7 @@ constexpr bool scan_reg_ok() {
 }
 
 template <int EK, int DPAD, int NBITS>
-int launch_scan(const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, bool rec, bool norm_d,
+int launch_scan(int qn, const Params& p, const uint16_t* qc, int64_t qc_qs, const float* tinv, bool rec, bool norm_d,
                 hipStream_t s) {
   if constexpr (!scan_reg_ok<DPAD, NBITS>()) {
     return LIK_ERR_UNSUPPORTED;
@@ -1009,6 +1044,14 @@ int launch_scan(const Params& p, const uint16_t* qc, int64_t qc_qs, const float*
   };
   const bool full = p.q.dim == DPAD;
   constexpr int LS = kScanLS;
+  if (rec && qn == 2) {
+    if (norm_d)
+      return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, true, LS, true, 2>)
+                  : go(plaid_scan_kernel<EK, DPAD, NBITS, false, true, LS, true, 2>);
+    return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, false, LS, true, 2>)
+                : go(plaid_scan_kernel<EK, DPAD, NBITS, false, false, LS, true, 2>);
+  }
+  if (qn != 1) return LIK_ERR_UNSUPPORTED;
   if (rec) {
     if (norm_d)
       return full ? go(plaid_scan_kernel<EK, DPAD, NBITS, true, true, LS, true>)
@@ -1025,26 +1068,24 @@ int launch_scan(const Params& p, const uint16_t* qc, int64_t qc_qs, const float*
 }
 
 template <int EK, int DPAD>
-int launch_qc(int qn, const Params& p, uint16_t* qc, int64_t qc_qs, const float* tinv, bool rec, bool norm_d,
-              hipStream_t s, const lik_launch_opts_t* opts) {
+int launch_qc(int qn, bool reg, const Params& p, uint16_t* qc, int64_t qc_qs, const float* tinv, bool rec,
+              bool norm_d, hipStream_t s, const lik_launch_opts_t* opts) {
   const int64_t ntile = (p.pl.ncent + 31) / 32;
   const int64_t waves = p.q.n * ntile;
   if ((waves + 3) / 4 > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
   // one query per wavefront: the register-direct scan, unless the caller
   // forces the LDS-staged one (plaid_variant 5)
-  const bool reg = qn == 1 && !(opts && opts->plaid_variant == 5) &&
-                   (p.pl.nbits == 2 || (p.pl.nbits == 4 && DPAD == 64));
   hipLaunchKernelGGL((centroid_scores_kernel<EK, DPAD>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, qc,
                      qc_qs, ntile, reg ? 1 : 0);
   if (hipGetLastError() != hipSuccess) return LIK_ERR_LAUNCH;
   TimingScope ts(opts);
   int rc;
   switch (p.pl.nbits) {
-    case 2: rc = reg ? launch_scan<EK, DPAD, 2>(p, qc, qc_qs, tinv, rec, norm_d, s)
+    case 2: rc = reg ? launch_scan<EK, DPAD, 2>(qn, p, qc, qc_qs, tinv, rec, norm_d, s)
                  : launch_qc_scan<EK, DPAD, 2>(qn, p, qc, qc_qs, tinv, rec, norm_d, s); break;
-    case 4: rc = reg ? launch_scan<EK, DPAD, 4>(p, qc, qc_qs, tinv, rec, norm_d, s)
+    case 4: rc = reg ? launch_scan<EK, DPAD, 4>(qn, p, qc, qc_qs, tinv, rec, norm_d, s)
                  : launch_qc_scan<EK, DPAD, 4>(qn, p, qc, qc_qs, tinv, rec, norm_d, s); break;
-    case 8: rc = reg ? launch_scan<EK, DPAD, 8>(p, qc, qc_qs, tinv, rec, norm_d, s)
+    case 8: rc = reg ? launch_scan<EK, DPAD, 8>(qn, p, qc, qc_qs, tinv, rec, norm_d, s)
                  : launch_qc_scan<EK, DPAD, 8>(qn, p, qc, qc_qs, tinv, rec, norm_d, s); break;
     default: rc = LIK_ERR_UNSUPPORTED;
   }
@@ -1137,13 +1178,15 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   p.osq = out_stride_q;
   p.osd = out_stride_d;
   p.LU = (int)Q->len;
-  // One query per wavefront on the register-direct scan wherever it applies
-  // (2-bit residuals, or 4-bit at d <= 64; measured faster per query than
-  // two queries per wavefront on the LDS-staged scan: 2.25 against 2.56 ms
-  // at 8 queries, C5 corpus); else two queries per wavefront when there are
+  // The register-direct scan wherever it applies (2-bit residuals, or 4-bit
+  // at d <= 64): one query per wavefront from separate codes and norms
+  // (faster per query than two queries per wavefront on the LDS-staged scan:
+  // 2.25 against 2.56 ms at 8 queries, C5 corpus), two with token records
+  // (they share each tile's residual bytes and records: 2.08 ms per query).
+  // Otherwise the LDS-staged scan, two queries per wavefront when there are
   // several.
   const bool reg_ok = !(opts && opts->plaid_variant == 5) && (docs->nbits == 2 || (docs->nbits == 4 && dpad == 64));
-  const int qn = (reg_ok || Q->n < 2) ? 1 : 2;
+  const int qn = Q->n < 2 ? 1 : reg_ok ? (rec ? 2 : 1) : 2;
   p.ngroups = (Q->n + qn - 1) / qn;
   // ~16k wavefronts over the corpus, at most kQcRMax docs each
   int64_t R = (docs->n + 16383) / 16384;
@@ -1157,8 +1200,8 @@ extern "C" int lik_plaid_maxsim_qc(const lik_seqs_t* Q, const lik_plaid_docs_t* 
   const float* tinv = rec ? token_inv : norm_d ? token_inv : nullptr;
   hipStream_t s = (hipStream_t)stream;
   if (Q->dtype == LIK_BF16)
-    return dpad == 64 ? launch_qc<EK_BF16, 64>(qn, p, qc, qc_qs, tinv, rec, norm_d, s, opts)
-                      : launch_qc<EK_BF16, 128>(qn, p, qc, qc_qs, tinv, rec, norm_d, s, opts);
-  return dpad == 64 ? launch_qc<EK_F16, 64>(qn, p, qc, qc_qs, tinv, rec, norm_d, s, opts)
-                    : launch_qc<EK_F16, 128>(qn, p, qc, qc_qs, tinv, rec, norm_d, s, opts);
+    return dpad == 64 ? launch_qc<EK_BF16, 64>(qn, reg_ok, p, qc, qc_qs, tinv, rec, norm_d, s, opts)
+                      : launch_qc<EK_BF16, 128>(qn, reg_ok, p, qc, qc_qs, tinv, rec, norm_d, s, opts);
+  return dpad == 64 ? launch_qc<EK_F16, 64>(qn, reg_ok, p, qc, qc_qs, tinv, rec, norm_d, s, opts)
+                    : launch_qc<EK_F16, 128>(qn, reg_ok, p, qc, qc_qs, tinv, rec, norm_d, s, opts);
 }

@@ -94,9 +94,9 @@ typedef struct {
  *       decode, 2 exact LDS-gather decode (bitwise equal to the tile
  *       kernel), 3 the tile kernel (no stream kernel). lik_plaid_maxsim_qc:
  *       0 automatic, 5 the LDS-staged scan (two queries per wavefront when
- *       there are several) instead of the register-direct one (one query per
- *       wavefront, the automatic choice for 2-bit residuals and for 4-bit
- *       residuals at d <= 64).
+ *       there are several) instead of the register-direct one (the automatic
+ *       choice for 2-bit residuals and for 4-bit residuals at d <= 64: one
+ *       query per wavefront, two with LIK_TOKEN_RECORDS).
  *   timing_start, timing_stop: hipEvent_t or NULL. When both are set, the
  *       call's MaxSim scoring launches carry them in their own dispatches
  *       (hipExtLaunchKernel): timing_start records the start of the first

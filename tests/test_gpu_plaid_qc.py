@@ -20,8 +20,9 @@ lik_plaid_token_records / lik_plaid_token_norms + lik_plaid_maxsim_qc).
   bitwise lik_plaid_token_norms' value (also when written in two token
   ranges), and scores from the records equal
   bitwise the scores from the separate codes and norms, on the register scan
-  (one query per wavefront) and the LDS-staged scan (plaid_variant 5, and
-  the residual widths the register scan does not take),
+  (two queries per wavefront with records, one without: the same arithmetic
+  per query) and the LDS-staged scan (plaid_variant 5, and the residual
+  widths the register scan does not take),
   with and without normalisation; the C ABI rejects a missing or misaligned
   record pointer.
 """

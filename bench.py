@@ -948,7 +948,7 @@ def main() -> None:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's hot path runs on a single MI355X "
-              "(multi-GPU sharding is described in DESIGN.md, not built). Use --gpus 1.", file=sys.stderr)
+              "(multi-GPU sharding is designed, not built). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if args.workload != "inbatch":
         args.cpu_baseline = False  # the CPU baseline is defined on the default workload

@@ -539,7 +539,9 @@ class ResidualIndex:
 
     @property
     def token_inv(self) -> torch.Tensor:
-        """``[T]`` fp32 inverse norms of the tokens (a strided view of the records)."""
+        """``[T]`` fp32 inverse norms of the tokens: a strided view of the
+        records (C-ABI callers pass ``token_rec`` with ``LIK_TOKEN_RECORDS``,
+        or a contiguous copy of this view without it)."""
         return self.token_rec[:, 1].view(torch.float32)
 
     def _docs(self) -> _lib.LikPlaidDocs:

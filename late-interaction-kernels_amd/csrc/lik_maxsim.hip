@@ -392,6 +392,7 @@ int pick_R(int64_t ngroups, int64_t ndocs, int dpad, const lik_launch_opts_t* op
 
 int launch_dense(int dt, const Plan& pl, const Params& p, int64_t nb, hipStream_t s) {
   if (p.amax) {
+    if (q1_eligible(dt, pl, p)) return launch_q1(dt, pl, p, s);
     switch (dt) {
       case LIK_BF16: return launch_dense_train_bf16(pl, p, nb, s);
       case LIK_F16: return launch_dense_train_f16(pl, p, nb, s);

@@ -38,11 +38,18 @@ constexpr int kQ1RMax = 128;  // docs per wavefront (the host routes larger R to
 constexpr int kQ1Scores = 256;  // doc scores per wavefront held until the loop ends (docs x units)
 
 // two workgroups per CU (their LDS rings take 2 x 64 KB): two waves per SIMD
-template <int EK, int DPAD, bool FULLD, bool NORMQ>
+// EXT (256-byte rows): with p.amax (the training forward) also the winner
+// doc-token index per (query token, doc), and with p.normalize & 2 the doc
+// rows L2-normalised in registers before their MFMAs, bitwise as the tile
+// kernel does it (a row's 16 chunk sums of squares added as a balanced tree
+// in chunk order: each lane holds chunks 0..7 or 8..15 of its row, the two
+// halves meet by one lane swap; scaled in fp32 and rounded once).
+template <int EK, int DPAD, bool FULLD, bool NORMQ, bool EXT = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) maxsim_q1_kernel(const Params p) {
   using T = KT<EK, DPAD>;
   constexpr int KS = T::KSTEPS;
   static_assert(T::FRAG_V == 1 && !T::SPLIT && T::IN_B == 2 && DPAD >= 64 && DPAD <= 512, "16-bit rows");
+  static_assert(!EXT || DPAD == 128, "argmax and doc normalise take 256-byte rows");
   // The ring moves units of 32 rows: a whole tile for rows of <= 256 bytes;
   // wider rows (d 256, 512) are split into NU units of 256 bytes per row,
   // unit c holding bytes [128 c, 128 c + 128) of each half row, which are
@@ -162,8 +169,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
             ((int64_t)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)o >> 32)) << 32);
   };
   struct Desc {
-    int nv, k;
-    bool docend;  // last unit of the doc's last tile
+    int nv, k, t;  // valid rows, local doc, tile of the doc
+    bool docend;   // last unit of the doc's last tile
   };
   // DMA of unit CU of the cursor's tile into ring slot S (exactly NI load
   // instructions, whether or not the tile exists); after the tile's last
@@ -174,6 +181,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
     const int rem = c.len - 32 * c.t;
     d.nv = rem < 32 ? rem : 32;
     d.k = c.k;
+    d.t = c.t;
     const bool tile_end = c.len > 0 && rem <= 32;
     d.docend = tile_end && CU == NU - 1;
     // the buffer covers rows [32 t, len) of the doc: later rows read 0
@@ -208,9 +216,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
   };
 
   float m = NEG_INF;
+  int mi = -1;  // argmax: doc-token index of m (-1: no valid token yet)
   // a doc ends: column maxima (max over lanes l, l ^ 32) summed per unit in
   // the tile kernel's flush order, written by lane 0
   auto doc_end = [&](int k) {
+    if (EXT && p.amax) {
+      // winner over lanes l, l ^ 32 (larger value; equal values: lower
+      // index), at argmax[(q * docs + j) * Lq + token], -1 for a non-finite max
+      const auto sv = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+      const auto si = __builtin_amdgcn_permlane32_swap((uint32_t)mi, (uint32_t)mi, false, false);
+      const float v0 = __uint_as_float(sv[0]), v1 = __uint_as_float(sv[1]);
+      const int i0 = (int)si[0], i1 = (int)si[1];
+      const bool take1 = v1 > v0 || (v1 == v0 && (unsigned)i1 < (unsigned)i0);
+      const int win = take1 ? i1 : i0;
+      const int ul = l32 / p.LU;
+      if (h == 0 && ul < p.QPG) {
+        const int64_t u = g * p.QPG + ul;
+        const int64_t q = u / p.nc;
+        const int64_t tok = p.q_tok0 + (u - q * p.nc) * p.LU + (l32 - ul * p.LU);
+        if (u < p.nunits && tok < p.amax_ld)
+          p.amax[(q * p.amax_qs + jl0 + k) * p.amax_ld + tok] = __builtin_isfinite(max_nan(v0, v1)) ? win : -1;
+      }
+      mi = -1;
+    }
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
     const float mm = max_nan(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
     const float v = __builtin_isfinite(mm) ? (NORMQ ? mm * qsc : mm) : 0.f;
@@ -252,6 +280,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
     // the fragments are in registers before the DMA overwrites the slot
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const Desc dn = fetch(SS, CN, c);
+    if constexpr (EXT) {
+      if (p.normalize & 2) {
+        float cs[KSU];
+#pragma unroll
+        for (int ks = 0; ks < KSU; ++ks) cs[ks] = chunk_sumsq<EK>(af[ks]);
+#pragma unroll
+        for (int w = 1; w < KSU; w <<= 1)
+#pragma unroll
+          for (int c0 = 0; c0 < KSU; c0 += 2 * w) cs[c0] = cs[c0] + cs[c0 + w];
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(cs[0]), __float_as_uint(cs[0]), false, false);
+        const float sc = inv_norm(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+#pragma unroll
+        for (int ks = 0; ks < KSU; ++ks)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t v = af[ks][e];
+            if constexpr (EK == EK_BF16)
+              af[ks][e] = f32_to_bf16_bits(bf16lo_to_f32(v) * sc) | (f32_to_bf16_bits(bf16hi_to_f32(v) * sc) << 16);
+            else
+              af[ks][e] = f32_to_f16_bits(f16_to_f32((uint16_t)(v & 0xffffu)) * sc) |
+                          (f32_to_f16_bits(f16_to_f32((uint16_t)(v >> 16)) * sc) << 16);
+          }
+      }
+    }
 #pragma unroll
     for (int ks = 0; ks < KSU; ++ks)
       acc = mfma32<EK>(CU == 0 && ks == 0 ? f32x16{} : acc, &af[ks], &bq[CU * KSU + ks]);
@@ -263,8 +315,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
         for (int e = 0; e < 16; ++e)
           if (8 * (e >> 2) + (e & 3) >= lim) acc[e] = NEG_INF;
       }
+      if (EXT && p.amax) {
+        // rows in increasing order; only a strictly larger value replaces
+        // the winner, so ties keep the lowest doc-token index
+        const int r0 = 32 * d.t + 4 * h;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) m = max_nan(m, acc[e]);
+        for (int e = 0; e < 16; ++e) {
+          mi = acc[e] > m ? r0 + 8 * (e >> 2) + (e & 3) : mi;
+          m = max_nan(m, acc[e]);  // a NaN row makes the max NaN (scored 0, argmax -1)
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) m = max_nan(m, acc[e]);
+      }
       if (d.docend) doc_end(d.k);
     }
     return dn;
@@ -316,6 +379,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) m
 
 template <int EK, int DPAD>
 int launch_q1_t(const Params& p, bool normq, hipStream_t s) {
+  if constexpr (DPAD == 128) {
+    if (p.amax || (p.normalize & 2)) {
+      const int64_t waves = p.ngroups * p.NR;
+      const int64_t nb = (waves + 3) / 4;
+      if (nb <= 0) return LIK_OK;
+      if (nb > 0x7fffffffLL) return LIK_ERR_UNSUPPORTED;
+      auto go = [&](auto kern) {
+        launch_kernel(kern, dim3((unsigned)nb), dim3(256), 0, s, p);
+        return hipGetLastError() == hipSuccess ? LIK_OK : LIK_ERR_LAUNCH;
+      };
+      const bool full = p.d.dim == DPAD && p.q.dim == DPAD;
+      if (full)
+        return normq ? go(maxsim_q1_kernel<EK, DPAD, true, true, true>) : go(maxsim_q1_kernel<EK, DPAD, true, false, true>);
+      return normq ? go(maxsim_q1_kernel<EK, DPAD, false, true, true>) : go(maxsim_q1_kernel<EK, DPAD, false, false, true>);
+    }
+  }
+  if (p.amax || (p.normalize & 2)) return LIK_ERR_UNSUPPORTED;
   const int64_t waves = p.ngroups * p.NR;
   const int64_t nb = (waves + 3) / 4;
   if (nb <= 0) return LIK_OK;
@@ -342,9 +422,10 @@ int q1_docs_per_wave(const Params& p) {
 // Routed here: 16-bit dense scoring in which one 32-column block holds the
 // columns of a group as planned (W = 1 plans, the KD layout) or of the
 // call's only group (a one-query call whose plan is wider), with nothing in
-// the tile loop beyond the plain max (no doc mask holes, token scales, doc
-// normalisation, argmax, pair lists or query-chunk accumulation), unless the
-// caller forced a column block of several waves (lik_launch_opts_t). (Two
+// the tile loop beyond the plain max (no doc mask holes, token scales, pair
+// lists or query-chunk accumulation; doc normalisation and argmax at
+// 256-byte rows only), unless the caller forced a column block of several
+// waves (lik_launch_opts_t). (Two
 // and four blocks per wavefront for queries of up to 128 tokens measured
 // slower than the tile kernel's four waves sharing a tile.)
 bool q1_eligible(int dt, const Plan& pl, const Params& p) {
@@ -352,7 +433,8 @@ bool q1_eligible(int dt, const Plan& pl, const Params& p) {
                          ((int64_t)pl.QPG * pl.LU <= 32) || (pl.ngroups == 1 && pl.nunits * pl.LU <= 32);
   return (dt == LIK_BF16 || dt == LIK_F16) && one_block && pl.dpad >= 64 && pl.dpad <= 512 &&
          ((uintptr_t)p.d.data) % 16 == 0 && p.d.sl_b % 16 == 0 && (p.d.cu || p.d.sn_b % 16 == 0) &&
-         !p.amax && !p.pair_q && !p.pair_d && !p.d.mask && !p.d.ts && !p.q.ts && !(p.normalize & 2) &&
+         ((!p.amax && !(p.normalize & 2)) || pl.dpad == 128) && !p.pair_q && !p.pair_d && !p.d.mask && !p.d.ts &&
+         !p.q.ts &&
          !p.scale_q && !p.scale_d && p.doc_filter != 2 && !p.accumulate &&
          (int64_t)q1_docs_per_wave(p) * pl.QPG <= kQ1Scores && p.forced_w <= 1;
 }

@@ -9,6 +9,13 @@ no workgroup barriers.
   a block, Lq = 16).
 * Against the float64 oracle (lik_oracle.maxsim / maxsim_kd / maxsim_varlen,
   reference.py:26-98) on the same 16-bit values within 1e-4.
+* The training forward (argmax) and doc normalisation at d = 128 run here
+  too: KD-layout winner indices equal, bitwise, those of the same queries
+  scored against all docs on the tile kernel (two queries, docs
+  pre-normalised there by its pre-pass), and so do the scores of the
+  query whose column sums start at the same chunk (the other: within fp32
+  reordering), with query masks, prefix masks at the tile edges and a NaN
+  doc token (score 0, winner -1).
 * Doc lengths around the tile edges (0, 1, 31, 32, 33, 63, 64, 65, Ld),
   masks with holes (their docs go to the masked tile kernel in the same
   call), query-only normalisation, d = 128 and 64 (full 256- and 128-byte
@@ -212,3 +219,35 @@ def test_one_query_c3_scale():
         assert rel_err(_np(got[:, j:j + 1]), ref) < 1e-4, j
     del Dp
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("norm", [0, 1, 2, 3])
+def test_kd_training_forward_matches_tile_kernel(dtype, norm):
+    from late_interaction_kernels._core import dense_maxsim_train
+
+    _case(f"q1 kd training forward {dtype} norm={norm}")
+    g = torch.Generator().manual_seed(11 + norm)
+    Nq, K, Lq, Ld, d = 2, 40, 32, 130, 128
+    Q = torch.randn(Nq, Lq, d, generator=g).to(dtype)
+    D = (torch.randn(Nq * K, Ld, d, generator=g) * 3.0).to(dtype)
+    D[7, 3, 5] = float("nan")  # doc 7: every query token's max is NaN
+    dm = torch.arange(Ld)[None] < _lens((Nq * K,), Ld, g)[:, None]
+    dm[7, :10] = True
+    qm = torch.arange(Lq)[None] < torch.tensor([32, 21])[:, None]
+    args = (Q.cuda(), D.cuda(), qm.cuda(), dm.cuda())
+    s_kd, am_kd = dense_maxsim_train(*args, norm=norm, kd=True)[:2]   # streaming kernel
+    s_x, am_x = dense_maxsim_train(*args, norm=norm, kd=False)[:2]    # tile kernel, all docs
+    am_kd = am_kd.view(Nq, K, Lq)
+    am_x = am_x.view(Nq, Nq * K, Lq)
+    for i in range(Nq):
+        sl = slice(i * K, (i + 1) * K)
+        assert torch.equal(am_kd[i], am_x[i, sl]), i
+        if i == 0:
+            assert torch.equal(s_kd[i], s_x[i, sl])
+        else:
+            # query i is unit i of the cross product's group, whose column
+            # sum starts at 4-column chunk i: the same maxima in another order
+            torch.testing.assert_close(s_kd[i], s_x[i, sl], rtol=1e-6, atol=0)
+    assert s_kd[0, 7].item() == 0.0 and bool((am_kd[0, 7] == -1).all())
+
